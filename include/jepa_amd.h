@@ -1,0 +1,77 @@
+/*
+ * jepa_amd.h - entry points of libjepa.so beyond the reference API (include/jepa.h).
+ *
+ * The reference has no counterpart for these; they exist for callers that keep data on the GPU
+ * (benchmarks, pipelines feeding decoded frames from device memory) and for parity tests that check
+ * one kernel at a time against the CPU oracle. Pointers named *_dev are HIP device pointers on the
+ * given device; every call is synchronous (it returns after its kernels finished) unless stated.
+ * Return values: >= 0 on success, -1 on failure with the reason in jepa_error_text().
+ */
+#pragma once
+#include "jepa.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- encoder on device-resident data -------------------------------------------------------- */
+/* jepa_encode without the host copies: in_dev is the NCTHW float32 input already on the model's
+ * device, out_dev receives [rows, embed_dim] float32 rows (same order as jepa_encode). Replaces the
+ * host-side patchify + tensor_set / tensor_get of reference src/jepa.cpp:990-1019 with device data.
+ * Returns the rows per item (jepa_token_grid) or -1. last_compute_ms is set as for jepa_encode. */
+int64_t jepa_amd_encode_device(jepa_context * ctx, const float * in_dev, int n_batch, int n_chans, int n_frames,
+                               int height, int width, float * out_dev, int64_t out_cap_floats);
+
+/* jepa_encode that also returns the residual stream after the patch embedding and after every
+ * block (before the final norm): trace [n_items][n_layer + 1][rows][dim] on the host. For per-layer
+ * parity checks; runs without graph replay. */
+int64_t jepa_amd_encode_trace(jepa_context * ctx, const jepa_input * in, float * out, int64_t out_cap_floats,
+                              float * trace, int64_t trace_cap_floats);
+
+/* ---- context knobs --------------------------------------------------------------------------- */
+/* Record hipEvents around every kernel launch of the next encodes (disables graph replay) and sum
+ * their device time per kernel class: "patchify", "patch_embed", "layernorm", "gemm_q8",
+ * "gemm_q4k", "gemm_f16", "gemm_f32", "attention", "quantize", "cls". */
+void jepa_amd_context_set_kernel_timing(jepa_context * ctx, bool on);
+int  jepa_amd_context_kernel_stats(const jepa_context * ctx, const char * kernel_class, int64_t * n_launches, double * total_ms);
+void jepa_amd_context_reset_kernel_stats(jepa_context * ctx);
+/* Capture the forward into a hipGraph and replay it (default on; $JEPA_HIP_GRAPH=0 turns it off). */
+void jepa_amd_context_set_graph(jepa_context * ctx, bool on);
+/* The HIP stream (hipStream_t) the context launches on. */
+void * jepa_amd_context_stream(const jepa_context * ctx);
+
+/* ---- single-kernel hooks (parity tests, micro-benchmarks) ------------------------------------ */
+/* ggml to_float of q8_0 / q4_0 / q4_K / f16 rows: blocks_dev holds n_rows rows of n_cols values in
+ * the ggml block layout (ggml_type ids 8 / 2 / 12 / 1). */
+int jepa_amd_dequantize(int device, int ggml_type, const void * blocks_dev, int64_t n_rows, int64_t n_cols, float * y_dev);
+
+/* Row-wise LayerNorm (ggml_norm + optional affine, normalize = 1) or plain conversion (normalize = 0)
+ * of x_dev [n_rows][n_cols], written as out_type: 0 f32 rows, 1 f16 rows, 8 q8_0 blocks (34 B per 32),
+ * 15 q8_K blocks (292 B per 256) in ggml's block layout - the activation quantization the GEMMs
+ * consume (x86 quantize_row_q8_0 / quantize_row_q8_K_ref semantics). */
+int jepa_amd_rownorm(int device, const float * x_dev, int64_t n_rows, int64_t n_cols, const float * w_dev,
+                     const float * b_dev, float eps, int normalize, int out_type, void * out_dev);
+
+/* Y = X W^T (+ bias): W_dev in ggml blocks of wtype (8 q8_0, 2 q4_0, 12 q4_K, 1 f16, 0 f32) [n_out][n_in],
+ * X_dev f32 [n_rows][n_in], Y_dev f32 [n_rows][n_out]; the activations are quantized to the weight's
+ * vec-dot type first, like ggml_mul_mat (reference src/jepa.cpp:365-375). reps > 1 repeats the GEMM
+ * (same result); *gemm_ms (optional) receives the mean device time of one GEMM launch. */
+int jepa_amd_matmul(int device, int wtype, const void * w_dev, int64_t n_out, int64_t n_in, const float * bias_dev,
+                    const float * x_dev, int64_t n_rows, float * y_dev, int reps, double * gemm_ms);
+
+/* Attention of one block from its fused qkv rows: qkv_dev f32 [n_items*n_tok][3*n_head*64] (rows
+ * [q | k | v], head-major), optional RoPE tables rope_c/rope_s [n_tok][64] (signed sine), out_dev f32
+ * [n_items*n_tok][n_head*64]. Runs the QKV epilogue's split/RoPE/f16 cast and the attention kernel. */
+int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64_t n_tok, int n_head,
+                       const float * rope_c_dev, const float * rope_s_dev, float * out_dev);
+
+/* One v_mfma_f32_32x32x16_f16 on host matrices a [32][16], b [16][32] -> d [32][32] (row-major),
+ * written back through the accumulator layout the GEMM epilogues assume. */
+int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * d);
+
+/* Copy of n float32 values between device buffers (a plain copy kernel, for counter calibration). */
+int jepa_amd_copy(int device, const float * src_dev, float * dst_dev, int64_t n, int reps, double * ms);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,251 @@
+// amd_api.cpp - entry points of include/jepa_amd.h (device-resident encode, kernel timing, single-kernel hooks).
+#include "../../include/jepa_amd.h"
+#include "model.h"
+#include "kernels.h"
+
+#include <cstring>
+#include <vector>
+
+namespace {
+
+// scoped device + stream for the synchronous hooks
+struct dev_scope {
+    int prev = 0;
+    hipStream_t s = nullptr;
+    bool ok = false;
+    std::vector<void *> allocs;
+    explicit dev_scope(int device) {
+        hipGetDevice(&prev);
+        if (!dev_check(device)) return;
+        if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+            jepa_log("jepa: cannot use HIP device %d\n", device);
+            return;
+        }
+        ok = true;
+    }
+    void * alloc(size_t bytes) {
+        void * p = nullptr;
+        if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) { jepa_log("jepa: hipMalloc(%zu) failed\n", bytes); return nullptr; }
+        allocs.push_back(p);
+        return p;
+    }
+    int finish() {
+        const hipError_t e = hipStreamSynchronize(s);
+        const hipError_t l = hipGetLastError();
+        if (e != hipSuccess || l != hipSuccess) {
+            jepa_log("jepa: kernel failed: %s\n", hipGetErrorString(e != hipSuccess ? e : l));
+            return -1;
+        }
+        return 0;
+    }
+    ~dev_scope() {
+        if (s) hipStreamSynchronize(s);
+        for (void * p : allocs) hipFree(p);
+        if (s) hipStreamDestroy(s);
+        hipSetDevice(prev);
+    }
+};
+
+bool alloc_act(dev_scope & d, act_view & a, int fmt, int64_t M, int64_t K) {
+    a.fmt = fmt;
+    a.ld = K;
+    a.q = d.alloc((size_t) M * K * 4);
+    a.d = d.alloc((size_t) M * (K / 32) * 4 + 16);
+    a.bsum = d.alloc((size_t) M * (K / 16) * 2 + 16);
+    return a.q && a.d && a.bsum;
+}
+
+}  // namespace
+
+extern "C" int64_t jepa_amd_encode_device(jepa_context * ctx, const float * in_dev, int n_batch, int n_chans, int n_frames,
+                                          int height, int width, float * out_dev, int64_t out_cap) {
+    if (!ctx || !in_dev || !out_dev) return -1;
+    return encode_device(ctx, in_dev, n_batch, n_chans, n_frames, height, width, out_dev, out_cap, nullptr, 0);
+}
+
+extern "C" int64_t jepa_amd_encode_trace(jepa_context * ctx, const jepa_input * in, float * out, int64_t out_cap, float * trace,
+                                         int64_t trace_cap) {
+    if (!ctx || !in || !in->data || !out || !trace) return -1;
+    jepa_model * m = ctx->model;
+    int64_t n_items = 0;
+    const int64_t R = encode_rows(m, in->n_batch, in->n_frames, in->height, in->width, &n_items);
+    if (R <= 0) { jepa_log("jepa: input shape is not encodable by this model\n"); return -1; }
+    const int64_t D = m->hp.enc.embed_dim, L = m->hp.enc.n_layer;
+    if (out_cap < n_items * R * D || trace_cap < n_items * (L + 1) * R * D) { jepa_log("jepa: output / trace buffer too small\n"); return -1; }
+    dev_scope d(ctx->device);
+    if (!d.ok) return -1;
+    const size_t n_in = (size_t) in->n_batch * in->n_chans * in->n_frames * in->height * in->width;
+    float * din = (float *) d.alloc(n_in * 4);
+    float * dout = (float *) d.alloc((size_t) n_items * R * D * 4);
+    float * dtr = (float *) d.alloc((size_t) n_items * (L + 1) * R * D * 4);
+    if (!din || !dout || !dtr) return -1;
+    if (hipMemcpy(din, in->data, n_in * 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    const int64_t r = encode_device(ctx, din, in->n_batch, in->n_chans, in->n_frames, in->height, in->width, dout, n_items * R * D, dtr,
+                                    n_items * (L + 1) * R * D);
+    if (r < 0) return -1;
+    // device trace is [layer][all rows]; the caller wants [item][layer][rows]
+    std::vector<float> tmp((size_t) (L + 1) * n_items * R * D);
+    if (hipMemcpy(tmp.data(), dtr, tmp.size() * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(out, dout, (size_t) n_items * R * D * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    for (int64_t it = 0; it < n_items; it++)
+        for (int64_t l = 0; l <= L; l++)
+            memcpy(trace + ((it * (L + 1) + l) * R) * D, tmp.data() + ((l * n_items + it) * R) * D, (size_t) R * D * 4);
+    return r;
+}
+
+extern "C" void jepa_amd_context_set_kernel_timing(jepa_context * ctx, bool on) { if (ctx) ctx->kernel_timing = on; }
+extern "C" int jepa_amd_context_kernel_stats(const jepa_context * ctx, const char * cls, int64_t * n, double * ms) {
+    if (!ctx || !cls) return -1;
+    auto it = ctx->kstats.find(cls);
+    if (n) *n = it == ctx->kstats.end() ? 0 : it->second.first;
+    if (ms) *ms = it == ctx->kstats.end() ? 0.0 : it->second.second;
+    return 0;
+}
+extern "C" void jepa_amd_context_reset_kernel_stats(jepa_context * ctx) { if (ctx) ctx->kstats.clear(); }
+extern "C" void jepa_amd_context_set_graph(jepa_context * ctx, bool on) { if (ctx) ctx->use_graph = on; }
+extern "C" void * jepa_amd_context_stream(const jepa_context * ctx) { return ctx ? (void *) ctx->stream : nullptr; }
+
+extern "C" int jepa_amd_dequantize(int device, int gtype, const void * blocks, int64_t n_rows, int64_t n_cols, float * y) {
+    if (!blocks || !y || n_rows <= 0 || n_cols <= 0) return -1;
+    const type_traits tt = ggml_traits(gtype);
+    if (!(gtype == T_Q8_0 || gtype == T_Q4_0 || gtype == T_Q4_K || gtype == T_F16 || gtype == T_F32) || n_cols % tt.blck) {
+        jepa_log("jepa: jepa_amd_dequantize: type %d / %lld columns not supported\n", gtype, (long long) n_cols);
+        return -1;
+    }
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    launch_dequant_rows(gtype, blocks, n_rows, n_cols, y, d.s);
+    return d.finish();
+}
+
+extern "C" int jepa_amd_rownorm(int device, const float * x, int64_t n_rows, int64_t n_cols, const float * w, const float * b, float eps,
+                                int normalize, int out_type, void * out) {
+    if (!x || !out || n_rows <= 0 || n_cols <= 0 || n_cols % 8 || n_cols > 2048) {
+        jepa_log("jepa: jepa_amd_rownorm: bad arguments (rows of %lld; 8 | cols <= 2048)\n", (long long) n_cols);
+        return -1;
+    }
+    int fmt;
+    switch (out_type) {
+        case T_F32: fmt = A_F32; break;
+        case T_F16: fmt = A_F16; break;
+        case T_Q8_0: fmt = A_Q8_0; if (n_cols % 32) return -1; break;
+        case T_Q8_K: fmt = A_Q8_K; if (n_cols % 256) return -1; break;
+        default: jepa_log("jepa: jepa_amd_rownorm: output type %d not supported\n", out_type); return -1;
+    }
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    act_view a;
+    if (fmt == A_F32 || fmt == A_F16) { a.fmt = fmt; a.q = out; a.ld = n_cols; }
+    else if (!alloc_act(d, a, fmt, n_rows, n_cols)) return -1;
+    launch_rownorm_quant(x, n_rows, n_cols, w, b, eps, normalize != 0, a, d.s);
+    if (fmt == A_Q8_0 || fmt == A_Q8_K) launch_pack_act_blocks(a, n_rows, n_cols, out, d.s);
+    return d.finish();
+}
+
+extern "C" int jepa_amd_matmul(int device, int wtype, const void * w, int64_t n_out, int64_t n_in, const float * bias, const float * x,
+                               int64_t n_rows, float * y, int reps, double * gemm_ms) {
+    if (!w || !x || !y || n_out <= 0 || n_in <= 0 || n_rows <= 0) return -1;
+    dev_linear L;
+    L.gtype = wtype; L.n_out = n_out; L.n_in = n_in; L.bias = (float *) bias;
+    switch (wtype) {
+        case T_F32: L.fmt = W_F32; break;
+        case T_F16: L.fmt = W_F16; break;
+        case T_Q8_0: case T_Q4_0: L.fmt = W_Q32; break;
+        case T_Q4_K: L.fmt = W_Q4K; break;
+        default: jepa_log("jepa: jepa_amd_matmul: weight type %d not supported\n", wtype); return -1;
+    }
+    if (L.fmt != W_F32 && (n_out % 128 || n_in % 64 || (L.fmt == W_Q4K && n_in % 256))) {
+        jepa_log("jepa: jepa_amd_matmul: [%lld x %lld] not supported by the MFMA GEMM (n_out %% 128, n_in %% 64)\n", (long long) n_out, (long long) n_in);
+        return -1;
+    }
+    if (L.fmt != W_F32 && n_in > 2048 * 8) return -1;
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    if (L.fmt == W_F32 || L.fmt == W_F16) {
+        L.w = (void *) w;
+    } else {
+        L.w = d.alloc((size_t) n_out * n_in * 2);
+        if (L.fmt == W_Q32) L.wd = d.alloc((size_t) n_out * (n_in / 32) * 2);
+        else {
+            L.wd = d.alloc((size_t) n_out * (n_in / 256) * 2);
+            L.wdmin = d.alloc((size_t) n_out * (n_in / 256) * 2);
+            L.wmin = d.alloc((size_t) n_out * (n_in / 256) * 32);
+        }
+        if (!L.w || !L.wd) return -1;
+        launch_repack(wtype, w, n_out, n_in, L.w, L.wd, L.wdmin, L.wmin, d.s);
+    }
+    act_view a;
+    if (!alloc_act(d, a, L.act(), n_rows, n_in)) return -1;
+    launch_rownorm_quant(x, n_rows, n_in, nullptr, nullptr, 0.0f, false, a, d.s);
+    gemm_epi ep;
+    ep.kind = EPI_F32;
+    ep.y = y; ep.ldy = n_out; ep.rin = n_rows; ep.rout = n_rows; ep.pre = 0;
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0); hipEventCreate(&e1);
+    if (reps < 1) reps = 1;
+    launch_gemm(L, a, n_rows, ep, d.s);   // warm-up (and the result when reps == 1)
+    hipEventRecord(e0, d.s);
+    for (int i = 0; i < reps; i++) launch_gemm(L, a, n_rows, ep, d.s);
+    hipEventRecord(e1, d.s);
+    const int rc = d.finish();
+    float ms = 0;
+    hipEventElapsedTime(&ms, e0, e1);
+    if (gemm_ms) *gemm_ms = ms / reps;
+    hipEventDestroy(e0); hipEventDestroy(e1);
+    return rc;
+}
+
+extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items, int64_t n_tok, int n_head, const float * rope_c,
+                                  const float * rope_s, float * out) {
+    if (!qkv || !out || n_items <= 0 || n_tok <= 0 || n_head <= 0) return -1;
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    const int hd = 64;
+    const int64_t R_pad = (n_tok + 127) / 128 * 128;
+    const size_t bytes = (size_t) n_items * n_head * R_pad * hd * 2;
+    void * q = d.alloc(bytes), * k = d.alloc(bytes), * vt = d.alloc(bytes);
+    if (!q || !k || !vt) return -1;
+    launch_fill_zero(q, bytes, d.s);
+    launch_fill_zero(k, bytes, d.s);
+    launch_fill_zero(vt, bytes, d.s);
+    gemm_epi ep;
+    ep.kind = EPI_QKV;
+    ep.q = q; ep.k = k; ep.vt = vt; ep.rope_c = rope_c; ep.rope_s = rope_s;
+    ep.n_head = n_head; ep.hd = hd; ep.D = n_head * hd; ep.R = n_tok; ep.R_pad = R_pad;
+    launch_qkv_split(qkv, n_items * n_tok, (int64_t) 3 * n_head * hd, ep, d.s);
+    launch_attention(q, k, vt, out, n_items, n_head, hd, n_tok, R_pad, 0.125f, d.s);
+    return d.finish();
+}
+
+extern "C" int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * dd) {
+    if (!a || !b || !dd) return -1;
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    float * da = (float *) d.alloc(32 * 16 * 4), * db = (float *) d.alloc(16 * 32 * 4), * dc = (float *) d.alloc(32 * 32 * 4);
+    if (!da || !db || !dc) return -1;
+    hipMemcpy(da, a, 32 * 16 * 4, hipMemcpyHostToDevice);
+    hipMemcpy(db, b, 16 * 32 * 4, hipMemcpyHostToDevice);
+    launch_mfma_probe(da, db, dc, d.s);
+    if (d.finish() != 0) return -1;
+    return hipMemcpy(dd, dc, 32 * 32 * 4, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+
+extern "C" int jepa_amd_copy(int device, const float * src, float * dst, int64_t n, int reps, double * ms) {
+    if (!src || !dst || n <= 0) return -1;
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    if (reps < 1) reps = 1;
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0); hipEventCreate(&e1);
+    launch_copy_f32(src, dst, n, d.s);
+    hipEventRecord(e0, d.s);
+    for (int i = 0; i < reps; i++) launch_copy_f32(src, dst, n, d.s);
+    hipEventRecord(e1, d.s);
+    const int rc = d.finish();
+    float t = 0;
+    hipEventElapsedTime(&t, e0, e1);
+    if (ms) *ms = t / reps;
+    hipEventDestroy(e0); hipEventDestroy(e1);
+    return rc;
+}

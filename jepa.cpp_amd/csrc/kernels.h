@@ -1,0 +1,80 @@
+// kernels.h - launchers of the hand-written gfx950 kernels (host-callable, stream-ordered).
+//
+// Data layouts in HBM (row-major unless stated):
+//   residual stream  x      f32 [rows][D]
+//   GEMM operands    W      f16 [N][K]  integer codes (q8_0 q, q4_0 q-8, q4_K sc*q) or f16 weights
+//                    X      f16 [M][K]  integer codes (q8_0 / q8_K activations) or f16-rounded values
+//   scales           q8_0   f16 [rows][K/32];  q8_K  f32 d [rows][K/256] + f16 bsums [rows][K/16]
+//   attention        Q, K   f16 [item*H][R_pad][hd];  V^T f16 [item*H][hd][R_pad] with the tokens of
+//                    every 16-token group stored in the order the PV MFMA reads them
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+struct act_view {            // a GEMM activation operand / a quantizer output
+    int       fmt = 0;       // afmt
+    void *    q = nullptr;   // f16 [M][K] (A_F16 / A_Q8_*) or f32 [M][K] (A_F32)
+    void *    d = nullptr;   // A_Q8_0: f16 [M][K/32]; A_Q8_K: f32 [M][K/256]
+    void *    bsum = nullptr;// A_Q8_K: f16 [M][K/16]
+    int64_t   ld = 0;        // K
+};
+
+enum epi_kind {
+    EPI_F32 = 0,      // y[map(m)][n] = acc + bias (+ addvec[n]) (+ addrows[pre + m%rin][n])
+    EPI_RESID,        // x[m][n] += (acc + bias) (* ls[n])
+    EPI_GELU_F32,     // y[m][n] = gelu(acc + bias)
+    EPI_GELU_F16,     // oh[m][n] = f16(gelu(acc + bias))
+    EPI_GELU_Q8_0,    // q8_0-quantize gelu(acc + bias) into (oq, od)
+    EPI_QKV,          // split into Q, K (RoPE'd) and V^T f16 attention operands
+};
+
+struct gemm_epi {
+    int kind = EPI_F32;
+    float * y = nullptr; int64_t ldy = 0;
+    int64_t rin = 0, rout = 0, pre = 0;     // EPI_F32 row map: row = (m/rin)*rout + pre + m%rin
+    const float * addvec = nullptr;
+    const float * addrows = nullptr;
+    const float * ls = nullptr;
+    void * oq = nullptr; void * od = nullptr; void * oh = nullptr;
+    // EPI_QKV
+    void * q = nullptr; void * k = nullptr; void * vt = nullptr;
+    const float * rope_c = nullptr; const float * rope_s = nullptr;
+    int n_head = 0, hd = 0, D = 0;
+    int64_t R = 0, R_pad = 0;
+};
+
+struct dev_linear;
+
+// Y = X W^T (+ epilogue). M = rows of X.
+void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm_epi & ep, hipStream_t s);
+
+// LayerNorm (ggml_norm + affine) of x [M][D] written in `out` format; w/b may be null (no affine).
+// out.fmt A_F32 writes f32 rows into out.q. When normalize == false the rows are only quantized.
+void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w, const float * b, float eps,
+                          bool normalize, const act_view & out, hipStream_t s);
+
+// Flash attention over (items*H) heads: O [item*R][H*hd] f32.
+void launch_attention(const void * q, const void * k, const void * vt, float * o, int64_t n_items, int n_head,
+                      int hd, int64_t R, int64_t R_pad, float scale, hipStream_t s);
+
+// Patch rows from NCTHW input: rows [items*Np][C*tub*P*P] in f16 (half_out) or f32.
+void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_items, int C, int T, int H, int W,
+                     int P, int tub, bool video, hipStream_t s);
+
+// prefix (CLS) rows: x[it*R + 0][n] = cls[n] (+ pos[n])
+void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D, hipStream_t s);
+
+// weight expansion at load: raw ggml blocks (device) -> dev_linear operand arrays
+void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd, void * wdmin,
+                   void * wmin, hipStream_t s);
+
+// test hooks
+void launch_qkv_split(const float * qkv, int64_t M, int64_t N, const gemm_epi & ep, hipStream_t s);
+void launch_dequant_rows(int gtype, const void * raw, int64_t n_rows, int64_t n_cols, float * y, hipStream_t s);
+void launch_pack_act_blocks(const act_view & a, int64_t M, int64_t K, void * blocks, hipStream_t s);
+void launch_fill_zero(void * p, size_t bytes, hipStream_t s);
+void launch_copy_f32(const float * src, float * dst, int64_t n, hipStream_t s);
+
+// MFMA layout probe (test hook): D = A * B for 32x32x16 f16 with A [32][16], B [16][32] row-major f32
+// inputs; writes D [32][32] using the register layout the GEMM epilogues assume.
+void launch_mfma_probe(const float * a, const float * b, float * d, hipStream_t s);

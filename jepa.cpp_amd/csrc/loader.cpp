@@ -1,0 +1,429 @@
+// loader.cpp - GGUF -> hparams -> validated weights on one HIP device.
+//
+// Follows reference src/jepa-gguf.cpp: the same jepa.* keys and defaults (254-596), the same range
+// refusals by key name (240-250), the file-extent check before any allocation (821-854), the same
+// tensor presence / shape / dtype rules (631-728, 942-1092). Differences: the tensors go to a HIP
+// device and the matmul weights are expanded into the GEMM kernel's operand layout (dev_linear).
+#include "model.h"
+#include "kernels.h"
+
+#include <cinttypes>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+
+const char * jepa_file_type_name_u32(uint32_t ft) {
+    switch ((int32_t) ft) {   // GGML_FTYPE_* numbering (reference src/jepa-gguf.cpp:62-93)
+        case 0: return "f32";   case 1: return "f16";   case 2: return "q4_0"; case 3: return "q4_1";
+        case 4: return "q4_1_some_f16"; case 7: return "q8_0"; case 8: return "q5_0"; case 9: return "q5_1";
+        case 10: return "q2_k"; case 11: return "q3_k"; case 12: return "q4_k"; case 13: return "q5_k";
+        case 14: return "q6_k"; case 24: return "bf16";
+        default: return "unknown";
+    }
+}
+
+family_id family_from_string(const std::string & s) {
+    if (s == "ijepa") return FAM_IJEPA;
+    if (s == "vjepa") return FAM_VJEPA;
+    if (s == "vjepa2") return FAM_VJEPA2;
+    if (s == "vjepa2_1") return FAM_VJEPA2_1;
+    if (s == "levjepa") return FAM_LEVJEPA;
+    if (s == "hfvit") return FAM_HFVIT;
+    if (s == "lewm") return FAM_LEWM;
+    if (s == "hjepa") return FAM_HJEPA;
+    return FAM_UNKNOWN;
+}
+
+namespace {
+
+struct kv {
+    const gguf::file & f;
+    bool has(const char * k) const { return f.find(k) != nullptr; }
+    int64_t geti(const char * k, int64_t def) const {
+        const gguf::value * v = f.find(k);
+        if (!v || v->type == gguf::STR || v->type == gguf::ARR) return def;
+        return v->i;
+    }
+    bool getb(const char * k, bool def) const { return geti(k, def ? 1 : 0) != 0; }
+    float getf(const char * k, float def) const {
+        const gguf::value * v = f.find(k);
+        if (!v || v->type == gguf::STR || v->type == gguf::ARR) return def;
+        return (float) v->f;
+    }
+    std::string gets(const char * k, const std::string & def) const {
+        const gguf::value * v = f.find(k);
+        return v && v->type == gguf::STR ? v->s : def;
+    }
+    bool farr(const char * k, float * out, size_t n) const {
+        const gguf::value * v = f.find(k);
+        if (!v || v->type != gguf::ARR || v->arr_type == gguf::STR || v->af.size() != n) return false;
+        for (size_t i = 0; i < n; i++) out[i] = (float) v->af[i];
+        return true;
+    }
+};
+
+bool kv_range(const char * key, int64_t v, int64_t lo, int64_t hi) {
+    if (v >= lo && v <= hi) return true;
+    jepa_log("jepa: %s = %" PRId64 " is out of range [%" PRId64 ", %" PRId64 "]\n", key, v, lo, hi);
+    return false;
+}
+
+bool kv_finite(const char * key, float v, float lo, float hi) {
+    if (v >= lo && v <= hi) return true;
+    jepa_log("jepa: %s = %g is not a finite value in [%g, %g]\n", key, (double) v, (double) lo, (double) hi);
+    return false;
+}
+
+bool act_from_string(const std::string & s, act_id & a) {
+    if (s == "gelu_erf" || s == "gelu") { a = ACT_GELU_ERF; return true; }
+    if (s == "gelu_tanh" || s == "gelu_new" || s == "gelu_pytorch_tanh") { a = ACT_GELU_TANH; return true; }
+    if (s == "silu" || s == "swish") { a = ACT_SILU; return true; }
+    if (s == "relu") { a = ACT_RELU; return true; }
+    jepa_log("jepa: unknown activation '%s' (expected gelu_erf | gelu_tanh | silu | relu)\n", s.c_str());
+    return false;
+}
+
+bool hparams_from_gguf(const gguf::file & f, hparams & hp, std::vector<std::pair<std::string, std::string>> & raw) {
+    kv r{f};
+    for (const auto & p : f.kv)
+        if (p.first.rfind("general.", 0) == 0 || p.first.rfind("jepa.", 0) == 0) raw.emplace_back(p.first, p.second.render());
+    hp.arch = r.gets("general.architecture", "");
+    hp.name = r.gets("general.name", "");
+    hp.file_type = (uint32_t) r.geti("general.file_type", 0);
+    if (hp.arch != "jepa") { jepa_log("jepa: general.architecture is '%s', expected 'jepa'\n", hp.arch.c_str()); return false; }
+    hp.family_str = r.gets("jepa.family", "");
+    hp.family = family_from_string(hp.family_str);
+    hp.modality = r.gets("jepa.modality", "image");
+    if (hp.family == FAM_UNKNOWN) { jepa_log("jepa: unknown jepa.family '%s'\n", hp.family_str.c_str()); return false; }
+
+    enc_hparams & e = hp.enc;
+    for (const char * k : {"jepa.enc.embed_dim", "jepa.enc.n_layer", "jepa.enc.n_head", "jepa.enc.ffn_dim", "jepa.enc.patch_size"})
+        if (!r.has(k)) { jepa_log("jepa: missing required key %s\n", k); return false; }
+    const int64_t ed = r.geti("jepa.enc.embed_dim", 0), nl = r.geti("jepa.enc.n_layer", 0), nh = r.geti("jepa.enc.n_head", 0);
+    const int64_t ff = r.geti("jepa.enc.ffn_dim", 0), ps = r.geti("jepa.enc.patch_size", 16), tb = r.geti("jepa.enc.tubelet_size", 1);
+    const int64_t is = r.geti("jepa.enc.img_size", 224), nf = r.geti("jepa.enc.n_frames", 1), ic = r.geti("jepa.enc.in_chans", 3);
+    if (!kv_range("jepa.enc.embed_dim", ed, 1, JEPA_LIMIT_EMBED_DIM) || !kv_range("jepa.enc.n_layer", nl, 1, JEPA_LIMIT_N_LAYER) ||
+        !kv_range("jepa.enc.n_head", nh, 1, JEPA_LIMIT_N_HEAD) || !kv_range("jepa.enc.ffn_dim", ff, 1, JEPA_LIMIT_FFN_DIM) ||
+        !kv_range("jepa.enc.patch_size", ps, 1, JEPA_LIMIT_PATCH_SIZE) || !kv_range("jepa.enc.tubelet_size", tb, 1, JEPA_LIMIT_PATCH_SIZE) ||
+        !kv_range("jepa.enc.img_size", is, 1, JEPA_LIMIT_IMG_SIZE) || !kv_range("jepa.enc.n_frames", nf, 1, JEPA_LIMIT_N_FRAMES) ||
+        !kv_range("jepa.enc.in_chans", ic, 1, JEPA_LIMIT_IN_CHANS)) return false;
+    e.embed_dim = (int) ed; e.n_layer = (int) nl; e.n_head = (int) nh; e.ffn_dim = (int) ff; e.patch_size = (int) ps;
+    e.tubelet_size = (int) tb; e.img_size = (int) is; e.n_frames = (int) nf; e.in_chans = (int) ic;
+    e.ln_eps = r.getf("jepa.enc.ln_eps", 1e-6f);
+    if (!kv_finite("jepa.enc.ln_eps", e.ln_eps, 0.0f, 1.0f)) return false;
+    if (!act_from_string(r.gets("jepa.enc.act", "gelu_erf"), e.act)) return false;
+    e.pos_type = r.gets("jepa.enc.pos_type", "");
+    e.rope_theta = r.getf("jepa.enc.rope_theta", 10000.0f);
+    e.rope_interpolate = r.getb("jepa.enc.rope_interpolate", false);
+    e.rope_freq_layout = r.gets("jepa.enc.rope_freq_layout", "");
+    e.rope_ref_grid = (int) r.geti("jepa.enc.rope_ref_grid", 0);
+    e.cls_token = r.getb("jepa.enc.cls_token", false);
+    const int64_t nreg = r.geti("jepa.enc.n_registers", 0);
+    e.qkv_fused = r.getb("jepa.enc.qkv_fused", true);
+    e.modality_embed = r.getb("jepa.enc.modality_embed", false);
+    e.image_patch_embed = r.getb("jepa.enc.image_patch_embed", false);
+    e.layer_scale = r.getb("jepa.enc.layer_scale", false);
+    e.attn_mode = r.gets("jepa.enc.attn_mode", "full");
+    if (e.attn_mode != "full" && e.attn_mode != "block_causal") {
+        jepa_log("jepa: unknown jepa.enc.attn_mode '%s' (expected full | block_causal)\n", e.attn_mode.c_str());
+        return false;
+    }
+    e.has_proj = r.has("jepa.enc.proj_act");
+    if (!kv_range("jepa.enc.n_registers", nreg, 0, JEPA_LIMIT_N_TOKENS)) return false;
+    e.n_registers = (int) nreg;
+    if (!kv_finite("jepa.enc.rope_theta", e.rope_theta, 1e-6f, 1e12f)) return false;
+    if (!kv_range("jepa.enc.rope_ref_grid", e.rope_ref_grid, 0, JEPA_LIMIT_IMG_SIZE)) return false;
+    if (e.rope_interpolate && e.rope_ref_grid < 1) {
+        jepa_log("jepa: jepa.enc.rope_interpolate is set but jepa.enc.rope_ref_grid is %d - interpolation has no training grid to rescale from\n",
+                 e.rope_ref_grid);
+        return false;
+    }
+    if (e.embed_dim % e.n_head != 0) { jepa_log("jepa: embed_dim %d not divisible by n_head %d\n", e.embed_dim, e.n_head); return false; }
+    const bool rope = is_video_family(hp.family) || hp.family == FAM_LEVJEPA || e.pos_type == "rope3d";
+    if (rope && e.head_dim() % 2 != 0) {
+        jepa_log("jepa: 3-D RoPE rotates pairs, so the encoder head width has to be even; embed_dim %d / n_head %d is %d\n",
+                 e.embed_dim, e.n_head, e.head_dim());
+        return false;
+    }
+    hp.has_pred = r.has("jepa.pred.kind") && r.gets("jepa.pred.kind", "none") != "none";
+    hp.pred_kind = r.gets("jepa.pred.kind", "");
+    hp.head_kind = r.gets("jepa.head.kind", "none");
+    hp.has_head = hp.head_kind != "none" && !hp.head_kind.empty();
+    if (hp.has_head) {
+        hp.n_classes = (int) r.geti("jepa.head.n_classes", 0);
+        const gguf::value * lv = f.find("jepa.head.labels");
+        if (lv && lv->type == gguf::ARR && lv->arr_type == gguf::STR) hp.labels = lv->as;
+        if (!kv_range("jepa.head.n_classes", hp.n_classes, 0, JEPA_LIMIT_N_TOKENS)) return false;
+    }
+    pre_hparams & pre = hp.pre;
+    r.farr("jepa.pre.mean", pre.mean, 3);
+    r.farr("jepa.pre.std", pre.std, 3);
+    pre.resize_short = (int) r.geti("jepa.pre.resize_short", e.img_size);
+    pre.crop = (int) r.geti("jepa.pre.crop", e.img_size);
+    pre.resample = r.gets("jepa.pre.resample", "bilinear");
+    pre.resize_mode = r.gets("jepa.pre.resize_mode", "shortest_edge");
+    pre.rescale = r.getf("jepa.pre.rescale", 1.0f / 255.0f);
+    if (!kv_range("jepa.pre.resize_short", pre.resize_short, 1, JEPA_LIMIT_IMG_SIZE) ||
+        !kv_range("jepa.pre.crop", pre.crop, 0, JEPA_LIMIT_IMG_SIZE) || !kv_finite("jepa.pre.rescale", pre.rescale, 1e-9f, 1e9f))
+        return false;
+    for (int i = 0; i < 3; i++) {
+        if (!kv_finite("jepa.pre.mean", pre.mean[i], -1e6f, 1e6f)) return false;
+        if (!kv_finite("jepa.pre.std", pre.std[i], 1e-9f, 1e6f)) return false;
+    }
+    return true;
+}
+
+struct loader {
+    jepa_model * m;
+    const gguf::file & f;
+    FILE * fp;
+    hipStream_t s;
+    void * staging = nullptr;
+    size_t staging_size = 0;
+    std::vector<uint8_t> host;
+
+    void * dalloc(size_t bytes) {
+        void * p = nullptr;
+        if (bytes == 0) bytes = 16;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            jepa_log("jepa: hipMalloc of %.1f MiB failed on device %d\n", bytes / 1048576.0, m->device);
+            return nullptr;
+        }
+        m->allocations.push_back(p);
+        m->n_bytes_weights += bytes;
+        return p;
+    }
+
+    bool read(const gguf::tensor_info & t) {
+        host.resize(t.nbytes);
+        if (fseeko(fp, (off_t) t.offset, SEEK_SET) != 0 || fread(host.data(), 1, t.nbytes, fp) != t.nbytes) {
+            jepa_log("jepa: short read for tensor %s (%" PRIu64 " bytes @ %" PRIu64 ")\n", t.name.c_str(), t.nbytes, t.offset);
+            return false;
+        }
+        m->n_bytes_file += t.nbytes;
+        return true;
+    }
+
+    bool to_staging(const gguf::tensor_info & t) {
+        if (!read(t)) return false;
+        if (staging_size < t.nbytes) {
+            if (staging) hipFree(staging);
+            staging = nullptr;
+            staging_size = 0;
+            if (hipMalloc(&staging, t.nbytes) != hipSuccess) { jepa_log("jepa: hipMalloc(staging) failed\n"); return false; }
+            staging_size = t.nbytes;
+        }
+        return hipMemcpyAsync(staging, host.data(), t.nbytes, hipMemcpyHostToDevice, s) == hipSuccess &&
+               hipStreamSynchronize(s) == hipSuccess;
+    }
+
+    // an f32 vector of exactly n values (norms, biases, tokens, tables) - src/jepa-gguf.cpp:675-701
+    bool vec(const std::string & name, int64_t n, float ** out, bool required = false) {
+        const gguf::tensor_info * t = f.tensor(name);
+        if (!t) {
+            if (required) { jepa_log("jepa: required tensor '%s' missing from %s\n", name.c_str(), m->path.c_str()); return false; }
+            return true;
+        }
+        if (t->type != T_F32) {
+            jepa_log("jepa: tensor %s is %s, but it is added to or concatenated with the f32 activations and has to be f32 "
+                     "(only the matmul weights may be quantized)\n", name.c_str(), ggml_traits(t->type).name);
+            return false;
+        }
+        int64_t nel = t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3];
+        if (n >= 0 && nel != n) {
+            jepa_log("jepa: tensor %s holds %" PRId64 " values, expected %" PRId64 "\n", name.c_str(), nel, n);
+            return false;
+        }
+        if (!read(*t)) return false;
+        float * d = (float *) dalloc(t->nbytes);
+        if (!d || hipMemcpy(d, host.data(), t->nbytes, hipMemcpyHostToDevice) != hipSuccess) return false;
+        *out = d;
+        return true;
+    }
+
+    bool linear(const std::string & wname, const std::string & bname, int64_t n_in, int64_t n_out, dev_linear & L, bool required) {
+        const gguf::tensor_info * t = f.tensor(wname);
+        if (!t) {
+            if (required) { jepa_log("jepa: required tensor '%s' missing from %s\n", wname.c_str(), m->path.c_str()); return false; }
+            return true;
+        }
+        if (t->ne[0] != n_in || t->ne[1] != n_out || t->ne[2] != 1 || t->ne[3] != 1) {
+            jepa_log("jepa: tensor %s has shape [%" PRId64 ", %" PRId64 "], expected [%" PRId64 ", %" PRId64 "]\n",
+                     wname.c_str(), t->ne[0], t->ne[1], n_in, n_out);
+            return false;
+        }
+        L.gtype = t->type; L.n_in = n_in; L.n_out = n_out;
+        switch (t->type) {
+            case T_F32: L.fmt = W_F32; break;
+            case T_F16: L.fmt = W_F16; break;
+            case T_Q8_0: case T_Q4_0: L.fmt = W_Q32; break;
+            case T_Q4_K: L.fmt = W_Q4K; break;
+            default:
+                jepa_log("jepa: tensor %s has dtype %s, which this engine has no GEMM kernel for "
+                         "(f32, f16, q8_0, q4_0 and q4_K are supported)\n", wname.c_str(), ggml_traits(t->type).name);
+                return false;
+        }
+        if (L.fmt != W_F32 && (n_out % 128 != 0 || n_in % 64 != 0)) {
+            jepa_log("jepa: tensor %s is [%" PRId64 " x %" PRId64 "]: the MFMA GEMM needs rows that are a multiple of 64 and a "
+                     "multiple of 128 outputs\n", wname.c_str(), n_in, n_out);
+            return false;
+        }
+        if (L.fmt == W_F32 && n_out % 4 != 0) {
+            jepa_log("jepa: tensor %s: %" PRId64 " outputs is not a multiple of 4\n", wname.c_str(), n_out);
+            return false;
+        }
+        if (!to_staging(*t)) return false;
+        if (L.fmt == W_F32 || L.fmt == W_F16) {
+            L.w = dalloc(t->nbytes);
+            if (!L.w || hipMemcpyAsync(L.w, staging, t->nbytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
+        } else {
+            L.w = dalloc((size_t) n_in * n_out * 2);
+            if (!L.w) return false;
+            if (L.fmt == W_Q32) {
+                L.wd = dalloc((size_t) n_out * (n_in / 32) * 2);
+                if (!L.wd) return false;
+            } else {
+                L.wd = dalloc((size_t) n_out * (n_in / 256) * 2);
+                L.wdmin = dalloc((size_t) n_out * (n_in / 256) * 2);
+                L.wmin = dalloc((size_t) n_out * (n_in / 256) * 16 * 2);
+                if (!L.wd || !L.wdmin || !L.wmin) return false;
+            }
+            launch_repack(t->type, staging, n_out, n_in, L.w, L.wd, L.wdmin, L.wmin, s);
+        }
+        if (hipStreamSynchronize(s) != hipSuccess) { jepa_log("jepa: weight upload of %s failed\n", wname.c_str()); return false; }
+        return vec(bname, n_out, &L.bias);
+    }
+};
+
+}  // namespace
+
+bool is_video_family(family_id f) { return f == FAM_VJEPA2 || f == FAM_VJEPA2_1; }
+bool is_image_family(family_id f) { return f == FAM_IJEPA || f == FAM_HFVIT || f == FAM_LEWM || f == FAM_HJEPA; }
+
+static void model_free_device(jepa_model * m) {
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(m->device);
+    for (void * p : m->allocations) hipFree(p);
+    m->allocations.clear();
+    hipSetDevice(prev);
+}
+
+extern "C" void jepa_model_free(jepa_model * m) {
+    if (!m) return;
+    model_free_device(m);
+    delete m;
+}
+
+extern "C" jepa_model_params jepa_model_default_params(void) {
+    jepa_model_params p;
+    p.verbose = false;
+    p.device = device_from_env();
+    return p;
+}
+
+extern "C" jepa_model * jepa_model_load(const char * path, bool verbose) {
+    jepa_model_params p = jepa_model_default_params();
+    p.verbose = verbose;
+    return jepa_model_load_ex(path, &p);
+}
+
+extern "C" jepa_model * jepa_model_load_ex(const char * path, const jepa_model_params * params) {
+    if (!path || !*path) { jepa_log("jepa: jepa_model_load: no path given\n"); return nullptr; }
+    const jepa_model_params mp = params ? *params : jepa_model_default_params();
+
+    // the file is parsed and its metadata checked before any device is touched, so a broken file
+    // is refused by name on any machine
+    gguf::file f;
+    std::string err;
+    if (!gguf::open(path, f, err)) { jepa_log("jepa: cannot open GGUF %s: %s\n", path, err.c_str()); return nullptr; }
+    std::unique_ptr<jepa_model> m(new jepa_model());
+    m->path = path;
+    if (!hparams_from_gguf(f, m->hp, m->raw_kv)) return nullptr;
+    const enc_hparams & e = m->hp.enc;
+    // every tensor in a jepa file is a weight, bias or table: float or quantized (src/jepa-gguf.cpp:685-701)
+    for (const auto & t : f.tensors) {
+        if (t.type == T_F32 || t.type == T_F16 || t.type == T_BF16 || ggml_traits(t.type).blck > 1) continue;
+        jepa_log("jepa: tensor %s has dtype %s, which is not a weight dtype\n", t.name.c_str(), ggml_traits(t.type).name);
+        return nullptr;
+    }
+    if (!is_image_family(m->hp.family) && !is_video_family(m->hp.family)) {
+        // the loader accepts the file; jepa_encode reports the family as not implemented on this path
+        if (mp.verbose) jepa_log("jepa: family '%s' has no encoder path in this library\n", m->hp.family_str.c_str());
+    }
+
+    const int device = dev_resolve(mp.device);
+    if (device < 0) return nullptr;
+    m->device = device;
+    if (hipSetDevice(device) != hipSuccess) { jepa_log("jepa: hipSetDevice(%d) failed\n", device); return nullptr; }
+    std::unique_ptr<FILE, int (*)(FILE *)> fp(fopen(path, "rb"), fclose);
+    if (!fp) { jepa_log("jepa: cannot reopen %s for tensor data\n", path); return nullptr; }
+    hipStream_t s = nullptr;
+    if (hipStreamCreate(&s) != hipSuccess) { jepa_log("jepa: hipStreamCreate failed\n"); return nullptr; }
+    loader L{m.get(), f, fp.get(), s};
+    bool ok = true;
+    const int64_t D = e.embed_dim;
+    const int64_t patch_in = (int64_t) e.in_chans * e.tubelet_size * e.patch_size * e.patch_size;
+    const bool video = is_video_family(m->hp.family);
+    const bool encoder = video || is_image_family(m->hp.family);
+    if (!f.tensor("enc.patch_embed.weight")) { jepa_log("jepa: enc.patch_embed.weight missing\n"); ok = false; }
+    if (ok && encoder) {
+        ok = L.linear("enc.patch_embed.weight", "enc.patch_embed.bias", patch_in, D, m->patch, true) &&
+             L.linear("enc.patch_embed_img.weight", "enc.patch_embed_img.bias", (int64_t) e.in_chans * e.patch_size * e.patch_size, D,
+                      m->patch_img, false) &&
+             L.vec("enc.cls_token", D, &m->cls_token) && L.vec("enc.mod_embed_img", D, &m->mod_img) &&
+             L.vec("enc.mod_embed_video", D, &m->mod_video) && L.vec("enc.norm.weight", D, &m->norm_w) &&
+             L.vec("enc.norm.bias", D, &m->norm_b);
+        if (ok && f.tensor("enc.pos_embed")) {
+            const gguf::tensor_info * t = f.tensor("enc.pos_embed");
+            if (t->ne[0] != D) { jepa_log("jepa: tensor enc.pos_embed has rows of %" PRId64 ", expected %" PRId64 "\n", t->ne[0], D); ok = false; }
+            else if (!kv_range("enc.pos_embed rows", t->ne[1], 1, JEPA_LIMIT_N_TOKENS)) ok = false;
+            else { m->pos_rows = t->ne[1]; ok = L.vec("enc.pos_embed", -1, &m->pos_embed); }
+        }
+        if (ok && e.cls_token && !m->cls_token) { jepa_log("jepa: cls_token=true but enc.cls_token missing\n"); ok = false; }
+        if (ok && e.n_registers > 0) {
+            jepa_log("jepa: jepa.enc.n_registers = %d: register tokens are not implemented on this path\n", e.n_registers);
+            ok = false;
+        }
+        if (ok && !e.qkv_fused) { jepa_log("jepa: separate attn_q/k/v weights are not implemented on this path (qkv_fused = false)\n"); ok = false; }
+        m->layers.resize((size_t) e.n_layer);
+        for (int i = 0; i < e.n_layer && ok; i++) {
+            const std::string p = "enc.blk." + std::to_string(i) + ".";
+            dev_layer & Ly = m->layers[(size_t) i];
+            if (!f.tensor(p + "ln1.weight") || !f.tensor(p + "ln2.weight") || !f.tensor(p + "attn_out.weight") || !f.tensor(p + "ffn_up.weight") ||
+                !f.tensor(p + "ffn_down.weight") || !f.tensor(p + "attn_qkv.weight")) {
+                jepa_log("jepa: block %d is incomplete (enc.blk.%d.*): needs ln1/ln2/attn_out/ffn_up/ffn_down and attn_qkv\n", i, i);
+                ok = false;
+                break;
+            }
+            ok = L.vec(p + "ln1.weight", D, &Ly.ln1_w) && L.vec(p + "ln1.bias", D, &Ly.ln1_b) &&
+                 L.vec(p + "ln2.weight", D, &Ly.ln2_w) && L.vec(p + "ln2.bias", D, &Ly.ln2_b) &&
+                 L.vec(p + "ls1", D, &Ly.ls1) && L.vec(p + "ls2", D, &Ly.ls2) &&
+                 L.linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * D, Ly.qkv, true) &&
+                 L.linear(p + "attn_out.weight", p + "attn_out.bias", D, D, Ly.out, true) &&
+                 L.linear(p + "ffn_up.weight", p + "ffn_up.bias", D, e.ffn_dim, Ly.up, true) &&
+                 L.linear(p + "ffn_down.weight", p + "ffn_down.bias", e.ffn_dim, D, Ly.down, true);
+        }
+        if (ok && e.modality_embed && video && !m->mod_video) {
+            jepa_log("jepa: jepa.enc.modality_embed is set but enc.mod_embed_video is missing\n");
+            ok = false;
+        }
+    }
+    if (L.staging) hipFree(L.staging);
+    hipStreamDestroy(s);
+    if (!ok) {
+        model_free_device(m.get());
+        return nullptr;
+    }
+    if (mp.verbose) {
+        hipDeviceProp_t prop;
+        hipGetDeviceProperties(&prop, device);
+        jepa_log("jepa: loaded %s: family=%s name='%s' ftype=%s D=%d L=%d H=%d ffn=%d patch=%d tubelet=%d img=%d on HIP%d (%s), "
+                 "%.1f MiB of device weights\n", path, m->hp.family_str.c_str(), m->hp.name.c_str(), jepa_file_type_name_u32(m->hp.file_type),
+                 e.embed_dim, e.n_layer, e.n_head, e.ffn_dim, e.patch_size, e.tubelet_size, e.img_size, device, prop.name,
+                 m->n_bytes_weights / 1048576.0);
+    }
+    return m.release();
+}

@@ -1,0 +1,413 @@
+// misc.hip - bandwidth-bound kernels: LayerNorm + activation quantization, patchify, prefix rows,
+// load-time weight expansion, and small test hooks.
+#include "kernels.h"
+#include "model.h"
+
+#include <hip/hip_fp16.h>
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+namespace {
+
+__device__ __forceinline__ uint16_t f2hbits(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
+__device__ __forceinline__ float h2f(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
+
+// ------------------------------------------------------------------------------------------------
+// Row kernel: one wave per row of D floats; lane owns octets o = lane + 64*i (8 consecutive values),
+// so a q8_0 block (32 values) is 4 adjacent lanes and a q8_K block (256) is 32 adjacent lanes.
+//   LayerNorm = ggml_norm (mean, centred variance, both accumulated in double like ggml_float)
+//   followed by * w and + b (reference src/jepa.cpp:356-361), then the output conversion:
+//   A_Q8_0: d = amax/127 (f16), q = rne(x * 127/amax)        x86 quantize_row_q8_0
+//   A_Q8_K: max = first largest-|x| value, iscale = -127/max, q = min(127, rne(iscale*x)),
+//           d = 1/iscale (f32), bsums of 16                  quantize_row_q8_K_ref
+// ------------------------------------------------------------------------------------------------
+constexpr int MAXOCT = 4;   // D <= 2048
+
+template <int OUT, bool NORM>
+__global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, int64_t M, int64_t D,
+                                                 const float * __restrict__ w, const float * __restrict__ b, float eps,
+                                                 act_view out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int n_oct = (int) (D / 8);
+    const float * xr = x + row * D;
+    float v[MAXOCT][8];
+#pragma unroll
+    for (int i = 0; i < MAXOCT; i++) {
+        const int o = lane + 64 * i;
+        if (o < n_oct) {
+            const float4 a = *(const float4 *) (xr + 8 * o), c = *(const float4 *) (xr + 8 * o + 4);
+            v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w; v[i][4] = c.x; v[i][5] = c.y; v[i][6] = c.z; v[i][7] = c.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[i][e] = 0.0f;
+        }
+    }
+    if constexpr (NORM) {
+        double s = 0.0;
+#pragma unroll
+        for (int i = 0; i < MAXOCT; i++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) s += (double) v[i][e];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        const float mean = (float) s / (float) D;
+        double s2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < MAXOCT; i++) {
+            const bool live = lane + 64 * i < n_oct;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float t = __fsub_rn(v[i][e], mean);
+                v[i][e] = t;
+                if (live) s2 += (double) __fmul_rn(t, t);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s2 += __shfl_xor(s2, off);
+        const float var = (float) (s2 / (double) D);
+        const float scale = 1.0f / sqrtf(__fadd_rn(var, eps));
+#pragma unroll
+        for (int i = 0; i < MAXOCT; i++) {
+            const int o = lane + 64 * i;
+            if (o >= n_oct) continue;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float t = __fmul_rn(v[i][e], scale);
+                if (w) t = __fmul_rn(t, w[8 * o + e]);
+                if (b) t = __fadd_rn(t, b[8 * o + e]);
+                v[i][e] = t;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXOCT; i++) {
+        const int o = lane + 64 * i;
+        const bool live = o < n_oct;
+        if (i * 64 >= n_oct) break;   // uniform across the wave
+        if constexpr (OUT == A_F32) {
+            if (live) {
+                float * dst = (float *) out.q + row * D + 8 * o;
+                *(float4 *) dst = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+                *(float4 *) (dst + 4) = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+            }
+        } else if constexpr (OUT == A_F16) {
+            if (live) {
+                h8 hv;
+#pragma unroll
+                for (int e = 0; e < 8; e++) hv[e] = (_Float16) v[i][e];
+                *(h8 *) ((_Float16 *) out.q + row * D + 8 * o) = hv;
+            }
+        } else if constexpr (OUT == A_Q8_0) {
+            float am = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) am = fmaxf(am, fabsf(v[i][e]));
+            am = fmaxf(am, __shfl_xor(am, 1));
+            am = fmaxf(am, __shfl_xor(am, 2));
+            const float d = am / 127.0f;
+            const float id = am != 0.0f ? 127.0f / am : 0.0f;
+            if (live) {
+                h8 hv;
+#pragma unroll
+                for (int e = 0; e < 8; e++) hv[e] = (_Float16) fminf(fmaxf(rintf(v[i][e] * id), -128.0f), 127.0f);
+                *(h8 *) ((_Float16 *) out.q + row * D + 8 * o) = hv;
+                if ((o & 3) == 0) ((uint16_t *) out.d)[row * (D / 32) + o / 4] = f2hbits(d);
+            }
+        } else {   // A_Q8_K
+            // largest |x| of the 256-block, first occurrence in element order
+            float am = 0.0f, mx = 0.0f;
+            int idx = 1 << 30;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float ax = fabsf(v[i][e]);
+                if (ax > am) { am = ax; mx = v[i][e]; idx = (lane & 31) * 8 + e; }
+            }
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) {
+                const float am2 = __shfl_xor(am, off), mx2 = __shfl_xor(mx, off);
+                const int idx2 = __shfl_xor(idx, off);
+                if (am2 > am || (am2 == am && idx2 < idx)) { am = am2; mx = mx2; idx = idx2; }
+            }
+            float q[8];
+            float d = 0.0f;
+            if (am != 0.0f) {
+                const float iscale = -127.0f / mx;
+#pragma unroll
+                for (int e = 0; e < 8; e++) q[e] = fminf(rintf(iscale * v[i][e]), 127.0f);
+                d = 1.0f / iscale;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) q[e] = 0.0f;
+            }
+            float bs = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) bs += q[e];
+            bs += __shfl_xor(bs, 1);
+            if (live) {
+                h8 hv;
+#pragma unroll
+                for (int e = 0; e < 8; e++) hv[e] = (_Float16) q[e];
+                *(h8 *) ((_Float16 *) out.q + row * D + 8 * o) = hv;
+                if ((o & 31) == 0) ((float *) out.d)[row * (D / 256) + o / 32] = d;
+                if ((o & 1) == 0) ((_Float16 *) out.bsum)[row * (D / 16) + o / 2] = (_Float16) bs;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// patchify (reference src/jepa.cpp:476-504): token order t, h, w; inner order c, tt, py, px.
+// One thread per (row, c, tt, py) copies P consecutive pixels.
+// ------------------------------------------------------------------------------------------------
+template <bool HALF>
+__global__ void k_patchify(const float * __restrict__ in, void * __restrict__ rows, int64_t n_items, int C, int T, int H,
+                           int W, int P, int tub, int video) {
+    const int GT = video ? T / tub : 1, GH = H / P, GW = W / P;
+    const int64_t Np = (int64_t) GT * GH * GW;
+    const int64_t K = (int64_t) C * tub * P * P;
+    const int64_t total = n_items * Np * C * tub * P;
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    int64_t r = id;
+    const int py = (int) (r % P); r /= P;
+    const int tt = (int) (r % tub); r /= tub;
+    const int c = (int) (r % C); r /= C;
+    const int64_t tok = r % Np; const int64_t item = r / Np;
+    const int t = (int) (tok / (GH * GW)), hh = (int) ((tok / GW) % GH), ww = (int) (tok % GW);
+    int64_t b, f;
+    if (video) { b = item; f = (int64_t) t * tub + tt; }
+    else { b = item / T; f = item % T; }
+    const float * src = in + (((b * C + c) * T + f) * H + (int64_t) hh * P + py) * W + (int64_t) ww * P;
+    const int64_t off = (item * Np + tok) * K + ((int64_t) (c * tub + tt) * P + py) * P;
+    if (HALF) {
+        _Float16 * dst = (_Float16 *) rows + off;
+        for (int px = 0; px < P; px++) dst[px] = (_Float16) src[px];
+    } else {
+        float * dst = (float *) rows + off;
+        for (int px = 0; px < P; px++) dst[px] = src[px];
+    }
+}
+
+__global__ void k_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D) {
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= n_items * D) return;
+    const int64_t it = id / D, n = id % D;
+    float v = cls[n];
+    if (pos) v = __fadd_rn(v, pos[n]);
+    x[it * R * D + n] = v;
+}
+
+// ------------------------------------------------------------------------------------------------
+// weight expansion at load (ggml blocks -> GEMM operand arrays)
+// ------------------------------------------------------------------------------------------------
+__global__ void k_repack_q8_0(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint16_t * wd) {
+    const int64_t nb = n_in / 32;
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= n_out * nb) return;
+    const uint8_t * blk = raw + id * 34;
+    wd[id] = (uint16_t) (blk[0] | (blk[1] << 8));
+    const int64_t n = id / nb, bi = id % nb;
+    _Float16 * dst = w + n * n_in + bi * 32;
+    for (int j = 0; j < 32; j++) dst[j] = (_Float16) (float) (int8_t) blk[2 + j];
+}
+
+__global__ void k_repack_q4_0(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint16_t * wd) {
+    const int64_t nb = n_in / 32;
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= n_out * nb) return;
+    const uint8_t * blk = raw + id * 18;
+    wd[id] = (uint16_t) (blk[0] | (blk[1] << 8));
+    const int64_t n = id / nb, bi = id % nb;
+    _Float16 * dst = w + n * n_in + bi * 32;
+    for (int j = 0; j < 16; j++) {
+        dst[j]      = (_Float16) (float) ((blk[2 + j] & 0xF) - 8);
+        dst[j + 16] = (_Float16) (float) ((blk[2 + j] >> 4) - 8);
+    }
+}
+
+__device__ __forceinline__ void q4k_scale_min(int j, const uint8_t * q, int & d, int & m) {
+    if (j < 4) { d = q[j] & 63; m = q[j + 4] & 63; }
+    else { d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4); m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4); }
+}
+
+__global__ void k_repack_q4_K(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint16_t * wd,
+                              uint16_t * wdmin, _Float16 * wmin) {
+    const int64_t nsb = n_in / 256;
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= n_out * nsb) return;
+    const int64_t n = id / nsb, sb = id % nsb;
+    const uint8_t * blk = raw + id * 144;
+    wd[sb * n_out + n] = (uint16_t) (blk[0] | (blk[1] << 8));
+    wdmin[sb * n_out + n] = (uint16_t) (blk[2] | (blk[3] << 8));
+    const uint8_t * sc = blk + 4;
+    const uint8_t * qs = blk + 16;
+    _Float16 * dst = w + n * n_in + sb * 256;
+    for (int j = 0; j < 8; j++) {
+        int s, m;
+        q4k_scale_min(j, sc, s, m);
+        wmin[id * 16 + 2 * j] = (_Float16) (float) m;
+        wmin[id * 16 + 2 * j + 1] = (_Float16) (float) m;
+        const uint8_t * qq = qs + 32 * (j / 2);
+        for (int l = 0; l < 32; l++) {
+            const int q = (j & 1) ? (qq[l] >> 4) : (qq[l] & 0xF);
+            dst[32 * j + l] = (_Float16) (float) (s * q);
+        }
+    }
+}
+
+// ggml to_float of the block types (test hook for bit-exact dequantization)
+__global__ void k_dequant(int gtype, const uint8_t * __restrict__ raw, int64_t n_rows, int64_t n_cols, float * y) {
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = n_rows * n_cols;
+    if (id >= total) return;
+    const int64_t r = id / n_cols, c = id % n_cols;
+    if (gtype == T_Q8_0) {
+        const uint8_t * blk = raw + (r * (n_cols / 32) + c / 32) * 34;
+        y[id] = __fmul_rn((float) (int8_t) blk[2 + c % 32], h2f((uint16_t) (blk[0] | (blk[1] << 8))));
+    } else if (gtype == T_Q4_0) {
+        const uint8_t * blk = raw + (r * (n_cols / 32) + c / 32) * 18;
+        const int j = (int) (c % 32);
+        const int q = j < 16 ? (blk[2 + j] & 0xF) : (blk[2 + j - 16] >> 4);
+        y[id] = __fmul_rn((float) (q - 8), h2f((uint16_t) (blk[0] | (blk[1] << 8))));
+    } else if (gtype == T_Q4_K) {
+        const uint8_t * blk = raw + (r * (n_cols / 256) + c / 256) * 144;
+        const int e = (int) (c % 256), j = e / 32, l = e % 32;
+        int s, m;
+        q4k_scale_min(j, blk + 4, s, m);
+        const uint8_t qq = blk[16 + 32 * (j / 2) + l];
+        const int q = (j & 1) ? (qq >> 4) : (qq & 0xF);
+        const float d = h2f((uint16_t) (blk[0] | (blk[1] << 8))), dmin = h2f((uint16_t) (blk[2] | (blk[3] << 8)));
+        y[id] = __fsub_rn(__fmul_rn(__fmul_rn(d, (float) s), (float) q), __fmul_rn(dmin, (float) m));
+    } else if (gtype == T_F16) {
+        y[id] = h2f(((const uint16_t *) raw)[id]);
+    } else {
+        y[id] = ((const float *) raw)[id];
+    }
+}
+
+// activation operand (f16 codes + scales) -> ggml block bytes (q8_0: 34 B, q8_K: 292 B)
+__global__ void k_pack_act(act_view a, int64_t M, int64_t K, uint8_t * out) {
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (a.fmt == A_Q8_0) {
+        const int64_t nb = K / 32;
+        if (id >= M * nb) return;
+        const int64_t m = id / nb, bi = id % nb;
+        uint8_t * o = out + id * 34;
+        const uint16_t d = ((const uint16_t *) a.d)[m * nb + bi];
+        o[0] = (uint8_t) (d & 0xFF); o[1] = (uint8_t) (d >> 8);
+        for (int j = 0; j < 32; j++) o[2 + j] = (uint8_t) (int8_t) (float) ((const _Float16 *) a.q)[m * K + bi * 32 + j];
+    } else if (a.fmt == A_Q8_K) {
+        const int64_t nb = K / 256;
+        if (id >= M * nb) return;
+        const int64_t m = id / nb, bi = id % nb;
+        uint8_t * o = out + id * 292;
+        const float d = ((const float *) a.d)[m * nb + bi];
+        const uint32_t db = __builtin_bit_cast(uint32_t, d);
+        for (int k = 0; k < 4; k++) o[k] = (uint8_t) (db >> (8 * k));
+        for (int j = 0; j < 256; j++) o[4 + j] = (uint8_t) (int8_t) (float) ((const _Float16 *) a.q)[m * K + bi * 256 + j];
+        for (int j = 0; j < 16; j++) {
+            const int16_t s = (int16_t) (float) ((const _Float16 *) a.bsum)[m * (K / 16) + bi * 16 + j];
+            o[260 + 2 * j] = (uint8_t) (s & 0xFF); o[261 + 2 * j] = (uint8_t) ((uint16_t) s >> 8);
+        }
+    }
+}
+
+__global__ void k_fill_zero(uint32_t * p, size_t n) {
+    const size_t id = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id < n) p[id] = 0;
+}
+
+__global__ void k_copy_f32(const float * __restrict__ src, float * __restrict__ dst, int64_t n) {
+    const int64_t id = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (id + 3 < n) *(float4 *) (dst + id) = *(const float4 *) (src + id);
+    else for (int64_t i = id; i < n; i++) dst[i] = src[i];
+}
+
+// D = A . B with one v_mfma_f32_32x32x16_f16, stored with the (row, col) <- (lane, reg) map the
+// GEMM epilogues rely on: row = 8*(r/4) + 4*(lane/32) + r%4, col = lane%32.
+__global__ void k_mfma_probe(const float * a, const float * b, float * d) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, g = lane >> 5;
+    h8 av, bv;
+    for (int s = 0; s < 8; s++) {
+        av[s] = (_Float16) a[l32 * 16 + 8 * g + s];      // A[i][k]
+        bv[s] = (_Float16) b[(8 * g + s) * 32 + l32];    // B[k][j]
+    }
+    const f16v z = {0};
+    const f16v r = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, z, 0, 0, 0);
+    for (int k = 0; k < 16; k++) d[(8 * (k / 4) + 4 * g + (k % 4)) * 32 + l32] = r[k];
+}
+
+inline unsigned nblk(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
+
+}  // namespace
+
+void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w, const float * b, float eps,
+                          bool normalize, const act_view & out, hipStream_t s) {
+    if (M <= 0) return;
+    if (!normalize && D > 64 * 8 * MAXOCT) {
+        // Plain conversion of rows longer than a wave holds: quantization blocks (32 / 256 values)
+        // never straddle a chunk of c columns when c is a multiple of 256 dividing D, and [M][D] is
+        // [M*D/c][c] in memory for the codes, the scales and the block sums alike.
+        int64_t c = 64 * 8 * MAXOCT;
+        while (c >= 256 && (D % c != 0 || c % 256 != 0)) c -= 256;
+        if (c >= 256) { M = M * (D / c); D = c; }
+    }
+    const dim3 grid(nblk(M, 4));
+#define RN(OUT) (normalize ? (void) k_rownorm<OUT, true><<<grid, 256, 0, s>>>(x, M, D, w, b, eps, out) \
+                           : (void) k_rownorm<OUT, false><<<grid, 256, 0, s>>>(x, M, D, w, b, eps, out))
+    switch (out.fmt) {
+        case A_F32:  RN(A_F32); break;
+        case A_F16:  RN(A_F16); break;
+        case A_Q8_0: RN(A_Q8_0); break;
+        case A_Q8_K: RN(A_Q8_K); break;
+    }
+#undef RN
+}
+
+void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_items, int C, int T, int H, int W, int P,
+                     int tub, bool video, hipStream_t s) {
+    const int GT = video ? T / tub : 1;
+    const int64_t total = n_items * (int64_t) GT * (H / P) * (W / P) * C * tub * P;
+    if (half_out) k_patchify<true><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, video ? 1 : 0);
+    else k_patchify<false><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, video ? 1 : 0);
+}
+
+void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D, hipStream_t s) {
+    k_cls_rows<<<nblk(n_items * D, 256), 256, 0, s>>>(x, cls, pos, n_items, R, D);
+}
+
+void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd, void * wdmin, void * wmin,
+                   hipStream_t s) {
+    switch (gtype) {
+        case T_Q8_0: k_repack_q8_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (_Float16 *) w, (uint16_t *) wd); break;
+        case T_Q4_0: k_repack_q4_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (_Float16 *) w, (uint16_t *) wd); break;
+        case T_Q4_K: k_repack_q4_K<<<nblk(n_out * (n_in / 256), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (_Float16 *) w,
+                                                                                  (uint16_t *) wd, (uint16_t *) wdmin, (_Float16 *) wmin); break;
+        default: break;
+    }
+}
+
+void launch_dequant_rows(int gtype, const void * raw, int64_t n_rows, int64_t n_cols, float * y, hipStream_t s) {
+    k_dequant<<<nblk(n_rows * n_cols, 256), 256, 0, s>>>(gtype, (const uint8_t *) raw, n_rows, n_cols, y);
+}
+
+void launch_pack_act_blocks(const act_view & a, int64_t M, int64_t K, void * blocks, hipStream_t s) {
+    const int64_t nb = a.fmt == A_Q8_K ? M * (K / 256) : M * (K / 32);
+    k_pack_act<<<nblk(nb, 256), 256, 0, s>>>(a, M, K, (uint8_t *) blocks);
+}
+
+void launch_fill_zero(void * p, size_t bytes, hipStream_t s) {
+    const size_t n = bytes / 4;
+    if (n) k_fill_zero<<<nblk((int64_t) n, 256), 256, 0, s>>>((uint32_t *) p, n);
+}
+
+void launch_copy_f32(const float * src, float * dst, int64_t n, hipStream_t s) {
+    k_copy_f32<<<nblk((n + 3) / 4, 256), 256, 0, s>>>(src, dst, n);
+}
+
+void launch_mfma_probe(const float * a, const float * b, float * d, hipStream_t s) {
+    k_mfma_probe<<<1, 64, 0, s>>>(a, b, d);
+}

@@ -1,0 +1,218 @@
+"""ctypes binding of libjepa.so (the role of the reference's python/src/jepa_cpp/_lib.py + _api.py).
+
+Loads the in-tree library built by `make -C jepa.cpp_amd`; there is no fallback: if the library is
+missing, every call fails loudly."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.abspath(os.path.join(PKG_DIR, "..", ".."))       # jepa.cpp_amd/
+LIB_PATH = os.path.join(ROOT, "libjepa.so")
+
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q8_K = 0, 1, 2, 8, 12, 15
+
+
+class ContextParams(C.Structure):
+    _fields_ = [("n_threads", C.c_int), ("use_flash_attn", C.c_bool), ("verbose", C.c_bool), ("flash_kv", C.c_int)]
+
+
+class Input(C.Structure):
+    _fields_ = [("data", C.POINTER(C.c_float)), ("n_batch", C.c_int), ("n_chans", C.c_int), ("n_frames", C.c_int),
+                ("height", C.c_int), ("width", C.c_int)]
+
+
+class Output(C.Structure):
+    _fields_ = [("data", C.POINTER(C.c_float)), ("n_tokens", C.c_int64), ("dim", C.c_int64)]
+
+
+class ModelParams(C.Structure):
+    _fields_ = [("verbose", C.c_bool), ("device", C.c_int)]
+
+
+class PreprocessParams(C.Structure):
+    _fields_ = [("mean", C.c_float * 3), ("std", C.c_float * 3), ("resize_short", C.c_int), ("crop", C.c_int),
+                ("resample", C.c_int), ("resize_mode", C.c_int), ("rescale", C.c_float), ("fused_norm", C.c_bool)]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C {ROOT}` (or __graft_entry__.build())")
+    L = C.CDLL(LIB_PATH)
+    vp, i64, cp = C.c_void_p, C.c_int64, C.c_char_p
+    sig = {
+        "jepa_version": (cp, []),
+        "jepa_error_reset": (None, []),
+        "jepa_error_text": (cp, []),
+        "jepa_context_default_params": (ContextParams, []),
+        "jepa_model_default_params": (ModelParams, []),
+        "jepa_model_load": (vp, [cp, C.c_bool]),
+        "jepa_model_load_ex": (vp, [cp, C.POINTER(ModelParams)]),
+        "jepa_model_free": (None, [vp]),
+        "jepa_context_new": (vp, [vp, ContextParams]),
+        "jepa_context_free": (None, [vp]),
+        "jepa_context_last_compute_ms": (C.c_double, [vp]),
+        "jepa_context_set_max_batch": (None, [vp, C.c_int]),
+        "jepa_context_last_batch": (C.c_int, [vp]),
+        "jepa_encode": (C.c_int, [vp, C.POINTER(Input), C.POINTER(Output)]),
+        "jepa_free": (None, [vp]),
+        "jepa_token_grid": (i64, [vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "jepa_model_embed_dim": (C.c_int, [vp]),
+        "jepa_model_n_layer": (C.c_int, [vp]),
+        "jepa_model_n_head": (C.c_int, [vp]),
+        "jepa_model_family": (cp, [vp]),
+        "jepa_model_name": (cp, [vp]),
+        "jepa_model_file_type": (C.c_int, [vp]),
+        "jepa_model_file_type_name": (cp, [vp]),
+        "jepa_model_n_bytes": (C.c_size_t, [vp]),
+        "jepa_model_has_cls": (C.c_bool, [vp]),
+        "jepa_model_n_prefix_tokens": (C.c_int, [vp]),
+        "jepa_model_device": (C.c_int, [vp]),
+        "jepa_model_device_name": (cp, [vp]),
+        "jepa_device_count": (C.c_int, []),
+        "jepa_device_name": (cp, [C.c_int]),
+        "jepa_device_description": (cp, [C.c_int]),
+        "jepa_preprocess_default_params": (PreprocessParams, [vp]),
+        "jepa_pool_mean": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
+        "jepa_pool_cls": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
+        "jepa_softmax": (None, [vp, C.c_int, vp]),
+        "jepa_top_k": (C.c_int, [vp, C.c_int, C.c_int, vp]),
+        "jepa_head": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
+        # jepa_amd.h
+        "jepa_amd_encode_device": (i64, [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64]),
+        "jepa_amd_encode_trace": (i64, [vp, C.POINTER(Input), vp, i64, vp, i64]),
+        "jepa_amd_context_set_kernel_timing": (None, [vp, C.c_bool]),
+        "jepa_amd_context_kernel_stats": (C.c_int, [vp, cp, C.POINTER(i64), C.POINTER(C.c_double)]),
+        "jepa_amd_context_reset_kernel_stats": (None, [vp]),
+        "jepa_amd_context_set_graph": (None, [vp, C.c_bool]),
+        "jepa_amd_context_stream": (vp, [vp]),
+        "jepa_amd_dequantize": (C.c_int, [C.c_int, C.c_int, vp, i64, i64, vp]),
+        "jepa_amd_rownorm": (C.c_int, [C.c_int, vp, i64, i64, vp, vp, C.c_float, C.c_int, C.c_int, vp]),
+        "jepa_amd_matmul": (C.c_int, [C.c_int, C.c_int, vp, i64, i64, vp, vp, i64, vp, C.c_int, C.POINTER(C.c_double)]),
+        "jepa_amd_attention": (C.c_int, [C.c_int, vp, i64, i64, C.c_int, vp, vp, vp]),
+        "jepa_amd_mfma_probe": (C.c_int, [C.c_int, vp, vp, vp]),
+        "jepa_amd_copy": (C.c_int, [C.c_int, vp, vp, i64, C.c_int, C.POINTER(C.c_double)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def error_text() -> str:
+    return (lib().jepa_error_text() or b"").decode(errors="replace")
+
+
+def check(rc, what: str):
+    if rc is None or (isinstance(rc, int) and rc < 0):
+        raise RuntimeError(f"{what} failed: {error_text().strip()}")
+    return rc
+
+
+def fptr(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+class Model:
+    def __init__(self, path: str, device: int = 0, verbose: bool = False):
+        L = lib()
+        L.jepa_error_reset()
+        p = ModelParams(verbose, device)
+        self.ptr = L.jepa_model_load_ex(path.encode(), C.byref(p))
+        if not self.ptr:
+            raise RuntimeError(f"jepa_model_load_ex({path}) failed: {error_text().strip()}")
+        self.dim = L.jepa_model_embed_dim(self.ptr)
+        self.n_layer = L.jepa_model_n_layer(self.ptr)
+
+    def token_grid(self, n_frames, h, w) -> int:
+        return int(lib().jepa_token_grid(self.ptr, n_frames, h, w, None, None, None))
+
+    def close(self):
+        if self.ptr:
+            lib().jepa_model_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, model: Model):
+        L = lib()
+        self.model = model
+        self.ptr = L.jepa_context_new(model.ptr, L.jepa_context_default_params())
+        if not self.ptr:
+            raise RuntimeError(f"jepa_context_new failed: {error_text().strip()}")
+
+    def encode(self, x: np.ndarray) -> np.ndarray:
+        """x: NCTHW float32 -> [rows, dim] float32 (jepa_encode)."""
+        L = lib()
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        B, Cc, T, H, W = x.shape
+        inp = Input(fptr(x), B, Cc, T, H, W)
+        out = Output()
+        L.jepa_error_reset()
+        check(L.jepa_encode(self.ptr, C.byref(inp), C.byref(out)), "jepa_encode")
+        y = np.ctypeslib.as_array(out.data, shape=(out.n_tokens, out.dim)).copy()
+        L.jepa_free(C.cast(out.data, C.c_void_p))
+        return y
+
+    def encode_trace(self, x: np.ndarray, n_items: int, rows: int):
+        L = lib()
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        B, Cc, T, H, W = x.shape
+        D, nl = self.model.dim, self.model.n_layer
+        out = np.zeros((n_items * rows, D), np.float32)
+        tr = np.zeros((n_items, nl + 1, rows, D), np.float32)
+        inp = Input(fptr(x), B, Cc, T, H, W)
+        L.jepa_error_reset()
+        check(L.jepa_amd_encode_trace(self.ptr, C.byref(inp), out.ctypes.data, out.size, tr.ctypes.data, tr.size), "jepa_amd_encode_trace")
+        return out, tr
+
+    def encode_device(self, in_ptr: int, shape, out_ptr: int, out_cap: int) -> int:
+        B, Cc, T, H, W = shape
+        return check(lib().jepa_amd_encode_device(self.ptr, in_ptr, B, Cc, T, H, W, out_ptr, out_cap), "jepa_amd_encode_device")
+
+    @property
+    def last_compute_ms(self) -> float:
+        return float(lib().jepa_context_last_compute_ms(self.ptr))
+
+    def set_kernel_timing(self, on: bool):
+        lib().jepa_amd_context_set_kernel_timing(self.ptr, on)
+
+    def kernel_stats(self, cls: str):
+        n = C.c_int64(0)
+        ms = C.c_double(0)
+        lib().jepa_amd_context_kernel_stats(self.ptr, cls.encode(), C.byref(n), C.byref(ms))
+        return int(n.value), float(ms.value)
+
+    def reset_kernel_stats(self):
+        lib().jepa_amd_context_reset_kernel_stats(self.ptr)
+
+    def set_graph(self, on: bool):
+        lib().jepa_amd_context_set_graph(self.ptr, on)
+
+    def close(self):
+        if self.ptr:
+            lib().jepa_context_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,204 @@
+"""Synthetic (random-init) jepa GGUF models for the encoder configurations.
+
+Tensor names, shapes, dtypes and metadata keys follow the reference schema (docs/gguf-schema.md:18-96)
+and its quantization rule (docs/gguf-schema.md "Quantization rules", tools/jepa-quantize.cpp:91-129):
+only the 2-D block matrices (attn_qkv, attn_out, ffn_up, ffn_down) take the file type, with the
+per-tensor K-quant fallback to q4_0 when the row length is not a multiple of 256; patch embeddings
+are F16 in video-family files and F32 in hfvit files (the converters' choice), everything else F32.
+
+Weights are N(0, 0.02) from a seeded numpy PCG64 generator. LayerNorm gamma/beta are 1/0 unless
+`ln_random` is set (then 1 + N(0, 0.1) / N(0, 0.1), which exercises the affine terms).
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass, replace
+
+import numpy as np
+
+from .gguf import (FTYPE, GGML_F16, GGML_F32, GGML_Q4_0, GGML_Q4_K, GGML_Q8_0, GGUFWriter, quantize)
+
+
+@dataclass(frozen=True)
+class EncoderConfig:
+    name: str
+    family: str            # hfvit | vjepa2 | vjepa2_1
+    embed_dim: int
+    n_layer: int
+    n_head: int
+    ffn_dim: int
+    patch: int = 16
+    tubelet: int = 1
+    img_size: int = 224
+    n_frames: int = 1
+    cls_token: bool = False
+    ftype: str = "q8_0"     # f16 | q8_0 | q4_0 | q4_k
+    rope_layout: str = ""   # tiled | interleaved ('' for non-rope families)
+    rope_interpolate: bool = False
+    rope_ref_grid: int = 0
+    modality_embed: bool = False
+    image_patch_embed: bool = False
+    layer_scale: bool = False
+    ln_random: bool = False
+    seed: int = 1234
+
+
+# The five configurations the benchmark and parity tests are quoted on.
+CONFIGS = {
+    # LeJEPA ViT-S/16 224x224, hfvit (CLS + learned position table), f16 weights
+    "vits16_f16": EncoderConfig("lejepa-vits16-synthetic", "hfvit", 384, 12, 6, 1536, patch=16, img_size=224,
+                                cls_token=True, ftype="f16"),
+    # V-JEPA 2.1 ViT-B/16 384x384 image path (1x16x16 tokenizer, image modality vector, interleaved RoPE)
+    "vitb16_2_1_q8_0": EncoderConfig("vjepa2_1-vitb16-384-synthetic", "vjepa2_1", 768, 12, 12, 3072, patch=16,
+                                     tubelet=2, img_size=384, n_frames=64, ftype="q8_0", rope_layout="interleaved",
+                                     rope_interpolate=True, rope_ref_grid=16, modality_embed=True,
+                                     image_patch_embed=True),
+    # V-JEPA 2 ViT-L/16 256x256, 16 frames (2048 tokens), tiled RoPE
+    "vitl16_q8_0": EncoderConfig("vjepa2-vitl16-256-synthetic", "vjepa2", 1024, 24, 16, 4096, patch=16, tubelet=2,
+                                 img_size=256, n_frames=16, ftype="q8_0", rope_layout="tiled"),
+    "vitl16_q4_k": EncoderConfig("vjepa2-vitl16-256-synthetic", "vjepa2", 1024, 24, 16, 4096, patch=16, tubelet=2,
+                                 img_size=256, n_frames=16, ftype="q4_k", rope_layout="tiled"),
+    # V-JEPA 2 ViT-g/16 256x256, 64 frames (8192 tokens)
+    "vitg16_q8_0": EncoderConfig("vjepa2-vitg16-256-synthetic", "vjepa2", 1408, 40, 22, 6144, patch=16, tubelet=2,
+                                 img_size=256, n_frames=64, ftype="q8_0", rope_layout="tiled"),
+}
+
+
+def tiny(family: str, ftype: str, **kw) -> EncoderConfig:
+    """Small models for parity tests (seconds on the oracle)."""
+    if family == "hfvit":
+        base = EncoderConfig("tiny-hfvit", "hfvit", 128, 2, 2, 512, patch=16, img_size=64, cls_token=True, ftype=ftype)
+    elif family == "vjepa2":
+        base = EncoderConfig("tiny-vjepa2", "vjepa2", 128, 2, 2, 512, patch=16, tubelet=2, img_size=64, n_frames=4,
+                             ftype=ftype, rope_layout="tiled")
+    elif family == "vjepa2_1":
+        base = EncoderConfig("tiny-vjepa2_1", "vjepa2_1", 128, 2, 2, 512, patch=16, tubelet=2, img_size=64,
+                             n_frames=4, ftype=ftype, rope_layout="interleaved", rope_interpolate=True,
+                             rope_ref_grid=16, modality_embed=True, image_patch_embed=True)
+    else:
+        raise ValueError(family)
+    return replace(base, **kw)
+
+
+_QTYPE = {"f16": GGML_F16, "q8_0": GGML_Q8_0, "q4_0": GGML_Q4_0, "q4_k": GGML_Q4_K, "f32": GGML_F32}
+
+
+def _block_type(cfg: EncoderConfig, n_in: int) -> int:
+    t = _QTYPE[cfg.ftype]
+    if t == GGML_Q4_K and n_in % 256:
+        return GGML_Q4_0          # K-quant fallback (tools/jepa-quantize.cpp:70-77)
+    return t
+
+
+def write_model(cfg: EncoderConfig, path: str) -> str:
+    """Write the synthetic GGUF for `cfg` to `path` (returns path)."""
+    rng = np.random.default_rng(cfg.seed)
+    D, F = cfg.embed_dim, cfg.ffn_dim
+    video = cfg.family in ("vjepa2", "vjepa2_1")
+    w = GGUFWriter()
+    w.add("general.architecture", "jepa")
+    w.add("general.name", cfg.name)
+    w.add("general.file_type", FTYPE[cfg.ftype])
+    w.add("jepa.schema_version", 1)
+    w.add("jepa.family", cfg.family)
+    w.add("jepa.modality", "video" if video else "image")
+    w.add("jepa.enc.embed_dim", D)
+    w.add("jepa.enc.n_layer", cfg.n_layer)
+    w.add("jepa.enc.n_head", cfg.n_head)
+    w.add("jepa.enc.ffn_dim", F)
+    w.add("jepa.enc.patch_size", cfg.patch)
+    w.add("jepa.enc.tubelet_size", cfg.tubelet)
+    w.add("jepa.enc.img_size", cfg.img_size)
+    w.add("jepa.enc.n_frames", cfg.n_frames)
+    w.add("jepa.enc.in_chans", 3)
+    w.add("jepa.enc.ln_eps", 1e-6)
+    w.add("jepa.enc.act", "gelu_erf")
+    w.add("jepa.enc.pos_type", "rope3d" if video else "learned")
+    if video:
+        w.add("jepa.enc.rope_theta", 10000.0)
+        w.add("jepa.enc.rope_freq_layout", cfg.rope_layout)
+        w.add("jepa.enc.rope_interpolate", cfg.rope_interpolate)
+        if cfg.rope_ref_grid:
+            w.add("jepa.enc.rope_ref_grid", cfg.rope_ref_grid)
+    w.add("jepa.enc.cls_token", cfg.cls_token)
+    w.add("jepa.enc.n_registers", 0)
+    w.add("jepa.enc.qkv_fused", True)
+    w.add("jepa.enc.modality_embed", cfg.modality_embed)
+    w.add("jepa.enc.image_patch_embed", cfg.image_patch_embed)
+    w.add("jepa.enc.layer_scale", cfg.layer_scale)
+    w.add("jepa.pre.mean", [0.485, 0.456, 0.406])
+    w.add("jepa.pre.std", [0.229, 0.224, 0.225])
+    w.add("jepa.pre.resize_short", cfg.img_size)
+    w.add("jepa.pre.crop", cfg.img_size)
+    w.add("jepa.pre.resample", "bilinear")
+    w.add("jepa.pre.rescale", 1.0 / 255.0)
+
+    def normal(*shape, std=0.02):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+    def mat(name, n_out, n_in, gtype):
+        x = normal(n_out, n_in)
+        w.add_tensor(name, gtype, (n_in, n_out), quantize(gtype, x))
+
+    def vec(name, n, value=None, std=0.02):
+        x = np.full(n, value, dtype=np.float32) if value is not None else normal(n, std=std)
+        w.add_tensor(name, GGML_F32, (n,), x)
+
+    def ln(prefix):
+        if cfg.ln_random:
+            w.add_tensor(prefix + ".weight", GGML_F32, (D,), (1.0 + normal(D, std=0.1)).astype(np.float32))
+            vec(prefix + ".bias", D, std=0.1)
+        else:
+            vec(prefix + ".weight", D, 1.0)
+            vec(prefix + ".bias", D, 0.0)
+
+    patch_type = GGML_F16 if video else GGML_F32
+    if cfg.ftype == "f32":
+        patch_type = GGML_F32
+    kin = 3 * cfg.tubelet * cfg.patch * cfg.patch
+    mat("enc.patch_embed.weight", D, kin, patch_type)
+    vec("enc.patch_embed.bias", D)
+    if cfg.image_patch_embed:
+        mat("enc.patch_embed_img.weight", D, 3 * cfg.patch * cfg.patch, patch_type)
+        vec("enc.patch_embed_img.bias", D)
+    if cfg.modality_embed:
+        vec("enc.mod_embed_img", D)
+        vec("enc.mod_embed_video", D)
+    if cfg.cls_token:
+        vec("enc.cls_token", D)
+    if not video:
+        n_tok = (cfg.img_size // cfg.patch) ** 2 + (1 if cfg.cls_token else 0)
+        w.add_tensor("enc.pos_embed", GGML_F32, (D, n_tok), normal(n_tok, D))
+    for i in range(cfg.n_layer):
+        p = f"enc.blk.{i}."
+        ln(p + "ln1")
+        mat(p + "attn_qkv.weight", 3 * D, D, _block_type(cfg, D))
+        vec(p + "attn_qkv.bias", 3 * D)
+        mat(p + "attn_out.weight", D, D, _block_type(cfg, D))
+        vec(p + "attn_out.bias", D)
+        ln(p + "ln2")
+        mat(p + "ffn_up.weight", F, D, _block_type(cfg, D))
+        vec(p + "ffn_up.bias", F)
+        mat(p + "ffn_down.weight", D, F, _block_type(cfg, F))
+        vec(p + "ffn_down.bias", D)
+        if cfg.layer_scale:
+            vec(p + "ls1", D, std=0.1)
+            vec(p + "ls2", D, std=0.1)
+    ln("enc.norm")
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    w.write(path)
+    return path
+
+
+def cached_model(cfg: EncoderConfig, cache_dir: str | None = None) -> str:
+    """Path of the synthetic GGUF for cfg, written once per (config, cache dir)."""
+    cache_dir = cache_dir or os.environ.get("JEPA_AMD_MODEL_CACHE", "/tmp/jepa_amd_models")
+    key = "_".join(str(getattr(cfg, f)) for f in cfg.__dataclass_fields__)
+    import hashlib
+    h = hashlib.sha1(key.encode()).hexdigest()[:12]
+    path = os.path.join(cache_dir, f"{cfg.name}-{cfg.ftype}-{h}.gguf")
+    if not os.path.exists(path):
+        tmp = path + f".tmp{os.getpid()}"
+        write_model(cfg, tmp)
+        os.replace(tmp, path)
+    return path

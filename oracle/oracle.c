@@ -1,0 +1,923 @@
+/*
+ * oracle.c - CPU restatement of jepa.cpp's encoder path with ggml CPU semantics (test infrastructure).
+ *
+ * See oracle.h for the scope. Reference citations are into aselimc/jepa.cpp; the ggml behaviour
+ * restated here is that of ggml @36da5713 (v0.22.0) on x86 as described in the reference's docs
+ * (docs/ggml-notes.md, docs/parity.md) and in ggml's public block layouts (ggml-common.h).
+ *
+ * Build: oracle/Makefile (gcc -O3 -march=x86-64-v3 -ffp-contract=off -fopenmp). Floating-point
+ * contraction is off so every rounding is the one written here; FMAs are explicit (fmaf).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define QK8_0 32
+#define QK4_0 32
+#define QK_K 256
+
+typedef struct { uint16_t d; int8_t qs[QK8_0]; } blk_q8_0;                 /* 34 B */
+typedef struct { uint16_t d; uint8_t qs[QK4_0 / 2]; } blk_q4_0;            /* 18 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; } blk_q4_K;  /* 144 B */
+typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_K;         /* 292 B */
+
+_Static_assert(sizeof(blk_q8_0) == 34, "q8_0 block");
+_Static_assert(sizeof(blk_q4_0) == 18, "q4_0 block");
+_Static_assert(sizeof(blk_q4_K) == 144, "q4_K block");
+_Static_assert(sizeof(blk_q8_K) == 292, "q8_K block");
+
+/* ------------------------------------------------------------------------------------------------
+ * IEEE binary16 <-> binary32, round to nearest even (what F16C's vcvtps2ph with imm 0 does, which is
+ * ggml's GGML_FP32_TO_FP16 on x86). Written from the IEEE-754 definition.
+ * ---------------------------------------------------------------------------------------------- */
+uint16_t or_fp32_to_fp16(float f) {
+    uint32_t x; memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {                       /* inf / nan */
+        return (uint16_t) (sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u | ((ax >> 13) & 0x3ffu) : 0));
+    }
+    if (ax >= 0x477ff000u) return (uint16_t) (sign | 0x7c00u);   /* >= 65520 rounds to inf */
+    if (ax < 0x38800000u) {                        /* below 2^-14: subnormal half (or zero) */
+        if (ax < 0x33000000u) return (uint16_t) sign;            /* < 2^-25 rounds to 0 (ties to even 0) */
+        const uint32_t e = ax >> 23;               /* biased exponent, 102..112 */
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126 - e;            /* value = m * 2^(e-150); half ulp unit 2^-24 */
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1);
+        const uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return (uint16_t) (sign | q);
+    }
+    /* normal range */
+    uint32_t h = ((ax >> 13) - (112u << 10));      /* rebias exponent 127 -> 15 */
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) h++;
+    return (uint16_t) (sign | h);
+}
+
+float or_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t) (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    const uint32_t m = h & 0x3ffu;
+    uint32_t x;
+    if (e == 0) {
+        if (m == 0) x = sign;
+        else {                                     /* subnormal: normalise */
+            int sh = 0; uint32_t mm = m;
+            while (!(mm & 0x400u)) { mm <<= 1; sh++; }
+            x = sign | ((uint32_t) (113 - sh) << 23) | ((mm & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else {
+        x = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f; memcpy(&f, &x, 4);
+    return f;
+}
+
+void or_fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n) { for (int64_t i = 0; i < n; i++) y[i] = or_fp32_to_fp16(x[i]); }
+void or_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n) { for (int64_t i = 0; i < n; i++) y[i] = or_fp16_to_fp32(x[i]); }
+
+size_t or_row_size(int type, int64_t n) {
+    switch (type) {
+        case OR_F32:  return (size_t) n * 4;
+        case OR_F16:  return (size_t) n * 2;
+        case OR_Q8_0: return n % QK8_0 ? 0 : (size_t) (n / QK8_0) * sizeof(blk_q8_0);
+        case OR_Q4_0: return n % QK4_0 ? 0 : (size_t) (n / QK4_0) * sizeof(blk_q4_0);
+        case OR_Q4_K: return n % QK_K ? 0 : (size_t) (n / QK_K) * sizeof(blk_q4_K);
+        case OR_Q8_K: return n % QK_K ? 0 : (size_t) (n / QK_K) * sizeof(blk_q8_K);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * quantizers
+ * ---------------------------------------------------------------------------------------------- */
+/* ggml quantize_row_q8_0_ref: d = amax/127, id = 1/d, q = roundf(x*id) (half away from zero).
+ * This is what ggml_quantize_chunk -> quantize_q8_0 writes into a q8_0 GGUF (tools/jepa-quantize.cpp:171). */
+void or_quantize_q8_0_ref(const float * x, void * vb, int64_t n) {
+    blk_q8_0 * y = (blk_q8_0 *) vb;
+    for (int64_t i = 0; i < n / QK8_0; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK8_0; j++) amax = fmaxf(amax, fabsf(x[i * QK8_0 + j]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = or_fp32_to_fp16(d);
+        for (int j = 0; j < QK8_0; j++) y[i].qs[j] = (int8_t) roundf(x[i * QK8_0 + j] * id);
+    }
+}
+
+/* ggml quantize_row_q4_0_ref: d = max/-8 (max = the signed value of largest magnitude),
+ * q = min(15, (int8)(x/d + 8.5)); low nibbles hold elements 0..15, high nibbles 16..31. */
+void or_quantize_q4_0_ref(const float * x, void * vb, int64_t n) {
+    blk_q4_0 * y = (blk_q4_0 *) vb;
+    for (int64_t i = 0; i < n / QK4_0; i++) {
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < QK4_0; j++) {
+            const float v = x[i * QK4_0 + j];
+            if (amax < fabsf(v)) { amax = fabsf(v); max = v; }
+        }
+        const float d = max / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = or_fp32_to_fp16(d);
+        for (int j = 0; j < QK4_0 / 2; j++) {
+            const float x0 = x[i * QK4_0 + j] * id;
+            const float x1 = x[i * QK4_0 + QK4_0 / 2 + j] * id;
+            int8_t t0 = (int8_t) (x0 + 8.5f), t1 = (int8_t) (x1 + 8.5f);
+            const uint8_t q0 = (uint8_t) (t0 < 15 ? t0 : 15), q1 = (uint8_t) (t1 < 15 ? t1 : 15);
+            y[i].qs[j] = (uint8_t) (q0 | (q1 << 4));
+        }
+    }
+}
+
+/* ggml nearest_int: round half to even through the 1.5*2^23 magic (valid for |v| < 2^22). */
+static inline int nearest_int(float v) {
+    float val = v + 12582912.0f;
+    int32_t i; memcpy(&i, &val, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+/* q4_K writer (not ggml's make_qkx2_quants search: a plain per-sub-block min/max fit). The format it
+ * produces is the ggml q4_K layout, which is all the dequantizer and the dot depend on. */
+void or_quantize_q4_K(const float * x, void * vb, int64_t n) {
+    blk_q4_K * y = (blk_q4_K *) vb;
+    for (int64_t i = 0; i < n / QK_K; i++) {
+        const float * xb = x + i * QK_K;
+        float scales[8], mins[8], max_scale = 0.0f, max_min = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            float mn = xb[32 * j], mx = xb[32 * j];
+            for (int l = 1; l < 32; l++) { mn = fminf(mn, xb[32 * j + l]); mx = fmaxf(mx, xb[32 * j + l]); }
+            if (mn > 0.0f) mn = 0.0f;
+            scales[j] = (mx - mn) / 15.0f;
+            mins[j] = -mn;
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        const float inv_scale = max_scale > 0 ? 63.0f / max_scale : 0.0f;
+        const float inv_min = max_min > 0 ? 63.0f / max_min : 0.0f;
+        uint8_t ls[8], lm[8];
+        for (int j = 0; j < 8; j++) {
+            int a = nearest_int(inv_scale * scales[j]); ls[j] = (uint8_t) (a < 0 ? 0 : a > 63 ? 63 : a);
+            int b = nearest_int(inv_min * mins[j]);     lm[j] = (uint8_t) (b < 0 ? 0 : b > 63 ? 63 : b);
+        }
+        memset(y[i].scales, 0, 12);
+        for (int j = 0; j < 8; j++) {
+            if (j < 4) { y[i].scales[j] = ls[j]; y[i].scales[j + 4] = lm[j]; }
+            else {
+                y[i].scales[j + 4] = (uint8_t) ((ls[j] & 0xF) | ((lm[j] & 0xF) << 4));
+                y[i].scales[j - 4] |= (uint8_t) ((ls[j] >> 4) << 6);
+                y[i].scales[j - 0] |= (uint8_t) ((lm[j] >> 4) << 6);
+            }
+        }
+        y[i].d = or_fp32_to_fp16(max_scale / 63.0f);
+        y[i].dmin = or_fp32_to_fp16(max_min / 63.0f);
+        const float d = or_fp16_to_fp32(y[i].d), dmin = or_fp16_to_fp32(y[i].dmin);
+        uint8_t L[QK_K];
+        for (int j = 0; j < 8; j++) {
+            const float dd = d * ls[j], dm = dmin * lm[j];
+            for (int l = 0; l < 32; l++) {
+                int q = dd != 0.0f ? nearest_int((xb[32 * j + l] + dm) / dd) : 0;
+                L[32 * j + l] = (uint8_t) (q < 0 ? 0 : q > 15 ? 15 : q);
+            }
+        }
+        for (int j = 0; j < QK_K; j += 64)
+            for (int l = 0; l < 32; l++) y[i].qs[j / 2 + l] = (uint8_t) (L[j + l] | (L[j + l + 32] << 4));
+    }
+}
+
+/* Activation q8_0 as the x86 CPU backend computes it inside mul_mat (quantize_row_q8_0, AVX2 path):
+ *   amax = max|x|, d = amax / 127 (stored f16), id = amax != 0 ? 127 / amax : 0,
+ *   q = round-to-nearest-even(x * id)   (_mm256_round_ps(_MM_ROUND_NEAREST), then packs)        */
+void or_quantize_q8_0_act(const float * x, void * vb, int64_t n) {
+    blk_q8_0 * y = (blk_q8_0 *) vb;
+    for (int64_t i = 0; i < n / QK8_0; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK8_0; j++) amax = fmaxf(amax, fabsf(x[i * QK8_0 + j]));
+        const float d = amax / 127.0f;
+        y[i].d = or_fp32_to_fp16(d);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        for (int j = 0; j < QK8_0; j++) {
+            float v = rintf(x[i * QK8_0 + j] * id);           /* default rounding mode: half even */
+            if (v > 127.0f) v = 127.0f;
+            if (v < -128.0f) v = -128.0f;
+            y[i].qs[j] = (int8_t) v;
+        }
+    }
+}
+
+/* Activation q8_K (quantize_row_q8_K_ref, which is what the x86 build uses):
+ *   max = signed value of largest |x|, iscale = -127/max, q = min(127, nearest_int(iscale*x)),
+ *   bsums = sums of 16 consecutive q, d = 1/iscale (f32). An all-zero block gives d = 0, q = 0. */
+void or_quantize_q8_K_act(const float * x, void * vb, int64_t n) {
+    blk_q8_K * y = (blk_q8_K *) vb;
+    for (int64_t i = 0; i < n / QK_K; i++) {
+        const float * xb = x + i * QK_K;
+        float max = 0.0f, amax = 0.0f;
+        for (int j = 0; j < QK_K; j++) {
+            const float ax = fabsf(xb[j]);
+            if (ax > amax) { amax = ax; max = xb[j]; }
+        }
+        if (amax == 0.0f) { memset(&y[i], 0, sizeof(blk_q8_K)); continue; }
+        const float iscale = -127.0f / max;
+        for (int j = 0; j < QK_K; j++) {
+            const int v = nearest_int(iscale * xb[j]);
+            y[i].qs[j] = (int8_t) (v < 127 ? v : 127);
+        }
+        for (int j = 0; j < QK_K / 16; j++) {
+            int s = 0;
+            for (int l = 0; l < 16; l++) s += y[i].qs[16 * j + l];
+            y[i].bsums[j] = (int16_t) s;
+        }
+        y[i].d = 1.0f / iscale;
+    }
+}
+
+static inline void q4k_scale_min(int j, const uint8_t * q, uint8_t * d, uint8_t * m) {
+    if (j < 4) { *d = q[j] & 63; *m = q[j + 4] & 63; }
+    else {
+        *d = (uint8_t) ((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t) ((q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4));
+    }
+}
+
+void or_dequantize(int type, const void * vb, float * y, int64_t n) {
+    switch (type) {
+        case OR_F32: memcpy(y, vb, (size_t) n * 4); return;
+        case OR_F16: or_fp16_to_fp32_row((const uint16_t *) vb, y, n); return;
+        case OR_Q8_0: {
+            const blk_q8_0 * b = (const blk_q8_0 *) vb;
+            for (int64_t i = 0; i < n / QK8_0; i++) {
+                const float d = or_fp16_to_fp32(b[i].d);
+                for (int j = 0; j < QK8_0; j++) y[i * QK8_0 + j] = b[i].qs[j] * d;
+            }
+            return;
+        }
+        case OR_Q4_0: {
+            const blk_q4_0 * b = (const blk_q4_0 *) vb;
+            for (int64_t i = 0; i < n / QK4_0; i++) {
+                const float d = or_fp16_to_fp32(b[i].d);
+                for (int j = 0; j < QK4_0 / 2; j++) {
+                    y[i * QK4_0 + j]             = ((b[i].qs[j] & 0xF) - 8) * d;
+                    y[i * QK4_0 + j + QK4_0 / 2] = ((b[i].qs[j] >> 4) - 8) * d;
+                }
+            }
+            return;
+        }
+        case OR_Q4_K: {
+            const blk_q4_K * b = (const blk_q4_K *) vb;
+            for (int64_t i = 0; i < n / QK_K; i++) {
+                const float d = or_fp16_to_fp32(b[i].d), dmin = or_fp16_to_fp32(b[i].dmin);
+                const uint8_t * q = b[i].qs;
+                float * yy = y + i * QK_K;
+                for (int j = 0, is = 0; j < QK_K; j += 64, is += 2, q += 32) {
+                    uint8_t sc, m;
+                    q4k_scale_min(is, b[i].scales, &sc, &m);
+                    const float d1 = d * sc, m1 = dmin * m;
+                    q4k_scale_min(is + 1, b[i].scales, &sc, &m);
+                    const float d2 = d * sc, m2 = dmin * m;
+                    for (int l = 0; l < 32; l++) *yy++ = d1 * (q[l] & 0xF) - m1;
+                    for (int l = 0; l < 32; l++) *yy++ = d2 * (q[l] >> 4) - m2;
+                }
+            }
+            return;
+        }
+        case OR_Q8_K: {
+            const blk_q8_K * b = (const blk_q8_K *) vb;
+            for (int64_t i = 0; i < n / QK_K; i++)
+                for (int j = 0; j < QK_K; j++) y[i * QK_K + j] = b[i].d * b[i].qs[j];
+            return;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * dots: exact integer sums per block, float epilogue per block (vec_dot_q8_0_q8_0 etc.)
+ * ---------------------------------------------------------------------------------------------- */
+static float dot_f32_8acc(const float * a, const float * b, int64_t n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+    float s = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+    for (; i < n; i++) s = fmaf(a[i], b[i], s);
+    return s;
+}
+
+float or_vec_dot(int wtype, int64_t n, const void * wrow, const void * arow) {
+    switch (wtype) {
+        case OR_F32: return dot_f32_8acc((const float *) wrow, (const float *) arow, n);
+        case OR_F16: {
+            /* both rows f16: widen and accumulate in f32 (ggml_vec_dot_f16) */
+            const uint16_t * w = (const uint16_t *) wrow; const uint16_t * a = (const uint16_t *) arow;
+            float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            int64_t i = 0;
+            for (; i + 8 <= n; i += 8)
+                for (int l = 0; l < 8; l++) acc[l] = fmaf(or_fp16_to_fp32(w[i + l]), or_fp16_to_fp32(a[i + l]), acc[l]);
+            float s = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+            for (; i < n; i++) s = fmaf(or_fp16_to_fp32(w[i]), or_fp16_to_fp32(a[i]), s);
+            return s;
+        }
+        case OR_Q8_0: {
+            const blk_q8_0 * x = (const blk_q8_0 *) wrow; const blk_q8_0 * y = (const blk_q8_0 *) arow;
+            float s = 0.0f;
+            for (int64_t b = 0; b < n / QK8_0; b++) {
+                int32_t si = 0;
+                for (int j = 0; j < QK8_0; j++) si += (int32_t) x[b].qs[j] * (int32_t) y[b].qs[j];
+                const float d = or_fp16_to_fp32(x[b].d) * or_fp16_to_fp32(y[b].d);
+                s = fmaf((float) si, d, s);
+            }
+            return s;
+        }
+        case OR_Q4_0: {
+            const blk_q4_0 * x = (const blk_q4_0 *) wrow; const blk_q8_0 * y = (const blk_q8_0 *) arow;
+            float s = 0.0f;
+            for (int64_t b = 0; b < n / QK4_0; b++) {
+                int32_t si = 0;
+                for (int j = 0; j < QK4_0 / 2; j++) {
+                    si += ((x[b].qs[j] & 0xF) - 8) * (int32_t) y[b].qs[j];
+                    si += ((x[b].qs[j] >> 4) - 8) * (int32_t) y[b].qs[j + QK4_0 / 2];
+                }
+                const float d = or_fp16_to_fp32(x[b].d) * or_fp16_to_fp32(y[b].d);
+                s = fmaf((float) si, d, s);
+            }
+            return s;
+        }
+        case OR_Q4_K: {
+            const blk_q4_K * x = (const blk_q4_K *) wrow; const blk_q8_K * y = (const blk_q8_K *) arow;
+            float s = 0.0f, sm = 0.0f;
+            for (int64_t b = 0; b < n / QK_K; b++) {
+                int32_t isum = 0, msum = 0;
+                const uint8_t * q4 = x[b].qs; const int8_t * q8 = y[b].qs;
+                for (int j = 0; j < 8; j++) {
+                    uint8_t sc, m;
+                    q4k_scale_min(j, x[b].scales, &sc, &m);
+                    const uint8_t * qq = q4 + 32 * (j / 2);
+                    int32_t si = 0;
+                    for (int l = 0; l < 32; l++) {
+                        const int v = (j & 1) ? (qq[l] >> 4) : (qq[l] & 0xF);
+                        si += v * (int32_t) q8[32 * j + l];
+                    }
+                    isum += (int32_t) sc * si;
+                    msum += (int32_t) m * ((int32_t) y[b].bsums[2 * j] + (int32_t) y[b].bsums[2 * j + 1]);
+                }
+                s  = fmaf(or_fp16_to_fp32(x[b].d) * y[b].d, (float) isum, s);
+                sm = fmaf(or_fp16_to_fp32(x[b].dmin) * y[b].d, (float) msum, sm);
+            }
+            return s - sm;
+        }
+    }
+    return 0.0f;
+}
+
+/* ggml_compute_forward_mul_mat: src1 rows converted to the weight's vec_dot_type once, then one
+ * vec_dot per output element; ggml_add of the bias afterwards (src/jepa.cpp:365-375).
+ * The codes and scales of both operands are expanded once per row (int8 codes, f32 scales); the
+ * arithmetic per output is exactly or_vec_dot's: exact int32 block sums, d = dw*da (an exact f32
+ * product of two f16 values), acc = fmaf(sum, d, acc) block by block in K order. */
+int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
+               const float * x, int64_t n_rows, const float * bias, float * y, int n_threads) {
+    const size_t wrow = or_row_size(wtype, n_in);
+    if (wrow == 0 || (wtype != OR_F32 && wtype != OR_F16 && wtype != OR_Q8_0 && wtype != OR_Q4_0 && wtype != OR_Q4_K)) {
+        fprintf(stderr, "oracle: mul_mat of type %d over rows of %lld not supported\n", wtype, (long long) n_in);
+        return -1;
+    }
+    const uint8_t * W = (const uint8_t *) w;
+    if (wtype == OR_F32 || wtype == OR_F16) {
+        /* f16 weights: activations rounded to f16 (ggml's vec_dot_type for F16 is F16) */
+        float * wf = (float *) malloc(sizeof(float) * n_out * n_in);
+        float * xf = (float *) malloc(sizeof(float) * n_rows * n_in);
+        if (!wf || !xf) { free(wf); free(xf); return -1; }
+        for (int64_t o = 0; o < n_out; o++) or_dequantize(wtype, W + (size_t) o * wrow, wf + o * n_in, n_in);
+        for (int64_t i = 0; i < n_rows * n_in; i++)
+            xf[i] = wtype == OR_F16 ? or_fp16_to_fp32(or_fp32_to_fp16(x[i])) : x[i];
+#pragma omp parallel for num_threads(n_threads) schedule(static) collapse(2)
+        for (int64_t m = 0; m < n_rows; m++)
+            for (int64_t o = 0; o < n_out; o++) {
+                float v = dot_f32_8acc(wf + o * n_in, xf + m * n_in, n_in);
+                if (bias) v = v + bias[o];
+                y[m * n_out + o] = v;
+            }
+        free(wf); free(xf);
+        return 0;
+    }
+    const int kq = wtype == OR_Q4_K ? QK_K : 32;
+    const int64_t nb = n_in / kq;
+    int8_t * qw = (int8_t *) malloc((size_t) n_out * n_in);
+    int8_t * qa = (int8_t *) malloc((size_t) n_rows * n_in);
+    float * dw = (float *) malloc(sizeof(float) * n_out * nb);
+    float * dmw = (float *) malloc(sizeof(float) * n_out * nb);
+    float * da = (float *) malloc(sizeof(float) * n_rows * nb);
+    int32_t * scw = (int32_t *) malloc(sizeof(int32_t) * n_out * nb * 8);
+    int32_t * mw = (int32_t *) malloc(sizeof(int32_t) * n_out * nb * 8);
+    int32_t * bsa = (int32_t *) malloc(sizeof(int32_t) * n_rows * nb * 8);
+    if (!qw || !qa || !dw || !dmw || !da || !scw || !mw || !bsa) {
+        free(qw); free(qa); free(dw); free(dmw); free(da); free(scw); free(mw); free(bsa);
+        return -1;
+    }
+    /* weights */
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+    for (int64_t o = 0; o < n_out; o++) {
+        const uint8_t * row = W + (size_t) o * wrow;
+        for (int64_t b = 0; b < nb; b++) {
+            int8_t * q = qw + o * n_in + b * kq;
+            if (wtype == OR_Q8_0) {
+                const blk_q8_0 * B = (const blk_q8_0 *) row + b;
+                dw[o * nb + b] = or_fp16_to_fp32(B->d);
+                for (int j = 0; j < 32; j++) q[j] = B->qs[j];
+            } else if (wtype == OR_Q4_0) {
+                const blk_q4_0 * B = (const blk_q4_0 *) row + b;
+                dw[o * nb + b] = or_fp16_to_fp32(B->d);
+                for (int j = 0; j < 16; j++) { q[j] = (int8_t) ((B->qs[j] & 0xF) - 8); q[j + 16] = (int8_t) ((B->qs[j] >> 4) - 8); }
+            } else {
+                const blk_q4_K * B = (const blk_q4_K *) row + b;
+                dw[o * nb + b] = or_fp16_to_fp32(B->d);
+                dmw[o * nb + b] = or_fp16_to_fp32(B->dmin);
+                for (int j = 0; j < 8; j++) {
+                    uint8_t sc, m;
+                    q4k_scale_min(j, B->scales, &sc, &m);
+                    scw[(o * nb + b) * 8 + j] = sc;
+                    mw[(o * nb + b) * 8 + j] = m;
+                    const uint8_t * qq = B->qs + 32 * (j / 2);
+                    for (int l = 0; l < 32; l++) q[32 * j + l] = (int8_t) ((j & 1) ? (qq[l] >> 4) : (qq[l] & 0xF));
+                }
+            }
+        }
+    }
+    /* activations: quantized per row exactly as ggml's from_float does */
+#pragma omp parallel num_threads(n_threads)
+    {
+        blk_q8_K * tmp = (blk_q8_K *) malloc(sizeof(blk_q8_K) * (size_t) (n_in / QK_K + 1));
+        blk_q8_0 * tmp0 = (blk_q8_0 *) malloc(sizeof(blk_q8_0) * (size_t) (n_in / 32 + 1));
+#pragma omp for schedule(static)
+        for (int64_t m = 0; m < n_rows; m++) {
+            if (wtype == OR_Q4_K) {
+                or_quantize_q8_K_act(x + m * n_in, tmp, n_in);
+                for (int64_t b = 0; b < nb; b++) {
+                    da[m * nb + b] = tmp[b].d;
+                    memcpy(qa + m * n_in + b * QK_K, tmp[b].qs, QK_K);
+                    for (int j = 0; j < 8; j++) bsa[(m * nb + b) * 8 + j] = (int32_t) tmp[b].bsums[2 * j] + (int32_t) tmp[b].bsums[2 * j + 1];
+                }
+            } else {
+                or_quantize_q8_0_act(x + m * n_in, tmp0, n_in);
+                for (int64_t b = 0; b < nb; b++) {
+                    da[m * nb + b] = or_fp16_to_fp32(tmp0[b].d);
+                    memcpy(qa + m * n_in + b * 32, tmp0[b].qs, 32);
+                }
+            }
+        }
+        free(tmp); free(tmp0);
+    }
+#pragma omp parallel for num_threads(n_threads) schedule(static) collapse(2)
+    for (int64_t m = 0; m < n_rows; m++) {
+        for (int64_t o = 0; o < n_out; o++) {
+            const int8_t * a = qa + m * n_in;
+            const int8_t * q = qw + o * n_in;
+            float s = 0.0f, sm = 0.0f;
+            if (wtype == OR_Q4_K) {
+                for (int64_t b = 0; b < nb; b++) {
+                    int32_t isum = 0, msum = 0;
+                    for (int j = 0; j < 8; j++) {
+                        int32_t si = 0;
+                        for (int l = 0; l < 32; l++) si += (int32_t) q[b * QK_K + 32 * j + l] * (int32_t) a[b * QK_K + 32 * j + l];
+                        isum += scw[(o * nb + b) * 8 + j] * si;
+                        msum += mw[(o * nb + b) * 8 + j] * bsa[(m * nb + b) * 8 + j];
+                    }
+                    s  = fmaf(dw[o * nb + b] * da[m * nb + b], (float) isum, s);
+                    sm = fmaf(dmw[o * nb + b] * da[m * nb + b], (float) msum, sm);
+                }
+                s = s - sm;
+            } else {
+                for (int64_t b = 0; b < nb; b++) {
+                    int32_t si = 0;
+                    for (int l = 0; l < 32; l++) si += (int32_t) q[b * 32 + l] * (int32_t) a[b * 32 + l];
+                    s = fmaf((float) si, dw[o * nb + b] * da[m * nb + b], s);
+                }
+            }
+            if (bias) s = s + bias[o];
+            y[m * n_out + o] = s;
+        }
+    }
+    free(qw); free(qa); free(dw); free(dmw); free(da); free(scw); free(mw); free(bsa);
+    return 0;
+}
+
+/* ggml_norm (two-pass: mean in double, centred variance in double, y = (x-mean) * 1/sqrt(var+eps))
+ * then ggml_mul(w) and ggml_add(b) as separate roundings (src/jepa.cpp:356-361). */
+void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, const float * b, float eps, float * y) {
+    for (int64_t r = 0; r < n_rows; r++) {
+        const float * xr = x + r * d;
+        float * yr = y + r * d;
+        double sum = 0.0;
+        for (int64_t i = 0; i < d; i++) sum += (double) xr[i];
+        const float mean = (float) sum / (float) d;
+        double sum2 = 0.0;
+        for (int64_t i = 0; i < d; i++) { const float v = xr[i] - mean; yr[i] = v; sum2 += (double) (v * v); }
+        const float variance = (float) (sum2 / (double) d);
+        const float scale = 1.0f / sqrtf(variance + eps);
+        for (int64_t i = 0; i < d; i++) {
+            float v = yr[i] * scale;
+            if (w) v = v * w[i];
+            if (b) v = v + b[i];
+            yr[i] = v;
+        }
+    }
+}
+
+/* ggml_vec_gelu_erf_f32 (docs/ggml-notes.md:291-292): 0.5*x*(1+erf(x/sqrt(2))) with libm erff */
+float or_gelu_erf(float x) {
+    const float SQRT_2_INV = 0.70710678118654752440084436210484f;
+    return 0.5f * x * (1.0f + erff(x * SQRT_2_INV));
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * 3-D RoPE (src/rope3d.cpp:9-164, math spec src/rope3d.h:1-62)
+ * ---------------------------------------------------------------------------------------------- */
+static void rope_position(const or_rope_params * p, int64_t i, float * t, float * h, float * w) {
+    const int64_t per_frame = (int64_t) p->grid_h * p->grid_w;
+    *t = (float) (i / per_frame);
+    *h = (float) ((i % per_frame) / p->grid_w);
+    *w = (float) (i % p->grid_w);
+    if (p->interpolate) {   /* rope3d.cpp:20-27: left-to-right float32, t never rescaled */
+        if (p->grid_h > 1) *h = (*h * (float) (p->train_grid_h - 1)) / (float) (p->grid_h - 1);
+        if (p->grid_w > 1) *w = (*w * (float) (p->train_grid_w - 1)) / (float) (p->grid_w - 1);
+    }
+}
+
+void or_rope_tables(const or_rope_params * p, const int32_t * ids, int64_t n_rows, float * c, float * s, int signed_sin) {
+    const int D = p->head_dim;
+    const int d = 2 * ((D / 3) / 2);           /* rope3d.cpp:9 */
+    const int half = d / 2;
+    for (int64_t i = 0; i < n_rows * D; i++) { c[i] = 1.0f; s[i] = 0.0f; }
+    if (d == 0) return;
+    float omega[512];
+    for (int k = 0; k < half; k++) omega[k] = 1.0f / powf(p->theta, (float) k / (float) half);   /* rope3d.cpp:45-53 */
+    for (int64_t r = 0; r < n_rows; r++) {
+        const int64_t id = ids ? ids[r] : r;
+        const int64_t per_frame = (int64_t) p->grid_h * p->grid_w;
+        const int64_t ti = id / per_frame, hi = (id % per_frame) / p->grid_w, wi = id % p->grid_w;
+        float pos[3], tt, hh, ww;
+        rope_position(p, ti * per_frame, &tt, &hh, &ww); pos[0] = tt;
+        rope_position(p, hi * p->grid_w, &tt, &hh, &ww); pos[1] = hh;
+        rope_position(p, wi, &tt, &hh, &ww); pos[2] = ww;
+        for (int a = 0; a < 3; a++) {
+            for (int j = 0; j < d; j++) {
+                const int k = p->variant == 0 ? (j % half) : (j / 2);   /* tiled vs interleaved, rope3d.cpp:33-41 */
+                const float ang = pos[a] * omega[k];
+                c[r * D + a * d + j] = cosf(ang);
+                s[r * D + a * d + j] = sinf(ang);
+            }
+        }
+        if (signed_sin) for (int j = 0; j < D; j += 2) s[r * D + j] = -s[r * D + j];   /* rope3d.cpp:106-108 */
+    }
+}
+
+/* out = x*C + swap(x)*S' with swap(x)[j] = x[j^1] (rope3d.cpp:136-164): two products then one add */
+void or_rope_apply(float * x, int64_t n_tok, int n_head, int hd, const float * ct, const float * st) {
+    float tmp[1024];
+    for (int64_t t = 0; t < n_tok; t++) {
+        for (int h = 0; h < n_head; h++) {
+            float * v = x + (t * n_head + h) * hd;
+            for (int j = 0; j < hd; j++) tmp[j] = v[j];
+            for (int j = 0; j < hd; j++) {
+                const float a = tmp[j] * ct[t * hd + j];
+                const float b = tmp[j ^ 1] * st[t * hd + j];
+                v[j] = a + b;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * attention: ggml_flash_attn_ext on the CPU tiled path: Q f32, K/V f16 tiles widened to f32,
+ * scores/softmax/accumulator f32 (docs/ggml-notes.md:48-58). Softmax written two-pass here.
+ * ---------------------------------------------------------------------------------------------- */
+void or_attention(const float * q, const float * k, const float * v, int64_t n_q, int64_t n_kv,
+                  int n_head, int hd, float scale, int kv_f16, float * out, int n_threads) {
+    const int64_t row = (int64_t) n_head * hd;
+    for (int h = 0; h < n_head; h++) {
+        float * kh = (float *) malloc(sizeof(float) * n_kv * hd);
+        float * vh = (float *) malloc(sizeof(float) * n_kv * hd);
+        for (int64_t j = 0; j < n_kv; j++)
+            for (int d = 0; d < hd; d++) {
+                float kv = k[j * row + h * hd + d], vv = v[j * row + h * hd + d];
+                if (kv_f16) { kv = or_fp16_to_fp32(or_fp32_to_fp16(kv)); vv = or_fp16_to_fp32(or_fp32_to_fp16(vv)); }
+                kh[j * hd + d] = kv; vh[j * hd + d] = vv;
+            }
+#pragma omp parallel num_threads(n_threads)
+        {
+            float * sc = (float *) malloc(sizeof(float) * n_kv);
+            float acc[1024];
+#pragma omp for schedule(static)
+            for (int64_t i = 0; i < n_q; i++) {
+                const float * qi = q + i * row + h * hd;
+                float mx = -INFINITY;
+                for (int64_t j = 0; j < n_kv; j++) {
+                    sc[j] = dot_f32_8acc(qi, kh + j * hd, hd) * scale;
+                    if (sc[j] > mx) mx = sc[j];
+                }
+                float sum = 0.0f;
+                for (int d = 0; d < hd; d++) acc[d] = 0.0f;
+                for (int64_t j = 0; j < n_kv; j++) {
+                    const float p = expf(sc[j] - mx);
+                    sum += p;
+                    const float * vj = vh + j * hd;
+                    for (int d = 0; d < hd; d++) acc[d] = fmaf(p, vj[d], acc[d]);
+                }
+                const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+                for (int d = 0; d < hd; d++) out[i * row + h * hd + d] = acc[d] * inv;
+            }
+            free(sc);
+        }
+        free(kh); free(vh);
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * minimal GGUF v2/v3 reader (its own code, independent of the product loader)
+ * ---------------------------------------------------------------------------------------------- */
+typedef struct { char name[128]; int type; int n_dims; int64_t ne[4]; uint64_t offset; } gg_tensor;
+typedef struct { char key[96]; int vtype; int64_t ival; double fval; char sval[128]; float farr[4]; int nfarr; } gg_kv;
+typedef struct {
+    uint8_t * buf; size_t size; size_t data_off;
+    gg_kv * kv; int n_kv;
+    gg_tensor * t; int n_t;
+} gg_file;
+
+static int rd(const gg_file * f, size_t * p, void * dst, size_t n) {
+    if (*p + n > f->size) return -1;
+    memcpy(dst, f->buf + *p, n); *p += n; return 0;
+}
+static int rd_str(const gg_file * f, size_t * p, char * dst, size_t cap) {
+    uint64_t n; if (rd(f, p, &n, 8)) return -1;
+    if (*p + n > f->size) return -1;
+    const size_t c = n < cap - 1 ? (size_t) n : cap - 1;
+    memcpy(dst, f->buf + *p, c); dst[c] = 0; *p += n; return 0;
+}
+static size_t gg_scalar_size(int t) {
+    switch (t) { case 0: case 1: case 7: return 1; case 2: case 3: return 2; case 4: case 5: case 6: return 4;
+                 case 10: case 11: case 12: return 8; }
+    return 0;
+}
+static int rd_scalar(const gg_file * f, size_t * p, int t, int64_t * iv, double * fv) {
+    uint8_t b[8] = {0}; const size_t n = gg_scalar_size(t); *iv = 0; *fv = 0;
+    if (!n || rd(f, p, b, n)) return -1;
+    switch (t) {
+        case 0: *iv = b[0]; break; case 1: *iv = (int8_t) b[0]; break; case 7: *iv = b[0] != 0; break;
+        case 2: { uint16_t v; memcpy(&v, b, 2); *iv = v; break; } case 3: { int16_t v; memcpy(&v, b, 2); *iv = v; break; }
+        case 4: { uint32_t v; memcpy(&v, b, 4); *iv = v; break; } case 5: { int32_t v; memcpy(&v, b, 4); *iv = v; break; }
+        case 6: { float v; memcpy(&v, b, 4); *fv = v; *iv = (int64_t) v; return 0; }
+        case 10: { uint64_t v; memcpy(&v, b, 8); *iv = (int64_t) v; break; } case 11: { int64_t v; memcpy(&v, b, 8); *iv = v; break; }
+        case 12: { double v; memcpy(&v, b, 8); *fv = v; *iv = (int64_t) v; return 0; }
+    }
+    *fv = (double) *iv;
+    return 0;
+}
+
+static void gg_close(gg_file * f) { free(f->buf); free(f->kv); free(f->t); memset(f, 0, sizeof(*f)); }
+
+static int gg_open(const char * path, gg_file * f) {
+    memset(f, 0, sizeof(*f));
+    FILE * fp = fopen(path, "rb");
+    if (!fp) { fprintf(stderr, "oracle: cannot open %s\n", path); return -1; }
+    fseeko(fp, 0, SEEK_END); f->size = (size_t) ftello(fp); fseeko(fp, 0, SEEK_SET);
+    f->buf = (uint8_t *) malloc(f->size);
+    if (!f->buf || fread(f->buf, 1, f->size, fp) != f->size) { fclose(fp); gg_close(f); return -1; }
+    fclose(fp);
+    size_t p = 0; uint32_t magic, ver; uint64_t nt, nkv;
+    if (rd(f, &p, &magic, 4) || memcmp(&magic, "GGUF", 4) || rd(f, &p, &ver, 4) || rd(f, &p, &nt, 8) || rd(f, &p, &nkv, 8)) { gg_close(f); return -1; }
+    f->kv = (gg_kv *) calloc(nkv + 1, sizeof(gg_kv)); f->t = (gg_tensor *) calloc(nt + 1, sizeof(gg_tensor));
+    f->n_kv = (int) nkv; f->n_t = (int) nt;
+    uint64_t alignment = 32;
+    for (uint64_t i = 0; i < nkv; i++) {
+        gg_kv * kv = &f->kv[i];
+        uint32_t vt;
+        if (rd_str(f, &p, kv->key, sizeof(kv->key)) || rd(f, &p, &vt, 4)) { gg_close(f); return -1; }
+        kv->vtype = (int) vt;
+        if (vt == 8) { if (rd_str(f, &p, kv->sval, sizeof(kv->sval))) { gg_close(f); return -1; } }
+        else if (vt == 9) {
+            uint32_t et; uint64_t n;
+            if (rd(f, &p, &et, 4) || rd(f, &p, &n, 8)) { gg_close(f); return -1; }
+            for (uint64_t j = 0; j < n; j++) {
+                if (et == 8) { char tmp[8]; if (rd_str(f, &p, tmp, sizeof(tmp))) { gg_close(f); return -1; } }
+                else { int64_t iv = 0; double fv = 0; if (rd_scalar(f, &p, (int) et, &iv, &fv)) { gg_close(f); return -1; }
+                       if (j < 4) { kv->farr[j] = (float) fv; kv->nfarr = (int) (j + 1); } }
+            }
+        } else if (rd_scalar(f, &p, (int) vt, &kv->ival, &kv->fval)) { gg_close(f); return -1; }
+        if (!strcmp(kv->key, "general.alignment")) alignment = (uint64_t) kv->ival;
+    }
+    for (uint64_t i = 0; i < nt; i++) {
+        gg_tensor * t = &f->t[i];
+        uint32_t nd, ty;
+        if (rd_str(f, &p, t->name, sizeof(t->name)) || rd(f, &p, &nd, 4) || nd > 4) { gg_close(f); return -1; }
+        t->n_dims = (int) nd;
+        for (int d = 0; d < 4; d++) t->ne[d] = 1;
+        for (uint32_t d = 0; d < nd; d++) { uint64_t v; if (rd(f, &p, &v, 8)) { gg_close(f); return -1; } t->ne[d] = (int64_t) v; }
+        if (rd(f, &p, &ty, 4) || rd(f, &p, &t->offset, 8)) { gg_close(f); return -1; }
+        t->type = (int) ty;
+    }
+    f->data_off = (p + alignment - 1) / alignment * alignment;
+    return 0;
+}
+
+static const gg_kv * gg_find(const gg_file * f, const char * key) {
+    for (int i = 0; i < f->n_kv; i++) if (!strcmp(f->kv[i].key, key)) return &f->kv[i];
+    return NULL;
+}
+static int64_t gg_int(const gg_file * f, const char * key, int64_t def) { const gg_kv * k = gg_find(f, key); return k && k->vtype != 8 && k->vtype != 9 ? k->ival : def; }
+static double gg_flt(const gg_file * f, const char * key, double def) { const gg_kv * k = gg_find(f, key); return k && k->vtype != 8 && k->vtype != 9 ? k->fval : def; }
+static const char * gg_str(const gg_file * f, const char * key, const char * def) { const gg_kv * k = gg_find(f, key); return k && k->vtype == 8 ? k->sval : def; }
+
+static const gg_tensor * gg_tensor_find(const gg_file * f, const char * name) {
+    for (int i = 0; i < f->n_t; i++) if (!strcmp(f->t[i].name, name)) return &f->t[i];
+    return NULL;
+}
+static const void * gg_data(const gg_file * f, const gg_tensor * t) { return f->buf + f->data_off + t->offset; }
+
+/* a float vector tensor (f32 required by the reference loader, src/jepa-gguf.cpp:675-701) */
+static const float * gg_vec(const gg_file * f, const char * name) {
+    const gg_tensor * t = gg_tensor_find(f, name);
+    if (!t) return NULL;
+    if (t->type != OR_F32) { fprintf(stderr, "oracle: %s is not f32\n", name); return NULL; }
+    return (const float *) gg_data(f, t);
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * encoder forward (src/jepa.cpp:444-471 block, 586-627 image graph, 846-895 video graph)
+ * ---------------------------------------------------------------------------------------------- */
+typedef struct { const gg_tensor * t; const void * data; } lin_w;
+
+static int linear(const gg_file * f, const char * wname, const char * bname, const float * x, int64_t n_rows,
+                  int64_t n_in, int64_t n_out, float * y, int n_threads) {
+    const gg_tensor * t = gg_tensor_find(f, wname);
+    if (!t || t->ne[0] != n_in || t->ne[1] != n_out) { fprintf(stderr, "oracle: bad/missing %s\n", wname); return -1; }
+    const float * b = bname ? gg_vec(f, bname) : NULL;
+    return or_mul_mat(t->type, gg_data(f, t), n_out, n_in, x, n_rows, b, y, n_threads);
+}
+
+static void patchify(const float * cthw, int C, int T, int H, int W, int P, int tub, float * rows) {
+    /* src/jepa.cpp:476-504: token order t, h, w; inner order c, tt, py, px */
+    const int GT = T / tub, GH = H / P, GW = W / P;
+    const int64_t K = (int64_t) C * tub * P * P;
+    for (int t = 0; t < GT; t++)
+        for (int h = 0; h < GH; h++)
+            for (int w = 0; w < GW; w++) {
+                float * row = rows + ((int64_t) t * GH * GW + (int64_t) h * GW + w) * K;
+                int64_t o = 0;
+                for (int c = 0; c < C; c++)
+                    for (int tt = 0; tt < tub; tt++) {
+                        const int64_t plane = ((int64_t) c * T + (int64_t) t * tub + tt) * H * W;
+                        for (int py = 0; py < P; py++) {
+                            memcpy(row + o, cthw + plane + (int64_t) (h * P + py) * W + (int64_t) w * P, sizeof(float) * P);
+                            o += P;
+                        }
+                    }
+            }
+}
+
+int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_chans, int n_frames,
+                       int height, int width, float * out, int64_t out_cap, float * trace, int64_t trace_cap,
+                       int n_layers_limit, int n_threads) {
+    gg_file f;
+    if (gg_open(path, &f)) return -1;
+    int64_t ret = -1;
+    const char * fam = gg_str(&f, "jepa.family", "");
+    const int video = !strcmp(fam, "vjepa2") || !strcmp(fam, "vjepa2_1");
+    const int image = !strcmp(fam, "hfvit") || !strcmp(fam, "ijepa") || !strcmp(fam, "lewm");
+    const int D = (int) gg_int(&f, "jepa.enc.embed_dim", 0), L = (int) gg_int(&f, "jepa.enc.n_layer", 0);
+    const int H = (int) gg_int(&f, "jepa.enc.n_head", 0), F = (int) gg_int(&f, "jepa.enc.ffn_dim", 0);
+    const int P = (int) gg_int(&f, "jepa.enc.patch_size", 16), C = (int) gg_int(&f, "jepa.enc.in_chans", 3);
+    const int cls = (int) gg_int(&f, "jepa.enc.cls_token", 0), n_reg = (int) gg_int(&f, "jepa.enc.n_registers", 0);
+    const float eps = (float) gg_flt(&f, "jepa.enc.ln_eps", 1e-6);
+    const int file_type = (int) gg_int(&f, "general.file_type", 0);
+    const int hd = H > 0 ? D / H : 0;
+    const int n_layers = n_layers_limit > 0 && n_layers_limit < L ? n_layers_limit : L;
+    if ((!video && !image) || D <= 0 || H <= 0 || n_chans != C || n_reg != 0) {
+        fprintf(stderr, "oracle: family '%s' / shape not covered by the oracle\n", fam);
+        gg_close(&f); return -1;
+    }
+    const char * act = gg_str(&f, "jepa.enc.act", "gelu_erf");
+    if (strcmp(act, "gelu_erf") != 0 && strcmp(act, "gelu") != 0) {
+        fprintf(stderr, "oracle: only gelu_erf is restated\n"); gg_close(&f); return -1;
+    }
+    const int kv_f16 = file_type != 0;   /* JEPA_KV_AUTO on the CPU, src/jepa.cpp:531-535 */
+
+    int tub = video ? (int) gg_int(&f, "jepa.enc.tubelet_size", 1) : 1;
+    int image_path = 0;
+    if (video && n_frames == 1 && gg_int(&f, "jepa.enc.image_patch_embed", 0) && gg_tensor_find(&f, "enc.patch_embed_img.weight")) {
+        image_path = 1; tub = 1;   /* src/jepa.cpp:771-775 */
+    }
+    const int n_items = video ? n_batch : n_batch * n_frames;
+    const int T = video ? n_frames : 1;
+    if (height % P || width % P || T % tub) { fprintf(stderr, "oracle: shape not encodable\n"); gg_close(&f); return -1; }
+    const int GT = T / tub, GH = height / P, GW = width / P;
+    const int64_t Np = (int64_t) GT * GH * GW;
+    const int64_t R = Np + (image && cls ? 1 : 0);
+    const int64_t K = (int64_t) C * tub * P * P;
+    if (out_cap < (int64_t) n_items * R * D) { fprintf(stderr, "oracle: output too small\n"); gg_close(&f); return -1; }
+
+    float * rope_c = NULL, * rope_s = NULL;
+    if (video) {
+        or_rope_params rp;
+        rp.grid_t = GT; rp.grid_h = GH; rp.grid_w = GW; rp.head_dim = hd;
+        rp.theta = (float) gg_flt(&f, "jepa.enc.rope_theta", 10000.0);
+        rp.variant = !strcmp(gg_str(&f, "jepa.enc.rope_freq_layout", ""), "interleaved") ? 1 : 0;
+        rp.interpolate = (int) gg_int(&f, "jepa.enc.rope_interpolate", 0);
+        rp.train_grid_h = rp.train_grid_w = (int) gg_int(&f, "jepa.enc.rope_ref_grid", 0);
+        rope_c = (float *) malloc(sizeof(float) * Np * hd); rope_s = (float *) malloc(sizeof(float) * Np * hd);
+        or_rope_tables(&rp, NULL, Np, rope_c, rope_s, 1);
+    }
+
+    float * rows = (float *) malloc(sizeof(float) * Np * K);
+    float * x = (float *) malloc(sizeof(float) * R * D);
+    float * h = (float *) malloc(sizeof(float) * R * D);
+    float * qkv = (float *) malloc(sizeof(float) * R * 3 * D);
+    float * q = (float *) malloc(sizeof(float) * R * D), * kk = (float *) malloc(sizeof(float) * R * D), * vv = (float *) malloc(sizeof(float) * R * D);
+    float * att = (float *) malloc(sizeof(float) * R * D);
+    float * o = (float *) malloc(sizeof(float) * R * D);
+    float * ff = (float *) malloc(sizeof(float) * R * F);
+    float * chw = (float *) malloc(sizeof(float) * C * height * width * (video ? T : 1));
+    const int64_t plane = (int64_t) height * width;
+
+    for (int it = 0; it < n_items; it++) {
+        /* gather the item (video: the whole clip; image: the (b, t) slice) and patchify */
+        if (video) {
+            memcpy(chw, in + (int64_t) it * C * T * plane, sizeof(float) * C * T * plane);
+            patchify(chw, C, T, height, width, P, tub, rows);
+        } else {
+            const int b = it / n_frames, t = it % n_frames;
+            for (int c = 0; c < C; c++) memcpy(chw + c * plane, in + (((int64_t) b * n_chans + c) * n_frames + t) * plane, sizeof(float) * plane);
+            patchify(chw, C, 1, height, width, P, 1, rows);
+        }
+        float * xp = x + (R - Np) * D;   /* patch rows after the prefix */
+        const char * pw = image_path ? "enc.patch_embed_img.weight" : "enc.patch_embed.weight";
+        const char * pb = image_path ? "enc.patch_embed_img.bias" : "enc.patch_embed.bias";
+        if (linear(&f, pw, pb, rows, Np, K, D, xp, n_threads)) goto done;
+        if (video && gg_int(&f, "jepa.enc.modality_embed", 0)) {
+            const float * mod = gg_vec(&f, image_path ? "enc.mod_embed_img" : "enc.mod_embed_video");
+            if (!mod) goto done;
+            for (int64_t r = 0; r < Np; r++) for (int d = 0; d < D; d++) xp[r * D + d] = xp[r * D + d] + mod[d];
+        }
+        if (image) {
+            if (cls) {
+                const float * ct = gg_vec(&f, "enc.cls_token");
+                if (!ct) goto done;
+                memcpy(x, ct, sizeof(float) * D);
+            }
+            const float * pos = gg_vec(&f, "enc.pos_embed");
+            if (pos) {
+                const gg_tensor * pt = gg_tensor_find(&f, "enc.pos_embed");
+                if (pt->ne[1] != R) { fprintf(stderr, "oracle: pos_embed rows %lld != %lld\n", (long long) pt->ne[1], (long long) R); goto done; }
+                for (int64_t r = 0; r < R; r++) for (int d = 0; d < D; d++) x[r * D + d] = x[r * D + d] + pos[r * D + d];
+            }
+        }
+        if (trace) {
+            const int64_t off = ((int64_t) it * (n_layers + 1)) * R * D;
+            if (off + R * D > trace_cap) { fprintf(stderr, "oracle: trace too small\n"); goto done; }
+            memcpy(trace + off, x, sizeof(float) * R * D);
+        }
+        for (int l = 0; l < n_layers; l++) {
+            char n1[96], n2[96];
+#define TN(buf, s) (snprintf(buf, sizeof(buf), "enc.blk.%d.%s", l, s), buf)
+            char a1[96], a2[96];
+            or_layer_norm(x, R, D, gg_vec(&f, TN(a1, "ln1.weight")), gg_vec(&f, TN(a2, "ln1.bias")), eps, h);
+            if (linear(&f, TN(n1, "attn_qkv.weight"), TN(n2, "attn_qkv.bias"), h, R, D, 3 * D, qkv, n_threads)) goto done;
+            for (int64_t r = 0; r < R; r++) {
+                memcpy(q + r * D, qkv + r * 3 * D, sizeof(float) * D);
+                memcpy(kk + r * D, qkv + r * 3 * D + D, sizeof(float) * D);
+                memcpy(vv + r * D, qkv + r * 3 * D + 2 * D, sizeof(float) * D);
+            }
+            if (video) {   /* q and k rotated before the 1/sqrt(d) scale (src/jepa.cpp:880-882) */
+                or_rope_apply(q, R, H, hd, rope_c, rope_s);
+                or_rope_apply(kk, R, H, hd, rope_c, rope_s);
+            }
+            or_attention(q, kk, vv, R, R, H, hd, 1.0f / sqrtf((float) hd), kv_f16, att, n_threads);
+            if (linear(&f, TN(n1, "attn_out.weight"), TN(n2, "attn_out.bias"), att, R, D, D, o, n_threads)) goto done;
+            const float * ls1 = gg_vec(&f, TN(a1, "ls1"));
+            for (int64_t i = 0; i < R * D; i++) x[i] = x[i] + (ls1 ? o[i] * ls1[i % D] : o[i]);
+            or_layer_norm(x, R, D, gg_vec(&f, TN(a1, "ln2.weight")), gg_vec(&f, TN(a2, "ln2.bias")), eps, h);
+            if (linear(&f, TN(n1, "ffn_up.weight"), TN(n2, "ffn_up.bias"), h, R, D, F, ff, n_threads)) goto done;
+#pragma omp parallel for num_threads(n_threads)
+            for (int64_t i = 0; i < R * F; i++) ff[i] = or_gelu_erf(ff[i]);
+            if (linear(&f, TN(n1, "ffn_down.weight"), TN(n2, "ffn_down.bias"), ff, R, F, D, o, n_threads)) goto done;
+            const float * ls2 = gg_vec(&f, TN(a1, "ls2"));
+            for (int64_t i = 0; i < R * D; i++) x[i] = x[i] + (ls2 ? o[i] * ls2[i % D] : o[i]);
+#undef TN
+            if (trace) memcpy(trace + (((int64_t) it * (n_layers + 1)) + l + 1) * R * D, x, sizeof(float) * R * D);
+        }
+        or_layer_norm(x, R, D, gg_vec(&f, "enc.norm.weight"), gg_vec(&f, "enc.norm.bias"), eps, out + (int64_t) it * R * D);
+    }
+    ret = R;
+done:
+    free(rows); free(x); free(h); free(qkv); free(q); free(kk); free(vv); free(att); free(o); free(ff); free(chw);
+    free(rope_c); free(rope_s);
+    gg_close(&f);
+    return ret;
+}

@@ -1,0 +1,190 @@
+"""ctypes wrapper of liboracle.so (test infrastructure only: imported by tests/, smoke() and the
+cpu_baseline leg of bench.py, never by the product path)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+OR_F32, OR_F16, OR_Q4_0, OR_Q8_0, OR_Q4_K, OR_Q8_K = 0, 1, 2, 8, 12, 15
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        vp, i64, f32p = C.c_void_p, C.c_int64, C.POINTER(C.c_float)
+        L.or_fp32_to_fp16.restype = C.c_uint16
+        L.or_fp32_to_fp16.argtypes = [C.c_float]
+        L.or_fp16_to_fp32.restype = C.c_float
+        L.or_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.or_row_size.restype = C.c_size_t
+        L.or_row_size.argtypes = [C.c_int, i64]
+        for fn in ("or_quantize_q8_0_ref", "or_quantize_q4_0_ref", "or_quantize_q4_K",
+                   "or_quantize_q8_0_act", "or_quantize_q8_K_act"):
+            getattr(L, fn).argtypes = [vp, vp, i64]
+            getattr(L, fn).restype = None
+        L.or_dequantize.argtypes = [C.c_int, vp, vp, i64]
+        L.or_dequantize.restype = None
+        L.or_vec_dot.argtypes = [C.c_int, i64, vp, vp]
+        L.or_vec_dot.restype = C.c_float
+        L.or_mul_mat.argtypes = [C.c_int, vp, i64, i64, vp, i64, vp, vp, C.c_int]
+        L.or_mul_mat.restype = C.c_int
+        L.or_layer_norm.argtypes = [vp, i64, i64, vp, vp, C.c_float, vp]
+        L.or_layer_norm.restype = None
+        L.or_gelu_erf.argtypes = [C.c_float]
+        L.or_gelu_erf.restype = C.c_float
+        L.or_rope_tables.argtypes = [vp, vp, i64, vp, vp, C.c_int]
+        L.or_rope_tables.restype = None
+        L.or_rope_apply.argtypes = [vp, i64, C.c_int, C.c_int, vp, vp]
+        L.or_rope_apply.restype = None
+        L.or_attention.argtypes = [vp, vp, vp, i64, i64, C.c_int, C.c_int, C.c_float, C.c_int, vp, C.c_int]
+        L.or_attention.restype = None
+        L.or_encode_file.argtypes = [C.c_char_p, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64,
+                                     vp, i64, C.c_int, C.c_int]
+        L.or_encode_file.restype = i64
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class RopeParams(C.Structure):
+    _fields_ = [("grid_t", C.c_int), ("grid_h", C.c_int), ("grid_w", C.c_int), ("head_dim", C.c_int),
+                ("theta", C.c_float), ("interpolate", C.c_int), ("train_grid_h", C.c_int),
+                ("train_grid_w", C.c_int), ("variant", C.c_int)]
+
+
+def threads() -> int:
+    return int(os.environ.get("ORACLE_THREADS", os.cpu_count() or 1))
+
+
+def row_size(t: int, n: int) -> int:
+    return int(lib().or_row_size(t, n))
+
+
+def quantize(fn: str, x: np.ndarray, block_type: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    rows = x.size // n
+    out = np.zeros((rows, row_size(block_type, n)), dtype=np.uint8)
+    for r in range(rows):
+        getattr(lib(), fn)(_p(x.reshape(rows, n)[r]), _p(out[r]), n)
+    return out.reshape(*x.shape[:-1], -1)
+
+
+def quantize_weight(t: int, x: np.ndarray) -> np.ndarray:
+    fn = {OR_Q8_0: "or_quantize_q8_0_ref", OR_Q4_0: "or_quantize_q4_0_ref", OR_Q4_K: "or_quantize_q4_K"}[t]
+    return quantize(fn, x, t)
+
+
+def quantize_act(t: int, x: np.ndarray) -> np.ndarray:
+    fn = {OR_Q8_0: "or_quantize_q8_0_act", OR_Q8_K: "or_quantize_q8_K_act"}[t]
+    return quantize(fn, x, t)
+
+
+def dequantize(t: int, raw: np.ndarray, n: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    rows = raw.size // row_size(t, n)
+    out = np.zeros((rows, n), dtype=np.float32)
+    r2 = raw.reshape(rows, -1)
+    for r in range(rows):
+        lib().or_dequantize(t, _p(r2[r]), _p(out[r]), n)
+    return out
+
+
+def mul_mat(wtype: int, w_raw: np.ndarray, n_out: int, n_in: int, x: np.ndarray, bias=None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, n_in)
+    w_raw = np.ascontiguousarray(w_raw, dtype=np.uint8)
+    y = np.zeros((x.shape[0], n_out), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    rc = lib().or_mul_mat(wtype, _p(w_raw), n_out, n_in, _p(x), x.shape[0], None if b is None else _p(b), _p(y), threads())
+    assert rc == 0
+    return y
+
+
+def layer_norm(x, w, b, eps=1e-6):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    d = x.shape[-1]
+    lib().or_layer_norm(_p(x), x.size // d, d, None if w is None else _p(np.ascontiguousarray(w, np.float32)),
+                        None if b is None else _p(np.ascontiguousarray(b, np.float32)), eps, _p(y))
+    return y
+
+
+def rope_tables(grid, head_dim, variant=0, interpolate=0, train=(0, 0), ids=None, signed=True, theta=10000.0):
+    p = RopeParams(grid[0], grid[1], grid[2], head_dim, theta, interpolate, train[0], train[1], variant)
+    n = len(ids) if ids is not None else grid[0] * grid[1] * grid[2]
+    c = np.zeros((n, head_dim), np.float32)
+    s = np.zeros((n, head_dim), np.float32)
+    idp = None
+    if ids is not None:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        idp = _p(ids)
+    lib().or_rope_tables(C.byref(p), idp, n, _p(c), _p(s), 1 if signed else 0)
+    return c, s
+
+
+def rope_apply(x, cos_t, sin_t):
+    """x [n_tok, n_head, hd] f32 -> rotated copy"""
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    n, h, d = x.shape
+    lib().or_rope_apply(_p(x), n, h, d, _p(np.ascontiguousarray(cos_t, np.float32)), _p(np.ascontiguousarray(sin_t, np.float32)))
+    return x
+
+
+def attention(q, k, v, n_head, scale=None, kv_f16=True):
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    n_q, row = q.shape
+    hd = row // n_head
+    out = np.zeros_like(q)
+    sc = scale if scale is not None else 1.0 / np.sqrt(hd)
+    lib().or_attention(_p(q), _p(k), _p(v), n_q, k.shape[0], n_head, hd, sc, 1 if kv_f16 else 0, _p(out), threads())
+    return out
+
+
+def encode_file(path: str, x: np.ndarray, rows_per_item: int, dim: int, n_layers: int = 0, trace: bool = False):
+    """Oracle encoder forward. x NCTHW float32. Returns (out [items*rows, dim], trace or None)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, Cc, T, H, W = x.shape
+    items = B if T > 1 or rows_per_item != (H // 16) * (W // 16) + 1 else B * T
+    return _encode(path, x, rows_per_item, dim, n_layers, trace, items)
+
+
+def _encode(path, x, rows, dim, n_layers, trace, items):
+    B, Cc, T, H, W = x.shape
+    out = np.zeros(items * rows * dim, dtype=np.float32)
+    tr = None
+    if trace:
+        tr = np.zeros(items * (n_layers + 1) * rows * dim, dtype=np.float32)
+    r = lib().or_encode_file(path.encode(), _p(x), B, Cc, T, H, W, _p(out), out.size,
+                             None if tr is None else _p(tr), 0 if tr is None else tr.size, n_layers, threads())
+    if r < 0:
+        raise RuntimeError("oracle encode failed")
+    out = out.reshape(-1, dim)
+    if tr is not None:
+        tr = tr.reshape(items, n_layers + 1, rows, dim)
+    return out, tr
+
+
+def encode(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, n_layers: int = 0, trace: bool = False):
+    """Oracle forward with an explicit item count (video: n_batch; image: n_batch * n_frames)."""
+    return _encode(path, np.ascontiguousarray(x, dtype=np.float32), rows, dim, n_layers, trace, n_items)
