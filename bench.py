@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""Throughput of the V-JEPA 2 ViT-L/16 encoder forward on one MI355X (the reference's headline
+jepa-bench configuration: 16 frames of 256x256 = 2048 tokens, 24 layers, q8_0 weights, 1 clip).
+
+One "step" is one encoder forward of one clip through the library's device-resident entry point
+(jepa_amd_encode_device: input already in HBM, output left in HBM; the captured hipGraph of the
+whole forward is replayed). The timed region is K steps bracketed by torch.cuda.synchronize().
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel class (the q8_0 GEMMs): algorithmic int8 ops of one launch (average
+                over the four ViT-L shapes) / its mean launch time, from hipEvents recorded around every
+                launch on the library's stream during a second pass of K steps; HBM traffic per launch
+                from the committed rocprofv3 counter summary when present.
+  q4_k          the same workload with q4_K weights.
+  cpu_baseline  the CPU oracle (a C restatement of ggml's CPU semantics, not ggml) on this host: one clip,
+                patch embedding + 1 and 2 blocks timed, extrapolated to 24 blocks.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "jepa.cpp_amd", "python"))
+
+METRIC = "clips/s ViT-L 16f q8_0/q4_K on 1 MI355X; GEMM MFMA util %; p50 latency"
+# algorithmic work per clip (2 ops per multiply-add): linear GEMMs 2*N*(4D^2 + 2DF)*L, attention 4*N^2*D*L
+N_TOK, D, F, L, H = 2048, 1024, 4096, 24, 16
+GEMM_OPS = 2 * N_TOK * (4 * D * D + 2 * D * F) * L          # 1.237e12
+ATTN_FLOP = 4 * N_TOK * N_TOK * D * L                         # 0.412e12
+PATCH_FLOP = 2 * N_TOK * 1536 * D
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 (the q8 GEMMs are priced against it)
+PEAK_F16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_model(name):
+    from jepa_amd import forge
+    t0 = time.time()
+    path = forge.cached_model(forge.CONFIGS[name])
+    log(f"bench: model {name} ready in {time.time() - t0:.1f} s ({path})")
+    return path
+
+
+def time_forward(path, x_host, steps, warmup, kernel_pass=True):
+    import numpy as np
+    import torch
+    from jepa_amd import _lib
+
+    m = _lib.Model(path, device=0)
+    ctx = _lib.Context(m)
+    B, C, T, Hh, W = x_host.shape
+    rows = m.token_grid(T, Hh, W)
+    xin = torch.from_numpy(np.ascontiguousarray(x_host)).to("cuda")
+    out = torch.empty((B * rows, m.dim), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        ctx.encode_device(xin.data_ptr(), x_host.shape, out.data_ptr(), out.numel())
+    torch.cuda.synchronize()
+    per_step = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.encode_device(xin.data_ptr(), x_host.shape, out.data_ptr(), out.numel())
+        per_step.append(ctx.last_compute_ms)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    res = {"elapsed_s": elapsed, "device_ms": per_step, "rows": rows}
+    # wall time of the host-buffer API (jepa_encode: H2D + forward + D2H), the PCIe-inclusive rate
+    walls = []
+    for _ in range(min(steps, 10)):
+        t1 = time.perf_counter()
+        ctx.encode(x_host)
+        walls.append((time.perf_counter() - t1) * 1e3)
+    res["host_api_ms"] = walls
+    if kernel_pass:
+        ctx.set_kernel_timing(True)
+        ctx.reset_kernel_stats()
+        for _ in range(steps):
+            ctx.encode_device(xin.data_ptr(), x_host.shape, out.data_ptr(), out.numel())
+        torch.cuda.synchronize()
+        stats = {}
+        for cls in ("patchify", "patch_embed", "layernorm", "gemm_q8", "gemm_q4k", "gemm_f16", "attention", "quantize"):
+            n, ms = ctx.kernel_stats(cls)
+            if n:
+                stats[cls] = {"launches": n, "total_ms": ms, "avg_ms": ms / n, "per_step_ms": ms / steps}
+        res["kernels"] = stats
+        ctx.set_kernel_timing(False)
+    ctx.close()
+    m.close()
+    return res
+
+
+def cpu_baseline(path, x_host):
+    """The oracle on the host cores: patch embedding + 1 block and + 2 blocks of one clip."""
+    from oracle import oracle as O
+    threads = int(os.environ.get("ORACLE_THREADS", min(16, os.cpu_count() or 1)))
+    os.environ["ORACLE_THREADS"] = str(threads)
+    O.build()
+    rows = N_TOK
+    t = {}
+    for nl in (1, 2):
+        t0 = time.perf_counter()
+        O.encode(path, x_host, 1, rows, D, n_layers=nl)
+        t[nl] = time.perf_counter() - t0
+    per_block = max(t[2] - t[1], 1e-9)
+    clip_s = t[1] + (L - 1) * per_block
+    return {"value": 1.0 / clip_s, "unit": "clips/s", "cores": threads, "kind": "port",
+            "sample": f"oracle (C restatement of ggml CPU semantics, OpenMP {threads} threads) on one ViT-L/16 16f q8_0 clip: "
+                      f"patch embed + 1 block = {t[1]:.2f} s, + 2 blocks = {t[2]:.2f} s, extrapolated to 24 blocks = {clip_s:.1f} s/clip"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-q4k", action="store_true", help="skip the q4_K line")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the encoder has no multi-GPU path; clips are "
+              "independent, so N GPUs would run N independent replicas). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from jepa_amd import inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    x = inputs.make_input(1, 16, 256, 256, seed=1234)          # jepa-bench's seeded pixels
+    path = make_model("vitl16_q8_0")
+    log("bench: timing q8_0")
+    r = time_forward(path, x, args.steps, args.warmup)
+    dev_ms = np.array(r["device_ms"])
+    ms_per_step = r["elapsed_s"] / args.steps * 1e3
+    value = args.steps / r["elapsed_s"]
+    k = r.get("kernels", {})
+    gq = k.get("gemm_q8")
+    roof = None
+    if gq:
+        launches_per_clip = gq["launches"] / args.steps
+        ops_per_launch = GEMM_OPS / launches_per_clip
+        achieved = ops_per_launch / (gq["avg_ms"] * 1e-3) / 1e12
+        traffic = None
+        tf = os.path.join(ROOT, "profiles", "gemm_q8_vitl16_counters.json")
+        if os.path.exists(tf):
+            with open(tf) as f:
+                traffic = json.load(f).get("hbm_bytes_per_launch")
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
+                "kernel": "gemm_q8 (q8_0 x q8_0 GEMMs: qkv, out, fc1, fc2)", "avg_launch_ms": round(gq["avg_ms"], 5),
+                "ops_per_launch": ops_per_launch, "peak_note": "int8 dense 5.0 POP/s (the int codes run on f16 MFMA, 2.5 PF)"}
+    extra = {}
+    att = k.get("attention")
+    if att:
+        extra["attention_roofline"] = {"bound": "mfma", "achieved": round(ATTN_FLOP / (att["per_step_ms"] * 1e-3) / 1e12, 2),
+                                       "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(ATTN_FLOP / (att["per_step_ms"] * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
+                                       "avg_launch_ms": round(att["avg_ms"], 5)}
+    extra["kernel_ms_per_clip"] = {c: round(v["per_step_ms"], 4) for c, v in k.items()}
+    if not args.no_q4k:
+        p4 = make_model("vitl16_q4_k")
+        log("bench: timing q4_K")
+        r4 = time_forward(p4, x, args.steps, args.warmup, kernel_pass=True)
+        g4 = r4.get("kernels", {}).get("gemm_q4k")
+        q4 = {"value": round(args.steps / r4["elapsed_s"], 3), "unit": "clips/s",
+              "ms_per_step": round(r4["elapsed_s"] / args.steps * 1e3, 4),
+              "p50_ms": round(float(np.median(r4["device_ms"])), 4)}
+        if g4:
+            ach = GEMM_OPS / (g4["per_step_ms"] * 1e-3) / 1e12
+            q4["gemm_roofline"] = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                                   "frac": round(ach / PEAK_INT8_TOPS, 4)}
+        extra["q4_k"] = q4
+    cpu = None
+    if not args.no_cpu:
+        log("bench: CPU baseline (oracle)")
+        cpu = cpu_baseline(path, x)
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "clips/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q8_0 (int8 codes x q8_0 activations, f32 accumulation); f16 attention",
+        "data": "synthetic (jepa-bench seeded pixels, random-init N(0,0.02) weights)",
+        "config": {"workload": "V-JEPA 2 ViT-L/16 encoder, 16 frames 256x256 (2048 tokens), 24 layers, D 1024, 16 heads, "
+                               "q8_0, batch 1 clip, device-resident input/output", "global_batch": 1, "seq_len": N_TOK,
+                   "parallelism": "single GPU"},
+        "p50_ms": round(float(np.median(dev_ms)), 4), "mean_ms": round(float(dev_ms.mean()), 4),
+        "min_ms": round(float(dev_ms.min()), 4),
+        "host_api_p50_ms": round(float(np.median(r["host_api_ms"])), 4),
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

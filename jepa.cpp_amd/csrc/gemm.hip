@@ -35,7 +35,7 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int BN = 128, BM = 128, KC = 64, LD = 72;   // LD: halves per LDS row (64 + 8 pad)
+constexpr int BN = 128, BM = 128, KC = 64;
 
 struct kargs {
     const _Float16 * A; const uint16_t * Ad; const uint16_t * Admin; const _Float16 * Amin;
@@ -129,12 +129,30 @@ __device__ __forceinline__ void epi4(const kargs & a, int64_t m, int64_t n, floa
     }
 }
 
+// LDS tile of 128 rows x 64 f16 (128 B per row, 8 chunks of 16 B). Chunk c of row r is stored at
+// position c ^ (r & 7): the 16-byte operand reads of 8 consecutive rows then hit 8 different bank
+// groups, and a wave's direct HBM->LDS load (64 lanes x 16 B) fills 8 whole rows contiguously.
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Stage rows [R0, R0 + 8) of a 128 x 64 f16 tile straight from HBM into LDS: lane L loads row
+// R0 + L/8, logical chunk (L%8) ^ (row & 7), and the hardware writes it at lds_row0 + 16 * L.
+__device__ __forceinline__ void lds_load_rows(const _Float16 * src, int64_t ld, int64_t row0_global, int64_t row_max,
+                                              int64_t k0, _Float16 * lds_tile, int R0, int lane) {
+    const int r = R0 + (lane >> 3);
+    const int c = (lane & 7) ^ (r & 7);
+    int64_t gr = row0_global + r;
+    if (gr > row_max) gr = row_max;        // rows past the end load a valid row; their results are dropped
+    __builtin_amdgcn_global_load_lds((const void *) (src + gr * ld + k0 + 8 * c), (lds_void *) (lds_tile + R0 * 64), 16, 0, 0);
+}
+
 template <int WF, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_mfma(kargs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 sA[BN * LD];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[BM * LD];
-    __shared__ uint16_t sAd[BN * 2];
-    __shared__ uint16_t sBd[BM * 2];
+__global__ __launch_bounds__(256, 2) void k_gemm_mfma(kargs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BN * KC];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][BM * KC];
+    __shared__ uint16_t sAd[2][BN * 2];
+    __shared__ uint16_t sBd[2][BM * 2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = wave & 1, wm = wave >> 1;
@@ -142,20 +160,22 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(kargs a) {
     const int64_t n0 = (int64_t) blockIdx.x * BN, m0 = (int64_t) blockIdx.y * BM;
     const int64_t K = a.K, M = a.M;
 
-    f16v acc[2][2], ssb[2][2];
+    f16v acc[2][2];
+    [[maybe_unused]] f16v ssb[2][2];
     const f16v zero = {0};
-    for (int i = 0; i < 2; i++) for (int j = 0; j < 2; j++) { acc[i][j] = zero; ssb[i][j] = zero; }
+    for (int i = 0; i < 2; i++) for (int j = 0; j < 2; j++) { acc[i][j] = zero; if constexpr (WF == W_Q4K) ssb[i][j] = zero; }
 
-    uint4 ra[4], rb[4];
-    uint16_t rad = 0, rbd = 0;
-    auto gload = [&](int64_t k0) {
+    // one stage = 2 x 16 wave-loads of 1 KB (A and B tiles), 8 per wave
+    auto issue_tiles = [&](int64_t k0, int buf) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int c = tid + 256 * i, row = c >> 3, col = (c & 7) * 8;
-            ra[i] = *(const uint4 *) (a.A + (n0 + row) * K + k0 + col);
-            const int64_t mr = m0 + row;
-            rb[i] = mr < M ? *(const uint4 *) (a.B + mr * K + k0 + col) : make_uint4(0, 0, 0, 0);
+            const int R0 = (wave * 4 + i) * 8;
+            lds_load_rows(a.A, K, n0, a.N - 1, k0, sA[buf], R0, lane);
+            lds_load_rows(a.B, K, m0, M - 1, k0, sB[buf], R0, lane);
         }
+    };
+    uint16_t rad = 0, rbd = 0;
+    auto load_scales = [&](int64_t k0) {
         if constexpr (WF == W_Q32) {
             const int row = tid >> 1, blk = tid & 1;
             rad = a.Ad[(n0 + row) * (K / 32) + k0 / 32 + blk];
@@ -163,89 +183,80 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(kargs a) {
             rbd = mr < M ? ((const uint16_t *) a.Bd)[mr * (K / 32) + k0 / 32 + blk] : (uint16_t) 0;
         }
     };
-    auto lstore = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + 256 * i, row = c >> 3, col = (c & 7) * 8;
-            *(uint4 *) &sA[row * LD + col] = ra[i];
-            *(uint4 *) &sB[row * LD + col] = rb[i];
-        }
-        if constexpr (WF == W_Q32) { sAd[tid] = rad; sBd[tid] = rbd; }
+    auto store_scales = [&](int buf) {
+        if constexpr (WF == W_Q32) { sAd[buf][tid] = rad; sBd[buf][tid] = rbd; }
     };
 
-    gload(0);
-    for (int64_t k0 = 0; k0 < K; k0 += KC) {
-        __syncthreads();
-        lstore();
-        __syncthreads();
-        if (k0 + KC < K) gload(k0 + KC);
-#pragma unroll
+    const int64_t nst = K / KC;
+    issue_tiles(0, 0);
+    load_scales(0);
+    store_scales(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int64_t st = 0; st < nst; st++) {
+        const int cur = (int) (st & 1);
+        const int64_t k0 = st * KC;
+        if (st + 1 < nst) { issue_tiles(k0 + KC, cur ^ 1); load_scales(k0 + KC); }
+        const _Float16 * A_ = sA[cur];
+        const _Float16 * B_ = sB[cur];
+#pragma unroll 1
         for (int blk = 0; blk < 2; blk++) {
-            h8 av[2][2], bv[2][2];
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int row = 64 * wn + 32 * i + l32;
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) av[i][hh] = *(const h8 *) &sA[row * LD + blk * 32 + hh * 16 + g * 8];
-            }
+            h8 bv[2][2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const int row = 64 * wm + 32 * j + l32;
 #pragma unroll
-                for (int hh = 0; hh < 2; hh++) bv[j][hh] = *(const h8 *) &sB[row * LD + blk * 32 + hh * 16 + g * 8];
+                for (int hh = 0; hh < 2; hh++) bv[j][hh] = *(const h8 *) &B_[swz(row, blk * 4 + hh * 2 + g)];
             }
-            if constexpr (WF == W_F16) {
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        acc[i][j] = MFMA16(av[i][0], bv[j][0], acc[i][j]);
-                        acc[i][j] = MFMA16(av[i][1], bv[j][1], acc[i][j]);
-                    }
-            } else if constexpr (WF == W_Q32) {
-                h8 sa[2], sb[2];
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    h8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-                    if (g == 0) v[0] = __builtin_bit_cast(_Float16, sAd[(64 * wn + 32 * i + l32) * 2 + blk]);
-                    sa[i] = v;
-                }
+            [[maybe_unused]] h8 sb[2];
+            if constexpr (WF == W_Q32) {
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
-                    h8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-                    if (g == 0) v[0] = __builtin_bit_cast(_Float16, sBd[(64 * wm + 32 * j + l32) * 2 + blk]);
-                    sb[j] = v;
+                    // da in K-slot 0 of lane group 0 only; group 1 contributes zeros
+                    const uint32_t d = g == 0 ? (uint32_t) sBd[cur][(64 * wm + 32 * j + l32) * 2 + blk] : 0u;
+                    sb[j] = __builtin_bit_cast(h8, make_uint4(d, 0u, 0u, 0u));
                 }
+            }
 #pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        f16v S = MFMA16(av[i][0], bv[j][0], zero);
-                        S = MFMA16(av[i][1], bv[j][1], S);
-                        const f16v sc = MFMA16(sa[i], sb[j], zero);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf(S[r], sc[r], acc[i][j][r]);
-                    }
-            } else {   // W_Q4K: integer sums over the 256-deep super-block
-#pragma unroll
-                for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 2; i++) {
+                if (i == 1) __builtin_amdgcn_sched_barrier(0);
+                const int row = 64 * wn + 32 * i + l32;
+                const h8 a0 = *(const h8 *) &A_[swz(row, blk * 4 + g)];
+                const h8 a1 = *(const h8 *) &A_[swz(row, blk * 4 + 2 + g)];
+                if constexpr (WF == W_F16) {
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
-                        ssb[i][j] = MFMA16(av[i][0], bv[j][0], ssb[i][j]);
-                        ssb[i][j] = MFMA16(av[i][1], bv[j][1], ssb[i][j]);
+                        acc[i][j] = MFMA16(a0, bv[j][0], acc[i][j]);
+                        acc[i][j] = MFMA16(a1, bv[j][1], acc[i][j]);
                     }
+                } else if constexpr (WF == W_Q32) {
+                    // dw in K-slot 0 (both lane groups hold row n's scale; group 1 meets zeros in B)
+                    const h8 sa = __builtin_bit_cast(h8, make_uint4((uint32_t) sAd[cur][row * 2 + blk], 0u, 0u, 0u));
+                    f16v S0 = MFMA16(a0, bv[0][0], zero);
+                    f16v S1 = MFMA16(a0, bv[1][0], zero);
+                    const f16v c0 = MFMA16(sa, sb[0], zero);
+                    const f16v c1 = MFMA16(sa, sb[1], zero);
+                    S0 = MFMA16(a1, bv[0][1], S0);
+                    S1 = MFMA16(a1, bv[1][1], S1);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        acc[i][0][r] = fmaf(S0[r], c0[r], acc[i][0][r]);
+                        acc[i][1][r] = fmaf(S1[r], c1[r], acc[i][1][r]);
+                    }
+                } else {   // W_Q4K: integer sums over the 256-deep super-block
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        ssb[i][j] = MFMA16(a0, bv[j][0], ssb[i][j]);
+                        ssb[i][j] = MFMA16(a1, bv[j][1], ssb[i][j]);
+                    }
+                }
             }
         }
         if constexpr (WF == W_Q4K) {
             if (((k0 + KC) & 255) == 0) {
                 const int64_t sbi = k0 >> 8, nsb = K >> 8;
-                h8 am[2], bs[2];
+                h8 bs[2];
                 float da[2];
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const int64_t n = n0 + 64 * wn + 32 * i + l32;
-                    am[i] = *(const h8 *) (a.Amin + (n * nsb + sbi) * 16 + g * 8);
-                }
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     const int64_t m = m0 + 64 * wm + 32 * j + l32;
@@ -256,6 +267,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(kargs a) {
                 }
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
+                    const int64_t nr = n0 + 64 * wn + 32 * i + l32;
+                    const h8 am = *(const h8 *) (a.Amin + (nr * nsb + sbi) * 16 + g * 8);
                     float dw[16], dm[16];
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
@@ -267,7 +280,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(kargs a) {
                     }
 #pragma unroll
                     for (int j = 0; j < 2; j++) {
-                        const f16v ms = MFMA16(am[i], bs[j], zero);
+                        const f16v ms = MFMA16(am, bs[j], zero);
 #pragma unroll
                         for (int r = 0; r < 16; r++) {
                             const float d1 = __fmul_rn(dw[r], da[j]), d2 = __fmul_rn(dm[r], da[j]);
@@ -279,6 +292,9 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(kargs a) {
                 }
             }
         }
+        if (st + 1 < nst) store_scales(cur ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);                // this wave's HBM->LDS copies have landed
+        __syncthreads();                              // ... and everyone else's
     }
 
     // epilogue: lane holds token m and features n0 + 64wn + 32i + 8q + 4g + e

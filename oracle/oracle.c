@@ -382,6 +382,13 @@ float or_vec_dot(int wtype, int64_t n, const void * wrow, const void * arow) {
  * The codes and scales of both operands are expanded once per row (int8 codes, f32 scales); the
  * arithmetic per output is exactly or_vec_dot's: exact int32 block sums, d = dw*da (an exact f32
  * product of two f16 values), acc = fmaf(sum, d, acc) block by block in K order. */
+/* Summation order of the per-block float epilogue over K: 0 = block 0 first (ggml's generic C order),
+ * 1 = last block first. Both are valid restatements of ggml's vec_dot (its SIMD builds differ in this
+ * order); tests run both to measure how far two correct implementations drift apart through a deep
+ * quantized encoder. */
+static int g_reverse_blocks = 0;
+void or_set_reverse_block_order(int on) { g_reverse_blocks = on; }
+
 int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
                const float * x, int64_t n_rows, const float * bias, float * y, int n_threads) {
     const size_t wrow = or_row_size(wtype, n_in);
@@ -482,7 +489,8 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
             const int8_t * q = qw + o * n_in;
             float s = 0.0f, sm = 0.0f;
             if (wtype == OR_Q4_K) {
-                for (int64_t b = 0; b < nb; b++) {
+                for (int64_t bb = 0; bb < nb; bb++) {
+                    const int64_t b = g_reverse_blocks ? nb - 1 - bb : bb;
                     int32_t isum = 0, msum = 0;
                     for (int j = 0; j < 8; j++) {
                         int32_t si = 0;
@@ -495,7 +503,8 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
                 }
                 s = s - sm;
             } else {
-                for (int64_t b = 0; b < nb; b++) {
+                for (int64_t bb = 0; bb < nb; bb++) {
+                    const int64_t b = g_reverse_blocks ? nb - 1 - bb : bb;
                     int32_t si = 0;
                     for (int l = 0; l < 32; l++) si += (int32_t) q[b * 32 + l] * (int32_t) a[b * 32 + l];
                     s = fmaf((float) si, dw[o * nb + b] * da[m * nb + b], s);

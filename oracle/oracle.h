@@ -57,6 +57,9 @@ float or_vec_dot(int wtype, int64_t n, const void * wrow, const void * arow);
 int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
                const float * x, int64_t n_rows, const float * bias, float * y, int n_threads);
 
+/* 1: sum the per-block terms of quantized dots from the last K-block to the first (see oracle.c) */
+void or_set_reverse_block_order(int on);
+
 void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, const float * b,
                    float eps, float * y);
 float or_gelu_erf(float x);

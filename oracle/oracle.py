@@ -57,6 +57,8 @@ def lib() -> C.CDLL:
         L.or_encode_file.argtypes = [C.c_char_p, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64,
                                      vp, i64, C.c_int, C.c_int]
         L.or_encode_file.restype = i64
+        L.or_set_reverse_block_order.argtypes = [C.c_int]
+        L.or_set_reverse_block_order.restype = None
         _lib = L
     return _lib
 
@@ -188,3 +190,7 @@ def _encode(path, x, rows, dim, n_layers, trace, items):
 def encode(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, n_layers: int = 0, trace: bool = False):
     """Oracle forward with an explicit item count (video: n_batch; image: n_batch * n_frames)."""
     return _encode(path, np.ascontiguousarray(x, dtype=np.float32), rows, dim, n_layers, trace, n_items)
+
+
+def set_reverse_block_order(on: bool) -> None:
+    lib().or_set_reverse_block_order(1 if on else 0)
