@@ -155,7 +155,7 @@ def main():
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
                 "kernel": "gemm_q8 (q8_0 x q8_0 GEMMs: qkv, out, fc1, fc2)", "avg_launch_ms": round(gq["avg_ms"], 5),
-                "ops_per_launch": ops_per_launch, "peak_note": "int8 dense 5.0 POP/s (the int codes run on f16 MFMA, 2.5 PF)"}
+                "ops_per_launch": ops_per_launch, "peak_note": "int8 dense 5.0 POP/s; block sums on v_mfma_i32_32x32x32_i8, per-32-block f32 scale epilogue on the VALU"}
     extra = {}
     att = k.get("attention")
     if att:

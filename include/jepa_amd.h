@@ -72,6 +72,12 @@ int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * d)
 /* Copy of n float32 values between device buffers (a plain copy kernel, for counter calibration). */
 int jepa_amd_copy(int device, const float * src_dev, float * dst_dev, int64_t n, int reps, double * ms);
 
+/* Force the MFMA GEMM onto workgroup tile `index` for later launches whose n_out it divides; -1
+ * restores the automatic choice. Process-wide (tests and tuning). Tiles (weight rows x tokens):
+ * 0: 256x128, 1: 192x128, 2: 128x128, 3: 128x128 (other wave shape), 4: 64x128, 5: 128x64.
+ * Returns 0, or -1 for an index past the table. */
+int jepa_amd_gemm_tile(int index);
+
 #ifdef __cplusplus
 }
 #endif

@@ -165,15 +165,14 @@ extern "C" int jepa_amd_matmul(int device, int wtype, const void * w, int64_t n_
     if (L.fmt == W_F32 || L.fmt == W_F16) {
         L.w = (void *) w;
     } else {
-        L.w = d.alloc((size_t) n_out * n_in * 2);
+        L.w = d.alloc((size_t) n_out * n_in * (L.fmt == W_Q32 ? 1 : 2));
         if (L.fmt == W_Q32) L.wd = d.alloc((size_t) n_out * (n_in / 32) * 2);
         else {
-            L.wd = d.alloc((size_t) n_out * (n_in / 256) * 2);
-            L.wdmin = d.alloc((size_t) n_out * (n_in / 256) * 2);
+            L.wd = d.alloc((size_t) n_out * (n_in / 256) * 4);
             L.wmin = d.alloc((size_t) n_out * (n_in / 256) * 32);
         }
         if (!L.w || !L.wd) return -1;
-        launch_repack(wtype, w, n_out, n_in, L.w, L.wd, L.wdmin, L.wmin, d.s);
+        launch_repack(wtype, w, n_out, n_in, L.w, L.wd, L.wmin, d.s);
     }
     act_view a;
     if (!alloc_act(d, a, L.act(), n_rows, n_in)) return -1;
@@ -194,6 +193,11 @@ extern "C" int jepa_amd_matmul(int device, int wtype, const void * w, int64_t n_
     if (gemm_ms) *gemm_ms = ms / reps;
     hipEventDestroy(e0); hipEventDestroy(e1);
     return rc;
+}
+
+extern "C" int jepa_amd_gemm_tile(int index) {
+    if (gemm_force_tile(index) != 0) { jepa_log("jepa: jepa_amd_gemm_tile: no tile %d\n", index); return -1; }
+    return 0;
 }
 
 extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items, int64_t n_tok, int n_head, const float * rope_c,

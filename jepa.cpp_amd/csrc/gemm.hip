@@ -28,20 +28,31 @@
 
 #include <hip/hip_fp16.h>
 
+#include <atomic>
+#include <type_traits>
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i16v __attribute__((ext_vector_type(16)));
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
+#define MFMA8(a, b, c) __builtin_amdgcn_mfma_f32_32x32x8f16((a), (b), (c), 0, 0, 0)
+#define MFMA_I8(a, b, c) __builtin_amdgcn_mfma_i32_32x32x32_i8((a), (b), (c), 0, 0, 0)
 
 namespace {
 
-constexpr int BN = 128, BM = 128, KC = 64;
-
 struct kargs {
-    const _Float16 * A; const uint16_t * Ad; const uint16_t * Admin; const _Float16 * Amin;
-    const _Float16 * B; const void * Bd; const _Float16 * Bsum;
+    const _Float16 * A;      // [N][K] weight codes (or f16 / f32 weights)
+    const uint16_t * Ad;     // W_Q32: f16 d [N][K/32]; W_Q4K: u32 (d | dmin << 16) [K/256][N]
+    const _Float16 * Amin;   // W_Q4K: [N][K/256][16] sub-block mins, each twice
+    const _Float16 * B;      // [M][K] activation codes (or f16 / f32 activations)
+    const void * Bd;         // A_Q8_0: f16 d [M][K/32]; A_Q8_K: f32 d [M][K/256]
+    const _Float16 * Bsum;   // A_Q8_K: f16 bsums [M][K/16]
     const float * bias;
     int64_t M, N, K;
+    int tn, tm;              // workgroup tiles along N and M
     gemm_epi ep;
 };
 
@@ -129,157 +140,272 @@ __device__ __forceinline__ void epi4(const kargs & a, int64_t m, int64_t n, floa
     }
 }
 
-// LDS tile of 128 rows x 64 f16 (128 B per row, 8 chunks of 16 B). Chunk c of row r is stored at
-// position c ^ (r & 7): the 16-byte operand reads of 8 consecutive rows then hit 8 different bank
-// groups, and a wave's direct HBM->LDS load (64 lanes x 16 B) fills 8 whole rows contiguously.
-__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
-
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Stage rows [R0, R0 + 8) of a 128 x 64 f16 tile straight from HBM into LDS: lane L loads row
-// R0 + L/8, logical chunk (L%8) ^ (row & 7), and the hardware writes it at lds_row0 + 16 * L.
-__device__ __forceinline__ void lds_load_rows(const _Float16 * src, int64_t ld, int64_t row0_global, int64_t row_max,
-                                              int64_t k0, _Float16 * lds_tile, int R0, int lane) {
-    const int r = R0 + (lane >> 3);
-    const int c = (lane & 7) ^ (r & 7);
-    int64_t gr = row0_global + r;
-    if (gr > row_max) gr = row_max;        // rows past the end load a valid row; their results are dropped
-    __builtin_amdgcn_global_load_lds((const void *) (src + gr * ld + k0 + 8 * c), (lds_void *) (lds_tile + R0 * 64), 16, 0, 0);
+// Stage barrier: wait until at most N_ of this wave's HBM->LDS copies are outstanding and its LDS reads
+// have returned (s_waitcnt vmcnt(N_) lgkmcnt(0); gfx9 encoding: vmcnt in bits [3:0] and [15:14],
+// expcnt [6:4], lgkmcnt [11:8]), then a bare s_barrier. __syncthreads() would add a workgroup fence,
+// which waits for every copy in flight and so drains the pipeline at each stage.
+template <int N_>
+__device__ __forceinline__ void stage_barrier() {
+    static_assert(N_ >= 0 && N_ < 64, "vmcnt is a 6-bit field");
+    __builtin_amdgcn_s_waitcnt((N_ & 15) | ((N_ >> 4) << 14) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
 }
 
-template <int WF, int EPI>
-__global__ __launch_bounds__(256, 2) void k_gemm_mfma(kargs a) {
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BN * KC];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[2][BM * KC];
-    __shared__ uint16_t sAd[2][BN * 2];
-    __shared__ uint16_t sBd[2][BM * 2];
+// Workgroup tile geometry. WN x WM waves (8: two per SIMD, so one wave's MFMAs fill the other's
+// barrier, LDS-latency and VALU phases, and eight waves keep enough HBM->LDS copies in flight: a wave
+// sustains only ~10 GB/s of loads), each owning TI x TJ MFMA tiles of 32 x 32. The workgroup tile is
+// BN = 32 WN TI weight rows by BM = 32 WM TJ tokens. One LDS stage holds 128 B of every one of the
+// BN + BM rows, with 16-byte chunk c of row r stored at chunk c ^ (r & 7): KC = 128 K-columns of int8
+// codes (q8_0 / q4_0, plus the four f16 block scales of every row) or 64 K-columns of f16 values
+// (f16 weights, q4_K codes). q4_K keeps its super-block data (d/dmin, mins, activation d, bsums) in a
+// separate double buffer.
+template <int WF, int WN, int WM, int TI, int TJ>
+struct tiling {
+    static constexpr int NW = WN * WM, NT = 64 * NW;
+    static constexpr int BN = 32 * WN * TI, BM = 32 * WM * TJ, ROWS = BN + BM;
+    static constexpr int ESZ = WF == W_Q32 ? 1 : 2;          // bytes per code
+    static constexpr int KC = 128 / ESZ;                      // K-columns per stage
+    static constexpr int TILE = ROWS * 128;
+    static constexpr int SCAL = WF == W_Q32 ? ROWS * 8 : 0;
+    static constexpr int STAGE = TILE + SCAL;
+    static constexpr int X_DW = 0, X_MIN = BN * 4, X_DA = X_MIN + BN * 32, X_BS = X_DA + BM * 4;
+    static constexpr int XSB = WF == W_Q4K ? X_BS + BM * 32 : 0;
+    // q4_K: the super-block buffer of sb+1 is filled while stage 4 sb + 5 - NST is computed, which must
+    // come after the epilogue of sb-1 (end of stage 4 sb - 1): NST <= 5
+    static constexpr int NST_MAX = WF == W_Q4K ? 5 : 6;
+    static constexpr int NST_FIT = (160 * 1024 - 2 * XSB) / STAGE;
+    static constexpr int NST = NST_FIT < NST_MAX ? NST_FIT : NST_MAX;
+    static constexpr int LDS = NST * STAGE + 2 * XSB;
+    static constexpr int LOADS = ROWS / 8 / NW;    // 1 KB tile loads per wave per stage
+    static_assert(NST >= 2, "LDS too small for two stages");
+    static_assert(BN % (8 * NW) == 0 && BN % 64 == 0 && BM % 64 == 0 && ROWS % (8 * NW) == 0, "load split");
+    static_assert((NST - 2) * LOADS < 64, "vmcnt range");
+};
+
+template <class V>
+__device__ __forceinline__ V lds_chunk(const unsigned char * base, int r, int c) {
+    return *(const V *) (base + r * 128 + ((c ^ (r & 7)) << 4));
+}
+
+// Y[m][n] over the workgroup tile (n0, m0). K advances one stage (KC) per iteration; NST - 1 stages
+// are in flight as direct HBM->LDS copies (global_load_lds_dwordx4: each lane moves 16 B, a wave
+// 8 rows), so a stage's loads have NST - 1 compute phases to land. One barrier per stage.
+template <int WF, int EPI, int WN, int WM, int TI, int TJ>
+__global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
+    using T = tiling<WF, WN, WM, TI, TJ>;
+    constexpr int BN = T::BN, NST = T::NST, NW = T::NW, KC = T::KC, ESZ = T::ESZ;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[T::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = wave & 1, wm = wave >> 1;
+    const int wn = wave % WN, wm = wave / WN;
     const int l32 = lane & 31, g = lane >> 5;
-    const int64_t n0 = (int64_t) blockIdx.x * BN, m0 = (int64_t) blockIdx.y * BM;
-    const int64_t K = a.K, M = a.M;
 
-    f16v acc[2][2];
-    [[maybe_unused]] f16v ssb[2][2];
-    const f16v zero = {0};
-    for (int i = 0; i < 2; i++) for (int j = 0; j < 2; j++) { acc[i][j] = zero; if constexpr (WF == W_Q4K) ssb[i][j] = zero; }
+    // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous run of tiles (M
+    // fastest) so that the tiles sharing weight rows also share an L2.
+    const int64_t ntile = (int64_t) a.tn * a.tm;
+    int64_t tile = blockIdx.x;
+    if ((ntile & 7) == 0) tile = (tile & 7) * (ntile >> 3) + (tile >> 3);
+    const int64_t tni = tile / a.tm;
+    const int64_t n0 = tni * BN, m0 = (tile - tni * a.tm) * T::BM;
+    const int64_t K = a.K, M = a.M, KB = K >> 5;
+    const int64_t nst = (K + KC - 1) / KC;            // q8_0 / q4_0: the last stage may hold 64 columns
+    const int64_t rowbytes = K * ESZ;
 
-    // one stage = 2 x 16 wave-loads of 1 KB (A and B tiles), 8 per wave
-    auto issue_tiles = [&](int64_t k0, int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int R0 = (wave * 4 + i) * 8;
-            lds_load_rows(a.A, K, n0, a.N - 1, k0, sA[buf], R0, lane);
-            lds_load_rows(a.B, K, m0, M - 1, k0, sB[buf], R0, lane);
-        }
-    };
-    uint16_t rad = 0, rbd = 0;
-    auto load_scales = [&](int64_t k0) {
-        if constexpr (WF == W_Q32) {
-            const int row = tid >> 1, blk = tid & 1;
-            rad = a.Ad[(n0 + row) * (K / 32) + k0 / 32 + blk];
-            const int64_t mr = m0 + row;
-            rbd = mr < M ? ((const uint16_t *) a.Bd)[mr * (K / 32) + k0 / 32 + blk] : (uint16_t) 0;
-        }
-    };
-    auto store_scales = [&](int buf) {
-        if constexpr (WF == W_Q32) { sAd[buf][tid] = rad; sBd[buf][tid] = rbd; }
-    };
-
-    const int64_t nst = K / KC;
-    issue_tiles(0, 0);
-    load_scales(0);
-    store_scales(0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int64_t st = 0; st < nst; st++) {
-        const int cur = (int) (st & 1);
+    auto issue = [&](int64_t st) {
+        unsigned char * base = smem + (int) (st % NST) * T::STAGE;
         const int64_t k0 = st * KC;
-        if (st + 1 < nst) { issue_tiles(k0 + KC, cur ^ 1); load_scales(k0 + KC); }
-        const _Float16 * A_ = sA[cur];
-        const _Float16 * B_ = sB[cur];
-#pragma unroll 1
-        for (int blk = 0; blk < 2; blk++) {
-            h8 bv[2][2];
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int row = 64 * wm + 32 * j + l32;
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) bv[j][hh] = *(const h8 *) &B_[swz(row, blk * 4 + hh * 2 + g)];
-            }
-            [[maybe_unused]] h8 sb[2];
-            if constexpr (WF == W_Q32) {
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    // da in K-slot 0 of lane group 0 only; group 1 contributes zeros
-                    const uint32_t d = g == 0 ? (uint32_t) sBd[cur][(64 * wm + 32 * j + l32) * 2 + blk] : 0u;
-                    sb[j] = __builtin_bit_cast(h8, make_uint4(d, 0u, 0u, 0u));
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                if (i == 1) __builtin_amdgcn_sched_barrier(0);
-                const int row = 64 * wn + 32 * i + l32;
-                const h8 a0 = *(const h8 *) &A_[swz(row, blk * 4 + g)];
-                const h8 a1 = *(const h8 *) &A_[swz(row, blk * 4 + 2 + g)];
-                if constexpr (WF == W_F16) {
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        acc[i][j] = MFMA16(a0, bv[j][0], acc[i][j]);
-                        acc[i][j] = MFMA16(a1, bv[j][1], acc[i][j]);
-                    }
-                } else if constexpr (WF == W_Q32) {
-                    // dw in K-slot 0 (both lane groups hold row n's scale; group 1 meets zeros in B)
-                    const h8 sa = __builtin_bit_cast(h8, make_uint4((uint32_t) sAd[cur][row * 2 + blk], 0u, 0u, 0u));
-                    f16v S0 = MFMA16(a0, bv[0][0], zero);
-                    f16v S1 = MFMA16(a0, bv[1][0], zero);
-                    const f16v c0 = MFMA16(sa, sb[0], zero);
-                    const f16v c1 = MFMA16(sa, sb[1], zero);
-                    S0 = MFMA16(a1, bv[0][1], S0);
-                    S1 = MFMA16(a1, bv[1][1], S1);
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        acc[i][0][r] = fmaf(S0[r], c0[r], acc[i][0][r]);
-                        acc[i][1][r] = fmaf(S1[r], c1[r], acc[i][1][r]);
-                    }
-                } else {   // W_Q4K: integer sums over the 256-deep super-block
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        ssb[i][j] = MFMA16(a0, bv[j][0], ssb[i][j]);
-                        ssb[i][j] = MFMA16(a1, bv[j][1], ssb[i][j]);
+        if constexpr (WF == W_Q4K) {
+            if ((st & 3) == 0) {
+                const int64_t sb = st >> 2, nsb = K >> 8;
+                unsigned char * xb = smem + NST * T::STAGE + (int) (sb & 1) * T::XSB;
+                constexpr int N1 = BN / 64, N2 = BN / 32, N3 = T::BM / 64, N4 = T::BM / 32;
+                for (int L = wave; L < N1 + N2 + N3 + N4; L += NW) {
+                    if (L < N1) {
+                        const uint32_t * src = (const uint32_t *) a.Ad + sb * a.N + n0 + 64 * L + lane;
+                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_DW + 256 * L), 4, 0, 0);
+                    } else if (L < N1 + N2) {
+                        const int L2 = L - N1;
+                        const int64_t n = n0 + 32 * L2 + (lane >> 1);
+                        const _Float16 * src = a.Amin + (n * nsb + sb) * 16 + 8 * (lane & 1);
+                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_MIN + 1024 * L2), 16, 0, 0);
+                    } else if (L < N1 + N2 + N3) {
+                        const int L3 = L - N1 - N2;
+                        int64_t m = m0 + 64 * L3 + lane;
+                        if (m > M - 1) m = M - 1;
+                        const float * src = (const float *) a.Bd + m * nsb + sb;
+                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_DA + 256 * L3), 4, 0, 0);
+                    } else {
+                        const int L4 = L - N1 - N2 - N3;
+                        int64_t m = m0 + 32 * L4 + (lane >> 1);
+                        if (m > M - 1) m = M - 1;
+                        const _Float16 * src = a.Bsum + m * (K >> 4) + sb * 16 + 8 * (lane & 1);
+                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_BS + 1024 * L4), 16, 0, 0);
                     }
                 }
+            }
+        }
+        if constexpr (WF == W_Q32) {
+            // the four f16 block scales of every row, two per lane (rows past M repeat row M-1; blocks
+            // past K, in a final half stage, repeat the stage's first pair)
+            int64_t kb = (k0 >> 5) + 2 * (lane & 1);
+            if (kb >= KB) kb = k0 >> 5;
+            for (int L = wave; L < T::ROWS / 32; L += NW) {
+                const int r = 32 * L + (lane >> 1);
+                const uint16_t * src;
+                if (32 * L < BN) {
+                    src = a.Ad + (n0 + r) * KB + kb;
+                } else {
+                    int64_t m = m0 + r - BN;
+                    if (m > M - 1) m = M - 1;
+                    src = (const uint16_t *) a.Bd + m * KB + kb;
+                }
+                __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (base + T::TILE + 256 * L), 4, 0, 0);
+            }
+        }
+        const int c = (lane & 7) ^ (lane >> 3);   // rows are loaded 8 at a time, so r & 7 == lane >> 3
+        int64_t cb = k0 * ESZ + 16 * c;            // byte offset of this lane's chunk in its row
+        if (cb >= rowbytes) cb = k0 * ESZ + 16 * (c & 3);   // final half stage: stay inside the row
+#pragma unroll
+        for (int i = 0; i < T::LOADS; i++) {
+            const int L = NW * i + wave;
+            const int r = 8 * L + (lane >> 3);
+            const unsigned char * src;
+            if (i < BN / (8 * NW)) {
+                src = (const unsigned char *) a.A + (n0 + r) * rowbytes;
+            } else {
+                int64_t m = m0 + r - BN;
+                if (m > M - 1) m = M - 1;          // rows past the end load a valid row; results dropped
+                src = (const unsigned char *) a.B + m * rowbytes;
+            }
+            __builtin_amdgcn_global_load_lds((const void *) (src + cb), (lds_void *) (base + 1024 * L), 16, 0, 0);
+        }
+    };
+
+    f16v acc[TI][TJ];
+    [[maybe_unused]] f16v ssb[TI][TJ];
+    const f16v zero = {};
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++) { acc[i][j] = zero; if constexpr (WF == W_Q4K) ssb[i][j] = zero; }
+
+    // q8_0 / q4_0 stage of NB 32-blocks. Steps u = (block, tile), tiles i-major: one int8 MFMA gives the
+    // exact block sum S, one f16 MFMA (32x32x8) of the scale operands (dw in K-slot 0 of both lane
+    // groups, da in K-slot 0 of group 0 only) gives the exact f32 dw[n] * da[m], and
+    // acc = fma(float(S), dw*da, acc).
+    // The 32 VALU ops per step (convert + fma) bound this path, not the two MFMAs.
+    [[maybe_unused]] auto q32_stage = [&](const unsigned char * base, auto nb_c) {
+        constexpr int NB = decltype(nb_c)::value;
+        constexpr int TT = TI * TJ, U = NB * TT;
+        const uint32_t * scl = (const uint32_t *) (base + T::TILE);
+        const uint32_t gmask = g == 0 ? 0xffffffffu : 0u;
+        i4v A[NB][TI], B[NB][TJ];
+        h4 SA[NB][TI], SB[NB][TJ];
+        auto scale_of = [&](int r, int blk) -> uint32_t {
+            const uint32_t h = scl[2 * r + (blk >> 1)];
+            return (blk & 1) ? h >> 16 : h & 0xffffu;
+        };
+        auto load_for = [&](int u) {
+            const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
+            if (j == 0) {
+                const int r = 32 * (wn * TI + i) + l32;
+                A[blk][i] = lds_chunk<i4v>(base, r, 2 * blk + g);
+                SA[blk][i] = __builtin_bit_cast(h4, make_uint2(scale_of(r, blk), 0u));
+            }
+            if (i == 0) {
+                const int r = BN + 32 * (wm * TJ + j) + l32;
+                B[blk][j] = lds_chunk<i4v>(base, r, 2 * blk + g);
+                SB[blk][j] = __builtin_bit_cast(h4, make_uint2(scale_of(r, blk) & gmask, 0u));
+            }
+        };
+        const i16v izero = {};
+        load_for(0);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (u + 1 < U) load_for(u + 1);
+            const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
+            const i16v S = MFMA_I8(A[blk][i], B[blk][j], izero);
+            const f16v C = MFMA8(SA[blk][i], SB[blk][j], zero);
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[r], C[r], acc[i][j][r]);
+            // one scheduling region per step: operand reads stay one step ahead instead of being
+            // hoisted to the top of the stage (which would not fit the 256 VGPRs of two waves/SIMD);
+            // the other wave on the SIMD covers this wave's MFMA latency
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    for (int s = 0; s < NST - 1; s++)
+        if (s < nst) issue(s);
+
+    for (int64_t st = 0; st < nst; st++) {
+        // stage st has landed once at most the loads of the NST - 2 younger stages are outstanding
+        // (all waves' copies of stage st visible; every wave done reading stage st-1's buffer)
+        if (st + NST - 2 < nst) stage_barrier<(NST - 2) * T::LOADS>();
+        else stage_barrier<0>();
+        if (st + NST - 1 < nst) issue(st + NST - 1);
+        const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
+        if constexpr (WF == W_Q32) {
+            if ((st + 1) * KC <= K) q32_stage(base, std::integral_constant<int, 4>{});
+            else q32_stage(base, std::integral_constant<int, 2>{});
+        } else {
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                h8 a0[TI], a1[TI], b0[TJ], b1[TJ];
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+                    const int r = 32 * (wn * TI + i) + l32;
+                    a0[i] = lds_chunk<h8>(base, r, 4 * blk + g);
+                    a1[i] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
+                }
+#pragma unroll
+                for (int j = 0; j < TJ; j++) {
+                    const int r = BN + 32 * (wm * TJ + j) + l32;
+                    b0[j] = lds_chunk<h8>(base, r, 4 * blk + g);
+                    b1[j] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
+                }
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int j = 0; j < TJ; j++) {
+                        if constexpr (WF == W_F16) {
+                            acc[i][j] = MFMA16(a0[i], b0[j], acc[i][j]);
+                            acc[i][j] = MFMA16(a1[i], b1[j], acc[i][j]);
+                        } else {   // W_Q4K: integer sums over the 256-deep super-block
+                            ssb[i][j] = MFMA16(a0[i], b0[j], ssb[i][j]);
+                            ssb[i][j] = MFMA16(a1[i], b1[j], ssb[i][j]);
+                        }
+                    }
             }
         }
         if constexpr (WF == W_Q4K) {
-            if (((k0 + KC) & 255) == 0) {
-                const int64_t sbi = k0 >> 8, nsb = K >> 8;
-                h8 bs[2];
-                float da[2];
+            if ((st & 3) == 3) {
+                // super-block epilogue (ggml vec_dot_q4_K_q8_K): acc += (dw*da) S - (dmin*da) sum_j m_j bsum_j
+                const unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 2) & 1) * T::XSB;
+                h8 bs[TJ];
+                float da[TJ];
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const int64_t m = m0 + 64 * wm + 32 * j + l32;
-                    const bool ok = m < M;
-                    const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-                    bs[j] = ok ? *(const h8 *) (a.Bsum + m * (K / 16) + sbi * 16 + g * 8) : z;
-                    da[j] = ok ? ((const float *) a.Bd)[m * nsb + sbi] : 0.0f;
+                for (int j = 0; j < TJ; j++) {
+                    const int rm = 32 * (wm * TJ + j) + l32;
+                    bs[j] = *(const h8 *) (xb + T::X_BS + rm * 32 + 16 * g);
+                    da[j] = *(const float *) (xb + T::X_DA + 4 * rm);
                 }
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const int64_t nr = n0 + 64 * wn + 32 * i + l32;
-                    const h8 am = *(const h8 *) (a.Amin + (nr * nsb + sbi) * 16 + g * 8);
+                for (int i = 0; i < TI; i++) {
+                    const int rn = 32 * (wn * TI + i);
+                    const h8 am = *(const h8 *) (xb + T::X_MIN + (rn + l32) * 32 + 16 * g);
                     float dw[16], dm[16];
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const int64_t n = n0 + 64 * wn + 32 * i + 8 * q + 4 * g;
-                        const ushort4 v = *(const ushort4 *) (a.Ad + sbi * a.N + n);
-                        const ushort4 u = *(const ushort4 *) (a.Admin + sbi * a.N + n);
-                        dw[4 * q + 0] = h2f(v.x); dw[4 * q + 1] = h2f(v.y); dw[4 * q + 2] = h2f(v.z); dw[4 * q + 3] = h2f(v.w);
-                        dm[4 * q + 0] = h2f(u.x); dm[4 * q + 1] = h2f(u.y); dm[4 * q + 2] = h2f(u.z); dm[4 * q + 3] = h2f(u.w);
+                        const uint4 v = *(const uint4 *) (xb + T::X_DW + 4 * (rn + 8 * q + 4 * g));
+                        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++) { dw[4 * q + e] = h2f((uint16_t) (vv[e] & 0xffffu)); dm[4 * q + e] = h2f((uint16_t) (vv[e] >> 16)); }
                     }
 #pragma unroll
-                    for (int j = 0; j < 2; j++) {
+                    for (int j = 0; j < TJ; j++) {
                         const f16v ms = MFMA16(am, bs[j], zero);
 #pragma unroll
                         for (int r = 0; r < 16; r++) {
@@ -292,18 +418,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(kargs a) {
                 }
             }
         }
-        if (st + 1 < nst) store_scales(cur ^ 1);
-        __builtin_amdgcn_s_waitcnt(0);                // this wave's HBM->LDS copies have landed
-        __syncthreads();                              // ... and everyone else's
     }
 
-    // epilogue: lane holds token m and features n0 + 64wn + 32i + 8q + 4g + e
+    // epilogue: lane holds token m and features nb + 8q + 4g + e of each tile
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < TI; i++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int64_t m = m0 + 64 * wm + 32 * j + l32;
-            const int64_t nb = n0 + 64 * wn + 32 * i;
+        for (int j = 0; j < TJ; j++) {
+            const int64_t m = m0 + 32 * (wm * TJ + j) + l32;
+            const int64_t nb = n0 + 32 * (wn * TI + i);
             if constexpr (EPI == EPI_GELU_Q8_0) {
                 // q8_0 activation of the next linear, x86 rule: d = amax/127 (f16), q = rne(x*127/amax)
                 float v[16];
@@ -323,14 +446,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mfma(kargs a) {
                 const float d = am / 127.0f;
                 const float id = am != 0.0f ? 127.0f / am : 0.0f;
                 if (m < M) {
-                    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         const int64_t n = nb + 8 * q + 4 * g;
-                        h4 o;
+                        uint32_t o = 0;
 #pragma unroll
-                        for (int e = 0; e < 4; e++) o[e] = (_Float16) fminf(fmaxf(rintf(v[4 * q + e] * id), -128.0f), 127.0f);
-                        *(h4 *) ((_Float16 *) a.ep.oq + m * a.N + n) = o;
+                        for (int e = 0; e < 4; e++) {
+                            const int qi = (int) fminf(fmaxf(rintf(v[4 * q + e] * id), -128.0f), 127.0f);
+                            o |= ((uint32_t) qi & 0xffu) << (8 * e);
+                        }
+                        *(uint32_t *) ((int8_t *) a.ep.oq + m * a.N + n) = o;   // int8 codes
                     }
                     if (g == 0) ((uint16_t *) a.ep.od)[m * (a.N / 32) + nb / 32] = f2hbits(d);
                 }
@@ -397,16 +522,71 @@ __global__ void k_qkv_split(kargs a, const float * __restrict__ qkv) {
     epi4<EPI_QKV>(a, m, n, t);
 }
 
+struct tile_cfg { int wn, wm, ti, tj; };
+// eight-wave workgroup tiles (BN x BM): 256x128, 192x128, 128x128 (two wave shapes), 64x128, 128x64
+constexpr tile_cfg k_tiles[] = {{4, 2, 2, 2}, {2, 4, 3, 1}, {2, 4, 2, 1}, {4, 2, 1, 2}, {2, 4, 1, 1}, {4, 2, 1, 1}};
+// relative efficiency of one workgroup tile (larger tiles re-read less from L2 and LDS)
+constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66};
+
+std::atomic<int> g_force_tile{-1};
+
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
+// The tile with the least estimated time: whole waves of workgroups over the CUs (one workgroup per
+// CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N.
+int pick_tile(int64_t N, int64_t M) {
+    const int f = g_force_tile.load();
+    const int nt = (int) (sizeof(k_tiles) / sizeof(k_tiles[0]));
+    if (f >= 0 && f < nt && N % (32 * k_tiles[f].wn * k_tiles[f].ti) == 0) return f;
+    const int cus = cu_count();
+    double best = 1e300;
+    int b = nt - 1;
+    for (int c = 0; c < nt; c++) {
+        const int64_t bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
+        if (N % bn) continue;
+        const int64_t t = (N / bn) * ((M + bm - 1) / bm);
+        const double waves = (double) ((t + cus - 1) / cus);
+        const double cost = waves * (double) (bn * bm) / k_tile_eff[c];
+        if (cost < best) { best = cost; b = c; }
+    }
+    return b;
+}
+
+template <int WF, int EPI>
+void launch_tiles(int c, const kargs & a, hipStream_t s) {
+    const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm);
+    switch (c) {
+        case 0: k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a); break;
+        case 1: k_gemm_mfma<WF, EPI, 2, 4, 3, 1><<<grid, 512, 0, s>>>(a); break;
+        case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(a); break;
+        case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(a); break;
+        case 4: k_gemm_mfma<WF, EPI, 2, 4, 1, 1><<<grid, 512, 0, s>>>(a); break;
+        default: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(a); break;
+    }
+}
+
 template <int WF>
-void dispatch_mfma(const kargs & a, hipStream_t s) {
-    dim3 grid((unsigned) (a.N / BN), (unsigned) ((a.M + BM - 1) / BM));
+void dispatch_mfma(kargs a, hipStream_t s) {
+    const int c = pick_tile(a.N, a.M);
+    a.tn = (int) (a.N / (32 * k_tiles[c].wn * k_tiles[c].ti));
+    a.tm = (int) ((a.M + 32 * k_tiles[c].wm * k_tiles[c].tj - 1) / (32 * k_tiles[c].wm * k_tiles[c].tj));
     switch (a.ep.kind) {
-        case EPI_F32:       k_gemm_mfma<WF, EPI_F32><<<grid, 256, 0, s>>>(a); break;
-        case EPI_RESID:     k_gemm_mfma<WF, EPI_RESID><<<grid, 256, 0, s>>>(a); break;
-        case EPI_GELU_F32:  k_gemm_mfma<WF, EPI_GELU_F32><<<grid, 256, 0, s>>>(a); break;
-        case EPI_GELU_F16:  k_gemm_mfma<WF, EPI_GELU_F16><<<grid, 256, 0, s>>>(a); break;
-        case EPI_GELU_Q8_0: k_gemm_mfma<WF, EPI_GELU_Q8_0><<<grid, 256, 0, s>>>(a); break;
-        case EPI_QKV:       k_gemm_mfma<WF, EPI_QKV><<<grid, 256, 0, s>>>(a); break;
+        case EPI_F32:       launch_tiles<WF, EPI_F32>(c, a, s); break;
+        case EPI_RESID:     launch_tiles<WF, EPI_RESID>(c, a, s); break;
+        case EPI_GELU_F32:  launch_tiles<WF, EPI_GELU_F32>(c, a, s); break;
+        case EPI_GELU_F16:  launch_tiles<WF, EPI_GELU_F16>(c, a, s); break;
+        case EPI_GELU_Q8_0: launch_tiles<WF, EPI_GELU_Q8_0>(c, a, s); break;
+        case EPI_QKV:       launch_tiles<WF, EPI_QKV>(c, a, s); break;
     }
 }
 
@@ -416,7 +596,6 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
     kargs a{};
     a.A = (const _Float16 *) W.w;
     a.Ad = (const uint16_t *) W.wd;
-    a.Admin = (const uint16_t *) W.wdmin;
     a.Amin = (const _Float16 *) W.wmin;
     a.B = (const _Float16 *) X.q;
     a.Bd = X.d;
@@ -441,6 +620,12 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
         case W_Q32: dispatch_mfma<W_Q32>(a, s); break;
         case W_Q4K: dispatch_mfma<W_Q4K>(a, s); break;
     }
+}
+
+int gemm_force_tile(int index) {
+    if (index >= (int) (sizeof(k_tiles) / sizeof(k_tiles[0]))) return -1;
+    g_force_tile.store(index < 0 ? -1 : index);
+    return 0;
 }
 
 void launch_qkv_split(const float * qkv, int64_t M, int64_t N, const gemm_epi & ep, hipStream_t s) {

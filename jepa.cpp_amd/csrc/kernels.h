@@ -2,8 +2,8 @@
 //
 // Data layouts in HBM (row-major unless stated):
 //   residual stream  x      f32 [rows][D]
-//   GEMM operands    W      f16 [N][K]  integer codes (q8_0 q, q4_0 q-8, q4_K sc*q) or f16 weights
-//                    X      f16 [M][K]  integer codes (q8_0 / q8_K activations) or f16-rounded values
+//   GEMM operands    W      int8 [N][K] codes (q8_0 q, q4_0 q-8); f16 [N][K] codes (q4_K sc*q) or f16 weights
+//                    X      int8 [M][K] q8_0 activation codes; f16 [M][K] q8_K codes or f16-rounded values
 //   scales           q8_0   f16 [rows][K/32];  q8_K  f32 d [rows][K/256] + f16 bsums [rows][K/16]
 //   attention        Q, K   f16 [item*H][R_pad][hd];  V^T f16 [item*H][hd][R_pad] with the tokens of
 //                    every 16-token group stored in the order the PV MFMA reads them
@@ -13,7 +13,7 @@
 
 struct act_view {            // a GEMM activation operand / a quantizer output
     int       fmt = 0;       // afmt
-    void *    q = nullptr;   // f16 [M][K] (A_F16 / A_Q8_*) or f32 [M][K] (A_F32)
+    void *    q = nullptr;   // int8 [M][K] (A_Q8_0), f16 [M][K] (A_F16 / A_Q8_K) or f32 [M][K] (A_F32)
     void *    d = nullptr;   // A_Q8_0: f16 [M][K/32]; A_Q8_K: f32 [M][K/256]
     void *    bsum = nullptr;// A_Q8_K: f16 [M][K/16]
     int64_t   ld = 0;        // K
@@ -65,10 +65,13 @@ void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_ite
 void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D, hipStream_t s);
 
 // weight expansion at load: raw ggml blocks (device) -> dev_linear operand arrays
-void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd, void * wdmin,
+void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd,
                    void * wmin, hipStream_t s);
 
 // test hooks
+// force the MFMA GEMM onto workgroup tile `index` (0..5) for every later launch whose N it divides;
+// -1 restores the automatic choice. Returns -1 for an index past the table.
+int gemm_force_tile(int index);
 void launch_qkv_split(const float * qkv, int64_t M, int64_t N, const gemm_epi & ep, hipStream_t s);
 void launch_dequant_rows(int gtype, const void * raw, int64_t n_rows, int64_t n_cols, float * y, hipStream_t s);
 void launch_pack_act_blocks(const act_view & a, int64_t M, int64_t K, void * blocks, hipStream_t s);

@@ -279,18 +279,17 @@ struct loader {
             L.w = dalloc(t->nbytes);
             if (!L.w || hipMemcpyAsync(L.w, staging, t->nbytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
         } else {
-            L.w = dalloc((size_t) n_in * n_out * 2);
+            L.w = dalloc((size_t) n_in * n_out * (L.fmt == W_Q32 ? 1 : 2));
             if (!L.w) return false;
             if (L.fmt == W_Q32) {
                 L.wd = dalloc((size_t) n_out * (n_in / 32) * 2);
                 if (!L.wd) return false;
             } else {
-                L.wd = dalloc((size_t) n_out * (n_in / 256) * 2);
-                L.wdmin = dalloc((size_t) n_out * (n_in / 256) * 2);
+                L.wd = dalloc((size_t) n_out * (n_in / 256) * 4);
                 L.wmin = dalloc((size_t) n_out * (n_in / 256) * 16 * 2);
-                if (!L.wd || !L.wdmin || !L.wmin) return false;
+                if (!L.wd || !L.wmin) return false;
             }
-            launch_repack(t->type, staging, n_out, n_in, L.w, L.wd, L.wdmin, L.wmin, s);
+            launch_repack(t->type, staging, n_out, n_in, L.w, L.wd, L.wmin, s);
         }
         if (hipStreamSynchronize(s) != hipSuccess) { jepa_log("jepa: weight upload of %s failed\n", wname.c_str()); return false; }
         return vec(bname, n_out, &L.bias);

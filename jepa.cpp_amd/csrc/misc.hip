@@ -19,7 +19,7 @@ __device__ __forceinline__ float h2f(uint16_t b) { return (float) __builtin_bit_
 // so a q8_0 block (32 values) is 4 adjacent lanes and a q8_K block (256) is 32 adjacent lanes.
 //   LayerNorm = ggml_norm (mean, centred variance, both accumulated in double like ggml_float)
 //   followed by * w and + b (reference src/jepa.cpp:356-361), then the output conversion:
-//   A_Q8_0: d = amax/127 (f16), q = rne(x * 127/amax)        x86 quantize_row_q8_0
+//   A_Q8_0: d = amax/127 (f16), q = rne(x * 127/amax)        x86 quantize_row_q8_0; int8 codes
 //   A_Q8_K: max = first largest-|x| value, iscale = -127/max, q = min(127, rne(iscale*x)),
 //           d = 1/iscale (f32), bsums of 16                  quantize_row_q8_K_ref
 // ------------------------------------------------------------------------------------------------
@@ -110,10 +110,13 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
             const float d = am / 127.0f;
             const float id = am != 0.0f ? 127.0f / am : 0.0f;
             if (live) {
-                h8 hv;
+                uint32_t qb[2] = {0u, 0u};
 #pragma unroll
-                for (int e = 0; e < 8; e++) hv[e] = (_Float16) fminf(fmaxf(rintf(v[i][e] * id), -128.0f), 127.0f);
-                *(h8 *) ((_Float16 *) out.q + row * D + 8 * o) = hv;
+                for (int e = 0; e < 8; e++) {
+                    const int qi = (int) fminf(fmaxf(rintf(v[i][e] * id), -128.0f), 127.0f);
+                    qb[e >> 2] |= ((uint32_t) qi & 0xffu) << (8 * (e & 3));
+                }
+                *(uint2 *) ((int8_t *) out.q + row * D + 8 * o) = make_uint2(qb[0], qb[1]);
                 if ((o & 3) == 0) ((uint16_t *) out.d)[row * (D / 32) + o / 4] = f2hbits(d);
             }
         } else {   // A_Q8_K
@@ -203,28 +206,29 @@ __global__ void k_cls_rows(float * x, const float * cls, const float * pos, int6
 // ------------------------------------------------------------------------------------------------
 // weight expansion at load (ggml blocks -> GEMM operand arrays)
 // ------------------------------------------------------------------------------------------------
-__global__ void k_repack_q8_0(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint16_t * wd) {
+// q8_0 / q4_0 weights -> int8 codes [n_out][n_in] (q, or q - 8) + f16 d [n_out][n_in/32]
+__global__ void k_repack_q8_0(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, int8_t * w, uint16_t * wd) {
     const int64_t nb = n_in / 32;
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= n_out * nb) return;
     const uint8_t * blk = raw + id * 34;
     wd[id] = (uint16_t) (blk[0] | (blk[1] << 8));
     const int64_t n = id / nb, bi = id % nb;
-    _Float16 * dst = w + n * n_in + bi * 32;
-    for (int j = 0; j < 32; j++) dst[j] = (_Float16) (float) (int8_t) blk[2 + j];
+    int8_t * dst = w + n * n_in + bi * 32;
+    for (int j = 0; j < 32; j++) dst[j] = (int8_t) blk[2 + j];
 }
 
-__global__ void k_repack_q4_0(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint16_t * wd) {
+__global__ void k_repack_q4_0(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, int8_t * w, uint16_t * wd) {
     const int64_t nb = n_in / 32;
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= n_out * nb) return;
     const uint8_t * blk = raw + id * 18;
     wd[id] = (uint16_t) (blk[0] | (blk[1] << 8));
     const int64_t n = id / nb, bi = id % nb;
-    _Float16 * dst = w + n * n_in + bi * 32;
+    int8_t * dst = w + n * n_in + bi * 32;
     for (int j = 0; j < 16; j++) {
-        dst[j]      = (_Float16) (float) ((blk[2 + j] & 0xF) - 8);
-        dst[j + 16] = (_Float16) (float) ((blk[2 + j] >> 4) - 8);
+        dst[j]      = (int8_t) ((blk[2 + j] & 0xF) - 8);
+        dst[j + 16] = (int8_t) ((blk[2 + j] >> 4) - 8);
     }
 }
 
@@ -233,15 +237,15 @@ __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t * q, int & d,
     else { d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4); m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4); }
 }
 
-__global__ void k_repack_q4_K(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint16_t * wd,
-                              uint16_t * wdmin, _Float16 * wmin) {
+__global__ void k_repack_q4_K(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint32_t * wd,
+                              _Float16 * wmin) {
     const int64_t nsb = n_in / 256;
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= n_out * nsb) return;
     const int64_t n = id / nsb, sb = id % nsb;
     const uint8_t * blk = raw + id * 144;
-    wd[sb * n_out + n] = (uint16_t) (blk[0] | (blk[1] << 8));
-    wdmin[sb * n_out + n] = (uint16_t) (blk[2] | (blk[3] << 8));
+    // (d, dmin) of the super-block as one word: d in the low half, dmin in the high half
+    wd[sb * n_out + n] = (uint32_t) blk[0] | ((uint32_t) blk[1] << 8) | ((uint32_t) blk[2] << 16) | ((uint32_t) blk[3] << 24);
     const uint8_t * sc = blk + 4;
     const uint8_t * qs = blk + 16;
     _Float16 * dst = w + n * n_in + sb * 256;
@@ -298,7 +302,7 @@ __global__ void k_pack_act(act_view a, int64_t M, int64_t K, uint8_t * out) {
         uint8_t * o = out + id * 34;
         const uint16_t d = ((const uint16_t *) a.d)[m * nb + bi];
         o[0] = (uint8_t) (d & 0xFF); o[1] = (uint8_t) (d >> 8);
-        for (int j = 0; j < 32; j++) o[2 + j] = (uint8_t) (int8_t) (float) ((const _Float16 *) a.q)[m * K + bi * 32 + j];
+        for (int j = 0; j < 32; j++) o[2 + j] = (uint8_t) ((const int8_t *) a.q)[m * K + bi * 32 + j];
     } else if (a.fmt == A_Q8_K) {
         const int64_t nb = K / 256;
         if (id >= M * nb) return;
@@ -379,13 +383,13 @@ void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_
     k_cls_rows<<<nblk(n_items * D, 256), 256, 0, s>>>(x, cls, pos, n_items, R, D);
 }
 
-void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd, void * wdmin, void * wmin,
+void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd, void * wmin,
                    hipStream_t s) {
     switch (gtype) {
-        case T_Q8_0: k_repack_q8_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (_Float16 *) w, (uint16_t *) wd); break;
-        case T_Q4_0: k_repack_q4_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (_Float16 *) w, (uint16_t *) wd); break;
+        case T_Q8_0: k_repack_q8_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd); break;
+        case T_Q4_0: k_repack_q4_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd); break;
         case T_Q4_K: k_repack_q4_K<<<nblk(n_out * (n_in / 256), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (_Float16 *) w,
-                                                                                  (uint16_t *) wd, (uint16_t *) wdmin, (_Float16 *) wmin); break;
+                                                                                  (uint32_t *) wd, (_Float16 *) wmin); break;
         default: break;
     }
 }

@@ -73,8 +73,8 @@ struct hparams {
 };
 
 // Weight formats on the device. Quantized matrices are expanded once at load into the operand
-// layout of the GEMM kernel: the integer codes as exact f16 values (q8_0: q; q4_0: q - 8;
-// q4_K: sc_j * q, the 6-bit sub-block scale folded in, still exact in f16) plus their scales.
+// layout of the GEMM kernel plus their scales: q8_0 / q4_0 as int8 codes (q; q - 8) for the int8
+// MFMA; q4_K as exact f16 values sc_j * q (the 6-bit sub-block scale folded in) for the f16 MFMA.
 enum wfmt { W_F32 = 0, W_F16 = 1, W_Q32 = 2 /* q8_0, q4_0: f16 scale per 32 */, W_Q4K = 3 };
 // Activation formats consumed by the GEMM (what the producer of a linear's input writes).
 enum afmt { A_F32 = 0, A_F16 = 1, A_Q8_0 = 2, A_Q8_K = 3 };
@@ -83,9 +83,8 @@ struct dev_linear {
     int      gtype = -1;          // ggml type in the file
     int      fmt = W_F32;
     int64_t  n_out = 0, n_in = 0;
-    void *   w = nullptr;         // [n_out][n_in]: f32 (W_F32) or f16 (others)
-    void *   wd = nullptr;        // W_Q32: f16 d [n_out][n_in/32]; W_Q4K: f16 d [n_in/256][n_out]
-    void *   wdmin = nullptr;     // W_Q4K: f16 dmin [n_in/256][n_out]
+    void *   w = nullptr;         // [n_out][n_in]: f32 (W_F32), int8 (W_Q32) or f16 (W_F16, W_Q4K)
+    void *   wd = nullptr;        // W_Q32: f16 d [n_out][n_in/32]; W_Q4K: u32 (f16 d | f16 dmin << 16) [n_in/256][n_out]
     void *   wmin = nullptr;      // W_Q4K: f16 mins [n_out][n_in/256][16] (m_{k/2}, k = 0..15)
     float *  bias = nullptr;      // [n_out] or null
     afmt act() const {

@@ -160,6 +160,50 @@ def test_matmul_full_m2048_q8_0(jlib, oracle):
     np.testing.assert_array_equal(host(y).view(np.uint32), want.view(np.uint32))
 
 
+# workgroup tiles of the MFMA GEMM (weight rows x tokens), by index
+TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64)}
+
+
+@pytest.mark.parametrize("tile", sorted(TILES))
+@pytest.mark.parametrize("gtype", [gguf.GGML_Q8_0, gguf.GGML_Q4_0, gguf.GGML_Q4_K, gguf.GGML_F16])
+def test_matmul_every_tile(jlib, oracle, gtype, tile):
+    """Every workgroup tile shape of the MFMA GEMM, forced, on a ragged token count (M = 389: partial
+    last tile, rows past M clamped) and K = 768 (12 stages, so the pipeline's prologue, steady state
+    and tail all run; three q4_K super-blocks). q8_0 / q4_0 bit-exact, others within f32 rounding."""
+    bn = TILES[tile][0]
+    n_out, n_in, M = bn * (3 if bn == 128 else 2) if bn != 64 else 256, 768, 389
+    rng = np.random.default_rng(tile * 100 + gtype)
+    w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    bias = (rng.standard_normal(n_out) * 0.02).astype(np.float32)
+    if gtype == gguf.GGML_F16:
+        raw = w.astype(np.float16).view(np.uint8)
+    else:
+        raw = gguf.quantize(gtype, w)
+    want = oracle.mul_mat(gtype, raw, n_out, n_in, x, bias)
+    dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
+    y = torch.zeros((M, n_out), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    L = jlib.lib()
+    assert L.jepa_amd_gemm_tile(tile) == 0
+    try:
+        rc = L.jepa_amd_matmul(0, gtype, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, y.data_ptr(), 1, None)
+    finally:
+        L.jepa_amd_gemm_tile(-1)
+    assert rc == 0, jlib.error_text()
+    got = host(y)
+    if gtype in (gguf.GGML_Q8_0, gguf.GGML_Q4_0):
+        diff = np.argwhere(got.view(np.uint32) != want.view(np.uint32))
+        assert diff.size == 0, f"{len(diff)} outputs differ, first {diff[:4].tolist()}, max abs {np.abs(got - want).max():.3e}"
+    else:
+        assert np.abs(got - want).max() <= 2e-5 * np.abs(want).max()
+
+
+def test_gemm_tile_hook_rejects_unknown(jlib):
+    assert jlib.lib().jepa_amd_gemm_tile(len(TILES)) == -1
+    assert jlib.lib().jepa_amd_gemm_tile(-1) == 0
+
+
 def _attention_ref(qkv, n_items, n_tok, H, rope=None):
     """double-precision softmax(q k^T / 8) v per head, K/V rounded to f16 like ggml_cast"""
     D = H * 64
