@@ -121,6 +121,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-q4k", action="store_true", help="skip the q4_K line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run the library's plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the encoder has no multi-GPU path; clips are "
@@ -151,7 +153,7 @@ def main():
         tf = os.path.join(ROOT, "profiles", "gemm_q8_vitl16_counters.json")
         if os.path.exists(tf):
             with open(tf) as f:
-                traffic = json.load(f).get("hbm_bytes_per_launch")
+                traffic = json.load(f).get("hbm_bytes_per_launch")    # rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": traffic,
                 "kernel": "gemm_q8 (q8_0 x q8_0 GEMMs: qkv, out, fc1, fc2)", "avg_launch_ms": round(gq["avg_ms"], 5),
@@ -177,6 +179,18 @@ def main():
             q4["gemm_roofline"] = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                                    "frac": round(ach / PEAK_INT8_TOPS, 4)}
         extra["q4_k"] = q4
+    if args.copy_mib > 0:
+        # a copy of known size: FETCH_SIZE / WRITE_SIZE of k_copy_f32 calibrate the counters
+        import ctypes as C
+        from jepa_amd import _lib
+        n = args.copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        ms = C.c_double(0)
+        _lib.lib().jepa_amd_copy(0, src.data_ptr(), dst.data_ptr(), n, 3, C.byref(ms))
+        extra["copy_calibration"] = {"bytes_read": n * 4, "bytes_written": n * 4, "ms": round(ms.value, 4),
+                                     "GB/s": round(2 * n * 4 / (ms.value * 1e-3) / 1e9, 1)}
     cpu = None
     if not args.no_cpu:
         log("bench: CPU baseline (oracle)")
@@ -184,7 +198,9 @@ def main():
     line = {
         "metric": METRIC, "value": round(value, 3), "unit": "clips/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "q8_0 (int8 codes x q8_0 activations, f32 accumulation); f16 attention",
+        "vs_baseline": None, "dtype": "int8",
+        "dtype_note": "q8_0 weight and activation codes on int8 MFMA (exact int32 block sums), f32 per-block scale "
+                      "epilogue and residual stream, f16 attention operands",
         "data": "synthetic (jepa-bench seeded pixels, random-init N(0,0.02) weights)",
         "config": {"workload": "V-JEPA 2 ViT-L/16 encoder, 16 frames 256x256 (2048 tokens), 24 layers, D 1024, 16 heads, "
                                "q8_0, batch 1 clip, device-resident input/output", "global_batch": 1, "seq_len": N_TOK,

@@ -283,7 +283,8 @@ int  jepa_context_max_batch(const jepa_context * ctx);
 int  jepa_context_last_batch(const jepa_context * ctx);
 
 /* ---- devices: reference include/jepa.h:554-594 ---- */
-/* device -1 = the CPU (the oracle path), >= 0 = the n-th HIP device. */
+/* device -1 = the default device (HIP device 0; this library has no CPU backend, so the reference's
+ * "cpu" choice also lands on device 0), >= 0 = the n-th HIP device. */
 typedef struct {
     bool verbose;
     int  device;

@@ -53,6 +53,7 @@ struct kargs {
     const float * bias;
     int64_t M, N, K;
     int tn, tm;              // workgroup tiles along N and M
+    int xa, xb;              // tiles per XCD block along N and M (0: plain order)
     gemm_epi ep;
 };
 
@@ -202,13 +203,20 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const int wn = wave % WN, wm = wave / WN;
     const int l32 = lane & 31, g = lane >> 5;
 
-    // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a contiguous run of tiles (M
-    // fastest) so that the tiles sharing weight rows also share an L2.
-    const int64_t ntile = (int64_t) a.tn * a.tm;
-    int64_t tile = blockIdx.x;
-    if ((ntile & 7) == 0) tile = (tile & 7) * (ntile >> 3) + (tile >> 3);
-    const int64_t tni = tile / a.tm;
-    const int64_t n0 = tni * BN, m0 = (tile - tni * a.tm) * T::BM;
+    // Workgroups are dealt to the 8 XCDs round-robin (workgroup w runs on XCD w % 8). Each XCD gets one
+    // block of xa x xb tiles, chosen on the host so that the weight and activation rows the XCD's L2
+    // has to fetch (xa BN + xb BM rows per K-column) are fewest.
+    int64_t tni, tmi;
+    if (a.xa > 0) {
+        const int x = (int) (blockIdx.x & 7), slot = (int) (blockIdx.x >> 3);
+        const int nbn = a.tn / a.xa;
+        tni = (int64_t) (x % nbn) * a.xa + slot / a.xb;
+        tmi = (int64_t) (x / nbn) * a.xb + slot % a.xb;
+    } else {
+        tni = blockIdx.x / a.tm;
+        tmi = blockIdx.x - tni * a.tm;
+    }
+    const int64_t n0 = tni * BN, m0 = tmi * T::BM;
     const int64_t K = a.K, M = a.M, KB = K >> 5;
     const int64_t nst = (K + KC - 1) / KC;            // q8_0 / q4_0: the last stage may hold 64 columns
     const int64_t rowbytes = K * ESZ;
@@ -284,12 +292,15 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     };
 
     f16v acc[TI][TJ];
-    [[maybe_unused]] f16v ssb[TI][TJ];
+    [[maybe_unused]] f16v ssb[TI][TJ], accm[TI][TJ];   // q4_K: super-block sums, mins accumulator
     const f16v zero = {};
 #pragma unroll
     for (int i = 0; i < TI; i++)
 #pragma unroll
-        for (int j = 0; j < TJ; j++) { acc[i][j] = zero; if constexpr (WF == W_Q4K) ssb[i][j] = zero; }
+        for (int j = 0; j < TJ; j++) {
+            acc[i][j] = zero;
+            if constexpr (WF == W_Q4K) { ssb[i][j] = zero; accm[i][j] = zero; }
+        }
 
     // q8_0 / q4_0 stage of NB 32-blocks. Steps u = (block, tile), tiles i-major: one int8 MFMA gives the
     // exact block sum S, one f16 MFMA (32x32x8) of the scale operands (dw in K-slot 0 of both lane
@@ -382,7 +393,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         }
         if constexpr (WF == W_Q4K) {
             if ((st & 3) == 3) {
-                // super-block epilogue (ggml vec_dot_q4_K_q8_K): acc += (dw*da) S - (dmin*da) sum_j m_j bsum_j
+                // super-block epilogue (ggml's x86 vec_dot_q4_K_q8_K): acc += (dw*da) S and, in a second
+                // accumulator, accm += (dmin*da) sum_j m_j bsum_j; the result is acc - accm
                 const unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 2) & 1) * T::XSB;
                 h8 bs[TJ];
                 float da[TJ];
@@ -411,13 +423,22 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                         for (int r = 0; r < 16; r++) {
                             const float d1 = __fmul_rn(dw[r], da[j]), d2 = __fmul_rn(dm[r], da[j]);
                             acc[i][j][r] = fmaf(d1, ssb[i][j][r], acc[i][j][r]);
-                            acc[i][j][r] = fmaf(-d2, ms[r], acc[i][j][r]);
+                            accm[i][j][r] = fmaf(d2, ms[r], accm[i][j][r]);
                         }
                         ssb[i][j] = zero;
                     }
                 }
             }
         }
+    }
+
+    if constexpr (WF == W_Q4K) {
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+            for (int j = 0; j < TJ; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = __fsub_rn(acc[i][j][r], accm[i][j][r]);
     }
 
     // epilogue: lane holds token m and features nb + 8q + 4g + e of each tile
@@ -543,8 +564,9 @@ int cu_count() {
 }
 
 // The tile with the least estimated time: whole waves of workgroups over the CUs (one workgroup per
-// CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N.
-int pick_tile(int64_t N, int64_t M) {
+// CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N; q4_K
+// skips the 256x128 tile (its three accumulator sets do not fit 256 VGPRs with two waves per SIMD).
+int pick_tile(int wf, int64_t N, int64_t M) {
     const int f = g_force_tile.load();
     const int nt = (int) (sizeof(k_tiles) / sizeof(k_tiles[0]));
     if (f >= 0 && f < nt && N % (32 * k_tiles[f].wn * k_tiles[f].ti) == 0) return f;
@@ -554,6 +576,7 @@ int pick_tile(int64_t N, int64_t M) {
     for (int c = 0; c < nt; c++) {
         const int64_t bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
         if (N % bn) continue;
+        if (wf == W_Q4K && c == 0) continue;
         const int64_t t = (N / bn) * ((M + bm - 1) / bm);
         const double waves = (double) ((t + cus - 1) / cus);
         const double cost = waves * (double) (bn * bm) / k_tile_eff[c];
@@ -577,9 +600,22 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
 
 template <int WF>
 void dispatch_mfma(kargs a, hipStream_t s) {
-    const int c = pick_tile(a.N, a.M);
-    a.tn = (int) (a.N / (32 * k_tiles[c].wn * k_tiles[c].ti));
-    a.tm = (int) ((a.M + 32 * k_tiles[c].wm * k_tiles[c].tj - 1) / (32 * k_tiles[c].wm * k_tiles[c].tj));
+    const int c = pick_tile(WF, a.N, a.M);
+    const int bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
+    a.tn = (int) (a.N / bn);
+    a.tm = (int) ((a.M + bm - 1) / bm);
+    // XCD blocks: eight xa x xb blocks tiling the tn x tm grid, least rows per block
+    a.xa = a.xb = 0;
+    const int64_t ntile = (int64_t) a.tn * a.tm;
+    if (ntile % 8 == 0) {
+        const int64_t per = ntile / 8;
+        int64_t best = -1;
+        for (int xa = 1; xa <= a.tn; xa++) {
+            if (a.tn % xa || per % xa || a.tm % (per / xa)) continue;
+            const int64_t rows = (int64_t) xa * bn + (per / xa) * bm;
+            if (best < 0 || rows < best) { best = rows; a.xa = xa; a.xb = (int) (per / xa); }
+        }
+    }
     switch (a.ep.kind) {
         case EPI_F32:       launch_tiles<WF, EPI_F32>(c, a, s); break;
         case EPI_RESID:     launch_tiles<WF, EPI_RESID>(c, a, s); break;

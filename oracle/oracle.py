@@ -57,6 +57,9 @@ def lib() -> C.CDLL:
         L.or_encode_file.argtypes = [C.c_char_p, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64,
                                      vp, i64, C.c_int, C.c_int]
         L.or_encode_file.restype = i64
+        for fn in ("or_fp32_to_fp16_row", "or_fp16_to_fp32_row"):
+            getattr(L, fn).argtypes = [vp, vp, i64]
+            getattr(L, fn).restype = None
         L.or_set_reverse_block_order.argtypes = [C.c_int]
         L.or_set_reverse_block_order.restype = None
         _lib = L
@@ -190,6 +193,32 @@ def _encode(path, x, rows, dim, n_layers, trace, items):
 def encode(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, n_layers: int = 0, trace: bool = False):
     """Oracle forward with an explicit item count (video: n_batch; image: n_batch * n_frames)."""
     return _encode(path, np.ascontiguousarray(x, dtype=np.float32), rows, dim, n_layers, trace, n_items)
+
+
+def fp32_to_fp16(x: np.ndarray) -> np.ndarray:
+    """uint16 bit patterns of x rounded to f16 by the oracle's software conversion"""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.zeros(x.size, dtype=np.uint16)
+    lib().or_fp32_to_fp16_row(_p(x), _p(out), x.size)
+    return out
+
+
+def fp16_to_fp32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16).reshape(-1)
+    out = np.zeros(h.size, dtype=np.float32)
+    lib().or_fp16_to_fp32_row(_p(h), _p(out), h.size)
+    return out
+
+
+def vec_dot(wtype: int, n: int, wrow: np.ndarray, arow: np.ndarray) -> float:
+    """one weight row (wtype blocks) . one activation row (its vec-dot type blocks)"""
+    w = np.ascontiguousarray(wrow, dtype=np.uint8)
+    a = np.ascontiguousarray(arow, dtype=np.uint8)
+    return float(lib().or_vec_dot(wtype, n, _p(w), _p(a)))
+
+
+def gelu_erf(x: float) -> float:
+    return float(lib().or_gelu_erf(x))
 
 
 def set_reverse_block_order(on: bool) -> None:

@@ -120,8 +120,9 @@ C2_SHAPES = [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)]
 @pytest.mark.parametrize("gtype", [gguf.GGML_Q8_0, gguf.GGML_Q4_0, gguf.GGML_Q4_K, gguf.GGML_F16])
 @pytest.mark.parametrize("shape", C2_SHAPES)
 def test_matmul_vs_oracle(jlib, oracle, gtype, shape):
-    """GEMM microbench shapes (ViT-L qkv / proj / fc1 / fc2). q8_0 and q4_0: bit-exact with the oracle's
-    ggml vec_dot restatement (same exact block sums, same fma per block in K order)."""
+    """GEMM microbench shapes (ViT-L qkv / proj / fc1 / fc2). q8_0, q4_0 and q4_K: bit-exact with the
+    oracle's ggml vec_dot restatement (same exact block sums, same fma per block in K order, q4_K's
+    mins in their own accumulator); f16 within f32 summation-order rounding."""
     n_out, n_in = shape
     rng = np.random.default_rng(n_out * 7 + n_in + gtype)
     M = 256
@@ -137,7 +138,7 @@ def test_matmul_vs_oracle(jlib, oracle, gtype, shape):
     rc = jlib.lib().jepa_amd_matmul(0, gtype, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, y.data_ptr(), 1, C.byref(ms))
     assert rc == 0, jlib.error_text()
     got = host(y)
-    if gtype in (gguf.GGML_Q8_0, gguf.GGML_Q4_0):
+    if gtype != gguf.GGML_F16:
         diff = np.argwhere(got.view(np.uint32) != want.view(np.uint32))
         assert diff.size == 0, f"{len(diff)} outputs differ, max abs {np.abs(got - want).max():.3e}"
     else:
@@ -169,7 +170,7 @@ TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128
 def test_matmul_every_tile(jlib, oracle, gtype, tile):
     """Every workgroup tile shape of the MFMA GEMM, forced, on a ragged token count (M = 389: partial
     last tile, rows past M clamped) and K = 768 (12 stages, so the pipeline's prologue, steady state
-    and tail all run; three q4_K super-blocks). q8_0 / q4_0 bit-exact, others within f32 rounding."""
+    and tail all run; three q4_K super-blocks). Block-quantized types bit-exact, f16 within f32 rounding."""
     bn = TILES[tile][0]
     n_out, n_in, M = bn * (3 if bn == 128 else 2) if bn != 64 else 256, 768, 389
     rng = np.random.default_rng(tile * 100 + gtype)
@@ -192,7 +193,7 @@ def test_matmul_every_tile(jlib, oracle, gtype, tile):
         L.jepa_amd_gemm_tile(-1)
     assert rc == 0, jlib.error_text()
     got = host(y)
-    if gtype in (gguf.GGML_Q8_0, gguf.GGML_Q4_0):
+    if gtype != gguf.GGML_F16:
         diff = np.argwhere(got.view(np.uint32) != want.view(np.uint32))
         assert diff.size == 0, f"{len(diff)} outputs differ, first {diff[:4].tolist()}, max abs {np.abs(got - want).max():.3e}"
     else:

@@ -1,0 +1,171 @@
+"""The oracle's whole encoder forward, pinned against an independent float64 forward written from the
+reference graph (no GPU): patchify row order (reference src/jepa.cpp:476-505), patch linear, CLS and
+learned positions for the image families (586-627), modality embedding, and 3-D RoPE on q and k for the
+video families (846-895), pre-LN blocks with fused qkv, attention with f16-rounded K/V, erf-GELU MLP,
+optional layer scale (444-471), final LayerNorm. Models are tiny f32 GGUFs, so the only differences
+left are float32 rounding (no activation quantization). Also: GGUF writer/reader round trip and the
+oracle's batch invariance."""
+import math
+
+import numpy as np
+import pytest
+
+from jepa_amd import forge, gguf, inputs
+from oracle import oracle as O
+
+
+def _ln(x, w, b, eps):
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps) * w + b
+
+
+def _gelu(x):
+    return 0.5 * x * (1.0 + np.vectorize(math.erf)(x / math.sqrt(2.0)))
+
+
+def _rope_tables64(grid, hd, variant, interp, train, theta):
+    """float64 cos / sin tables from the definitions (reference src/rope3d.h:9-48), lanes past 3d identity."""
+    gt, gh, gw = grid
+    d = 2 * ((hd // 3) // 2)
+    omega = 1.0 / theta ** (np.arange(d // 2) / (d // 2))
+    lane = np.arange(d) % (d // 2) if variant == 0 else np.arange(d) // 2
+    n = gt * gh * gw
+    C, S = np.ones((n, hd)), np.zeros((n, hd))
+    for i in range(n):
+        t, h, w = i // (gh * gw), (i % (gh * gw)) // gw, i % gw
+        if interp:
+            h = h * (train[0] - 1) / (gh - 1) if gh > 1 else h
+            w = w * (train[1] - 1) / (gw - 1) if gw > 1 else w
+        for a, pos in enumerate((t, h, w)):
+            C[i, a * d:(a + 1) * d] = np.cos(pos * omega[lane])
+            S[i, a * d:(a + 1) * d] = np.sin(pos * omega[lane])
+    return C, S
+
+
+def _rot(x, C, S):
+    """out[2k] = x[2k] C[2k] - x[2k+1] S[2k]; out[2k+1] = x[2k+1] C[2k+1] + x[2k] S[2k+1]"""
+    sw = x.copy()
+    sw[..., 0::2], sw[..., 1::2] = -x[..., 1::2], x[..., 0::2]
+    return x * C + sw * S
+
+
+def forward64(path, x):
+    g = gguf.read_gguf(path)
+    kv = g.kv
+    T = lambda n: g.tensor_f32(n).astype(np.float64)
+    has = lambda n: n in g.tensors
+    fam = kv["jepa.family"]
+    D, L, H, P = kv["jepa.enc.embed_dim"], kv["jepa.enc.n_layer"], kv["jepa.enc.n_head"], kv["jepa.enc.patch_size"]
+    hd, eps = D // H, float(kv["jepa.enc.ln_eps"])
+    video = fam in ("vjepa2", "vjepa2_1")
+    B, Cc, Tt, Hh, Ww = x.shape
+    tub = kv["jepa.enc.tubelet_size"] if video else 1
+    items = []
+    for b in range(B):
+        clips = [x[b]] if video else [x[b][:, t:t + 1] for t in range(Tt)]
+        for clip in clips:
+            gt, gh, gw = clip.shape[1] // tub, Hh // P, Ww // P
+            rows = []
+            for t in range(gt):
+                for h in range(gh):
+                    for w in range(gw):
+                        rows.append(clip[:, t * tub:(t + 1) * tub, h * P:(h + 1) * P, w * P:(w + 1) * P].reshape(-1))
+            items.append((np.array(rows, np.float64), (gt, gh, gw)))
+    outs, streams = [], []
+    for rows, grid in items:
+        h = rows @ T("enc.patch_embed.weight").T + T("enc.patch_embed.bias")
+        if has("enc.mod_embed_video"):
+            h = h + T("enc.mod_embed_video")
+        if kv.get("jepa.enc.cls_token"):
+            h = np.concatenate([T("enc.cls_token")[None], h])
+        if has("enc.pos_embed"):
+            h = h + T("enc.pos_embed")
+        rope = None
+        if video:
+            ref = kv.get("jepa.enc.rope_ref_grid", 0)
+            rope = _rope_tables64(grid, hd, 0 if kv["jepa.enc.rope_freq_layout"] == "tiled" else 1,
+                                  bool(kv.get("jepa.enc.rope_interpolate")), (ref, ref), float(kv["jepa.enc.rope_theta"]))
+        n = h.shape[0]
+        for i in range(L):
+            p = f"enc.blk.{i}."
+            a = _ln(h, T(p + "ln1.weight"), T(p + "ln1.bias"), eps)
+            qkv = a @ T(p + "attn_qkv.weight").T + T(p + "attn_qkv.bias")
+            q, k, v = (qkv[:, j * D:(j + 1) * D].reshape(n, H, hd) for j in range(3))
+            if rope is not None:
+                q, k = _rot(q, rope[0][:, None], rope[1][:, None]), _rot(k, rope[0][:, None], rope[1][:, None])
+            k = k.astype(np.float32).astype(np.float16).astype(np.float64)
+            v = v.astype(np.float32).astype(np.float16).astype(np.float64)
+            att = np.zeros((n, H, hd))
+            for hh in range(H):
+                s = q[:, hh] @ k[:, hh].T / math.sqrt(hd)
+                pr = np.exp(s - s.max(1, keepdims=True))
+                att[:, hh] = (pr / pr.sum(1, keepdims=True)) @ v[:, hh]
+            o = att.reshape(n, D) @ T(p + "attn_out.weight").T + T(p + "attn_out.bias")
+            if has(p + "ls1"):
+                o = o * T(p + "ls1")
+            h = h + o
+            f = _ln(h, T(p + "ln2.weight"), T(p + "ln2.bias"), eps) @ T(p + "ffn_up.weight").T + T(p + "ffn_up.bias")
+            f = _gelu(f) @ T(p + "ffn_down.weight").T + T(p + "ffn_down.bias")
+            if has(p + "ls2"):
+                f = f * T(p + "ls2")
+            h = h + f
+        streams.append(h)
+        outs.append(_ln(h, T("enc.norm.weight"), T("enc.norm.bias"), eps))
+    return np.concatenate(outs), np.stack(streams), outs[0].shape[0], len(outs)
+
+
+@pytest.mark.parametrize("family,kw", [("hfvit", {}), ("hfvit", {"layer_scale": True}), ("vjepa2", {}),
+                                       ("vjepa2_1", {})])
+def test_oracle_encoder_matches_float64_forward(family, kw, tmp_path):
+    cfg = forge.tiny(family, "f32", ln_random=True, **kw)
+    path = forge.cached_model(cfg, str(tmp_path))
+    x = inputs.make_input(2, 1 if family == "hfvit" else 4, 64, 64, seed=11)
+    want, stream, rows, items = forward64(path, x)
+    got, tr = O.encode(path, x, items, rows, cfg.embed_dim, n_layers=cfg.n_layer, trace=True)
+    # residual stream after the last block: float32 vs float64 rounding only (~1e-6 of its scale)
+    err_stream = np.abs(tr[:, -1] - stream).max() / np.abs(stream).max()
+    assert err_stream < 2e-5, err_stream
+    # final LayerNorm output: rows with a small residual (the CLS row) have their rounding scaled up
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err < 5e-4, err
+
+
+def test_oracle_items_are_independent(tmp_path):
+    """Items of one call equal separate calls bit for bit (reference tests/test-batch.cpp:12-21)."""
+    cfg = forge.tiny("vjepa2", "q8_0")
+    path = forge.cached_model(cfg, str(tmp_path))
+    x = inputs.make_input(2, 4, 64, 64, seed=2)
+    both, _ = O.encode(path, x, 2, 16 * 2, cfg.embed_dim, n_layers=cfg.n_layer)
+    for b in range(2):
+        one, _ = O.encode(path, x[b:b + 1], 1, 32, cfg.embed_dim, n_layers=cfg.n_layer)
+        np.testing.assert_array_equal(one.view(np.uint32), both[b * 32:(b + 1) * 32].view(np.uint32))
+
+
+def test_gguf_roundtrip(tmp_path):
+    rng = np.random.default_rng(1)
+    w = gguf.GGUFWriter()
+    w.add("a.u32", 7)
+    w.add("a.i32", -3)
+    w.add("a.f32", 0.25)
+    w.add("a.bool", True)
+    w.add("a.str", "héllo")
+    w.add("a.strs", ["x", "yz"])
+    w.add("a.ints", [1, -2, 3])
+    w.add("a.floats", [0.5, 1.5])
+    t32 = rng.standard_normal((3, 64)).astype(np.float32)
+    t16 = rng.standard_normal((2, 64)).astype(np.float16)
+    q8 = gguf.quantize(gguf.GGML_Q8_0, rng.standard_normal((4, 64)).astype(np.float32))
+    w.add_tensor("t.f32", gguf.GGML_F32, (64, 3), t32)
+    w.add_tensor("t.f16", gguf.GGML_F16, (64, 2), t16)
+    w.add_tensor("t.q8", gguf.GGML_Q8_0, (64, 4), q8)
+    p = str(tmp_path / "r.gguf")
+    w.write(p)
+    g = gguf.read_gguf(p)
+    assert g.kv["a.u32"] == 7 and g.kv["a.i32"] == -3 and g.kv["a.f32"] == 0.25 and g.kv["a.bool"] is True
+    assert g.kv["a.str"] == "héllo" and list(g.kv["a.strs"]) == ["x", "yz"] and list(g.kv["a.ints"]) == [1, -2, 3]
+    np.testing.assert_array_equal(g.tensor_f32("t.f32"), t32)
+    np.testing.assert_array_equal(g.tensor_f32("t.f16"), t16.astype(np.float32))
+    np.testing.assert_array_equal(np.asarray(g.tensor_bytes("t.q8")).reshape(q8.shape), q8)
+    for t in g.tensors.values():
+        assert t.offset % 32 == 0

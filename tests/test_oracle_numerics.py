@@ -1,0 +1,265 @@
+"""Pinning of the CPU oracle's scalar numerics and ggml block formats (no GPU).
+
+Each check is chosen so that a plausible slip in the restatement (a rounding mode, a sign, a block
+layout, a dropped term, a summation order) fails it: exhaustive f16 conversion against numpy's IEEE
+routines, quantizers against an independent numpy implementation plus closed-form round-trip bounds,
+rounding-mode and tie-break known answers, dots against exact integer block sums, and LayerNorm /
+GELU / attention against float64 references.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from jepa_amd import gguf
+from oracle import oracle as O
+
+
+# ------------------------------------------------------------------------------------------------- f16
+def test_fp16_to_fp32_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.fp16_to_fp32(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_fp32_to_fp16_round_to_nearest_even():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * np.float32(8),
+        (rng.standard_normal(50000) * 1e-5).astype(np.float32),          # subnormal halves
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, 6e-8, 2.98e-8, 5.96e-8,
+                  np.inf, -np.inf, 1.00048828125, 1.0009765625, 1.00146484375], np.float32),   # overflow -> inf
+        # exact ties between two halves: 1 + (2k + 1) * 2^-11 must go to the even neighbour
+        (1.0 + (2 * np.arange(64) + 1) * 2.0 ** -11).astype(np.float32),
+    ])
+    got = O.fp32_to_fp16(x)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, want)
+
+
+# ---------------------------------------------------------------------------------- weight quantizers
+@pytest.mark.parametrize("gtype", [gguf.GGML_Q8_0, gguf.GGML_Q4_0, gguf.GGML_Q4_K])
+def test_weight_quantizers_match_independent_numpy(gtype):
+    """The oracle's C quantizers and jepa_amd.gguf's numpy ones are separate implementations of the
+    same ggml *_ref rules; they must agree byte for byte."""
+    rng = np.random.default_rng(gtype)
+    x = (rng.standard_normal((64, 512)) * 0.05).astype(np.float32)
+    x[3] = 0.0                                   # all-zero row
+    x[5, :32] = 1e-3                             # constant block
+    np.testing.assert_array_equal(O.quantize_weight(gtype, x), gguf.quantize(gtype, x))
+
+
+def test_q8_0_weight_roundtrip_bound_and_layout():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((16, 256)).astype(np.float32)
+    raw = O.quantize_weight(O.OR_Q8_0, x)
+    assert raw.shape == (16, 8 * 34)
+    y = O.dequantize(O.OR_Q8_0, raw, 256)
+    blocks = raw.reshape(-1, 34)
+    d = blocks[:, :2].copy().view(np.float16).astype(np.float32).reshape(16, 8)
+    q = blocks[:, 2:].view(np.int8)
+    # d = amax/127 as f16, the largest element maps to +-127, every element within d/2 (+ f16 slack)
+    amax = np.abs(x.reshape(16, 8, 32)).max(-1)
+    np.testing.assert_array_equal(d, (amax / np.float32(127)).astype(np.float16).astype(np.float32))
+    assert np.abs(q).max() == 127
+    err = np.abs(y - x).reshape(16, 8, 32).max(-1)
+    assert np.all(err <= d * 0.5 + amax * 2e-3)
+
+
+def test_q4_0_codes_and_roundtrip():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((8, 128)).astype(np.float32)
+    raw = O.quantize_weight(O.OR_Q4_0, x)
+    b = raw.reshape(-1, 18)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32)[:, 0]
+    # d = max / -8 where max is the signed value of largest magnitude: that element gets code 0
+    xb = x.reshape(-1, 32)
+    idx = np.argmax(np.abs(xb), axis=1)
+    mx = xb[np.arange(len(idx)), idx]
+    np.testing.assert_array_equal(d, (mx / np.float32(-8)).astype(np.float16).astype(np.float32))
+    lo, hi = b[:, 2:] & 0xF, b[:, 2:] >> 4
+    codes = np.concatenate([lo, hi], axis=1)
+    assert np.all(codes[np.arange(len(idx)), idx] == 0)
+    y = O.dequantize(O.OR_Q4_0, raw, 128).reshape(-1, 32)
+    # codes span [-8, 7] d with the extreme at -8 d: same-sign elements round to within d/2, elements of
+    # the opposite sign beyond 7.5 d clamp to 7 d (error up to d)
+    same = np.sign(xb) == np.sign(mx)[:, None]
+    err = np.abs(y - xb)
+    slack = np.abs(mx)[:, None] * 2e-3
+    half = np.broadcast_to(np.abs(d)[:, None] * 0.5 + slack, err.shape)
+    assert np.all(err[same] <= half[same])
+    assert np.all(err <= np.abs(d)[:, None] + slack)
+
+
+def test_q4_K_dequantize_matches_numpy_and_bounds():
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((4, 512)) * 0.1).astype(np.float32)
+    raw = O.quantize_weight(O.OR_Q4_K, x)
+    y = O.dequantize(O.OR_Q4_K, raw, 512)
+    np.testing.assert_array_equal(y.view(np.uint32), gguf.dequantize(gguf.GGML_Q4_K, raw, 512).view(np.uint32))
+    # 4-bit codes over a per-sub-block [min, max] range: error within ~ one code step of the range
+    xs = x.reshape(-1, 32)
+    step = (xs.max(1) - np.minimum(xs.min(1), 0)) / 15
+    assert np.all(np.abs(y.reshape(-1, 32) - xs).max(1) <= step * 0.75 + 2e-3)
+
+
+# ------------------------------------------------------------------------------ activation quantizers
+def test_q8_0_activation_rounds_half_to_even():
+    """The x86 CPU path rounds x*127/amax half-to-even (quantize_row_q8_0, AVX2); roundf (half away
+    from zero) would give 1, 3, -1, -3 below."""
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0                                 # amax = 127, so id = 1 exactly
+    x[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -3.5]
+    raw = O.quantize_act(O.OR_Q8_0, x)
+    d = raw[:2].copy().view(np.float16)[0]
+    q = raw[2:].view(np.int8)
+    assert d == np.float16(1.0)
+    assert q[0] == 127
+    np.testing.assert_array_equal(q[1:9], [0, 2, 2, 0, -2, -2, 126, -4])
+
+
+def test_q8_0_activation_scale_and_zero_block():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(64).astype(np.float32)
+    x[32:] = 0.0
+    raw = O.quantize_act(O.OR_Q8_0, x).reshape(2, 34)
+    d0 = raw[0, :2].copy().view(np.float16)[0]
+    assert d0 == np.float16(np.abs(x[:32]).max() / np.float32(127))
+    assert np.abs(raw[0, 2:].view(np.int8)).max() == 127
+    assert raw[1, :2].copy().view(np.uint16)[0] == 0 and not raw[1, 2:].any()
+
+
+def test_q8_K_first_largest_and_sign_convention():
+    """quantize_row_q8_K_ref: max = the FIRST element of largest |x| (kept signed), iscale = -127/max,
+    q = min(127, nearest_int(iscale * x)), d = 1/iscale, bsums over 16."""
+    x = np.zeros(256, np.float32)
+    x[3] = -5.0
+    x[10] = 5.0                                  # same magnitude, later: must not be chosen
+    x[20:36] = np.linspace(-4, 4, 16, dtype=np.float32)
+    raw = O.quantize_act(O.OR_Q8_K, x)
+    assert raw.size == 4 + 256 + 32
+    d = raw[:4].copy().view(np.float32)[0]
+    q = raw[4:260].view(np.int8)
+    bs = raw[260:].copy().view(np.int16)
+    iscale = np.float32(-127.0) / np.float32(-5.0)
+    assert d == np.float32(1.0) / iscale
+    assert q[3] == -127 and q[10] == 127
+    np.testing.assert_array_equal(bs, q.reshape(16, 16).astype(np.int32).sum(1))
+
+
+# ------------------------------------------------------------------------------------------- vec dot
+def _f32_fma(a, b, c):
+    # a*b is exact in float64 here (|a| < 2^24 integer, b a product of two f16 values); one rounding
+    # of the float64 sum to float32 differs from a true fma only on exact halfway cases
+    return np.float32(float(a) * float(b) + float(c))
+
+
+def test_vec_dot_q8_0_is_blockwise_fma_of_exact_integer_sums():
+    rng = np.random.default_rng(6)
+    n = 1024
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    wr = O.quantize_weight(O.OR_Q8_0, w)
+    ar = O.quantize_act(O.OR_Q8_0, x)
+    got = O.vec_dot(O.OR_Q8_0, n, wr, ar)
+    wb, ab = wr.reshape(-1, 34), ar.reshape(-1, 34)
+    acc = np.float32(0)
+    for b in range(n // 32):
+        S = int((wb[b, 2:].view(np.int8).astype(np.int64) * ab[b, 2:].view(np.int8).astype(np.int64)).sum())
+        dw = np.float32(wb[b, :2].copy().view(np.float16)[0])
+        da = np.float32(ab[b, :2].copy().view(np.float16)[0])
+        acc = _f32_fma(np.float32(S), dw * da, acc)
+    assert np.float32(got) == acc
+
+
+def test_vec_dot_q4_K_matches_superblock_formula():
+    """Per super-block: s += (d*da) * sum_j sc_j S_j and sm += (dmin*da) * sum_j m_j (bsum_2j + bsum_2j+1),
+    two accumulators joined at the end as s - sm (the structure of ggml's x86 q4_K x q8_K dot)."""
+    rng = np.random.default_rng(7)
+    n = 512
+    w = (rng.standard_normal(n) * 0.05).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    wr = O.quantize_weight(O.OR_Q4_K, w)
+    ar = O.quantize_act(O.OR_Q8_K, x)
+    got = O.vec_dot(O.OR_Q4_K, n, wr, ar)
+    acc = accm = np.float32(0)
+    for sb in range(n // 256):
+        blk = wr[sb * 144:(sb + 1) * 144]
+        a = ar[sb * 292:(sb + 1) * 292]
+        d = np.float32(blk[0:2].copy().view(np.float16)[0]); dmin = np.float32(blk[2:4].copy().view(np.float16)[0])
+        sc, m = gguf.q4k_scales_mins(blk[None, 4:16])
+        qs = blk[16:]
+        q8 = a[4:260].view(np.int8).astype(np.int64)
+        da = a[:4].copy().view(np.float32)[0]
+        bs = a[260:].copy().view(np.int16).astype(np.int64)
+        sumi = summ = 0
+        for j in range(8):
+            c = j // 2
+            q4 = (qs[32 * c:32 * c + 32] & 0xF) if j % 2 == 0 else (qs[32 * c:32 * c + 32] >> 4)
+            sumi += int(sc[0, j]) * int((q4.astype(np.int64) * q8[32 * j:32 * j + 32]).sum())
+            summ += int(m[0, j]) * int(bs[2 * j] + bs[2 * j + 1])
+        acc = _f32_fma(np.float32(sumi), np.float32(d * da), acc)
+        accm = _f32_fma(np.float32(summ), np.float32(dmin * da), accm)
+    assert np.float32(got) == np.float32(acc - accm)
+
+
+@pytest.mark.parametrize("gtype", [O.OR_Q8_0, O.OR_Q4_0, O.OR_Q4_K, O.OR_F16])
+def test_mul_mat_equals_vec_dot(gtype):
+    """or_mul_mat's pre-expanded fast path gives exactly or_vec_dot's value for every output."""
+    rng = np.random.default_rng(8 + gtype)
+    n_out, n_in, M = 8, 512, 5
+    w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    bias = (rng.standard_normal(n_out) * 0.1).astype(np.float32)
+    raw = w.astype(np.float16).view(np.uint8) if gtype == O.OR_F16 else O.quantize_weight(gtype, w)
+    y = O.mul_mat(gtype, raw, n_out, n_in, x, bias)
+    if gtype == O.OR_F16:
+        act = [O.fp32_to_fp16(x[m]).view(np.uint8) for m in range(M)]
+    else:
+        act = [O.quantize_act(O.OR_Q8_K if gtype == O.OR_Q4_K else O.OR_Q8_0, x[m]) for m in range(M)]
+    for m in range(M):
+        for o in range(n_out):
+            want = np.float32(np.float32(O.vec_dot(gtype, n_in, raw[o], act[m])) + bias[o])
+            assert y[m, o].view(np.uint32) == want.view(np.uint32), (m, o)
+
+
+# ------------------------------------------------------------------------------ LayerNorm, GELU, attn
+def test_layer_norm_against_float64():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((33, 1024)) * 3 + 0.5).astype(np.float32)
+    w = rng.standard_normal(1024).astype(np.float32)
+    b = rng.standard_normal(1024).astype(np.float32)
+    y = O.layer_norm(x, w, b, 1e-6)
+    x64 = x.astype(np.float64)
+    ref = (x64 - x64.mean(1, keepdims=True)) / np.sqrt(x64.var(1, keepdims=True) + 1e-6) * w + b
+    assert np.abs(y - ref).max() <= 2e-6 * np.abs(ref).max()
+
+
+def test_gelu_erf_against_math_erf():
+    xs = np.concatenate([np.linspace(-8, 8, 4001), [0.0, -0.0, 1e-30, -1e-30, 20.0, -20.0]]).astype(np.float32)
+    for v in xs:
+        ref = 0.5 * float(v) * (1.0 + math.erf(float(v) / math.sqrt(2.0)))
+        got = O.gelu_erf(float(v))
+        assert abs(got - ref) <= 4e-7 * max(1.0, abs(ref)), (v, got, ref)
+
+
+def test_attention_against_float64():
+    rng = np.random.default_rng(10)
+    n, H, hd = 77, 3, 64
+    q = rng.standard_normal((n, H * hd)).astype(np.float32)
+    k = rng.standard_normal((n, H * hd)).astype(np.float32)
+    v = rng.standard_normal((n, H * hd)).astype(np.float32)
+    out = O.attention(q, k, v, H, kv_f16=True)
+    ref = np.zeros((n, H * hd))
+    for h in range(H):
+        sl = slice(h * hd, (h + 1) * hd)
+        kh = k[:, sl].astype(np.float16).astype(np.float64)
+        vh = v[:, sl].astype(np.float16).astype(np.float64)
+        s = q[:, sl].astype(np.float64) @ kh.T / 8.0
+        p = np.exp(s - s.max(1, keepdims=True))
+        ref[:, sl] = (p / p.sum(1, keepdims=True)) @ vh
+    assert np.abs(out - ref).max() <= 2e-5 * np.abs(ref).max()
