@@ -25,6 +25,36 @@ __device__ __forceinline__ float h2f(uint16_t b) { return (float) __builtin_bit_
 // ------------------------------------------------------------------------------------------------
 constexpr int MAXOCT = 4;   // D <= 2048
 
+// Cross-lane moves through DPP (VALU, a few cycles) instead of ds_bpermute shuffles (an LDS round
+// trip each). update_dpp(0, v, ...) gives 0 in lanes of rows the row mask leaves out.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, false));
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(0, p.x, CTRL, ROW_MASK, 0xF, false);
+    r.y = __builtin_amdgcn_update_dpp(0, p.y, CTRL, ROW_MASK, 0xF, false);
+    return __builtin_bit_cast(double, r);
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E;                 // quad_perm [1,0,3,2], [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+
+// Sum over the 64 lanes, returned to every lane: within rows of 16 by xor / mirror steps, then
+// row 0 -> 1 and 2 -> 3 (row_bcast:15), rows 0+1 -> 3 (row_bcast:31); lane 63 holds the total.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_f64<DPP_XOR1>(v);
+    v += dpp_f64<DPP_XOR2>(v);
+    v += dpp_f64<DPP_HALF_MIRROR>(v);
+    v += dpp_f64<DPP_MIRROR>(v);
+    v += dpp_f64<DPP_BCAST15, 0xA>(v);
+    v += dpp_f64<DPP_BCAST31, 0xC>(v);
+    const int2 p = __builtin_bit_cast(int2, v);
+    return __builtin_bit_cast(double, make_int2(__builtin_amdgcn_readlane(p.x, 63), __builtin_amdgcn_readlane(p.y, 63)));
+}
+
 template <int OUT, bool NORM>
 __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, int64_t M, int64_t D,
                                                  const float * __restrict__ w, const float * __restrict__ b, float eps,
@@ -35,12 +65,21 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
     const int n_oct = (int) (D / 8);
     const float * xr = x + row * D;
     float v[MAXOCT][8];
+    [[maybe_unused]] float gw[MAXOCT][8], gb[MAXOCT][8];   // affine parameters, loaded with x
 #pragma unroll
     for (int i = 0; i < MAXOCT; i++) {
         const int o = lane + 64 * i;
         if (o < n_oct) {
             const float4 a = *(const float4 *) (xr + 8 * o), c = *(const float4 *) (xr + 8 * o + 4);
             v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w; v[i][4] = c.x; v[i][5] = c.y; v[i][6] = c.z; v[i][7] = c.w;
+            if constexpr (NORM) {
+                const float4 w0 = w ? *(const float4 *) (w + 8 * o) : make_float4(1.f, 1.f, 1.f, 1.f);
+                const float4 w1 = w ? *(const float4 *) (w + 8 * o + 4) : make_float4(1.f, 1.f, 1.f, 1.f);
+                const float4 b0 = b ? *(const float4 *) (b + 8 * o) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 b1 = b ? *(const float4 *) (b + 8 * o + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                gw[i][0] = w0.x; gw[i][1] = w0.y; gw[i][2] = w0.z; gw[i][3] = w0.w; gw[i][4] = w1.x; gw[i][5] = w1.y; gw[i][6] = w1.z; gw[i][7] = w1.w;
+                gb[i][0] = b0.x; gb[i][1] = b0.y; gb[i][2] = b0.z; gb[i][3] = b0.w; gb[i][4] = b1.x; gb[i][5] = b1.y; gb[i][6] = b1.z; gb[i][7] = b1.w;
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++) v[i][e] = 0.0f;
@@ -52,8 +91,7 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
         for (int i = 0; i < MAXOCT; i++)
 #pragma unroll
             for (int e = 0; e < 8; e++) s += (double) v[i][e];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+        s = wave_sum_f64(s);
         const float mean = (float) s / (float) D;
         double s2 = 0.0;
 #pragma unroll
@@ -66,8 +104,7 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
                 if (live) s2 += (double) __fmul_rn(t, t);
             }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) s2 += __shfl_xor(s2, off);
+        s2 = wave_sum_f64(s2);
         const float var = (float) (s2 / (double) D);
         const float scale = 1.0f / sqrtf(__fadd_rn(var, eps));
 #pragma unroll
@@ -77,8 +114,8 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 float t = __fmul_rn(v[i][e], scale);
-                if (w) t = __fmul_rn(t, w[8 * o + e]);
-                if (b) t = __fadd_rn(t, b[8 * o + e]);
+                if (w) t = __fmul_rn(t, gw[i][e]);
+                if (b) t = __fadd_rn(t, gb[i][e]);
                 v[i][e] = t;
             }
         }
@@ -105,8 +142,8 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
             float am = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; e++) am = fmaxf(am, fabsf(v[i][e]));
-            am = fmaxf(am, __shfl_xor(am, 1));
-            am = fmaxf(am, __shfl_xor(am, 2));
+            am = fmaxf(am, dpp_f32<DPP_XOR1>(am));      // the 4 lanes of a 32-value block are one quad
+            am = fmaxf(am, dpp_f32<DPP_XOR2>(am));
             const float d = am / 127.0f;
             const float id = am != 0.0f ? 127.0f / am : 0.0f;
             if (live) {
