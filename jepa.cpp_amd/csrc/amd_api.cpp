@@ -201,8 +201,9 @@ extern "C" int jepa_amd_gemm_tile(int index) {
 }
 
 extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items, int64_t n_tok, int n_head, const float * rope_c,
-                                  const float * rope_s, float * out) {
+                                  const float * rope_s, int out_type, void * out) {
     if (!qkv || !out || n_items <= 0 || n_tok <= 0 || n_head <= 0) return -1;
+    if (out_type != T_F32 && out_type != T_Q8_0) { jepa_log("jepa: jepa_amd_attention: output type %d\n", out_type); return -1; }
     dev_scope d(device);
     if (!d.ok) return -1;
     const int hd = 64;
@@ -218,7 +219,18 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
     ep.q = q; ep.k = k; ep.vt = vt; ep.rope_c = rope_c; ep.rope_s = rope_s;
     ep.n_head = n_head; ep.hd = hd; ep.D = n_head * hd; ep.R = n_tok; ep.R_pad = R_pad;
     launch_qkv_split(qkv, n_items * n_tok, (int64_t) 3 * n_head * hd, ep, d.s);
-    launch_attention(q, k, vt, out, n_items, n_head, hd, n_tok, R_pad, 0.125f, d.s);
+    act_view o;
+    const int64_t rows = n_items * n_tok, D = (int64_t) n_head * hd;
+    if (out_type == T_F32) {
+        o.fmt = A_F32; o.q = out; o.ld = D;
+    } else {
+        o.fmt = A_Q8_0; o.ld = D;
+        o.q = d.alloc((size_t) rows * D);
+        o.d = d.alloc((size_t) rows * (D / 32) * 2);
+        if (!o.q || !o.d) return -1;
+    }
+    launch_attention(q, k, vt, o, n_items, n_head, hd, n_tok, R_pad, 0.125f, d.s);
+    if (out_type == T_Q8_0) launch_pack_act_blocks(o, rows, D, out, d.s);
     return d.finish();
 }
 

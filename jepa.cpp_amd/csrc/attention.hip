@@ -4,8 +4,12 @@
 // src/jepa.cpp:416-442 (no mask, K/V in f16 as the reference's ggml_cast does, f32 softmax and f32
 // accumulation). Q arrives with 3-D RoPE already applied by the QKV GEMM epilogue.
 //
-// Work split: one workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries and
-// sweeps all keys in tiles of 64 (K and V^T tiles staged in LDS, shared by the 4 waves).
+// Work split: one workgroup = 8 waves = 128 queries of one head. Waves 0-3 own 32 queries each and
+// sweep the first half of the key tiles, waves 4-7 the same queries over the second half (two waves
+// per SIMD: one wave's exp2 / VALU phase overlaps the other's MFMAs); the two halves are merged
+// through LDS at the end. Keys come in tiles of 64: the K tile (64 keys x 64 dims) and the V^T tile
+// (64 dims x 64 keys), 128 B per row, are copied HBM->LDS directly (global_load_lds_dwordx4) into
+// an XOR-swizzled layout, NST - 1 tiles ahead of the one being used.
 // MFMA roles are chosen so that softmax statistics need no cross-lane reduction beyond one
 // xor-32 exchange:
 //   S^T[key][q] = K . Q^T     A = K tile rows (keys), B = Q^T (held in registers for the sweep)
@@ -14,32 +18,82 @@
 // The B operand of the PV MFMA takes the 8 keys (4g..4g+3, 8+4g..8+4g+3 of each 16) that the S
 // accumulator layout leaves in lane group g; V^T is stored with the same key order inside every
 // 16-token group (written that way by the QKV epilogue), so both operands agree without shuffles.
+// The running maximum is only moved when a tile's maximum exceeds it by more than 2^8 (in the
+// exp2 domain), so the accumulators are rescaled a few times per sweep instead of every tile.
 #include "kernels.h"
+#include "model.h"
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
 
 namespace {
 
-constexpr int HD = 64, QB = 128, KT = 64, LDK = 72;
+constexpr int HD = 64, QB = 128, KT = 64, NST = 4;
+constexpr int TILE = KT * 128;                  // one K or V^T tile: 64 rows of 128 B
+constexpr int STAGE = 2 * TILE;                 // K + V^T
+constexpr int HALF = NST * STAGE;               // LDS of one key half
+constexpr float LAZY = 8.0f;                    // keep the running max while growth <= 2^8
 
-__global__ __launch_bounds__(256) void k_attn_hd64(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
-                                                   const _Float16 * __restrict__ Vt, float * __restrict__ O,
-                                                   int n_head, int64_t R, int64_t R_pad, float c) {
-    __shared__ __attribute__((aligned(16))) _Float16 sK[KT * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[HD * LDK];
+__device__ __forceinline__ uint16_t f2hbits(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
+
+__device__ __forceinline__ h8 lds_chunk(const unsigned char * base, int r, int c) {
+    return *(const h8 *) (base + r * 128 + ((c ^ (r & 7)) << 4));
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), then a bare s_barrier (no fence: copies of later tiles stay in flight)
+template <int N_>
+__device__ __forceinline__ void tile_barrier() {
+    static_assert(N_ >= 0 && N_ < 64, "vmcnt is a 6-bit field");
+    __builtin_amdgcn_s_waitcnt((N_ & 15) | ((N_ >> 4) << 14) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
+}
+
+// OUT: A_F32 writes O f32 [item*R][H*64]; A_Q8_0 writes the q8_0 activation of the next linear
+// (int8 codes [item*R][H*64] + f16 d per 32), the same values the separate quantizer would produce.
+template <int OUT>
+__global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
+                                                      const _Float16 * __restrict__ Vt, void * __restrict__ O,
+                                                      void * __restrict__ Od, int n_head, int64_t R, int64_t R_pad,
+                                                      float c) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * HALF];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, g = lane >> 5;
+    const int qg = wave & 3, kh = wave >> 2;            // query group, key half
+    const int hw = wave & 3;                            // wave index inside its half (loads)
     const int64_t head = blockIdx.y;
     const int64_t item = head / n_head;
     const int h = (int) (head - item * n_head);
-    const int64_t q0 = (int64_t) blockIdx.x * QB + wave * 32;
+    const int64_t q0 = (int64_t) blockIdx.x * QB + qg * 32;
 
     const _Float16 * Qh = Q + head * R_pad * HD;
-    const _Float16 * Kh = Kp + head * R_pad * HD;
-    const _Float16 * Vh = Vt + head * HD * R_pad;
+    const unsigned char * Kh = (const unsigned char *) (Kp + head * R_pad * HD);
+    const unsigned char * Vh = (const unsigned char *) (Vt + head * HD * R_pad);
+
+    const int ntile = (int) ((R + KT - 1) / KT);
+    const int nt = (ntile + 1) / 2;                     // tiles per half (the second may have one less)
+    const int t0 = kh * nt;                             // first tile of this half
+    const int my_nt = kh == 0 ? nt : ntile - nt;
+    unsigned char * hbase = smem + kh * HALF;
+
+    // stage s of this half: tile t0 + s. Each of the half's 4 waves copies 4 of the 16 row-groups.
+    auto issue = [&](int s) {
+        if (s >= my_nt) return;
+        unsigned char * base = hbase + (s % NST) * STAGE;
+        const int64_t key0 = (int64_t) (t0 + s) * KT;
+        const int cch = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int L = 4 * i + hw;                   // 0..7: K rows 8L..8L+7; 8..15: V^T rows
+            const int r = 8 * (L & 7) + (lane >> 3);
+            const unsigned char * src = L < 8 ? Kh + (key0 + r) * (HD * 2) + 16 * cch
+                                              : Vh + (int64_t) r * R_pad * 2 + key0 * 2 + 16 * cch;
+            __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (base + (L < 8 ? 0 : TILE) + 1024 * (L & 7)),
+                                             16, 0, 0);
+        }
+    };
 
     h8 qv[4];
 #pragma unroll
@@ -48,25 +102,23 @@ __global__ __launch_bounds__(256) void k_attn_hd64(const _Float16 * __restrict__
     const f16v zero = {0};
     f16v acc0 = zero, acc1 = zero;
     float m_run = -INFINITY, l_run = 0.0f;
-    const int64_t kend = (R + KT - 1) / KT * KT;
 
-    for (int64_t kt = 0; kt < kend; kt += KT) {
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int cidx = tid + 256 * i, row = cidx >> 3, col = (cidx & 7) * 8;
-            *(uint4 *) &sK[row * LDK + col] = *(const uint4 *) (Kh + (kt + row) * HD + col);
-            *(uint4 *) &sV[row * LDK + col] = *(const uint4 *) (Vh + (int64_t) row * R_pad + kt + col);
-        }
-        __syncthreads();
+    for (int s = 0; s < NST - 1; s++) issue(s);
+    for (int s = 0; s < nt; s++) {
+        // tile s has landed once only the copies of the NST - 2 younger tiles are outstanding; the
+        // half with fewer tiles issues fewer, so its waits are conservative
+        if (s + NST - 2 < my_nt) tile_barrier<(NST - 2) * 4>();
+        else tile_barrier<0>();
+        issue(s + NST - 1);
+        if (s >= my_nt) continue;                       // (second half, odd tile count) barrier only
+        const unsigned char * sK = hbase + (s % NST) * STAGE;
+        const unsigned char * sV = sK + TILE;
+        const int64_t kt = (int64_t) (t0 + s) * KT;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
             f16v S = zero;
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const h8 a = *(const h8 *) &sK[(32 * kb + l32) * LDK + 16 * kk + 8 * g];
-                S = MFMA16(a, qv[kk], S);
-            }
+            for (int kk = 0; kk < 4; kk++) S = MFMA16(lds_chunk(sK, 32 * kb + l32, 2 * kk + g), qv[kk], S);
             const int64_t key0 = kt + 32 * kb + 4 * g;
             if (kt + 32 * kb + 32 > R) {
 #pragma unroll
@@ -77,49 +129,113 @@ __global__ __launch_bounds__(256) void k_attn_hd64(const _Float16 * __restrict__
 #pragma unroll
             for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, S[r]);
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-            const float m_new = fmaxf(m_run, mloc);
-            const float alpha = exp2f((m_run - m_new) * c);
-            const float mc = m_new * c;
+            if (mloc > m_run && (m_run == -INFINITY || (mloc - m_run) * c > LAZY)) {
+                // move the reference maximum; rescale what was accumulated against the old one
+                const float alpha = exp2f((m_run - mloc) * c);
+                l_run *= alpha;
+#pragma unroll
+                for (int r = 0; r < 16; r++) { acc0[r] *= alpha; acc1[r] *= alpha; }
+                m_run = mloc;
+            }
+            const float mc = m_run == -INFINITY ? 0.0f : m_run * c;   // no key seen yet: S is -inf too
             float p[16], lsum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) { p[r] = exp2f(fmaf(S[r], c, -mc)); lsum += p[r]; }
             lsum += __shfl_xor(lsum, 32);
-            l_run = fmaf(l_run, alpha, lsum);
-            m_run = m_new;
-            if (alpha != 1.0f) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) { acc0[r] *= alpha; acc1[r] *= alpha; }
-            }
+            l_run += lsum;
 #pragma unroll
             for (int kk2 = 0; kk2 < 2; kk2++) {
                 h8 pb;
 #pragma unroll
-                for (int s = 0; s < 8; s++) pb[s] = (_Float16) p[8 * kk2 + s];
-                const h8 a0 = *(const h8 *) &sV[(l32) * LDK + 32 * kb + 16 * kk2 + 8 * g];
-                const h8 a1 = *(const h8 *) &sV[(32 + l32) * LDK + 32 * kb + 16 * kk2 + 8 * g];
-                acc0 = MFMA16(a0, pb, acc0);
-                acc1 = MFMA16(a1, pb, acc1);
+                for (int e = 0; e < 8; e++) pb[e] = (_Float16) p[8 * kk2 + e];
+                const int ch = 4 * kb + 2 * kk2 + g;
+                acc0 = MFMA16(lds_chunk(sV, l32, ch), pb, acc0);
+                acc1 = MFMA16(lds_chunk(sV, 32 + l32, ch), pb, acc1);
             }
         }
     }
-    const int64_t q = q0 + l32;
-    if (q >= R) return;
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    float * orow = O + (item * R + q) * (int64_t) (n_head * HD) + h * HD;
+
+    // merge the two key halves: the second half's waves publish (m, l, acc) through LDS
+    __syncthreads();
+    float * xs = (float *) smem + (size_t) (qg * 64 + lane) * 34;
+    if (kh == 1) {
+        xs[0] = m_run; xs[1] = l_run;
 #pragma unroll
-    for (int qq = 0; qq < 4; qq++) {
-        const int d = 8 * qq + 4 * g;
-        *(float4 *) (orow + d) = make_float4(acc0[4 * qq] * inv, acc0[4 * qq + 1] * inv, acc0[4 * qq + 2] * inv, acc0[4 * qq + 3] * inv);
-        *(float4 *) (orow + 32 + d) = make_float4(acc1[4 * qq] * inv, acc1[4 * qq + 1] * inv, acc1[4 * qq + 2] * inv, acc1[4 * qq + 3] * inv);
+        for (int r = 0; r < 16; r++) { xs[2 + r] = acc0[r]; xs[18 + r] = acc1[r]; }
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    {
+        const float m1 = xs[0], l1 = xs[1];
+        const float m = fmaxf(m_run, m1);
+        const float a0 = m_run == -INFINITY ? 0.0f : exp2f((m_run - m) * c);
+        const float a1 = m1 == -INFINITY ? 0.0f : exp2f((m1 - m) * c);
+        l_run = fmaf(l_run, a0, l1 * a1);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            acc0[r] = fmaf(acc0[r], a0, xs[2 + r] * a1);
+            acc1[r] = fmaf(acc1[r], a0, xs[18 + r] * a1);
+        }
+    }
+
+    const int64_t q = q0 + l32;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    float o0[16], o1[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) { o0[r] = acc0[r] * inv; o1[r] = acc1[r] * inv; }
+    const int64_t DD = (int64_t) n_head * HD;
+    if constexpr (OUT == A_Q8_0) {
+        // dims 0-31 (acc0) and 32-63 (acc1) are one q8_0 block each, split over lanes l32 and l32+32
+        float am0 = 0.0f, am1 = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) { am0 = fmaxf(am0, fabsf(o0[r])); am1 = fmaxf(am1, fabsf(o1[r])); }
+        am0 = fmaxf(am0, __shfl_xor(am0, 32));
+        am1 = fmaxf(am1, __shfl_xor(am1, 32));
+        if (q >= R) return;
+        const float id0 = am0 != 0.0f ? 127.0f / am0 : 0.0f, id1 = am1 != 0.0f ? 127.0f / am1 : 0.0f;
+        int8_t * crow = (int8_t *) O + (item * R + q) * DD + h * HD;
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int c0 = (int) fminf(fmaxf(rintf(o0[4 * qq + e] * id0), -128.0f), 127.0f);
+                const int c1 = (int) fminf(fmaxf(rintf(o1[4 * qq + e] * id1), -128.0f), 127.0f);
+                w0 |= ((uint32_t) c0 & 0xffu) << (8 * e);
+                w1 |= ((uint32_t) c1 & 0xffu) << (8 * e);
+            }
+            const int d = 8 * qq + 4 * g;
+            *(uint32_t *) (crow + d) = w0;
+            *(uint32_t *) (crow + 32 + d) = w1;
+        }
+        if (g == 0) {
+            uint16_t * drow = (uint16_t *) Od + (item * R + q) * (DD / 32) + h * 2;
+            drow[0] = f2hbits(am0 / 127.0f);
+            drow[1] = f2hbits(am1 / 127.0f);
+        }
+    } else {
+        if (q >= R) return;
+        float * orow = (float *) O + (item * R + q) * DD + h * HD;
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const int d = 8 * qq + 4 * g;
+            *(float4 *) (orow + d) = make_float4(o0[4 * qq], o0[4 * qq + 1], o0[4 * qq + 2], o0[4 * qq + 3]);
+            *(float4 *) (orow + 32 + d) = make_float4(o1[4 * qq], o1[4 * qq + 1], o1[4 * qq + 2], o1[4 * qq + 3]);
+        }
     }
 }
 
 }  // namespace
 
-void launch_attention(const void * q, const void * k, const void * vt, float * o, int64_t n_items, int n_head,
-                      int hd, int64_t R, int64_t R_pad, float scale, hipStream_t s) {
+void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items,
+                      int n_head, int hd, int64_t R, int64_t R_pad, float scale, hipStream_t s) {
     (void) hd;   // only 64 (checked by the caller)
     const float c = scale * 1.4426950408889634f;   // exp(x*scale) = exp2(x*scale*log2(e))
     dim3 grid((unsigned) ((R + QB - 1) / QB), (unsigned) (n_items * n_head));
-    k_attn_hd64<<<grid, 256, 0, s>>>((const _Float16 *) q, (const _Float16 *) k, (const _Float16 *) vt, o, n_head, R, R_pad, c);
+    if (out.fmt == A_Q8_0)
+        k_attn_hd64<A_Q8_0><<<grid, 512, 0, s>>>((const _Float16 *) q, (const _Float16 *) k, (const _Float16 *) vt, out.q,
+                                                  out.d, n_head, R, R_pad, c);
+    else
+        k_attn_hd64<A_F32><<<grid, 512, 0, s>>>((const _Float16 *) q, (const _Float16 *) k, (const _Float16 *) vt, out.q,
+                                                 nullptr, n_head, R, R_pad, c);
 }

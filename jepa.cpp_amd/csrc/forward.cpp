@@ -281,9 +281,16 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
             ep.n_head = H; ep.hd = hd; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
             kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s); });
         }
-        kt.run("attention", [&] { launch_attention(w.Q, w.Kt, w.Vt, w.attn, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), s); });
         w.actA.fmt = L.out.act();
-        kt.run("quantize", [&] { launch_rownorm_quant(w.attn, rows, D, nullptr, nullptr, 0.0f, false, w.actA, s); });
+        if (w.actA.fmt == A_Q8_0) {
+            // the attention epilogue writes the out-projection's q8_0 input directly
+            kt.run("attention", [&] { launch_attention(w.Q, w.Kt, w.Vt, w.actA, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), s); });
+        } else {
+            act_view o;
+            o.fmt = A_F32; o.q = w.attn; o.ld = D;
+            kt.run("attention", [&] { launch_attention(w.Q, w.Kt, w.Vt, o, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), s); });
+            kt.run("quantize", [&] { launch_rownorm_quant(w.attn, rows, D, nullptr, nullptr, 0.0f, false, w.actA, s); });
+        }
         {
             gemm_epi ep;
             ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls1;

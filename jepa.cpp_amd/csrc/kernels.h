@@ -53,8 +53,9 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
 void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w, const float * b, float eps,
                           bool normalize, const act_view & out, hipStream_t s);
 
-// Flash attention over (items*H) heads: O [item*R][H*hd] f32.
-void launch_attention(const void * q, const void * k, const void * vt, float * o, int64_t n_items, int n_head,
+// Flash attention over (items*H) heads into `out` [item*R][H*hd]: A_F32 (f32 rows in out.q) or
+// A_Q8_0 (the next linear's q8_0 activation: int8 codes in out.q, f16 d per 32 in out.d).
+void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items, int n_head,
                       int hd, int64_t R, int64_t R_pad, float scale, hipStream_t s);
 
 // Patch rows from NCTHW input: rows [items*Np][C*tub*P*P] in f16 (half_out) or f32.

@@ -229,7 +229,13 @@ def _attention_ref(qkv, n_items, n_tok, H, rope=None):
     return out
 
 
-@pytest.mark.parametrize("n_items,n_tok,H,rope", [(1, 2048, 4, True), (2, 197, 6, False), (1, 576, 2, True), (3, 17, 2, False)])
+# token counts cover: even / odd numbers of 64-key tiles (the two key halves of a workgroup get equal or
+# unequal shares), one tile (the second half is empty), a last tile with a single valid key, padding
+ATTN_CASES = [(1, 2048, 4, True), (2, 197, 6, False), (1, 576, 2, True), (3, 17, 2, False), (1, 129, 1, False),
+              (1, 64, 1, False), (2, 65, 2, True)]
+
+
+@pytest.mark.parametrize("n_items,n_tok,H,rope", ATTN_CASES)
 def test_attention(jlib, oracle, n_items, n_tok, H, rope):
     rng = np.random.default_rng(n_tok + H)
     D = H * 64
@@ -243,7 +249,7 @@ def test_attention(jlib, oracle, n_items, n_tok, H, rope):
     out = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
     dq = dev(qkv)
     r = jlib.lib().jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, rc.data_ptr() if rope else None,
-                                      rs.data_ptr() if rope else None, out.data_ptr())
+                                      rs.data_ptr() if rope else None, 0, out.data_ptr())
     assert r == 0, jlib.error_text()
     got = host(out).astype(np.float64)
     ref = _attention_ref(qkv, n_items, n_tok, H, (c.astype(np.float64), s.astype(np.float64)) if rope else None)
@@ -251,3 +257,20 @@ def test_attention(jlib, oracle, n_items, n_tok, H, rope):
     cos = (got * ref).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(ref, axis=1))
     assert rel <= 1e-2, rel
     assert cos.min() >= 0.9999, cos.min()
+
+
+@pytest.mark.parametrize("n_items,n_tok,H", [(1, 2048, 4), (2, 197, 6), (1, 65, 2)])
+def test_attention_fused_q8_0_equals_separate_quantizer(jlib, oracle, n_items, n_tok, H):
+    """The attention epilogue's q8_0 output is byte-identical to quantizing the f32 attention output
+    with the activation quantizer (what the out-projection would otherwise get)."""
+    rng = np.random.default_rng(n_tok * 3 + H)
+    D = H * 64
+    qkv = (rng.standard_normal((n_items * n_tok, 3 * D)) * 1.5).astype(np.float32)
+    dq = dev(qkv)
+    o32 = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
+    oq = torch.zeros((n_items * n_tok, D // 32 * 34), dtype=torch.uint8, device="cuda")
+    L = jlib.lib()
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, 0, o32.data_ptr()) == 0
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, gguf.GGML_Q8_0, oq.data_ptr()) == 0
+    want = oracle.quantize_act(oracle.OR_Q8_0, host(o32))
+    np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))
