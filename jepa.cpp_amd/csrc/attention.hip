@@ -37,6 +37,11 @@ constexpr int STAGE = 2 * TILE;                 // K + V^T
 constexpr int HALF = NST * STAGE;               // LDS of one key half
 constexpr float LAZY = 8.0f;                    // keep the running max while growth <= 2^8
 
+// 2^x by the hardware v_exp_f32 alone: exp2f adds a denormal-range fix-up (compare, select, add,
+// ldexp) around it, which softmax weights do not need (a weight below 2^-126 next to a running
+// sum >= 1 is lost to rounding either way; exp2(-inf) is still 0)
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ uint16_t f2hbits(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
 
 __device__ __forceinline__ h8 lds_chunk(const unsigned char * base, int r, int c) {
@@ -131,7 +136,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
             if (mloc > m_run && (m_run == -INFINITY || (mloc - m_run) * c > LAZY)) {
                 // move the reference maximum; rescale what was accumulated against the old one
-                const float alpha = exp2f((m_run - mloc) * c);
+                const float alpha = fast_exp2((m_run - mloc) * c);
                 l_run *= alpha;
 #pragma unroll
                 for (int r = 0; r < 16; r++) { acc0[r] *= alpha; acc1[r] *= alpha; }
@@ -140,7 +145,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
             const float mc = m_run == -INFINITY ? 0.0f : m_run * c;   // no key seen yet: S is -inf too
             float p[16], lsum = 0.0f;
 #pragma unroll
-            for (int r = 0; r < 16; r++) { p[r] = exp2f(fmaf(S[r], c, -mc)); lsum += p[r]; }
+            for (int r = 0; r < 16; r++) { p[r] = fast_exp2(fmaf(S[r], c, -mc)); lsum += p[r]; }
             lsum += __shfl_xor(lsum, 32);
             l_run += lsum;
 #pragma unroll
@@ -168,8 +173,8 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     {
         const float m1 = xs[0], l1 = xs[1];
         const float m = fmaxf(m_run, m1);
-        const float a0 = m_run == -INFINITY ? 0.0f : exp2f((m_run - m) * c);
-        const float a1 = m1 == -INFINITY ? 0.0f : exp2f((m1 - m) * c);
+        const float a0 = m_run == -INFINITY ? 0.0f : fast_exp2((m_run - m) * c);
+        const float a1 = m1 == -INFINITY ? 0.0f : fast_exp2((m1 - m) * c);
         l_run = fmaf(l_run, a0, l1 * a1);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
