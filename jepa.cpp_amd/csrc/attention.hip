@@ -8,8 +8,8 @@
 // sweep the first half of the key tiles, waves 4-7 the same queries over the second half (two waves
 // per SIMD: one wave's exp2 / VALU phase overlaps the other's MFMAs); the two halves are merged
 // through LDS at the end. Keys come in tiles of 64: the K tile (64 keys x 64 dims) and the V^T tile
-// (64 dims x 64 keys), 128 B per row, are copied HBM->LDS directly (global_load_lds_dwordx4) into
-// an XOR-swizzled layout, NST - 1 tiles ahead of the one being used.
+// (64 dims x 64 keys), 128 B per row, are copied HBM->LDS directly (buffer_load_dwordx4 ... lds) into
+// a swizzled layout (lds_slot), NST - 1 tiles ahead of the one being used.
 // MFMA roles are chosen so that softmax statistics need no cross-lane reduction beyond one
 // xor-32 exchange:
 //   S^T[key][q] = K . Q^T     A = K tile rows (keys), B = Q^T (held in registers for the sweep)
@@ -22,10 +22,10 @@
 // exp2 domain), so the accumulators are rescaled a few times per sweep instead of every tile.
 #include "kernels.h"
 #include "model.h"
+#include "lds_dma.h"
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
 
@@ -44,8 +44,12 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ uint16_t f2hbits(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
 
+// 16-byte chunk c of LDS row r sits in slot c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128 serves
+// together land in 16 different 4-bank groups (128-B rows alternate between the two bank halves)
+__device__ __forceinline__ int lds_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
+
 __device__ __forceinline__ h8 lds_chunk(const unsigned char * base, int r, int c) {
-    return *(const h8 *) (base + r * 128 + ((c ^ (r & 7)) << 4));
+    return *(const h8 *) (base + r * 128 + (lds_slot(r, c) << 4));
 }
 
 // s_waitcnt vmcnt(N) lgkmcnt(0), then a bare s_barrier (no fence: copies of later tiles stay in flight)
@@ -64,7 +68,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
                                                       void * __restrict__ Od, int n_head, int64_t R, int64_t R_pad,
                                                       float c) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * HALF];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, g = lane >> 5;
     const int qg = wave & 3, kh = wave >> 2;            // query group, key half
     const int hw = wave & 3;                            // wave index inside its half (loads)
@@ -74,8 +78,9 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     const int64_t q0 = (int64_t) blockIdx.x * QB + qg * 32;
 
     const _Float16 * Qh = Q + head * R_pad * HD;
-    const unsigned char * Kh = (const unsigned char *) (Kp + head * R_pad * HD);
-    const unsigned char * Vh = (const unsigned char *) (Vt + head * HD * R_pad);
+    // buffer resources over this head's K rows and V^T rows (offsets below 4 GiB per head)
+    const brsrc rK = make_brsrc(Kp + head * R_pad * HD, R_pad * HD * 2);
+    const brsrc rV = make_brsrc(Vt + head * HD * R_pad, R_pad * HD * 2);
 
     const int ntile = (int) ((R + KT - 1) / KT);
     const int nt = (ntile + 1) / 2;                     // tiles per half (the second may have one less)
@@ -88,15 +93,14 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
         if (s >= my_nt) return;
         unsigned char * base = hbase + (s % NST) * STAGE;
         const int64_t key0 = (int64_t) (t0 + s) * KT;
-        const int cch = (lane & 7) ^ (lane >> 3);
+        // lane fills slot lane % 8 of row r; all rows this wave copies are 8 hw + lane / 8 modulo 32
+        const int cch = lds_slot(8 * hw + (lane >> 3), lane & 7);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int L = 4 * i + hw;                   // 0..7: K rows 8L..8L+7; 8..15: V^T rows
-            const int r = 8 * (L & 7) + (lane >> 3);
-            const unsigned char * src = L < 8 ? Kh + (key0 + r) * (HD * 2) + 16 * cch
-                                              : Vh + (int64_t) r * R_pad * 2 + key0 * 2 + 16 * cch;
-            __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (base + (L < 8 ? 0 : TILE) + 1024 * (L & 7)),
-                                             16, 0, 0);
+            const uint32_t r = 8 * (L & 7) + (lane >> 3);
+            if (i < 2) dma_to_lds<16>(rK, r * (HD * 2) + 16 * cch, (uint32_t) key0 * (HD * 2), base + 1024 * (L & 7));
+            else dma_to_lds<16>(rV, r * (uint32_t) R_pad * 2 + 16 * cch, (uint32_t) key0 * 2, base + TILE + 1024 * (L & 7));
         }
     };
 

@@ -25,6 +25,7 @@
 // rows hit disjoint banks.
 #include "kernels.h"
 #include "model.h"
+#include "lds_dma.h"
 
 #include <hip/hip_fp16.h>
 
@@ -141,8 +142,6 @@ __device__ __forceinline__ void epi4(const kargs & a, int64_t m, int64_t n, floa
     }
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // Stage barrier: wait until at most N_ of this wave's HBM->LDS copies are outstanding and its LDS reads
 // have returned (s_waitcnt vmcnt(N_) lgkmcnt(0); gfx9 encoding: vmcnt in bits [3:0] and [15:14],
 // expcnt [6:4], lgkmcnt [11:8]), then a bare s_barrier. __syncthreads() would add a workgroup fence,
@@ -158,7 +157,7 @@ __device__ __forceinline__ void stage_barrier() {
 // barrier, LDS-latency and VALU phases, and eight waves keep enough HBM->LDS copies in flight: a wave
 // sustains only ~10 GB/s of loads), each owning TI x TJ MFMA tiles of 32 x 32. The workgroup tile is
 // BN = 32 WN TI weight rows by BM = 32 WM TJ tokens. One LDS stage holds 128 B of every one of the
-// BN + BM rows, with 16-byte chunk c of row r stored at chunk c ^ (r & 7): KC = 128 K-columns of int8
+// BN + BM rows, 16-byte chunks swizzled by lds_slot(): KC = 128 K-columns of int8
 // codes (q8_0 / q4_0, plus the four f16 block scales of every row) or 64 K-columns of f16 values
 // (f16 weights, q4_K codes). q4_K keeps its super-block data (d/dmin, mins, activation d, bsums) in a
 // separate double buffer.
@@ -185,13 +184,18 @@ struct tiling {
     static_assert((NST - 2) * LOADS < 64, "vmcnt range");
 };
 
+// 16-byte chunk c of LDS row r sits in slot c ^ ((r >> 1) & 7). Rows are 128 B, so even and odd rows
+// start in opposite halves of the 64 banks; keying the slot on r >> 1 gives the 16 rows a ds_read_b128
+// serves together (one chunk each) 16 different 4-bank groups.
+__device__ __forceinline__ int lds_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
+
 template <class V>
 __device__ __forceinline__ V lds_chunk(const unsigned char * base, int r, int c) {
-    return *(const V *) (base + r * 128 + ((c ^ (r & 7)) << 4));
+    return *(const V *) (base + r * 128 + (lds_slot(r, c) << 4));
 }
 
 // Y[m][n] over the workgroup tile (n0, m0). K advances one stage (KC) per iteration; NST - 1 stages
-// are in flight as direct HBM->LDS copies (global_load_lds_dwordx4: each lane moves 16 B, a wave
+// are in flight as direct HBM->LDS copies (buffer_load_dwordx4 ... lds: each lane moves 16 B, a wave
 // 8 rows), so a stage's loads have NST - 1 compute phases to land. One barrier per stage.
 template <int WF, int EPI, int WN, int WM, int TI, int TJ>
 __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
@@ -199,7 +203,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     constexpr int BN = T::BN, NST = T::NST, NW = T::NW, KC = T::KC, ESZ = T::ESZ;
     __shared__ __attribute__((aligned(16))) unsigned char smem[T::LDS];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave index made uniform (readfirstlane) so the per-wave copy selection stays scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave % WN, wm = wave / WN;
     const int l32 = lane & 31, g = lane >> 5;
 
@@ -221,73 +226,76 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const int64_t nst = (K + KC - 1) / KC;            // q8_0 / q4_0: the last stage may hold 64 columns
     const int64_t rowbytes = K * ESZ;
 
+    // buffer resources rebased at the tile's first weight row and first token, so that every copy's
+    // offset stays below 4 GiB
+    const brsrc rA = make_brsrc((const unsigned char *) a.A + n0 * rowbytes, (a.N - n0) * rowbytes);
+    const brsrc rB = make_brsrc((const unsigned char *) a.B + m0 * rowbytes, (M - m0) * rowbytes);
+    [[maybe_unused]] brsrc rAd, rBd, rAmin, rBs;
+    [[maybe_unused]] const int64_t nsb = K >> 8;
+    if constexpr (WF == W_Q32) {
+        rAd = make_brsrc(a.Ad + n0 * KB, (a.N - n0) * KB * 2);
+        rBd = make_brsrc((const uint16_t *) a.Bd + m0 * KB, (M - m0) * KB * 2);
+    }
+    if constexpr (WF == W_Q4K) {
+        rAd = make_brsrc((const uint32_t *) a.Ad + n0, (nsb * a.N - n0) * 4);
+        rAmin = make_brsrc(a.Amin + n0 * nsb * 16, (a.N - n0) * nsb * 32);
+        rBd = make_brsrc((const float *) a.Bd + m0 * nsb, (M - m0) * nsb * 4);
+        rBs = make_brsrc(a.Bsum + m0 * (K >> 4), (M - m0) * (K >> 4) * 2);
+    }
+    // token row of this tile for tile-relative row r (rows past M repeat row M - 1; results dropped)
+    auto tok_row = [&](int r) -> uint32_t { return (uint32_t) (m0 + r < M ? r : M - 1 - m0); };
+
     auto issue = [&](int64_t st) {
         unsigned char * base = smem + (int) (st % NST) * T::STAGE;
         const int64_t k0 = st * KC;
         if constexpr (WF == W_Q4K) {
             if ((st & 3) == 0) {
-                const int64_t sb = st >> 2, nsb = K >> 8;
+                const uint32_t sb = (uint32_t) (st >> 2);
                 unsigned char * xb = smem + NST * T::STAGE + (int) (sb & 1) * T::XSB;
                 constexpr int N1 = BN / 64, N2 = BN / 32, N3 = T::BM / 64, N4 = T::BM / 32;
                 for (int L = wave; L < N1 + N2 + N3 + N4; L += NW) {
                     if (L < N1) {
-                        const uint32_t * src = (const uint32_t *) a.Ad + sb * a.N + n0 + 64 * L + lane;
-                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_DW + 256 * L), 4, 0, 0);
+                        dma_to_lds<4>(rAd, (uint32_t) (sb * a.N + 64 * L + lane) * 4, 0, xb + T::X_DW + 256 * L);
                     } else if (L < N1 + N2) {
                         const int L2 = L - N1;
-                        const int64_t n = n0 + 32 * L2 + (lane >> 1);
-                        const _Float16 * src = a.Amin + (n * nsb + sb) * 16 + 8 * (lane & 1);
-                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_MIN + 1024 * L2), 16, 0, 0);
+                        const uint32_t n = 32 * L2 + (lane >> 1);
+                        dma_to_lds<16>(rAmin, ((n * (uint32_t) nsb + sb) * 16 + 8 * (lane & 1)) * 2, 0, xb + T::X_MIN + 1024 * L2);
                     } else if (L < N1 + N2 + N3) {
                         const int L3 = L - N1 - N2;
-                        int64_t m = m0 + 64 * L3 + lane;
-                        if (m > M - 1) m = M - 1;
-                        const float * src = (const float *) a.Bd + m * nsb + sb;
-                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_DA + 256 * L3), 4, 0, 0);
+                        const uint32_t m = tok_row(64 * L3 + lane);
+                        dma_to_lds<4>(rBd, (m * (uint32_t) nsb + sb) * 4, 0, xb + T::X_DA + 256 * L3);
                     } else {
                         const int L4 = L - N1 - N2 - N3;
-                        int64_t m = m0 + 32 * L4 + (lane >> 1);
-                        if (m > M - 1) m = M - 1;
-                        const _Float16 * src = a.Bsum + m * (K >> 4) + sb * 16 + 8 * (lane & 1);
-                        __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (xb + T::X_BS + 1024 * L4), 16, 0, 0);
+                        const uint32_t m = tok_row(32 * L4 + (lane >> 1));
+                        dma_to_lds<16>(rBs, (m * (uint32_t) (K >> 4) + sb * 16 + 8 * (lane & 1)) * 2, 0, xb + T::X_BS + 1024 * L4);
                     }
                 }
             }
         }
         if constexpr (WF == W_Q32) {
-            // the four f16 block scales of every row, two per lane (rows past M repeat row M-1; blocks
-            // past K, in a final half stage, repeat the stage's first pair)
-            int64_t kb = (k0 >> 5) + 2 * (lane & 1);
-            if (kb >= KB) kb = k0 >> 5;
+            // the four f16 block scales of every row, two per lane (blocks past K, in a final half
+            // stage, repeat the stage's first pair)
+            const uint32_t kb0 = (uint32_t) (k0 >> 5);
+            const uint32_t kbo = (kb0 + 2 < KB) ? 2 * (lane & 1) : 0;
             for (int L = wave; L < T::ROWS / 32; L += NW) {
                 const int r = 32 * L + (lane >> 1);
-                const uint16_t * src;
-                if (32 * L < BN) {
-                    src = a.Ad + (n0 + r) * KB + kb;
-                } else {
-                    int64_t m = m0 + r - BN;
-                    if (m > M - 1) m = M - 1;
-                    src = (const uint16_t *) a.Bd + m * KB + kb;
-                }
-                __builtin_amdgcn_global_load_lds((const void *) src, (lds_void *) (base + T::TILE + 256 * L), 4, 0, 0);
+                if (32 * L < BN) dma_to_lds<4>(rAd, ((uint32_t) r * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
+                else dma_to_lds<4>(rBd, (tok_row(r - BN) * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
             }
         }
-        const int c = (lane & 7) ^ (lane >> 3);   // rows are loaded 8 at a time, so r & 7 == lane >> 3
-        int64_t cb = k0 * ESZ + 16 * c;            // byte offset of this lane's chunk in its row
-        if (cb >= rowbytes) cb = k0 * ESZ + 16 * (c & 3);   // final half stage: stay inside the row
+        // lane L fills slot L % 8 of row r, i.e. chunk lds_slot(r, L % 8); the rows one wave copies are
+        // equal modulo 16 (8 NW is a multiple of 16), so the chunk is the same for all of them. In a
+        // final half stage (64 bytes left in the row) chunks 4..7 repeat 0..3 and are never read.
+        static_assert((8 * NW) % 16 == 0, "copy rows of a wave must agree modulo 16");
+        const int c = lds_slot(8 * wave + (lane >> 3), lane & 7);
+        const uint32_t soff = (uint32_t) (k0 * ESZ);
+        const uint32_t cb = 16 * ((k0 * ESZ + 128 > rowbytes) ? (c & 3) : c);
 #pragma unroll
         for (int i = 0; i < T::LOADS; i++) {
             const int L = NW * i + wave;
             const int r = 8 * L + (lane >> 3);
-            const unsigned char * src;
-            if (i < BN / (8 * NW)) {
-                src = (const unsigned char *) a.A + (n0 + r) * rowbytes;
-            } else {
-                int64_t m = m0 + r - BN;
-                if (m > M - 1) m = M - 1;          // rows past the end load a valid row; results dropped
-                src = (const unsigned char *) a.B + m * rowbytes;
-            }
-            __builtin_amdgcn_global_load_lds((const void *) (src + cb), (lds_void *) (base + 1024 * L), 16, 0, 0);
+            if (i < BN / (8 * NW)) dma_to_lds<16>(rA, (uint32_t) r * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
+            else dma_to_lds<16>(rB, tok_row(r - BN) * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
         }
     };
 
@@ -312,39 +320,71 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         constexpr int TT = TI * TJ, U = NB * TT;
         const uint32_t * scl = (const uint32_t *) (base + T::TILE);
         const uint32_t gmask = g == 0 ? 0xffffffffu : 0u;
+        // operands and the raw scale words are read a step (or two) ahead; the scale operands are only
+        // assembled in the step that uses them, so no s_waitcnt for those reads lands right after them
         i4v A[NB][TI], B[NB][TJ];
-        h4 SA[NB][TI], SB[NB][TJ];
-        auto scale_of = [&](int r, int blk) -> uint32_t {
-            const uint32_t h = scl[2 * r + (blk >> 1)];
-            return (blk & 1) ? h >> 16 : h & 0xffffu;
-        };
+        uint32_t WA[NB][TI], WB[NB][TJ];
         auto load_for = [&](int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
             if (j == 0) {
                 const int r = 32 * (wn * TI + i) + l32;
                 A[blk][i] = lds_chunk<i4v>(base, r, 2 * blk + g);
-                SA[blk][i] = __builtin_bit_cast(h4, make_uint2(scale_of(r, blk), 0u));
+                WA[blk][i] = scl[2 * r + (blk >> 1)];
             }
             if (i == 0) {
                 const int r = BN + 32 * (wm * TJ + j) + l32;
                 B[blk][j] = lds_chunk<i4v>(base, r, 2 * blk + g);
-                SB[blk][j] = __builtin_bit_cast(h4, make_uint2(scale_of(r, blk) & gmask, 0u));
+                WB[blk][j] = scl[2 * r + (blk >> 1)];
             }
         };
+        // the empty asm makes the word a fresh value at the point of use, so the compiler cannot hoist
+        // the half extraction (and the wait for the LDS read) back next to the read
+        auto half_of = [](uint32_t w, int blk) -> uint32_t {
+            asm volatile("" : "+v"(w));
+            return (blk & 1) ? w >> 16 : w & 0xffffu;
+        };
+        auto sa_of = [&](int blk, int i) { return __builtin_bit_cast(h4, make_uint2(half_of(WA[blk][i], blk), 0u)); };
+        auto sb_of = [&](int blk, int j) { return __builtin_bit_cast(h4, make_uint2(half_of(WB[blk][j], blk) & gmask, 0u)); };
         const i16v izero = {};
+        if constexpr (TT <= 2) {
+        // software pipeline (small wave tiles, where the second S/C pair fits the register budget): the
+        // MFMAs of step u+1 are in flight while the VALU epilogue of step u runs; operands are read
+        // from LDS two steps ahead
+        i16v S[2];
+        f16v C[2];
+        auto mfma_step = [&](int u) {
+            const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
+            S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], izero);
+            C[u & 1] = MFMA8(sa_of(blk, i), sb_of(blk, j), zero);
+        };
+        load_for(0);
+        if (U > 1) load_for(1);
+        mfma_step(0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (u + 2 < U) load_for(u + 2);
+            if (u + 1 < U) mfma_step(u + 1);
+            const int t = u % TT, i = t / TJ, j = t % TJ;
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[u & 1][r], C[u & 1][r], acc[i][j][r]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        } else {
         load_for(0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (u + 1 < U) load_for(u + 1);
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
             const i16v S = MFMA_I8(A[blk][i], B[blk][j], izero);
-            const f16v C = MFMA8(SA[blk][i], SB[blk][j], zero);
+            const f16v C = MFMA8(sa_of(blk, i), sb_of(blk, j), zero);
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[r], C[r], acc[i][j][r]);
             // one scheduling region per step: operand reads stay one step ahead instead of being
             // hoisted to the top of the stage (which would not fit the 256 VGPRs of two waves/SIMD);
             // the other wave on the SIMD covers this wave's MFMA latency
             __builtin_amdgcn_sched_barrier(0);
+        }
         }
     };
 
