@@ -210,26 +210,31 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
 
 struct ktimer {   // optional per-kernel-class event timing (jepa_amd_context_set_kernel_timing)
     jepa_context * ctx;
-    std::vector<std::pair<std::string, std::pair<hipEvent_t, hipEvent_t>>> evs;
-    template <typename F> void run(const char * name, F && f) {
+    struct rec { std::string name, detail; hipEvent_t a, b; };
+    std::vector<rec> evs;
+    // the launch counts under `name` and, when given, also under "name.detail" (e.g. gemm_q8.qkv)
+    template <typename F> void run(const char * name, F && f, const char * detail = nullptr) {
         if (!ctx->kernel_timing) { f(); return; }
         hipEvent_t a, b;
         hipEventCreate(&a); hipEventCreate(&b);
         hipEventRecord(a, ctx->stream);
         f();
         hipEventRecord(b, ctx->stream);
-        evs.push_back({name, {a, b}});
+        evs.push_back({name, detail ? std::string(name) + "." + detail : std::string(), a, b});
     }
     void collect() {
         for (auto & e : evs) {
-            hipEventSynchronize(e.second.second);
+            hipEventSynchronize(e.b);
             float ms = 0;
-            hipEventElapsedTime(&ms, e.second.first, e.second.second);
-            auto & st = ctx->kstats[e.first];
-            st.first += 1;
-            st.second += ms;
-            hipEventDestroy(e.second.first);
-            hipEventDestroy(e.second.second);
+            hipEventElapsedTime(&ms, e.a, e.b);
+            for (const std::string * k : {&e.name, &e.detail}) {
+                if (k->empty()) continue;
+                auto & st = ctx->kstats[*k];
+                st.first += 1;
+                st.second += ms;
+            }
+            hipEventDestroy(e.a);
+            hipEventDestroy(e.b);
         }
         evs.clear();
     }
@@ -279,7 +284,7 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
             ep.q = w.Q; ep.k = w.Kt; ep.vt = w.Vt;
             ep.rope_c = w.rope_c; ep.rope_s = w.rope_s;
             ep.n_head = H; ep.hd = hd; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
-            kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s); });
+            kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s); }, "qkv");
         }
         w.actA.fmt = L.out.act();
         if (w.actA.fmt == A_Q8_0) {
@@ -294,7 +299,7 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
         {
             gemm_epi ep;
             ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls1;
-            kt.run(gemm_class(L.out), [&] { launch_gemm(L.out, w.actA, rows, ep, s); });
+            kt.run(gemm_class(L.out), [&] { launch_gemm(L.out, w.actA, rows, ep, s); }, "out");
         }
         // MLP half
         w.actA.fmt = L.up.act();
@@ -307,14 +312,14 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
             if (mfma && w.actB.fmt == A_Q8_0) { ep.kind = EPI_GELU_Q8_0; ep.oq = w.actB.q; ep.od = w.actB.d; }
             else if (mfma && w.actB.fmt == A_F16) { ep.kind = EPI_GELU_F16; ep.oh = w.actB.q; }
             else { ep.kind = EPI_GELU_F32; ep.y = w.ff; }
-            kt.run(gemm_class(L.up), [&] { launch_gemm(L.up, w.actA, rows, ep, s); });
+            kt.run(gemm_class(L.up), [&] { launch_gemm(L.up, w.actA, rows, ep, s); }, "up");
             if (ep.kind == EPI_GELU_F32)
                 kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, w.actB, s); });
         }
         {
             gemm_epi ep;
             ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls2;
-            kt.run(gemm_class(L.down), [&] { launch_gemm(L.down, w.actB, rows, ep, s); });
+            kt.run(gemm_class(L.down), [&] { launch_gemm(L.down, w.actB, rows, ep, s); }, "down");
         }
         if (trace) launch_copy_f32(w.x, trace + (int64_t) (l + 1) * rows * D, rows * D, s);
     }

@@ -179,9 +179,11 @@ struct tiling {
     static constexpr int NST = NST_FIT < NST_MAX ? NST_FIT : NST_MAX;
     static constexpr int LDS = NST * STAGE + 2 * XSB;
     static constexpr int LOADS = ROWS / 8 / NW;    // 1 KB tile loads per wave per stage
+    static constexpr int SL = WF == W_Q32 ? (ROWS / 32 + NW - 1) / NW : 0;   // scale copies per wave per stage
+    static constexpr int PARTS = LOADS + SL;       // copies per wave per stage (q4_K adds its own)
     static_assert(NST >= 2, "LDS too small for two stages");
     static_assert(BN % (8 * NW) == 0 && BN % 64 == 0 && BM % 64 == 0 && ROWS % (8 * NW) == 0, "load split");
-    static_assert((NST - 2) * LOADS < 64, "vmcnt range");
+    static_assert((NST - 2) * PARTS < 64, "vmcnt range");
 };
 
 // 16-byte chunk c of LDS row r sits in slot c ^ ((r >> 1) & 7). Rows are 128 B, so even and odd rows
@@ -225,6 +227,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const int64_t K = a.K, M = a.M, KB = K >> 5;
     const int64_t nst = (K + KC - 1) / KC;            // q8_0 / q4_0: the last stage may hold 64 columns
     const int64_t rowbytes = K * ESZ;
+    // q8_0 / q4_0: issue the next stage's copies one per compute step instead of all at the stage start
+    constexpr bool SPREAD = true;
 
     // buffer resources rebased at the tile's first weight row and first token, so that every copy's
     // offset stays below 4 GiB
@@ -245,9 +249,47 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // token row of this tile for tile-relative row r (rows past M repeat row M - 1; results dropped)
     auto tok_row = [&](int r) -> uint32_t { return (uint32_t) (m0 + r < M ? r : M - 1 - m0); };
 
-    auto issue = [&](int64_t st) {
+    // Copy i (0 <= i < LOADS) of stage st: this wave's 1 KB of 8 tile rows (128 B each). Lane L fills
+    // slot L % 8 of row r, i.e. chunk lds_slot(r, L % 8); the rows one wave copies are equal modulo 16
+    // (8 NW is a multiple of 16), so the chunk is the same for all of them. In a final half stage
+    // (64 bytes left in the row) chunks 4..7 repeat 0..3 and are never read.
+    static_assert((8 * NW) % 16 == 0, "copy rows of a wave must agree modulo 16");
+    auto issue_tile = [&](int64_t st, int64_t sa, int i) {
         unsigned char * base = smem + (int) (st % NST) * T::STAGE;
-        const int64_t k0 = st * KC;
+        const int64_t k0 = sa * KC;
+        const int c = lds_slot(8 * wave + (lane >> 3), lane & 7);
+        const uint32_t soff = (uint32_t) (k0 * ESZ);
+        const uint32_t cb = 16 * ((k0 * ESZ + 128 > rowbytes) ? (c & 3) : c);
+        const int L = NW * i + wave;
+        const int r = 8 * L + (lane >> 3);
+        if (i < BN / (8 * NW)) dma_to_lds<16>(rA, (uint32_t) r * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
+        else dma_to_lds<16>(rB, tok_row(r - BN) * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
+    };
+    // q8_0 / q4_0 copy p (0 <= p < SL) of stage st: the four f16 block scales of 32 rows, two per lane
+    // (blocks past K, in a final half stage, repeat the stage's first pair). Every wave issues SL
+    // copies, so that the stage barrier can count them; a wave without a row group of its own repeats
+    // another wave's copy (the same bytes to the same place).
+    [[maybe_unused]] auto issue_scales = [&](int64_t st, int64_t sa, int p) {
+        unsigned char * base = smem + (int) (st % NST) * T::STAGE;
+        const uint32_t kb0 = (uint32_t) ((sa * KC) >> 5);
+        const uint32_t kbo = (kb0 + 2 < KB) ? 2 * (lane & 1) : 0;
+        int L = wave + NW * p;
+        if (L >= T::ROWS / 32) L = wave % (T::ROWS / 32);
+        const int r = 32 * L + (lane >> 1);
+        if (32 * L < BN) dma_to_lds<4>(rAd, ((uint32_t) r * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
+        else dma_to_lds<4>(rBd, (tok_row(r - BN) * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
+    };
+    // q8_0 / q4_0 stages issue their PARTS copies one per compute step of the stage NST - 1 earlier
+    // (spread, so that no wave stalls behind a burst of copies). Stages past the end copy the last
+    // stage's data again into the buffer of the stage just finished, which no one reads any more:
+    // the copies stay unconditional (a branch around them would split the software pipeline).
+    [[maybe_unused]] auto issue_part = [&](int64_t st, int p) {
+        const int64_t sa = st < nst ? st : nst - 1;
+        if (p < T::LOADS) issue_tile(st, sa, p);
+        else issue_scales(st, sa, p - T::LOADS);
+    };
+
+    auto issue = [&](int64_t st) {
         if constexpr (WF == W_Q4K) {
             if ((st & 3) == 0) {
                 const uint32_t sb = (uint32_t) (st >> 2);
@@ -273,30 +315,11 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             }
         }
         if constexpr (WF == W_Q32) {
-            // the four f16 block scales of every row, two per lane (blocks past K, in a final half
-            // stage, repeat the stage's first pair)
-            const uint32_t kb0 = (uint32_t) (k0 >> 5);
-            const uint32_t kbo = (kb0 + 2 < KB) ? 2 * (lane & 1) : 0;
-            for (int L = wave; L < T::ROWS / 32; L += NW) {
-                const int r = 32 * L + (lane >> 1);
-                if (32 * L < BN) dma_to_lds<4>(rAd, ((uint32_t) r * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
-                else dma_to_lds<4>(rBd, (tok_row(r - BN) * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
-            }
-        }
-        // lane L fills slot L % 8 of row r, i.e. chunk lds_slot(r, L % 8); the rows one wave copies are
-        // equal modulo 16 (8 NW is a multiple of 16), so the chunk is the same for all of them. In a
-        // final half stage (64 bytes left in the row) chunks 4..7 repeat 0..3 and are never read.
-        static_assert((8 * NW) % 16 == 0, "copy rows of a wave must agree modulo 16");
-        const int c = lds_slot(8 * wave + (lane >> 3), lane & 7);
-        const uint32_t soff = (uint32_t) (k0 * ESZ);
-        const uint32_t cb = 16 * ((k0 * ESZ + 128 > rowbytes) ? (c & 3) : c);
 #pragma unroll
-        for (int i = 0; i < T::LOADS; i++) {
-            const int L = NW * i + wave;
-            const int r = 8 * L + (lane >> 3);
-            if (i < BN / (8 * NW)) dma_to_lds<16>(rA, (uint32_t) r * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
-            else dma_to_lds<16>(rB, tok_row(r - BN) * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
+            for (int p = 0; p < T::SL; p++) issue_scales(st, st, p);
         }
+#pragma unroll
+        for (int i = 0; i < T::LOADS; i++) issue_tile(st, st, i);
     };
 
     f16v acc[TI][TJ];
@@ -311,51 +334,48 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         }
 
     // q8_0 / q4_0 stage of NB 32-blocks. Steps u = (block, tile), tiles i-major: one int8 MFMA gives the
-    // exact block sum S, one f16 MFMA (32x32x8) of the scale operands (dw in K-slot 0 of both lane
-    // groups, da in K-slot 0 of group 0 only) gives the exact f32 dw[n] * da[m], and
-    // acc = fma(float(S), dw*da, acc).
+    // exact block sum S, one f16 MFMA (32x32x8) of the scale operands gives the exact f32 dw[n] * da[m],
+    // and acc = fma(float(S), dw*da, acc).
+    // Scale operands, built once per stage: the weight row's four f16 block scales, read as they lie
+    // in LDS, fill K-slots 0-3 (both lane groups); the token's scale of block blk alone fills K-slot
+    // blk of lane group 0 (group 1 is zero), so the product picks dw_blk * da_blk.
     // The 32 VALU ops per step (convert + fma) bound this path, not the two MFMAs.
-    [[maybe_unused]] auto q32_stage = [&](const unsigned char * base, auto nb_c) {
+    const uint32_t msk_lo = g == 0 ? 0x0000ffffu : 0u, msk_hi = g == 0 ? 0xffff0000u : 0u;
+    [[maybe_unused]] auto q32_stage = [&](const unsigned char * base, auto nb_c, int64_t st_next) {
         constexpr int NB = decltype(nb_c)::value;
         constexpr int TT = TI * TJ, U = NB * TT;
-        const uint32_t * scl = (const uint32_t *) (base + T::TILE);
-        const uint32_t gmask = g == 0 ? 0xffffffffu : 0u;
-        // operands and the raw scale words are read a step (or two) ahead; the scale operands are only
-        // assembled in the step that uses them, so no s_waitcnt for those reads lands right after them
+        static_assert(NB < 4 || T::PARTS <= U, "a full stage has a step for every copy of the stage it issues");
+        const unsigned char * scl = base + T::TILE;      // 8 B per row: f16 d of the stage's 4 blocks
+        h4 SA[TI], SB[NB][TJ];
+#pragma unroll
+        for (int i = 0; i < TI; i++) SA[i] = *(const h4 *) (scl + 8 * (32 * (wn * TI + i) + l32));
+#pragma unroll
+        for (int j = 0; j < TJ; j++) {
+            const uint2 w = *(const uint2 *) (scl + 8 * (BN + 32 * (wm * TJ + j) + l32));
+#pragma unroll
+            for (int blk = 0; blk < NB; blk++) {
+                const uint32_t msk = (blk & 1) ? msk_hi : msk_lo;
+                const uint2 o = blk < 2 ? make_uint2(w.x & msk, 0u) : make_uint2(0u, w.y & msk);
+                SB[blk][j] = __builtin_bit_cast(h4, o);
+            }
+        }
+        // operand chunks are read from LDS a step (or two) ahead of their MFMA
         i4v A[NB][TI], B[NB][TJ];
-        uint32_t WA[NB][TI], WB[NB][TJ];
         auto load_for = [&](int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            if (j == 0) {
-                const int r = 32 * (wn * TI + i) + l32;
-                A[blk][i] = lds_chunk<i4v>(base, r, 2 * blk + g);
-                WA[blk][i] = scl[2 * r + (blk >> 1)];
-            }
-            if (i == 0) {
-                const int r = BN + 32 * (wm * TJ + j) + l32;
-                B[blk][j] = lds_chunk<i4v>(base, r, 2 * blk + g);
-                WB[blk][j] = scl[2 * r + (blk >> 1)];
-            }
+            if (j == 0) A[blk][i] = lds_chunk<i4v>(base, 32 * (wn * TI + i) + l32, 2 * blk + g);
+            if (i == 0) B[blk][j] = lds_chunk<i4v>(base, BN + 32 * (wm * TJ + j) + l32, 2 * blk + g);
         };
-        // the empty asm makes the word a fresh value at the point of use, so the compiler cannot hoist
-        // the half extraction (and the wait for the LDS read) back next to the read
-        auto half_of = [](uint32_t w, int blk) -> uint32_t {
-            asm volatile("" : "+v"(w));
-            return (blk & 1) ? w >> 16 : w & 0xffffu;
-        };
-        auto sa_of = [&](int blk, int i) { return __builtin_bit_cast(h4, make_uint2(half_of(WA[blk][i], blk), 0u)); };
-        auto sb_of = [&](int blk, int j) { return __builtin_bit_cast(h4, make_uint2(half_of(WB[blk][j], blk) & gmask, 0u)); };
         const i16v izero = {};
-        if constexpr (TT <= 2) {
-        // software pipeline (small wave tiles, where the second S/C pair fits the register budget): the
-        // MFMAs of step u+1 are in flight while the VALU epilogue of step u runs; operands are read
-        // from LDS two steps ahead
+        if constexpr (TT <= 4) {
+        // software pipeline (where the second S/C pair fits the register budget): the MFMAs of step
+        // u+1 are in flight while the VALU epilogue of step u runs
         i16v S[2];
         f16v C[2];
         auto mfma_step = [&](int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
             S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], izero);
-            C[u & 1] = MFMA8(sa_of(blk, i), sb_of(blk, j), zero);
+            C[u & 1] = MFMA8(SA[i], SB[blk][j], zero);
         };
         load_for(0);
         if (U > 1) load_for(1);
@@ -363,6 +383,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
+            if (SPREAD && u < T::PARTS && NB == 4) issue_part(st_next, u);
             if (u + 2 < U) load_for(u + 2);
             if (u + 1 < U) mfma_step(u + 1);
             const int t = u % TT, i = t / TJ, j = t % TJ;
@@ -374,10 +395,11 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         load_for(0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
+            if (SPREAD && u < T::PARTS && NB == 4) issue_part(st_next, u);
             if (u + 1 < U) load_for(u + 1);
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
             const i16v S = MFMA_I8(A[blk][i], B[blk][j], izero);
-            const f16v C = MFMA8(sa_of(blk, i), sb_of(blk, j), zero);
+            const f16v C = MFMA8(SA[i], SB[blk][j], zero);
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[r], C[r], acc[i][j][r]);
             // one scheduling region per step: operand reads stay one step ahead instead of being
@@ -391,16 +413,21 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     for (int s = 0; s < NST - 1; s++)
         if (s < nst) issue(s);
 
-    for (int64_t st = 0; st < nst; st++) {
-        // stage st has landed once at most the loads of the NST - 2 younger stages are outstanding
-        // (all waves' copies of stage st visible; every wave done reading stage st-1's buffer)
-        if (st + NST - 2 < nst) stage_barrier<(NST - 2) * T::LOADS>();
+    // stage st has landed once at most the loads of the NST - 2 younger stages are outstanding (all
+    // waves' copies of stage st visible; every wave done reading stage st-1's buffer)
+    auto stage_begin = [&](int64_t st, bool spread) -> const unsigned char * {
+        if (st + NST - 2 < nst) stage_barrier<(NST - 2) * T::PARTS>();
         else stage_barrier<0>();
-        if (st + NST - 1 < nst) issue(st + NST - 1);
-        const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
+        if (!spread && st + NST - 1 < nst) issue(st + NST - 1);
+        return smem + (int) (st % NST) * T::STAGE;
+    };
+    // q8_0 / q4_0 with K % 128 == 64 end in a half stage, peeled off the loop so that the loop body
+    // has one path (the accumulators then stay in place across iterations)
+    const int64_t nfull = WF == W_Q32 ? K / KC : nst;
+    for (int64_t st = 0; st < nfull; st++) {
+        const unsigned char * base = stage_begin(st, SPREAD && WF == W_Q32);
         if constexpr (WF == W_Q32) {
-            if ((st + 1) * KC <= K) q32_stage(base, std::integral_constant<int, 4>{});
-            else q32_stage(base, std::integral_constant<int, 2>{});
+            q32_stage(base, std::integral_constant<int, 4>{}, st + NST - 1);
         } else {
 #pragma unroll
             for (int blk = 0; blk < 2; blk++) {
@@ -471,6 +498,11 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             }
         }
     }
+    if constexpr (WF == W_Q32) {
+        if (nfull < nst) q32_stage(stage_begin(nfull, SPREAD), std::integral_constant<int, 2>{}, -1);
+        // the copies issued during the last stages must land before the workgroup's LDS is released
+        if constexpr (SPREAD) __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+    }
 
     if constexpr (WF == W_Q4K) {
 #pragma unroll
@@ -519,6 +551,50 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                         *(uint32_t *) ((int8_t *) a.ep.oq + m * a.N + n) = o;   // int8 codes
                     }
                     if (g == 0) ((uint16_t *) a.ep.od)[m * (a.N / 32) + nb / 32] = f2hbits(d);
+                }
+            } else if constexpr (EPI == EPI_QKV) {
+                // the tile's 32 features lie in one head of one of Q, K, V (D and hd are multiples of 32):
+                // head and offset are wave-uniform, the token is one 32-bit division per lane
+                const gemm_epi & ep = a.ep;
+                const int hd = ep.hd;
+                const int nbi = __builtin_amdgcn_readfirstlane((int) nb);
+                const int which = nbi / ep.D, nn = nbi - which * ep.D;
+                const int h = nn / hd, dbase = nn - h * hd + 4 * g;
+                if (m >= M) continue;
+                const uint32_t mu = (uint32_t) m, Ru = (uint32_t) ep.R;
+                const uint32_t item = mu / Ru, tok = mu - item * Ru;
+                const int64_t head = (int64_t) item * ep.n_head + h;
+                float t[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 b = a.bias ? *(const float4 *) (a.bias + nb + 8 * q + 4 * g) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) t[4 * q + e] = a.bias ? __fadd_rn(acc[i][j][4 * q + e], bb[e]) : acc[i][j][4 * q + e];
+                }
+                if (which < 2) {
+                    _Float16 * dst = (_Float16 *) (which == 0 ? ep.q : ep.k) + (head * ep.R_pad + tok) * hd + dbase;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float o[4] = {t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]};
+                        if (ep.rope_c) {
+                            // out = x*C + swap(x)*S' (reference src/rope3d.cpp:136-164): two products, one add
+                            const float4 c = *(const float4 *) (ep.rope_c + (int64_t) tok * hd + dbase + 8 * q);
+                            const float4 sn = *(const float4 *) (ep.rope_s + (int64_t) tok * hd + dbase + 8 * q);
+                            o[0] = __fadd_rn(__fmul_rn(t[4 * q + 0], c.x), __fmul_rn(t[4 * q + 1], sn.x));
+                            o[1] = __fadd_rn(__fmul_rn(t[4 * q + 1], c.y), __fmul_rn(t[4 * q + 0], sn.y));
+                            o[2] = __fadd_rn(__fmul_rn(t[4 * q + 2], c.z), __fmul_rn(t[4 * q + 3], sn.z));
+                            o[3] = __fadd_rn(__fmul_rn(t[4 * q + 3], c.w), __fmul_rn(t[4 * q + 2], sn.w));
+                        }
+                        h4 v = {(_Float16) o[0], (_Float16) o[1], (_Float16) o[2], (_Float16) o[3]};
+                        *(h4 *) (dst + 8 * q) = v;
+                    }
+                } else {
+                    _Float16 * vt = (_Float16 *) ep.vt + (head * hd + dbase) * ep.R_pad + perm16(tok);
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) vt[(int64_t) (8 * q + e) * ep.R_pad] = (_Float16) t[4 * q + e];
                 }
             } else {
                 if (m >= M) continue;
