@@ -227,8 +227,6 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const int64_t K = a.K, M = a.M, KB = K >> 5;
     const int64_t nst = (K + KC - 1) / KC;            // q8_0 / q4_0: the last stage may hold 64 columns
     const int64_t rowbytes = K * ESZ;
-    // q8_0 / q4_0: issue the next stage's copies one per compute step instead of all at the stage start
-    constexpr bool SPREAD = true;
 
     // buffer resources rebased at the tile's first weight row and first token, so that every copy's
     // offset stays below 4 GiB
@@ -288,7 +286,6 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         if (p < T::LOADS) issue_tile(st, sa, p);
         else issue_scales(st, sa, p - T::LOADS);
     };
-
     auto issue = [&](int64_t st) {
         if constexpr (WF == W_Q4K) {
             if ((st & 3) == 0) {
@@ -333,102 +330,154 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             if constexpr (WF == W_Q4K) { ssb[i][j] = zero; accm[i][j] = zero; }
         }
 
-    // q8_0 / q4_0 stage of NB 32-blocks. Steps u = (block, tile), tiles i-major: one int8 MFMA gives the
-    // exact block sum S, one f16 MFMA (32x32x8) of the scale operands gives the exact f32 dw[n] * da[m],
-    // and acc = fma(float(S), dw*da, acc).
-    // Scale operands, built once per stage: the weight row's four f16 block scales, read as they lie
-    // in LDS, fill K-slots 0-3 (both lane groups); the token's scale of block blk alone fills K-slot
-    // blk of lane group 0 (group 1 is zero), so the product picks dw_blk * da_blk.
-    // The 32 VALU ops per step (convert + fma) bound this path, not the two MFMAs.
+    // ---- q8_0 / q4_0 ----
+    // A stage holds 4 blocks of 32 K-columns. Steps u = (block, tile), tiles i-major, U = 4 TI TJ per
+    // stage: one int8 MFMA gives the exact block sum S, one f16 MFMA (32x32x8) of the scale operands
+    // gives the exact f32 dw[n] * da[m], and acc = fma(float(S), dw*da, acc).
+    // Scale operands, read once per stage: the weight row's four f16 block scales, as they lie in LDS,
+    // fill K-slots 0-3 (both lane groups); the token's scale of block blk alone fills K-slot blk of lane
+    // group 0 (group 1 is zero), so the product picks dw_blk * da_blk.
+    // The 32 VALU ops per step (convert + fma) and the two MFMAs, which the SIMD does not overlap
+    // well, bound this path; everything else is hidden behind them:
+    //  - software pipeline: operand chunks are read two steps ahead, the MFMAs of step u+1 are issued
+    //    before the VALU work of step u, across stage boundaries;
+    //  - the barrier that publishes stage st+1 sits two steps before the end of stage st, after the
+    //    wave's last LDS read of stage st, so the first reads of stage st+1 overlap the last steps;
+    //  - each step issues one of the HBM->LDS copies of stage st + NST - 1 (spread, not a burst).
     const uint32_t msk_lo = g == 0 ? 0x0000ffffu : 0u, msk_hi = g == 0 ? 0xffff0000u : 0u;
-    [[maybe_unused]] auto q32_stage = [&](const unsigned char * base, auto nb_c, int64_t st_next) {
-        constexpr int NB = decltype(nb_c)::value;
-        constexpr int TT = TI * TJ, U = NB * TT;
-        static_assert(NB < 4 || T::PARTS <= U, "a full stage has a step for every copy of the stage it issues");
+    auto q32_scales = [&](const unsigned char * base, h4 (&sa)[TI], h4 (&sb)[4][TJ]) {
         const unsigned char * scl = base + T::TILE;      // 8 B per row: f16 d of the stage's 4 blocks
-        h4 SA[TI], SB[NB][TJ];
 #pragma unroll
-        for (int i = 0; i < TI; i++) SA[i] = *(const h4 *) (scl + 8 * (32 * (wn * TI + i) + l32));
+        for (int i = 0; i < TI; i++) sa[i] = *(const h4 *) (scl + 8 * (32 * (wn * TI + i) + l32));
 #pragma unroll
         for (int j = 0; j < TJ; j++) {
             const uint2 w = *(const uint2 *) (scl + 8 * (BN + 32 * (wm * TJ + j) + l32));
 #pragma unroll
-            for (int blk = 0; blk < NB; blk++) {
+            for (int blk = 0; blk < 4; blk++) {
                 const uint32_t msk = (blk & 1) ? msk_hi : msk_lo;
                 const uint2 o = blk < 2 ? make_uint2(w.x & msk, 0u) : make_uint2(0u, w.y & msk);
-                SB[blk][j] = __builtin_bit_cast(h4, o);
+                sb[blk][j] = __builtin_bit_cast(h4, o);
             }
         }
-        // operand chunks are read from LDS a step (or two) ahead of their MFMA
-        i4v A[NB][TI], B[NB][TJ];
-        auto load_for = [&](int u) {
+    };
+    [[maybe_unused]] auto q32_main = [&](int64_t nfull) {
+      if constexpr (WF == W_Q32) {
+        constexpr int TT = TI * TJ, U = 4 * TT;
+        static_assert(NST >= 3, "the in-stage barrier needs a stage in flight beyond the next one");
+        // copies of this wave still allowed in flight at the barrier that publishes stage st+1 (held
+        // in stage st at step U-2): the NST-3 stages after st+1, plus those of stage st+NST-1 that
+        // steps 0..U-2 of stage st have issued
+        // per stage every wave issues the PARTS copies of one stage, spread over the steps of a body
+        // (step u issues copies [u PARTS / U, (u+1) PARTS / U))
+        constexpr int P1 = T::PARTS;
+        auto items_before = [](int u) { return u * P1 / U; };
+        // copies issued after the last copy of stage st+1 when stage st publishes it (step U-2, after
+        // that step's copies): the NST-3 stages after it, and this body's copies so far
+        constexpr int NBAR = (NST - 3) * P1 + (U - 1) * P1 / U;
+        i4v A[4][TI], B[4][TJ];
+        h4 SA[TI], SB[4][TJ];
+        i16v S[2];
+        f16v C[2];
+        const i16v izero = {};
+        auto ld_step = [&](const unsigned char * base, int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
             if (j == 0) A[blk][i] = lds_chunk<i4v>(base, 32 * (wn * TI + i) + l32, 2 * blk + g);
             if (i == 0) B[blk][j] = lds_chunk<i4v>(base, BN + 32 * (wm * TJ + j) + l32, 2 * blk + g);
         };
-        const i16v izero = {};
-        if constexpr (TT <= 4) {
-        // software pipeline (where the second S/C pair fits the register budget): the MFMAs of step
-        // u+1 are in flight while the VALU epilogue of step u runs
-        i16v S[2];
-        f16v C[2];
-        auto mfma_step = [&](int u) {
+        auto mma = [&](int u, const h4 (&sa)[TI], const h4 (&sb)[4][TJ]) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
             S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], izero);
-            C[u & 1] = MFMA8(SA[i], SB[blk][j], zero);
+            C[u & 1] = MFMA8(sa[i], sb[blk][j], zero);
         };
-        load_for(0);
-        if (U > 1) load_for(1);
-        mfma_step(0);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (SPREAD && u < T::PARTS && NB == 4) issue_part(st_next, u);
-            if (u + 2 < U) load_for(u + 2);
-            if (u + 1 < U) mfma_step(u + 1);
+        auto valu = [&](int u) {
             const int t = u % TT, i = t / TJ, j = t % TJ;
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[u & 1][r], C[u & 1][r], acc[i][j][r]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        } else {
-        load_for(0);
+        };
+        // prologue: stages 0..NST-2 in flight (unconditionally, so that every barrier count is exact:
+        // stages past the end copy the last stage again into buffers no stage uses), stage 0 landed,
+        // its scales and first two steps read, its first MFMAs issued
+        for (int s0 = 0; s0 < NST - 1; s0++)
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (SPREAD && u < T::PARTS && NB == 4) issue_part(st_next, u);
-            if (u + 1 < U) load_for(u + 1);
-            const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            const i16v S = MFMA_I8(A[blk][i], B[blk][j], izero);
-            const f16v C = MFMA8(SA[i], SB[blk][j], zero);
+            for (int p = 0; p < T::PARTS; p++) issue_part(s0, p);
+        stage_barrier<(NST - 2) * P1>();
+        q32_scales(smem, SA, SB);
+        ld_step(smem, 0);
+        ld_step(smem, 1);
+        mma(0, SA, SB);
+        __builtin_amdgcn_sched_barrier(0);
+        // one full stage; CROSS: publish stage st+1 and start its pipeline in the last two steps
+        auto body = [&](int64_t st, auto cross_c) {
+            constexpr bool CROSS = decltype(cross_c)::value;
+            const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
+            const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
+            h4 SAn[TI], SBn[4][TJ];
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[r], C[r], acc[i][j][r]);
-            // one scheduling region per step: operand reads stay one step ahead instead of being
-            // hoisted to the top of the stage (which would not fit the 256 VGPRs of two waves/SIMD);
-            // the other wave on the SIMD covers this wave's MFMA latency
-            __builtin_amdgcn_sched_barrier(0);
+            for (int u = 0; u < U; u++) {
+#pragma unroll
+                for (int k = items_before(u); k < items_before(u + 1); k++) issue_part(st + NST - 1, k);
+                if (u + 2 < U) ld_step(base, u + 2);
+                if constexpr (CROSS) {
+                    if (u == U - 2) {
+                        stage_barrier<NBAR>();
+                        q32_scales(nbase, SAn, SBn);
+                        ld_step(nbase, 0);
+                    }
+                    if (u == U - 1) ld_step(nbase, 1);
+                }
+                if (u + 1 < U) mma(u + 1, SA, SB);
+                else if constexpr (CROSS) mma(0, SAn, SBn);
+                valu(u);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (CROSS) {
+#pragma unroll
+                for (int i = 0; i < TI; i++) SA[i] = SAn[i];
+#pragma unroll
+                for (int blk = 0; blk < 4; blk++)
+#pragma unroll
+                    for (int j = 0; j < TJ; j++) SB[blk][j] = SBn[blk][j];
+            }
+        };
+        for (int64_t st = 0; st + 1 < nfull; st++) body(st, std::true_type{});
+        if (nfull > 0) body(nfull - 1, std::false_type{});
+        // final half stage (K % 128 == 64): blocks 0 and 1 of stage nfull, after all copies landed
+        if (nfull < nst) {
+            stage_barrier<0>();
+            const unsigned char * base = smem + (int) (nfull % NST) * T::STAGE;
+            q32_scales(base, SA, SB);
+#pragma unroll
+            for (int u = 0; u < 2 * TT; u++) {
+                ld_step(base, u);
+                mma(u, SA, SB);
+                valu(u);
+            }
         }
-        }
+        // the copies issued during the last stages must land before the workgroup's LDS is released
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+      }
     };
 
+    // q8_0 / q4_0 with K % 128 == 64 end in a half stage, peeled off the loop so that the loop body
+    // has one path (the accumulators then stay in place across iterations)
+    const int64_t nfull = WF == W_Q32 ? K / KC : nst;
+    if constexpr (WF == W_Q32) {
+        q32_main(nfull);
+    } else {
     for (int s = 0; s < NST - 1; s++)
         if (s < nst) issue(s);
 
     // stage st has landed once at most the loads of the NST - 2 younger stages are outstanding (all
     // waves' copies of stage st visible; every wave done reading stage st-1's buffer)
-    auto stage_begin = [&](int64_t st, bool spread) -> const unsigned char * {
+    auto stage_begin = [&](int64_t st) -> const unsigned char * {
         if (st + NST - 2 < nst) stage_barrier<(NST - 2) * T::PARTS>();
         else stage_barrier<0>();
-        if (!spread && st + NST - 1 < nst) issue(st + NST - 1);
+        if (st + NST - 1 < nst) issue(st + NST - 1);
         return smem + (int) (st % NST) * T::STAGE;
     };
-    // q8_0 / q4_0 with K % 128 == 64 end in a half stage, peeled off the loop so that the loop body
-    // has one path (the accumulators then stay in place across iterations)
-    const int64_t nfull = WF == W_Q32 ? K / KC : nst;
     for (int64_t st = 0; st < nfull; st++) {
-        const unsigned char * base = stage_begin(st, SPREAD && WF == W_Q32);
-        if constexpr (WF == W_Q32) {
-            q32_stage(base, std::integral_constant<int, 4>{}, st + NST - 1);
-        } else {
+        const unsigned char * base = stage_begin(st);
+        {
 #pragma unroll
             for (int blk = 0; blk < 2; blk++) {
                 h8 a0[TI], a1[TI], b0[TJ], b1[TJ];
@@ -498,10 +547,6 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             }
         }
     }
-    if constexpr (WF == W_Q32) {
-        if (nfull < nst) q32_stage(stage_begin(nfull, SPREAD), std::integral_constant<int, 2>{}, -1);
-        // the copies issued during the last stages must land before the workgroup's LDS is released
-        if constexpr (SPREAD) __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
     }
 
     if constexpr (WF == W_Q4K) {

@@ -15,10 +15,11 @@ typedef __amdgpu_buffer_rsrc_t brsrc;
 // dword 3 of a raw (untyped, stride 0) buffer resource on gfx9: 32-bit data format, no swizzle
 #define BRSRC_DWORD3 0x00020000
 
-// Resource over [base, base + bytes): offsets at or past `bytes` read as zero (bytes is clamped to
-// the 32-bit num_records field). Callers rebase per workgroup tile so offsets stay below 4 GiB.
+// Resource over [base, base + bytes): offsets at or past `bytes` read as zero. bytes is clamped to
+// 2 GiB, so that an offset of 0xfffffff0 is always out of range; callers rebase per workgroup tile
+// so that real offsets stay below that.
 __device__ __forceinline__ brsrc make_brsrc(const void * base, int64_t bytes) {
-    const uint32_t n = bytes <= 0 ? 0u : bytes >= 0xffffffffLL ? 0xffffffffu : (uint32_t) bytes;
+    const uint32_t n = bytes <= 0 ? 0u : bytes >= 0x80000000LL ? 0x80000000u : (uint32_t) bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short) 0, (int) n, BRSRC_DWORD3);
 }
 
@@ -30,3 +31,4 @@ __device__ __forceinline__ void dma_to_lds(brsrc r, uint32_t voff, uint32_t soff
     if constexpr (SIZE == 4) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *) dst, 4, voff, soff, 0, 0);
     else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *) dst, 16, voff, soff, 0, 0);
 }
+
