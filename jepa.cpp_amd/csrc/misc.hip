@@ -200,11 +200,50 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
 
 // ------------------------------------------------------------------------------------------------
 // patchify (reference src/jepa.cpp:476-504): token order t, h, w; inner order c, tt, py, px.
-// One thread per (row, c, tt, py) copies P consecutive pixels.
+// One thread per 8 consecutive outputs of a patch row (P % 8 == 0): consecutive threads write
+// consecutive 16- or 32-byte pieces of the output, and read 32 contiguous bytes of one image row.
 // ------------------------------------------------------------------------------------------------
 template <bool HALF>
 __global__ void k_patchify(const float * __restrict__ in, void * __restrict__ rows, int64_t n_items, int C, int T, int H,
                            int W, int P, int tub, int video) {
+    const int GT = video ? T / tub : 1, GH = H / P, GW = W / P;
+    const int64_t Np = (int64_t) GT * GH * GW;
+    const int64_t K = (int64_t) C * tub * P * P;
+    const int per_row = P / 8;
+    const int64_t total = n_items * Np * C * tub * P * per_row;
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    int64_t r = id;
+    const int px0 = 8 * (int) (r % per_row); r /= per_row;
+    const int py = (int) (r % P); r /= P;
+    const int tt = (int) (r % tub); r /= tub;
+    const int c = (int) (r % C); r /= C;
+    const int64_t tok = r % Np; const int64_t item = r / Np;
+    const int t = (int) (tok / (GH * GW)), hh = (int) ((tok / GW) % GH), ww = (int) (tok % GW);
+    int64_t b, f;
+    if (video) { b = item; f = (int64_t) t * tub + tt; }
+    else { b = item / T; f = item % T; }
+    const float * src = in + (((b * C + c) * T + f) * H + (int64_t) hh * P + py) * W + (int64_t) ww * P + px0;
+    const int64_t off = (item * Np + tok) * K + ((int64_t) (c * tub + tt) * P + py) * P + px0;
+    // P % 8 == 0 (the launcher's choice) and W % P == 0 make src and the output 32-byte aligned
+    const float4 lo = *(const float4 *) src, hi = *(const float4 *) (src + 4);
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    if (HALF) {
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (_Float16) v[e];
+        *(h8 *) ((_Float16 *) rows + off) = o;
+    } else {
+        float * dst = (float *) rows + off;
+        *(float4 *) dst = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4 *) (dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// patch sizes that are not a multiple of 8 (e.g. 14): one thread per patch row of P pixels
+template <bool HALF>
+__global__ void k_patchify_rows(const float * __restrict__ in, void * __restrict__ rows, int64_t n_items, int C, int T,
+                                int H, int W, int P, int tub, int video) {
     const int GT = video ? T / tub : 1, GH = H / P, GW = W / P;
     const int64_t Np = (int64_t) GT * GH * GW;
     const int64_t K = (int64_t) C * tub * P * P;
@@ -411,9 +450,16 @@ void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w
 void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_items, int C, int T, int H, int W, int P,
                      int tub, bool video, hipStream_t s) {
     const int GT = video ? T / tub : 1;
-    const int64_t total = n_items * (int64_t) GT * (H / P) * (W / P) * C * tub * P;
-    if (half_out) k_patchify<true><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, video ? 1 : 0);
-    else k_patchify<false><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, video ? 1 : 0);
+    const int64_t total = n_items * (int64_t) GT * (H / P) * (W / P) * C * tub * P;   // patch rows
+    const int v = video ? 1 : 0;
+    if (P % 8 == 0) {
+        const int64_t n = total * (P / 8);
+        if (half_out) k_patchify<true><<<nblk(n, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, v);
+        else k_patchify<false><<<nblk(n, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, v);
+    } else {
+        if (half_out) k_patchify_rows<true><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, v);
+        else k_patchify_rows<false><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, v);
+    }
 }
 
 void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D, hipStream_t s) {
