@@ -23,6 +23,7 @@
 #include "kernels.h"
 #include "model.h"
 #include "lds_dma.h"
+#include "lanes.h"
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
             float mloc = S[0];
 #pragma unroll
             for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, S[r]);
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+            mloc = halves_max(mloc);
             if (mloc > m_run && (m_run == -INFINITY || (mloc - m_run) * c > LAZY)) {
                 // move the reference maximum; rescale what was accumulated against the old one
                 const float alpha = fast_exp2((m_run - mloc) * c);
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
             float p[16], lsum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) { p[r] = fast_exp2(fmaf(S[r], c, -mc)); lsum += p[r]; }
-            lsum += __shfl_xor(lsum, 32);
+            lsum = halves_sum(lsum);
             l_run += lsum;
 #pragma unroll
             for (int kk2 = 0; kk2 < 2; kk2++) {
@@ -198,8 +199,8 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
         float am0 = 0.0f, am1 = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; r++) { am0 = fmaxf(am0, fabsf(o0[r])); am1 = fmaxf(am1, fabsf(o1[r])); }
-        am0 = fmaxf(am0, __shfl_xor(am0, 32));
-        am1 = fmaxf(am1, __shfl_xor(am1, 32));
+        am0 = halves_max(am0);
+        am1 = halves_max(am1);
         if (q >= R) return;
         const float id0 = am0 != 0.0f ? 127.0f / am0 : 0.0f, id1 = am1 != 0.0f ? 127.0f / am1 : 0.0f;
         int8_t * crow = (int8_t *) O + (item * R + q) * DD + h * HD;

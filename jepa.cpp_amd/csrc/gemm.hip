@@ -26,6 +26,7 @@
 #include "kernels.h"
 #include "model.h"
 #include "lds_dma.h"
+#include "lanes.h"
 
 #include <hip/hip_fp16.h>
 
@@ -580,7 +581,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 float am = 0.0f;
 #pragma unroll
                 for (int r = 0; r < 16; r++) am = fmaxf(am, fabsf(v[r]));
-                am = fmaxf(am, __shfl_xor(am, 32));
+                am = halves_max(am);
                 const float d = am / 127.0f;
                 const float id = am != 0.0f ? 127.0f / am : 0.0f;
                 if (m < M) {
