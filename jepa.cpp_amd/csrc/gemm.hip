@@ -371,7 +371,6 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         // per stage every wave issues the PARTS copies of one stage, spread over the steps of a body
         // (step u issues copies [u PARTS / U, (u+1) PARTS / U))
         constexpr int P1 = T::PARTS;
-        auto items_before = [](int u) { return u * P1 / U; };
         // copies issued after the last copy of stage st+1 when stage st publishes it (step U-2, after
         // that step's copies): the NST-3 stages after it, and this body's copies so far
         constexpr int NBAR = (NST - 3) * P1 + (U - 1) * P1 / U;
@@ -395,32 +394,40 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[u & 1][r], C[u & 1][r], acc[i][j][r]);
         };
-        // prologue: stages 0..NST-2 in flight (unconditionally, so that every barrier count is exact:
-        // stages past the end copy the last stage again into buffers no stage uses), stage 0 landed,
-        // its scales and first two steps read, its first MFMAs issued
-        for (int s0 = 0; s0 < NST - 1; s0++)
+        // prologue: only stage 0 is copied before the first barrier (the waves would otherwise stall
+        // behind NST-1 stages of copies before any compute); stages 1..NST-1 follow spread over the
+        // steps of stage 0. Copies are unconditional, so that every barrier count is exact: stages
+        // past the end copy the last stage again into buffers no stage uses.
 #pragma unroll
-            for (int p = 0; p < T::PARTS; p++) issue_part(s0, p);
-        stage_barrier<(NST - 2) * P1>();
+        for (int p = 0; p < T::PARTS; p++) issue_part(0, p);
+        stage_barrier<0>();
         q32_scales(smem, SA, SB);
         ld_step(smem, 0);
         ld_step(smem, 1);
         mma(0, SA, SB);
         __builtin_amdgcn_sched_barrier(0);
-        // one full stage; CROSS: publish stage st+1 and start its pipeline in the last two steps
-        auto body = [&](int64_t st, auto cross_c) {
-            constexpr bool CROSS = decltype(cross_c)::value;
+        // one full stage; CROSS: publish stage st+1 and start its pipeline in the last two steps;
+        // FIRST (stage 0): issue the copies of stages 1..NST-1 instead of those of stage NST-1 alone
+        auto body = [&](int64_t st, auto cross_c, auto first_c) {
+            constexpr bool CROSS = decltype(cross_c)::value, FIRST = decltype(first_c)::value;
+            constexpr int Q = FIRST ? (NST - 1) * P1 : P1;          // copies this stage issues
+            // copies younger than the last one of stage st+1 at its publication (step U-2)
+            constexpr int NB = FIRST ? (U - 1) * Q / U - P1 : NBAR;
+            static_assert(NB >= 0 && NB < 64, "barrier count");
             const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
             const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
             h4 SAn[TI], SBn[4][TJ];
 #pragma unroll
             for (int u = 0; u < U; u++) {
 #pragma unroll
-                for (int k = items_before(u); k < items_before(u + 1); k++) issue_part(st + NST - 1, k);
+                for (int k = u * Q / U; k < (u + 1) * Q / U; k++) {
+                    if constexpr (FIRST) issue_part(1 + k / P1, k % P1);
+                    else issue_part(st + NST - 1, k);
+                }
                 if (u + 2 < U) ld_step(base, u + 2);
                 if constexpr (CROSS) {
                     if (u == U - 2) {
-                        stage_barrier<NBAR>();
+                        stage_barrier<NB>();
                         q32_scales(nbase, SAn, SBn);
                         ld_step(nbase, 0);
                     }
@@ -440,8 +447,11 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                     for (int j = 0; j < TJ; j++) SB[blk][j] = SBn[blk][j];
             }
         };
-        for (int64_t st = 0; st + 1 < nfull; st++) body(st, std::true_type{});
-        if (nfull > 0) body(nfull - 1, std::false_type{});
+        // stage 0 always publishes stage 1 (with a single full stage that is a copy of stage 0 into an
+        // unused buffer, read and discarded)
+        if (nfull > 0) body(0, std::true_type{}, std::true_type{});
+        for (int64_t st = 1; st + 1 < nfull; st++) body(st, std::true_type{}, std::false_type{});
+        if (nfull > 1) body(nfull - 1, std::false_type{}, std::false_type{});
         // final half stage (K % 128 == 64): blocks 0 and 1 of stage nfull, after all copies landed
         if (nfull < nst) {
             stage_barrier<0>();
@@ -459,11 +469,85 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
       }
     };
 
+    // ---- f16 ----
+    // A stage holds 64 K-columns (two 32-deep halves); steps u = (half, tile), tiles i-major, two f16
+    // MFMAs (32x32x16) per step, U = 2 TI TJ per stage. The same pipeline as q8_0 / q4_0: operand
+    // chunks two steps ahead, copies spread over the steps of the stage NST - 1 earlier (stage 0's
+    // alone before the first barrier), stage st+1 published two steps before the end of stage st.
+    [[maybe_unused]] auto f16_main = [&]() {
+      if constexpr (WF == W_F16) {
+        constexpr int TT = TI * TJ, U = 2 * TT;
+        static_assert(NST >= 3, "the in-stage barrier needs a stage in flight beyond the next one");
+        constexpr int P1 = T::PARTS;
+        constexpr int NBAR = (NST - 3) * P1 + (U - 1) * P1 / U;
+        h8 A0[2][TI], A1[2][TI], B0[2][TJ], B1[2][TJ];
+        auto ld_step = [&](const unsigned char * base, int u) {
+            const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
+            if (j == 0) {
+                const int r = 32 * (wn * TI + i) + l32;
+                A0[blk][i] = lds_chunk<h8>(base, r, 4 * blk + g);
+                A1[blk][i] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
+            }
+            if (i == 0) {
+                const int r = BN + 32 * (wm * TJ + j) + l32;
+                B0[blk][j] = lds_chunk<h8>(base, r, 4 * blk + g);
+                B1[blk][j] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
+            }
+        };
+        auto mma = [&](int u) {
+            const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
+            acc[i][j] = MFMA16(A0[blk][i], B0[blk][j], acc[i][j]);
+            acc[i][j] = MFMA16(A1[blk][i], B1[blk][j], acc[i][j]);
+        };
+#pragma unroll
+        for (int p = 0; p < P1; p++) issue_part(0, p);
+        stage_barrier<0>();
+        ld_step(smem, 0);
+        if (U > 1) ld_step(smem, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        auto body = [&](int64_t st, auto cross_c, auto first_c) {
+            constexpr bool CROSS = decltype(cross_c)::value, FIRST = decltype(first_c)::value;
+            constexpr int Q = FIRST ? (NST - 1) * P1 : P1;
+            constexpr int NB = FIRST ? (U - 1) * Q / U - P1 : NBAR;
+            static_assert(NB >= 0 && NB < 64, "barrier count");
+            const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
+            const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+#pragma unroll
+                for (int k = u * Q / U; k < (u + 1) * Q / U; k++) {
+                    if constexpr (FIRST) issue_part(1 + k / P1, k % P1);
+                    else issue_part(st + NST - 1, k);
+                }
+                // the MFMAs of this step come first: with one tile per wave the next stage's first
+                // operands go to the registers this step reads
+                mma(u);
+                if (u + 2 < U) ld_step(base, u + 2);
+                if constexpr (CROSS) {
+                    if (u == U - 2) {
+                        stage_barrier<NB>();
+                        ld_step(nbase, 0);
+                    }
+                    if (u == U - 1) ld_step(nbase, 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        if (nst > 0) body(0, std::true_type{}, std::true_type{});
+        for (int64_t st = 1; st + 1 < nst; st++) body(st, std::true_type{}, std::false_type{});
+        if (nst > 1) body(nst - 1, std::false_type{}, std::false_type{});
+        // the copies issued during the last stages must land before the workgroup's LDS is released
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+      }
+    };
+
     // q8_0 / q4_0 with K % 128 == 64 end in a half stage, peeled off the loop so that the loop body
     // has one path (the accumulators then stay in place across iterations)
     const int64_t nfull = WF == W_Q32 ? K / KC : nst;
     if constexpr (WF == W_Q32) {
         q32_main(nfull);
+    } else if constexpr (WF == W_F16) {
+        f16_main();
     } else {
     for (int s = 0; s < NST - 1; s++)
         if (s < nst) issue(s);
