@@ -174,8 +174,9 @@ struct tiling {
     static constexpr int X_DW = 0, X_MIN = BN * 4, X_DA = X_MIN + BN * 32, X_BS = X_DA + BM * 4;
     static constexpr int XSB = WF == W_Q4K ? X_BS + BM * 32 : 0;
     // q4_K: the super-block buffer of sb+1 is filled while stage 4 sb + 5 - NST is computed, which must
-    // come after the epilogue of sb-1 (end of stage 4 sb - 1): NST <= 5
-    static constexpr int NST_MAX = WF == W_Q4K ? 5 : 6;
+    // come after the epilogue of sb-1 (end of stage 4 sb - 1) has been passed by every wave: NST <= 4
+    // in the pipelined loop, whose barrier sits inside a stage
+    static constexpr int NST_MAX = WF == W_Q4K ? 4 : 6;
     static constexpr int NST_FIT = (160 * 1024 - 2 * XSB) / STAGE;
     static constexpr int NST = NST_FIT < NST_MAX ? NST_FIT : NST_MAX;
     static constexpr int LDS = NST * STAGE + 2 * XSB;
@@ -287,7 +288,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         if (p < T::LOADS) issue_tile(st, sa, p);
         else issue_scales(st, sa, p - T::LOADS);
     };
-    auto issue = [&](int64_t st) {
+    // q4_K super-block data of super-block st / 4, copied with stage st when st % 4 == 0
+    auto issue_xsb = [&](int64_t st) {
         if constexpr (WF == W_Q4K) {
             if ((st & 3) == 0) {
                 const uint32_t sb = (uint32_t) (st >> 2);
@@ -312,10 +314,10 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 }
             }
         }
-        if constexpr (WF == W_Q32) {
-#pragma unroll
-            for (int p = 0; p < T::SL; p++) issue_scales(st, st, p);
-        }
+    };
+    // all copies of stage st (the prologue of the q4_K fallback loop)
+    auto issue = [&](int64_t st) {
+        issue_xsb(st);
 #pragma unroll
         for (int i = 0; i < T::LOADS; i++) issue_tile(st, st, i);
     };
@@ -469,13 +471,59 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
       }
     };
 
-    // ---- f16 ----
+    // q4_K super-block epilogue after stage st (st % 4 == 3)
+    [[maybe_unused]] auto q4k_epilogue = [&](int64_t st) {
+        // super-block epilogue (ggml's x86 vec_dot_q4_K_q8_K): acc += (dw*da) S and, in a second
+        // accumulator, accm += (dmin*da) sum_j m_j bsum_j; the result is acc - accm
+        const unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 2) & 1) * T::XSB;
+        h8 bs[TJ];
+        float da[TJ];
+#pragma unroll
+        for (int j = 0; j < TJ; j++) {
+            const int rm = 32 * (wm * TJ + j) + l32;
+            bs[j] = *(const h8 *) (xb + T::X_BS + rm * 32 + 16 * g);
+            da[j] = *(const float *) (xb + T::X_DA + 4 * rm);
+        }
+#pragma unroll
+        for (int i = 0; i < TI; i++) {
+            const int rn = 32 * (wn * TI + i);
+            const h8 am = *(const h8 *) (xb + T::X_MIN + (rn + l32) * 32 + 16 * g);
+            float dw[16], dm[16];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint4 v = *(const uint4 *) (xb + T::X_DW + 4 * (rn + 8 * q + 4 * g));
+                const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) { dw[4 * q + e] = h2f((uint16_t) (vv[e] & 0xffffu)); dm[4 * q + e] = h2f((uint16_t) (vv[e] >> 16)); }
+            }
+#pragma unroll
+            for (int j = 0; j < TJ; j++) {
+                const f16v ms = MFMA16(am, bs[j], zero);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float d1 = __fmul_rn(dw[r], da[j]), d2 = __fmul_rn(dm[r], da[j]);
+                    acc[i][j][r] = fmaf(d1, ssb[i][j][r], acc[i][j][r]);
+                    accm[i][j][r] = fmaf(d2, ms[r], accm[i][j][r]);
+                }
+                ssb[i][j] = zero;
+            }
+        }
+    };
+
+    // ---- f16 and q4_K ----
     // A stage holds 64 K-columns (two 32-deep halves); steps u = (half, tile), tiles i-major, two f16
     // MFMAs (32x32x16) per step, U = 2 TI TJ per stage. The same pipeline as q8_0 / q4_0: operand
     // chunks two steps ahead, copies spread over the steps of the stage NST - 1 earlier (stage 0's
     // alone before the first barrier), stage st+1 published two steps before the end of stage st.
+    // q4_K accumulates the super-block sums in ssb and runs its epilogue after every fourth stage.
+    // Its super-block data (one copy set per 4 stages, not the same count on every wave) is left out
+    // of the barrier counts, which only makes the waits longer; it is issued with the first copies of
+    // stage 4 sb, so it has landed when that stage is published. Its double buffer for sb + 1 is
+    // refilled from stage 4 sb + 5 - NST >= 4 sb + 1 (NST <= 4), whose copies follow the barrier
+    // that every wave reaches only after the epilogue of sb - 1.
+    constexpr bool PIPE16 = WF == W_F16 || (WF == W_Q4K && NST >= 3 && NST <= 4);
     [[maybe_unused]] auto f16_main = [&]() {
-      if constexpr (WF == W_F16) {
+      if constexpr (PIPE16) {
         constexpr int TT = TI * TJ, U = 2 * TT;
         static_assert(NST >= 3, "the in-stage barrier needs a stage in flight beyond the next one");
         constexpr int P1 = T::PARTS;
@@ -496,9 +544,11 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         };
         auto mma = [&](int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            acc[i][j] = MFMA16(A0[blk][i], B0[blk][j], acc[i][j]);
-            acc[i][j] = MFMA16(A1[blk][i], B1[blk][j], acc[i][j]);
+            f16v & d = WF == W_Q4K ? ssb[i][j] : acc[i][j];
+            d = MFMA16(A0[blk][i], B0[blk][j], d);
+            d = MFMA16(A1[blk][i], B1[blk][j], d);
         };
+        issue_xsb(0);
 #pragma unroll
         for (int p = 0; p < P1; p++) issue_part(0, p);
         stage_barrier<0>();
@@ -514,6 +564,9 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
 #pragma unroll
             for (int u = 0; u < U; u++) {
+                if constexpr (WF == W_Q4K && !FIRST) {
+                    if (u == 0) issue_xsb(st + NST - 1);   // copies only when (st + NST - 1) % 4 == 0
+                }
 #pragma unroll
                 for (int k = u * Q / U; k < (u + 1) * Q / U; k++) {
                     if constexpr (FIRST) issue_part(1 + k / P1, k % P1);
@@ -532,6 +585,9 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            if constexpr (WF == W_Q4K) {
+                if ((st & 3) == 3) q4k_epilogue(st);
+            }
         };
         if (nst > 0) body(0, std::true_type{}, std::true_type{});
         for (int64_t st = 1; st + 1 < nst; st++) body(st, std::true_type{}, std::false_type{});
@@ -546,7 +602,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const int64_t nfull = WF == W_Q32 ? K / KC : nst;
     if constexpr (WF == W_Q32) {
         q32_main(nfull);
-    } else if constexpr (WF == W_F16) {
+    } else if constexpr (PIPE16) {
         f16_main();
     } else {
     for (int s = 0; s < NST - 1; s++)
@@ -593,43 +649,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             }
         }
         if constexpr (WF == W_Q4K) {
-            if ((st & 3) == 3) {
-                // super-block epilogue (ggml's x86 vec_dot_q4_K_q8_K): acc += (dw*da) S and, in a second
-                // accumulator, accm += (dmin*da) sum_j m_j bsum_j; the result is acc - accm
-                const unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 2) & 1) * T::XSB;
-                h8 bs[TJ];
-                float da[TJ];
-#pragma unroll
-                for (int j = 0; j < TJ; j++) {
-                    const int rm = 32 * (wm * TJ + j) + l32;
-                    bs[j] = *(const h8 *) (xb + T::X_BS + rm * 32 + 16 * g);
-                    da[j] = *(const float *) (xb + T::X_DA + 4 * rm);
-                }
-#pragma unroll
-                for (int i = 0; i < TI; i++) {
-                    const int rn = 32 * (wn * TI + i);
-                    const h8 am = *(const h8 *) (xb + T::X_MIN + (rn + l32) * 32 + 16 * g);
-                    float dw[16], dm[16];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const uint4 v = *(const uint4 *) (xb + T::X_DW + 4 * (rn + 8 * q + 4 * g));
-                        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                        for (int e = 0; e < 4; e++) { dw[4 * q + e] = h2f((uint16_t) (vv[e] & 0xffffu)); dm[4 * q + e] = h2f((uint16_t) (vv[e] >> 16)); }
-                    }
-#pragma unroll
-                    for (int j = 0; j < TJ; j++) {
-                        const f16v ms = MFMA16(am, bs[j], zero);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            const float d1 = __fmul_rn(dw[r], da[j]), d2 = __fmul_rn(dm[r], da[j]);
-                            acc[i][j][r] = fmaf(d1, ssb[i][j][r], acc[i][j][r]);
-                            accm[i][j][r] = fmaf(d2, ms[r], accm[i][j][r]);
-                        }
-                        ssb[i][j] = zero;
-                    }
-                }
-            }
+            if ((st & 3) == 3) q4k_epilogue(st);
         }
     }
     }
