@@ -59,6 +59,14 @@ int jepa_amd_rownorm(int device, const float * x_dev, int64_t n_rows, int64_t n_
 int jepa_amd_matmul(int device, int wtype, const void * w_dev, int64_t n_out, int64_t n_in, const float * bias_dev,
                     const float * x_dev, int64_t n_rows, float * y_dev, int reps, double * gemm_ms);
 
+/* The MLP's first linear with its fused epilogue: out = gelu_erf(X W^T + bias) (reference
+ * src/jepa.cpp:365-385), written the way the encoder hands it to the second linear. out_type 0 (f32):
+ * out_dev f32 [n_rows][n_out]; 1 (f16): f16 values; 8 (q8_0) / 15 (q8_K): ggml blocks of the quantized
+ * rows (q8_K needs n_out % 256 == 0). W, X, bias as for jepa_amd_matmul. reps > 1 repeats the GEMM
+ * (same result); *gemm_ms (optional) receives the mean device time of one repeat. */
+int jepa_amd_matmul_gelu(int device, int wtype, const void * w_dev, int64_t n_out, int64_t n_in, const float * bias_dev,
+                         const float * x_dev, int64_t n_rows, int out_type, void * out_dev, int reps, double * gemm_ms);
+
 /* Attention of one block from its fused qkv rows: qkv_dev f32 [n_items*n_tok][3*n_head*64] (rows
  * [q | k | v], head-major), optional RoPE tables rope_c/rope_s [n_tok][64] (signed sine). Runs the QKV
  * epilogue's split/RoPE/f16 cast and the attention kernel. out_type 0 (f32): out_dev f32

@@ -143,37 +143,48 @@ extern "C" int jepa_amd_rownorm(int device, const float * x, int64_t n_rows, int
     return d.finish();
 }
 
-extern "C" int jepa_amd_matmul(int device, int wtype, const void * w, int64_t n_out, int64_t n_in, const float * bias, const float * x,
-                               int64_t n_rows, float * y, int reps, double * gemm_ms) {
-    if (!w || !x || !y || n_out <= 0 || n_in <= 0 || n_rows <= 0) return -1;
-    dev_linear L;
+namespace {
+
+// a dev_linear over ggml weight blocks in device memory (repacked into the GEMM's operand layout)
+bool make_linear(dev_scope & d, const char * who, int wtype, const void * w, int64_t n_out, int64_t n_in, const float * bias,
+                 dev_linear & L) {
     L.gtype = wtype; L.n_out = n_out; L.n_in = n_in; L.bias = (float *) bias;
     switch (wtype) {
         case T_F32: L.fmt = W_F32; break;
         case T_F16: L.fmt = W_F16; break;
         case T_Q8_0: case T_Q4_0: L.fmt = W_Q32; break;
         case T_Q4_K: L.fmt = W_Q4K; break;
-        default: jepa_log("jepa: jepa_amd_matmul: weight type %d not supported\n", wtype); return -1;
+        default: jepa_log("jepa: %s: weight type %d not supported\n", who, wtype); return false;
     }
-    if (L.fmt != W_F32 && (n_out % 128 || n_in % 64 || (L.fmt == W_Q4K && n_in % 256))) {
-        jepa_log("jepa: jepa_amd_matmul: [%lld x %lld] not supported by the MFMA GEMM (n_out %% 128, n_in %% 64)\n", (long long) n_out, (long long) n_in);
-        return -1;
+    if (L.fmt != W_F32 && (n_out % 128 || n_in % 64 || (L.fmt == W_Q4K && n_in % 256) || n_in > 2048 * 8)) {
+        jepa_log("jepa: %s: [%lld x %lld] not supported by the MFMA GEMM (n_out %% 128, n_in %% 64)\n", who, (long long) n_out,
+                 (long long) n_in);
+        return false;
     }
-    if (L.fmt != W_F32 && n_in > 2048 * 8) return -1;
-    dev_scope d(device);
-    if (!d.ok) return -1;
     if (L.fmt == W_F32 || L.fmt == W_F16) {
         L.w = (void *) w;
-    } else {
-        L.w = d.alloc((size_t) n_out * n_in * (L.fmt == W_Q32 ? 1 : 2));
-        if (L.fmt == W_Q32) L.wd = d.alloc((size_t) n_out * (n_in / 32) * 2);
-        else {
-            L.wd = d.alloc((size_t) n_out * (n_in / 256) * 4);
-            L.wmin = d.alloc((size_t) n_out * (n_in / 256) * 32);
-        }
-        if (!L.w || !L.wd) return -1;
-        launch_repack(wtype, w, n_out, n_in, L.w, L.wd, L.wmin, d.s);
+        return true;
     }
+    L.w = d.alloc((size_t) n_out * n_in * (L.fmt == W_Q32 ? 1 : 2));
+    if (L.fmt == W_Q32) L.wd = d.alloc((size_t) n_out * (n_in / 32) * 2);
+    else {
+        L.wd = d.alloc((size_t) n_out * (n_in / 256) * 4);
+        L.wmin = d.alloc((size_t) n_out * (n_in / 256) * 32);
+    }
+    if (!L.w || !L.wd || (L.fmt == W_Q4K && !L.wmin)) return false;
+    launch_repack(wtype, w, n_out, n_in, L.w, L.wd, L.wmin, d.s);
+    return true;
+}
+
+}  // namespace
+
+extern "C" int jepa_amd_matmul(int device, int wtype, const void * w, int64_t n_out, int64_t n_in, const float * bias, const float * x,
+                               int64_t n_rows, float * y, int reps, double * gemm_ms) {
+    if (!w || !x || !y || n_out <= 0 || n_in <= 0 || n_rows <= 0) return -1;
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    dev_linear L;
+    if (!make_linear(d, "jepa_amd_matmul", wtype, w, n_out, n_in, bias, L)) return -1;
     act_view a;
     if (!alloc_act(d, a, L.act(), n_rows, n_in)) return -1;
     launch_rownorm_quant(x, n_rows, n_in, nullptr, nullptr, 0.0f, false, a, d.s);
@@ -191,6 +202,52 @@ extern "C" int jepa_amd_matmul(int device, int wtype, const void * w, int64_t n_
     float ms = 0;
     hipEventElapsedTime(&ms, e0, e1);
     if (gemm_ms) *gemm_ms = ms / reps;
+    hipEventDestroy(e0); hipEventDestroy(e1);
+    return rc;
+}
+
+extern "C" int jepa_amd_matmul_gelu(int device, int wtype, const void * w, int64_t n_out, int64_t n_in, const float * bias,
+                                    const float * x, int64_t n_rows, int out_type, void * out, int reps, double * gemm_ms) {
+    if (!w || !x || !out || n_out <= 0 || n_in <= 0 || n_rows <= 0) return -1;
+    if (!(out_type == T_F32 || out_type == T_F16 || out_type == T_Q8_0 || out_type == T_Q8_K) ||
+        (out_type == T_Q8_K && n_out % 256) || (out_type == T_F16 && wtype == T_F32)) {
+        jepa_log("jepa: jepa_amd_matmul_gelu: output type %d not supported for weight type %d, n_out %lld\n", out_type, wtype,
+                 (long long) n_out);
+        return -1;
+    }
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    dev_linear L;
+    if (!make_linear(d, "jepa_amd_matmul_gelu", wtype, w, n_out, n_in, bias, L)) return -1;
+    if (L.fmt == W_F32 && out_type != T_F32) {
+        jepa_log("jepa: jepa_amd_matmul_gelu: f32 weights have the f32 epilogue only\n");
+        return -1;
+    }
+    act_view a;
+    if (!alloc_act(d, a, L.act(), n_rows, n_in)) return -1;
+    launch_rownorm_quant(x, n_rows, n_in, nullptr, nullptr, 0.0f, false, a, d.s);
+    gemm_epi ep;
+    ep.ldy = n_out;
+    act_view o;
+    if (out_type == T_F32) { ep.kind = EPI_GELU_F32; ep.y = (float *) out; }
+    else if (out_type == T_F16) { ep.kind = EPI_GELU_F16; ep.oh = out; }
+    else {
+        if (!alloc_act(d, o, out_type == T_Q8_0 ? A_Q8_0 : A_Q8_K, n_rows, n_out)) return -1;
+        if (out_type == T_Q8_0) { ep.kind = EPI_GELU_Q8_0; ep.oq = o.q; ep.od = o.d; }
+        else { ep.kind = EPI_GELU_Q8_K; ep.oh = o.q; ep.od = o.d; ep.ob = o.bsum; }
+    }
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0); hipEventCreate(&e1);
+    if (reps < 1) reps = 1;
+    launch_gemm(L, a, n_rows, ep, d.s);   // warm-up (and the result when reps == 1)
+    hipEventRecord(e0, d.s);
+    for (int i = 1; i < reps; i++) launch_gemm(L, a, n_rows, ep, d.s);
+    hipEventRecord(e1, d.s);
+    if (out_type == T_Q8_0 || out_type == T_Q8_K) launch_pack_act_blocks(o, n_rows, n_out, out, d.s);
+    const int rc = d.finish();
+    float ms = 0;
+    hipEventElapsedTime(&ms, e0, e1);
+    if (gemm_ms) *gemm_ms = reps > 1 ? ms / (reps - 1) : 0.0;
     hipEventDestroy(e0); hipEventDestroy(e1);
     return rc;
 }

@@ -294,7 +294,7 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
             act_view o;
             o.fmt = A_F32; o.q = w.attn; o.ld = D;
             kt.run("attention", [&] { launch_attention(w.Q, w.Kt, w.Vt, o, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), s); });
-            kt.run("quantize", [&] { launch_rownorm_quant(w.attn, rows, D, nullptr, nullptr, 0.0f, false, w.actA, s); });
+            kt.run("quantize", [&] { launch_rownorm_quant(w.attn, rows, D, nullptr, nullptr, 0.0f, false, w.actA, s); }, "attn");
         }
         {
             gemm_epi ep;
@@ -310,11 +310,14 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
             ep.ldy = F;
             const bool mfma = L.up.fmt != W_F32;
             if (mfma && w.actB.fmt == A_Q8_0) { ep.kind = EPI_GELU_Q8_0; ep.oq = w.actB.q; ep.od = w.actB.d; }
+            else if (mfma && w.actB.fmt == A_Q8_K && F % 256 == 0) {
+                ep.kind = EPI_GELU_Q8_K; ep.oh = w.actB.q; ep.od = w.actB.d; ep.ob = w.actB.bsum;
+            }
             else if (mfma && w.actB.fmt == A_F16) { ep.kind = EPI_GELU_F16; ep.oh = w.actB.q; }
             else { ep.kind = EPI_GELU_F32; ep.y = w.ff; }
             kt.run(gemm_class(L.up), [&] { launch_gemm(L.up, w.actA, rows, ep, s); }, "up");
             if (ep.kind == EPI_GELU_F32)
-                kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, w.actB, s); });
+                kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, w.actB, s); }, "ff");
         }
         {
             gemm_epi ep;

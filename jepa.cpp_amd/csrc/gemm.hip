@@ -62,10 +62,39 @@ struct kargs {
 __device__ __forceinline__ float h2f(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2hbits(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
 
+// erf(z) for z >= 0 without a divergent branch: both pieces are evaluated and one is selected.
+//   z <  0.875: z * P(z^2), P of degree 5
+//   z >= 0.875: 1 - 2^Q(min(z, 4)), Q of degree 6 ~ log2(erfc(z)); erfc(4) = 1.5e-8 gives exactly 1.0f
+// Coefficients from fit_gelu_erf.py (least squares toward equal ripple); the float32 evaluation stays
+// within 1.5 * 2^-24 of erf, about the accuracy of a library erff, at some 24 VALU ops per value
+// instead of the ~35 (plus branch masks) of erff's two-branch form.
+__device__ __forceinline__ float erf_nonneg(float z) {
+    const float s = __fmul_rn(z, z);
+    float p = -6.065624184e-04f;
+    p = fmaf(p, s, 5.004569888e-03f);
+    p = fmaf(p, s, -2.677160688e-02f);
+    p = fmaf(p, s, 1.128184572e-01f);
+    p = fmaf(p, s, -3.761247694e-01f);
+    p = fmaf(p, s, 1.128379107e+00f);
+    const float small = __fmul_rn(z, p);
+    const float zc = fminf(z, 4.0f);
+    float q = 3.032335662e-04f;
+    q = fmaf(q, zc, -4.579299595e-03f);
+    q = fmaf(q, zc, 3.277245909e-02f);
+    q = fmaf(q, zc, -1.513156891e-01f);
+    q = fmaf(q, zc, -9.177885652e-01f);
+    q = fmaf(q, zc, -1.627714038e+00f);
+    q = fmaf(q, zc, -9.482709720e-05f);
+    const float large = __fsub_rn(1.0f, __builtin_amdgcn_exp2f(q));
+    return z < 0.875f ? small : large;
+}
+
 __device__ __forceinline__ float gelu_erf(float x) {
-    // 0.5*x*(1 + erf(x/sqrt(2))) - ggml_vec_gelu_erf_f32 (reference docs/ggml-notes.md:291-292)
+    // 0.5*x*(1 + erf(x/sqrt(2))) - ggml_vec_gelu_erf_f32 (reference docs/ggml-notes.md:291-292);
+    // erf is odd and |x| * c rounds like x * c, so erf(x c) = sign(x) erf_nonneg(|x| c)
     const float SQRT_2_INV = 0.70710678118654752440084436210484f;
-    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, erff(__fmul_rn(x, SQRT_2_INV))));
+    const float e = copysignf(erf_nonneg(__fmul_rn(fabsf(x), SQRT_2_INV)), x);
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
 }
 
 __device__ __forceinline__ int perm16(int64_t tok) {
@@ -663,6 +692,96 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 for (int r = 0; r < 16; r++) acc[i][j][r] = __fsub_rn(acc[i][j][r], accm[i][j][r]);
     }
 
+    if constexpr (EPI == EPI_GELU_Q8_K) {
+        // q8_K activation of the next linear (quantize_row_q8_K_ref): per token and 256 features,
+        // max = the first value of largest |x|, iscale = -127/max, q = min(127, rne(iscale*x)),
+        // d = 1/iscale, bsums of 16. A workgroup row of WN waves covers one 256-block: each wave
+        // reduces its 64 features (lane pair l, l^32), then the WN partial results of every token
+        // meet in LDS. A wave's first element of its own largest magnitude is the block's first one
+        // of that magnitude whenever the wave holds the block maximum, so one exchange of
+        // (max, key = 2*index + sign) per wave suffices.
+        static_assert(BN == 256, "one q8_K block per workgroup row of waves");
+        float * xmax = (float *) smem;                                        // [TJ][WM*32][WN]
+        uint32_t * xkey = (uint32_t *) (smem + TJ * WM * 32 * WN * 4);
+        // no HBM->LDS copy of this wave is still in flight (the pipelines' tail copies land in stage
+        // buffers), and every wave is past its last read of the stage buffers
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TJ; j++) {
+            const int64_t m = m0 + 32 * (wm * TJ + j) + l32;
+            float v[TI][16];
+            float am = 0.0f;
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int64_t n = n0 + 32 * (wn * TI + i) + 8 * q + 4 * g;
+                    const float4 b = a.bias ? *(const float4 *) (a.bias + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    const float bb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        v[i][4 * q + e] = gelu_erf(__fadd_rn(acc[i][j][4 * q + e], bb[e]));
+                        am = fmaxf(am, fabsf(v[i][4 * q + e]));
+                    }
+                }
+            am = halves_max(am);
+            uint32_t key = 0xffffffffu;
+#pragma unroll
+            for (int i = TI - 1; i >= 0; i--)
+#pragma unroll
+                for (int r = 15; r >= 0; r--)
+                    if (fabsf(v[i][r]) == am)
+                        key = 2u * (uint32_t) (64 * wn + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3)) + (__float_as_uint(v[i][r]) >> 31);
+            key = halves_min_u32(key);
+            const int slot = ((j * WM + wm) * 32 + l32) * WN;
+            if (g == 0) { xmax[slot + wn] = am; xkey[slot + wn] = key; }
+            __syncthreads();
+            float bmax = xmax[slot];
+            uint32_t bkey = xkey[slot];
+#pragma unroll
+            for (int w = 1; w < WN; w++) {
+                const float a2 = xmax[slot + w];
+                const uint32_t k2 = xkey[slot + w];
+                if (a2 > bmax) { bmax = a2; bkey = k2; }
+                else if (a2 == bmax) bkey = min(bkey, k2);
+            }
+            const float mx = (bkey & 1u) ? -bmax : bmax;
+            const float iscale = bmax != 0.0f ? -127.0f / mx : 0.0f;
+            float bs[TI][2];
+#pragma unroll
+            for (int i = 0; i < TI; i++) {
+                bs[i][0] = bs[i][1] = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    v[i][r] = fminf(rintf(iscale * v[i][r]), 127.0f);
+                    bs[i][r >> 3] += v[i][r];
+                }
+                bs[i][0] = halves_sum(bs[i][0]);   // features 16h..16h+15 of the tile: q = 2h, 2h+1 of both lane groups
+                bs[i][1] = halves_sum(bs[i][1]);
+            }
+            if (m < M) {
+#pragma unroll
+                for (int i = 0; i < TI; i++) {
+                    const int64_t nb = n0 + 32 * (wn * TI + i);
+                    _Float16 * o = (_Float16 *) a.ep.oh + m * a.N + nb + 4 * g;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const h4 hv = {(_Float16) v[i][4 * q], (_Float16) v[i][4 * q + 1], (_Float16) v[i][4 * q + 2], (_Float16) v[i][4 * q + 3]};
+                        *(h4 *) (o + 8 * q) = hv;
+                    }
+                    if (g == 0) {
+                        _Float16 * ob = (_Float16 *) a.ep.ob + m * (a.N / 16) + nb / 16;
+                        ob[0] = (_Float16) bs[i][0];
+                        ob[1] = (_Float16) bs[i][1];
+                    }
+                }
+                if (wn == 0 && g == 0) ((float *) a.ep.od)[m * (a.N / 256) + n0 / 256] = bmax != 0.0f ? 1.0f / iscale : 0.0f;
+            }
+        }
+        return;
+    }
+
     // epilogue: lane holds token m and features nb + 8q + 4g + e of each tile
 #pragma unroll
     for (int i = 0; i < TI; i++) {
@@ -810,10 +929,11 @@ __global__ void k_qkv_split(kargs a, const float * __restrict__ qkv) {
 }
 
 struct tile_cfg { int wn, wm, ti, tj; };
-// eight-wave workgroup tiles (BN x BM): 256x128, 192x128, 128x128 (two wave shapes), 64x128, 128x64
-constexpr tile_cfg k_tiles[] = {{4, 2, 2, 2}, {2, 4, 3, 1}, {2, 4, 2, 1}, {4, 2, 1, 2}, {2, 4, 1, 1}, {4, 2, 1, 1}};
+// eight-wave workgroup tiles (BN x BM): 256x128, 192x128, 128x128 (two wave shapes), 64x128, 128x64,
+// 256x64
+constexpr tile_cfg k_tiles[] = {{4, 2, 2, 2}, {2, 4, 3, 1}, {2, 4, 2, 1}, {4, 2, 1, 2}, {2, 4, 1, 1}, {4, 2, 1, 1}, {4, 2, 2, 1}};
 // relative efficiency of one workgroup tile (larger tiles re-read less from L2 and LDS)
-constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66};
+constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66, 0.8};
 
 std::atomic<int> g_force_tile{-1};
 
@@ -832,16 +952,17 @@ int cu_count() {
 // The tile with the least estimated time: whole waves of workgroups over the CUs (one workgroup per
 // CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N; q4_K
 // skips the 256x128 tile (its three accumulator sets do not fit 256 VGPRs with two waves per SIMD).
-int pick_tile(int wf, int64_t N, int64_t M) {
+int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0) {
     const int f = g_force_tile.load();
     const int nt = (int) (sizeof(k_tiles) / sizeof(k_tiles[0]));
-    if (f >= 0 && f < nt && N % (32 * k_tiles[f].wn * k_tiles[f].ti) == 0) return f;
+    const auto bn_of = [](int c) { return 32 * k_tiles[c].wn * k_tiles[c].ti; };
+    if (f >= 0 && f < nt && N % bn_of(f) == 0 && (need_bn == 0 || (bn_of(f) == need_bn && !(wf == W_Q4K && f == 0)))) return f;
     const int cus = cu_count();
     double best = 1e300;
-    int b = nt - 1;
+    int b = need_bn ? -1 : 5;
     for (int c = 0; c < nt; c++) {
         const int64_t bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
-        if (N % bn) continue;
+        if (N % bn || (need_bn && bn != need_bn)) continue;
         if (wf == W_Q4K && c == 0) continue;
         const int64_t t = (N / bn) * ((M + bm - 1) / bm);
         const double waves = (double) ((t + cus - 1) / cus);
@@ -854,19 +975,30 @@ int pick_tile(int wf, int64_t N, int64_t M) {
 template <int WF, int EPI>
 void launch_tiles(int c, const kargs & a, hipStream_t s) {
     const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm);
-    switch (c) {
-        case 0: k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a); break;
-        case 1: k_gemm_mfma<WF, EPI, 2, 4, 3, 1><<<grid, 512, 0, s>>>(a); break;
-        case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(a); break;
-        case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(a); break;
-        case 4: k_gemm_mfma<WF, EPI, 2, 4, 1, 1><<<grid, 512, 0, s>>>(a); break;
-        default: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(a); break;
+    if constexpr (EPI == EPI_GELU_Q8_K) {   // 256-wide tiles only (pick_tile keeps to them)
+        if (c == 6) k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a);
+        if constexpr (WF != W_Q4K)   // q4_K never takes the 256x128 tile
+            if (c == 0) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a);
+    } else {
+        switch (c) {
+            case 0: k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a); break;
+            case 1: k_gemm_mfma<WF, EPI, 2, 4, 3, 1><<<grid, 512, 0, s>>>(a); break;
+            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(a); break;
+            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(a); break;
+            case 4: k_gemm_mfma<WF, EPI, 2, 4, 1, 1><<<grid, 512, 0, s>>>(a); break;
+            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(a); break;
+            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a); break;
+        }
     }
 }
 
 template <int WF>
 void dispatch_mfma(kargs a, hipStream_t s) {
-    const int c = pick_tile(WF, a.N, a.M);
+    const int c = pick_tile(WF, a.N, a.M, a.ep.kind == EPI_GELU_Q8_K ? 256 : 0);
+    if (c < 0) {
+        jepa_log("jepa: internal error: no 256-wide GEMM tile for the q8_K epilogue (N = %lld)\n", (long long) a.N);
+        return;
+    }
     const int bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
     a.tn = (int) (a.N / bn);
     a.tm = (int) ((a.M + bm - 1) / bm);
@@ -889,6 +1021,7 @@ void dispatch_mfma(kargs a, hipStream_t s) {
         case EPI_GELU_F16:  launch_tiles<WF, EPI_GELU_F16>(c, a, s); break;
         case EPI_GELU_Q8_0: launch_tiles<WF, EPI_GELU_Q8_0>(c, a, s); break;
         case EPI_QKV:       launch_tiles<WF, EPI_QKV>(c, a, s); break;
+        case EPI_GELU_Q8_K: launch_tiles<WF, EPI_GELU_Q8_K>(c, a, s); break;
     }
 }
 

@@ -26,6 +26,7 @@ enum epi_kind {
     EPI_GELU_F16,     // oh[m][n] = f16(gelu(acc + bias))
     EPI_GELU_Q8_0,    // q8_0-quantize gelu(acc + bias) into (oq, od)
     EPI_QKV,          // split into Q, K (RoPE'd) and V^T f16 attention operands
+    EPI_GELU_Q8_K,    // q8_K-quantize gelu(acc + bias) into (oh codes, od d, ob bsums); 256-wide tiles
 };
 
 struct gemm_epi {
@@ -35,7 +36,7 @@ struct gemm_epi {
     const float * addvec = nullptr;
     const float * addrows = nullptr;
     const float * ls = nullptr;
-    void * oq = nullptr; void * od = nullptr; void * oh = nullptr;
+    void * oq = nullptr; void * od = nullptr; void * oh = nullptr; void * ob = nullptr;
     // EPI_QKV
     void * q = nullptr; void * k = nullptr; void * vt = nullptr;
     const float * rope_c = nullptr; const float * rope_s = nullptr;

@@ -23,7 +23,7 @@ __device__ __forceinline__ float h2f(uint16_t b) { return (float) __builtin_bit_
 //   A_Q8_K: max = first largest-|x| value, iscale = -127/max, q = min(127, rne(iscale*x)),
 //           d = 1/iscale (f32), bsums of 16                  quantize_row_q8_K_ref
 // ------------------------------------------------------------------------------------------------
-constexpr int MAXOCT = 4;   // D <= 2048
+constexpr int MAXOCT = 4;   // D <= 2048 (octets per lane: 1, 2 or 4, by row length)
 
 // Cross-lane moves through DPP (VALU, a few cycles) instead of ds_bpermute shuffles (an LDS round
 // trip each). update_dpp(0, v, ...) gives 0 in lanes of rows the row mask leaves out.
@@ -55,7 +55,37 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return __builtin_bit_cast(double, make_int2(__builtin_amdgcn_readlane(p.x, 63), __builtin_amdgcn_readlane(p.y, 63)));
 }
 
-template <int OUT, bool NORM>
+// v_permlane16_swap: lanes of 16-lane rows 2r and 2r+1 exchange; r[0] is the even row's value and
+// r[1] the odd row's, in both rows
+__device__ __forceinline__ uint2 rows16_pair(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return make_uint2(r[0], r[1]);
+}
+
+// Over the 32 lanes of each half-wave, returned to all of them: the largest |x| (am) and, among the
+// elements equal to it in magnitude, the first in element order, as key = 2 * index + sign bit.
+__device__ __forceinline__ float half_max_f32(float v) {
+    v = fmaxf(v, dpp_f32<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f32<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f32<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f32<DPP_MIRROR>(v));
+    const uint2 r = rows16_pair(__float_as_uint(v));
+    return fmaxf(__uint_as_float(r.x), __uint_as_float(r.y));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t half_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<DPP_XOR1>(v));
+    v = min(v, dpp_u32<DPP_XOR2>(v));
+    v = min(v, dpp_u32<DPP_HALF_MIRROR>(v));
+    v = min(v, dpp_u32<DPP_MIRROR>(v));
+    const uint2 r = rows16_pair(v);
+    return min(r.x, r.y);
+}
+
+template <int OUT, bool NORM, int NOCT>
 __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, int64_t M, int64_t D,
                                                  const float * __restrict__ w, const float * __restrict__ b, float eps,
                                                  act_view out) {
@@ -64,10 +94,10 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
     if (row >= M) return;
     const int n_oct = (int) (D / 8);
     const float * xr = x + row * D;
-    float v[MAXOCT][8];
-    [[maybe_unused]] float gw[MAXOCT][8], gb[MAXOCT][8];   // affine parameters, loaded with x
+    float v[NOCT][8];
+    [[maybe_unused]] float gw[NOCT][8], gb[NOCT][8];   // affine parameters, loaded with x
 #pragma unroll
-    for (int i = 0; i < MAXOCT; i++) {
+    for (int i = 0; i < NOCT; i++) {
         const int o = lane + 64 * i;
         if (o < n_oct) {
             const float4 a = *(const float4 *) (xr + 8 * o), c = *(const float4 *) (xr + 8 * o + 4);
@@ -88,14 +118,14 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
     if constexpr (NORM) {
         double s = 0.0;
 #pragma unroll
-        for (int i = 0; i < MAXOCT; i++)
+        for (int i = 0; i < NOCT; i++)
 #pragma unroll
             for (int e = 0; e < 8; e++) s += (double) v[i][e];
         s = wave_sum_f64(s);
         const float mean = (float) s / (float) D;
         double s2 = 0.0;
 #pragma unroll
-        for (int i = 0; i < MAXOCT; i++) {
+        for (int i = 0; i < NOCT; i++) {
             const bool live = lane + 64 * i < n_oct;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
@@ -108,7 +138,7 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
         const float var = (float) (s2 / (double) D);
         const float scale = 1.0f / sqrtf(__fadd_rn(var, eps));
 #pragma unroll
-        for (int i = 0; i < MAXOCT; i++) {
+        for (int i = 0; i < NOCT; i++) {
             const int o = lane + 64 * i;
             if (o >= n_oct) continue;
 #pragma unroll
@@ -121,7 +151,7 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
         }
     }
 #pragma unroll
-    for (int i = 0; i < MAXOCT; i++) {
+    for (int i = 0; i < NOCT; i++) {
         const int o = lane + 64 * i;
         const bool live = o < n_oct;
         if (i * 64 >= n_oct) break;   // uniform across the wave
@@ -157,20 +187,18 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
                 if ((o & 3) == 0) ((uint16_t *) out.d)[row * (D / 32) + o / 4] = f2hbits(d);
             }
         } else {   // A_Q8_K
-            // largest |x| of the 256-block, first occurrence in element order
-            float am = 0.0f, mx = 0.0f;
-            int idx = 1 << 30;
+            // largest |x| of the 256-block, then the first element of that magnitude (its sign gives
+            // the scale's sign): max over the half-wave, then min of 2 * index + sign
+            float am = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float ax = fabsf(v[i][e]);
-                if (ax > am) { am = ax; mx = v[i][e]; idx = (lane & 31) * 8 + e; }
-            }
+            for (int e = 0; e < 8; e++) am = fmaxf(am, fabsf(v[i][e]));
+            am = half_max_f32(am);
+            uint32_t key = 0xffffffffu;
 #pragma unroll
-            for (int off = 1; off < 32; off <<= 1) {
-                const float am2 = __shfl_xor(am, off), mx2 = __shfl_xor(mx, off);
-                const int idx2 = __shfl_xor(idx, off);
-                if (am2 > am || (am2 == am && idx2 < idx)) { am = am2; mx = mx2; idx = idx2; }
-            }
+            for (int e = 7; e >= 0; e--)
+                if (fabsf(v[i][e]) == am) key = 2u * (uint32_t) ((lane & 31) * 8 + e) + (__float_as_uint(v[i][e]) >> 31);
+            key = half_min_u32(key);
+            const float mx = (key & 1u) ? -am : am;
             float q[8];
             float d = 0.0f;
             if (am != 0.0f) {
@@ -185,7 +213,7 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
             float bs = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; e++) bs += q[e];
-            bs += __shfl_xor(bs, 1);
+            bs += dpp_f32<DPP_XOR1>(bs);   // the other 8 values of the 16-group
             if (live) {
                 h8 hv;
 #pragma unroll
@@ -427,23 +455,31 @@ inline unsigned nblk(int64_t n, int t) { return (unsigned) ((n + t - 1) / t); }
 void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w, const float * b, float eps,
                           bool normalize, const act_view & out, hipStream_t s) {
     if (M <= 0) return;
-    if (!normalize && D > 64 * 8 * MAXOCT) {
-        // Plain conversion of rows longer than a wave holds: quantization blocks (32 / 256 values)
-        // never straddle a chunk of c columns when c is a multiple of 256 dividing D, and [M][D] is
-        // [M*D/c][c] in memory for the codes, the scales and the block sums alike.
-        int64_t c = 64 * 8 * MAXOCT;
-        while (c >= 256 && (D % c != 0 || c % 256 != 0)) c -= 256;
-        if (c >= 256) { M = M * (D / c); D = c; }
+    if (!normalize && D > 512) {
+        // Plain conversion: quantization blocks (32 / 256 values) never straddle a chunk of c columns
+        // when c is a multiple of 256 dividing D, and [M][D] is [M*D/c][c] in memory for the codes,
+        // the scales and the block sums alike. Chunks of 512 (one octet per lane) give the most
+        // waves and the shortest dependency chain per wave.
+        int64_t c = 0;
+        if (D % 512 == 0) c = 512;
+        else
+            for (int64_t t = 64 * 8 * MAXOCT; t >= 256 && c == 0; t -= 256)
+                if (D % t == 0) c = t;
+        if (c > 0) { M = M * (D / c); D = c; }
     }
     const dim3 grid(nblk(M, 4));
-#define RN(OUT) (normalize ? (void) k_rownorm<OUT, true><<<grid, 256, 0, s>>>(x, M, D, w, b, eps, out) \
-                           : (void) k_rownorm<OUT, false><<<grid, 256, 0, s>>>(x, M, D, w, b, eps, out))
+    const int noct = D <= 512 ? 1 : D <= 1024 ? 2 : 4;
+#define RN3(OUT, NORM) (noct == 1 ? (void) k_rownorm<OUT, NORM, 1><<<grid, 256, 0, s>>>(x, M, D, w, b, eps, out) \
+                      : noct == 2 ? (void) k_rownorm<OUT, NORM, 2><<<grid, 256, 0, s>>>(x, M, D, w, b, eps, out) \
+                                  : (void) k_rownorm<OUT, NORM, 4><<<grid, 256, 0, s>>>(x, M, D, w, b, eps, out))
+#define RN(OUT) (normalize ? RN3(OUT, true) : RN3(OUT, false))
     switch (out.fmt) {
         case A_F32:  RN(A_F32); break;
         case A_F16:  RN(A_F16); break;
         case A_Q8_0: RN(A_Q8_0); break;
         case A_Q8_K: RN(A_Q8_K); break;
     }
+#undef RN3
 #undef RN
 }
 

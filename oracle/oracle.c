@@ -546,6 +546,11 @@ float or_gelu_erf(float x) {
     return 0.5f * x * (1.0f + erff(x * SQRT_2_INV));
 }
 
+/* the same over n values (the MLP activation, src/jepa.cpp:377-385) */
+void or_gelu_erf_n(const float * x, float * y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = or_gelu_erf(x[i]);
+}
+
 /* ------------------------------------------------------------------------------------------------
  * 3-D RoPE (src/rope3d.cpp:9-164, math spec src/rope3d.h:1-62)
  * ---------------------------------------------------------------------------------------------- */

@@ -63,6 +63,7 @@ void or_set_reverse_block_order(int on);
 void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, const float * b,
                    float eps, float * y);
 float or_gelu_erf(float x);
+void or_gelu_erf_n(const float * x, float * y, int64_t n);
 
 typedef struct {
     int   grid_t, grid_h, grid_w, head_dim;

@@ -48,6 +48,8 @@ def lib() -> C.CDLL:
         L.or_layer_norm.restype = None
         L.or_gelu_erf.argtypes = [C.c_float]
         L.or_gelu_erf.restype = C.c_float
+        L.or_gelu_erf_n.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
+        L.or_gelu_erf_n.restype = None
         L.or_rope_tables.argtypes = [vp, vp, i64, vp, vp, C.c_int]
         L.or_rope_tables.restype = None
         L.or_rope_apply.argtypes = [vp, i64, C.c_int, C.c_int, vp, vp]
@@ -219,6 +221,13 @@ def vec_dot(wtype: int, n: int, wrow: np.ndarray, arow: np.ndarray) -> float:
 
 def gelu_erf(x: float) -> float:
     return float(lib().or_gelu_erf(x))
+
+
+def gelu_erf_array(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().or_gelu_erf_n(_p(x), _p(y), x.size)
+    return y
 
 
 def set_reverse_block_order(on: bool) -> None:

@@ -161,8 +161,94 @@ def test_matmul_full_m2048_q8_0(jlib, oracle):
     np.testing.assert_array_equal(host(y).view(np.uint32), want.view(np.uint32))
 
 
+def _q8k_blocks(raw, n_rows, n_cols):
+    """ggml block_q8_K bytes -> (d f32 [rows][nb], codes int8 [rows][n_cols], bsums int16 [rows][nb*16])"""
+    b = raw.reshape(n_rows, n_cols // 256, 292)
+    d = b[:, :, 0:4].copy().view(np.float32)[..., 0]
+    q = b[:, :, 4:260].copy().view(np.int8).reshape(n_rows, n_cols)
+    bs = b[:, :, 260:292].copy().view(np.int16).reshape(n_rows, -1)
+    return d, q, bs
+
+
+@pytest.mark.parametrize("gtype,out_type", [(gguf.GGML_Q4_K, gguf.GGML_Q8_K), (gguf.GGML_Q8_0, gguf.GGML_Q8_K),
+                                            (gguf.GGML_F16, gguf.GGML_Q8_K), (gguf.GGML_Q8_0, gguf.GGML_Q8_0),
+                                            (gguf.GGML_Q4_0, gguf.GGML_F32)])
+def test_matmul_gelu_epilogue(jlib, oracle, gtype, out_type):
+    """fc1 with its fused epilogue: gelu_erf(X W^T + b) quantized for fc2 in the GEMM (q8_K: one
+    256-block per workgroup row, cross-wave max in LDS). Against the oracle's exact GEMM, libm GELU and
+    ggml quantizer: the GPU's erff and libm's may round differently, so a code can differ where a value
+    sits at a rounding tie; rows 256..511 of W and b are zero (all-zero blocks, d = 0). M = 389 is
+    ragged. The q8_K output must also hold its own invariants: bsums = sums of the codes, and the block
+    maximum coded as -127 at its first position."""
+    n_out, n_in, M = 768, 512 if gtype != gguf.GGML_Q4_K else 768, 389
+    rng = np.random.default_rng(gtype * 31 + out_type)
+    w = (rng.standard_normal((n_out, n_in)) * 0.05).astype(np.float32)
+    w[256:512] = 0.0
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    bias = (rng.standard_normal(n_out) * 0.1).astype(np.float32)
+    bias[256:512] = 0.0
+    raw = w.astype(np.float16).view(np.uint8) if gtype == gguf.GGML_F16 else gguf.quantize(gtype, w)
+    pre = oracle.mul_mat(gtype, raw, n_out, n_in, x, bias)
+    ref = oracle.gelu_erf_array(pre)
+    dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
+    if out_type == gguf.GGML_F32:
+        out = torch.zeros((M, n_out), dtype=torch.float32, device="cuda")
+    else:
+        out = torch.zeros(oracle.quantize_act(out_type, ref[:1]).size * M, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    rc = jlib.lib().jepa_amd_matmul_gelu(0, gtype, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, out_type, out.data_ptr(),
+                                         1, None)
+    assert rc == 0, jlib.error_text()
+    got = host(out)
+    if out_type == gguf.GGML_F32:
+        assert np.abs(got - ref).max() <= 4e-7 * np.abs(ref).max()
+        return
+    want = oracle.quantize_act(out_type, ref).reshape(-1)
+    frac = (got != want).mean()
+    assert frac < (5e-3 if gtype == gguf.GGML_F16 else 1e-3), f"{frac:.2e} of the bytes differ"
+    if out_type == gguf.GGML_Q8_K:
+        d, q, bs = _q8k_blocks(got, M, n_out)
+        np.testing.assert_array_equal(bs, q.reshape(M, -1, 16).astype(np.int32).sum(-1))
+        assert (d[:, 1] == 0).all() and (q[:, 256:512] == 0).all()
+        live = np.delete(np.arange(n_out // 256), 1)
+        qb = q.reshape(M, -1, 256)[:, live]
+        assert (qb.min(-1) == -127).all()
+        vals = ref.reshape(M, -1, 256)[:, live]
+        first = np.abs(vals).argmax(-1)
+        assert (np.take_along_axis(qb, first[..., None], -1) == -127).all()
+
+
+def test_gelu_epilogue_every_f16_input(jlib, oracle):
+    """The fused GELU (branch-free erf: z P(z^2) below 0.875, 1 - 2^Q(z) above) on every finite f16
+    value in [-12, 12], through an f16 identity GEMM (exact: one product of 1.0 per output), against
+    the oracle's libm form 0.5 x (1 + erff(x / sqrt 2)). Both erf evaluations are within ~1.5 units of
+    2^-24 of erf, so outputs agree to 0.5 |x| 3.6e-7 plus an output rounding; subnormal and zero
+    inputs, the branch point z = 0.875 and the saturation of erf to 1 are all in the set."""
+    h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    h = h[h <= 12.0]
+    x = np.concatenate([h, -h[1:]])
+    n = 256
+    rows = -(-x.size // n)
+    xs = np.zeros(rows * n, dtype=np.float32)
+    xs[:x.size] = x
+    xs = xs.reshape(rows, n)
+    w = np.eye(n, dtype=np.float16)
+    dw, dx = dev(w.view(np.uint8).reshape(-1)), dev(xs)
+    out = torch.zeros((rows, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    rc = jlib.lib().jepa_amd_matmul_gelu(0, gguf.GGML_F16, dw.data_ptr(), n, n, None, dx.data_ptr(), rows, gguf.GGML_F32,
+                                         out.data_ptr(), 1, None)
+    assert rc == 0, jlib.error_text()
+    got = host(out).reshape(-1)[:x.size]
+    want = oracle.gelu_erf_array(x)
+    bound = 0.5 * np.abs(x) * 3.6e-7 + np.abs(want) * 2.0 ** -23
+    bad = np.abs(got.astype(np.float64) - want) > bound
+    assert not bad.any(), f"{bad.sum()} values out of bound, worst x = {x[np.argmax(np.abs(got - want) - bound)]}"
+    assert np.array_equal(got[x == 0], want[x == 0]) and np.all(got[x >= 6] == x[x >= 6])
+
+
 # workgroup tiles of the MFMA GEMM (weight rows x tokens), by index
-TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64)}
+TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64), 6: (256, 64)}
 
 
 @pytest.mark.parametrize("tile", sorted(TILES))
