@@ -69,11 +69,15 @@ int jepa_amd_matmul_gelu(int device, int wtype, const void * w_dev, int64_t n_ou
 
 /* Attention of one block from its fused qkv rows: qkv_dev f32 [n_items*n_tok][3*n_head*64] (rows
  * [q | k | v], head-major), optional RoPE tables rope_c/rope_s [n_tok][64] (signed sine). Runs the QKV
- * epilogue's split/RoPE/f16 cast and the attention kernel. out_type 0 (f32): out_dev f32
- * [n_items*n_tok][n_head*64]; 8 (q8_0): out_dev ggml q8_0 blocks of those rows, as the attention
- * kernel's fused epilogue quantizes them for the out-projection. */
+ * epilogue's split/RoPE/f16 cast and the attention kernel. tokens_per_slot > 0 applies the LeVJEPA
+ * block-causal mask (reference src/jepa.cpp:827-844): the n_prefix leading rows read every key, a patch
+ * row reads the patch keys of its own and earlier temporal slots of tokens_per_slot rows, and no
+ * prefix key; 0 is full attention. out_type 0 (f32): out_dev f32 [n_items*n_tok][n_head*64]; 8 (q8_0):
+ * out_dev ggml q8_0 blocks of those rows, as the attention kernel's fused epilogue quantizes them for
+ * the out-projection. */
 int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64_t n_tok, int n_head,
-                       const float * rope_c_dev, const float * rope_s_dev, int out_type, void * out_dev);
+                       const float * rope_c_dev, const float * rope_s_dev, int n_prefix, int64_t tokens_per_slot,
+                       int out_type, void * out_dev);
 
 /* One v_mfma_f32_32x32x16_f16 on host matrices a [32][16], b [16][32] -> d [32][32] (row-major),
  * written back through the accumulator layout the GEMM epilogues assume. */

@@ -258,8 +258,9 @@ extern "C" int jepa_amd_gemm_tile(int index) {
 }
 
 extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items, int64_t n_tok, int n_head, const float * rope_c,
-                                  const float * rope_s, int out_type, void * out) {
-    if (!qkv || !out || n_items <= 0 || n_tok <= 0 || n_head <= 0) return -1;
+                                  const float * rope_s, int n_prefix, int64_t tokens_per_slot, int out_type, void * out) {
+    if (!qkv || !out || n_items <= 0 || n_tok <= 0 || n_head <= 0 || n_prefix < 0 || tokens_per_slot < 0 ||
+        n_tok > 0x40000000) return -1;
     if (out_type != T_F32 && out_type != T_Q8_0) { jepa_log("jepa: jepa_amd_attention: output type %d\n", out_type); return -1; }
     dev_scope d(device);
     if (!d.ok) return -1;
@@ -286,7 +287,7 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
         o.d = d.alloc((size_t) rows * (D / 32) * 2);
         if (!o.q || !o.d) return -1;
     }
-    launch_attention(q, k, vt, o, n_items, n_head, hd, n_tok, R_pad, 0.125f, d.s);
+    launch_attention(q, k, vt, o, n_items, n_head, hd, n_tok, R_pad, 0.125f, n_prefix, tokens_per_slot, d.s);
     if (out_type == T_Q8_0) launch_pack_act_blocks(o, rows, D, out, d.s);
     return d.finish();
 }

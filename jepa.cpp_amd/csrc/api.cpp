@@ -237,7 +237,7 @@ extern "C" int64_t jepa_token_grid(const jepa_model * model, int n_frames, int h
         if (gw) *gw = vs.gw;
         return vs.n_rows();
     }
-    if (model->hp.family == FAM_VJEPA || model->hp.family == FAM_LEVJEPA) {
+    if (model->hp.family == FAM_VJEPA) {
         jepa_log("jepa: jepa_token_grid: family '%s' is not implemented on this path\n", model->hp.family_str.c_str());
         return 0;
     }

@@ -61,13 +61,23 @@ __device__ __forceinline__ void tile_barrier() {
     __builtin_amdgcn_s_barrier();
 }
 
+// Keys visible to query row q of an item (block-causal attention, reference src/jepa.cpp:827-844):
+// the np prefix rows read every key; a patch row of temporal slot f = (q - np) / tpf reads the patch
+// keys of slots 0..f and no prefix key. tpf = 0: every query reads every key. Returns [lo, hi).
+__device__ __forceinline__ int2 key_range(int q, int R, int np, int tpf) {
+    if (tpf <= 0 || q < np) return make_int2(0, R);
+    return make_int2(np, min(R, np + ((q - np) / tpf + 1) * tpf));
+}
+
 // OUT: A_F32 writes O f32 [item*R][H*64]; A_Q8_0 writes the q8_0 activation of the next linear
 // (int8 codes [item*R][H*64] + f16 d per 32), the same values the separate quantizer would produce.
+// np / tpf select the block-causal mask (tpf = 0: none); key tiles that no query of the workgroup
+// sees are not visited, 32-key blocks that no query of a wave sees are skipped by that wave.
 template <int OUT>
 __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
                                                       const _Float16 * __restrict__ Vt, void * __restrict__ O,
                                                       void * __restrict__ Od, int n_head, int64_t R, int64_t R_pad,
-                                                      float c) {
+                                                      float c, int np, int tpf) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * HALF];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, g = lane >> 5;
@@ -83,9 +93,15 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     const brsrc rK = make_brsrc(Kp + head * R_pad * HD, R_pad * HD * 2);
     const brsrc rV = make_brsrc(Vt + head * HD * R_pad, R_pad * HD * 2);
 
-    const int ntile = (int) ((R + KT - 1) / KT);
+    // key tiles of this workgroup: the union of its queries' key ranges (the first query has the
+    // lowest bound, the last the highest; a prefix row among them reads everything)
+    const int qa = (int) blockIdx.x * QB, qz = min((int) R, qa + QB) - 1;
+    const int klo_wg = key_range(qa, (int) R, np, tpf).x;
+    const int khi_wg = qa < np ? (int) R : key_range(qz, (int) R, np, tpf).y;
+    const int tfirst = klo_wg / KT;
+    const int ntile = (khi_wg + KT - 1) / KT - tfirst;
     const int nt = (ntile + 1) / 2;                     // tiles per half (the second may have one less)
-    const int t0 = kh * nt;                             // first tile of this half
+    const int t0 = tfirst + kh * nt;                    // first tile of this half
     const int my_nt = kh == 0 ? nt : ntile - nt;
     unsigned char * hbase = smem + kh * HALF;
 
@@ -113,6 +129,14 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     f16v acc0 = zero, acc1 = zero;
     float m_run = -INFINITY, l_run = 0.0f;
 
+    // this lane's key range, and the wave's bounds on it: a 32-key block below lo_max or reaching
+    // past hi_min needs the per-key mask, one below lo_min or past hi_max is invisible to all lanes
+    const int2 kr = key_range((int) q0 + l32, (int) R, np, tpf);
+    const int qw = (int) q0, qp = max(qw, np);
+    const int lo_min = key_range(qw, (int) R, np, tpf).x, lo_max = key_range(qw + 31, (int) R, np, tpf).x;
+    const int hi_min = qp <= qw + 31 ? key_range(qp, (int) R, np, tpf).y : (int) R;
+    const int hi_max = qw < np ? (int) R : key_range(qw + 31, (int) R, np, tpf).y;
+
     for (int s = 0; s < NST - 1; s++) issue(s);
     for (int s = 0; s < nt; s++) {
         // tile s has landed once only the copies of the NST - 2 younger tiles are outstanding; the
@@ -126,14 +150,18 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
         const int64_t kt = (int64_t) (t0 + s) * KT;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++) {
+            const int kb0 = (int) kt + 32 * kb;
+            if (kb0 + 32 <= lo_min || kb0 >= hi_max) continue;     // no query of this wave sees them
             f16v S = zero;
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) S = MFMA16(lds_chunk(sK, 32 * kb + l32, 2 * kk + g), qv[kk], S);
-            const int64_t key0 = kt + 32 * kb + 4 * g;
-            if (kt + 32 * kb + 32 > R) {
+            if (kb0 < lo_max || kb0 + 32 > hi_min) {                 // keys past R or outside a lane's range
+                const int key0 = kb0 + 4 * g;
 #pragma unroll
-                for (int r = 0; r < 16; r++)
-                    if (key0 + 8 * (r >> 2) + (r & 3) >= R) S[r] = -INFINITY;
+                for (int r = 0; r < 16; r++) {
+                    const int key = key0 + 8 * (r >> 2) + (r & 3);
+                    if (key < kr.x || key >= kr.y) S[r] = -INFINITY;
+                }
             }
             float mloc = S[0];
 #pragma unroll
@@ -238,14 +266,16 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
 }  // namespace
 
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items,
-                      int n_head, int hd, int64_t R, int64_t R_pad, float scale, hipStream_t s) {
+                      int n_head, int hd, int64_t R, int64_t R_pad, float scale, int n_prefix, int64_t tokens_per_slot,
+                      hipStream_t s) {
     (void) hd;   // only 64 (checked by the caller)
     const float c = scale * 1.4426950408889634f;   // exp(x*scale) = exp2(x*scale*log2(e))
+    const int tpf = (int) tokens_per_slot;
     dim3 grid((unsigned) ((R + QB - 1) / QB), (unsigned) (n_items * n_head));
     if (out.fmt == A_Q8_0)
         k_attn_hd64<A_Q8_0><<<grid, 512, 0, s>>>((const _Float16 *) q, (const _Float16 *) k, (const _Float16 *) vt, out.q,
-                                                  out.d, n_head, R, R_pad, c);
+                                                  out.d, n_head, R, R_pad, c, n_prefix, tpf);
     else
         k_attn_hd64<A_F32><<<grid, 512, 0, s>>>((const _Float16 *) q, (const _Float16 *) k, (const _Float16 *) vt, out.q,
-                                                 nullptr, n_head, R, R_pad, c);
+                                                 nullptr, n_head, R, R_pad, c, n_prefix, tpf);
 }

@@ -270,9 +270,15 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
         if (w.video && e.modality_embed) ep.addvec = w.image_path ? m->mod_img : m->mod_video;
         if (!w.video && m->pos_embed) ep.addrows = m->pos_embed;
         kt.run("patch_embed", [&] { launch_gemm(pe, pa, n_items * w.Np, ep, s); });
-        if (!w.video && e.cls_token) kt.run("cls", [&] { launch_cls_rows(w.x, m->cls_token, m->pos_embed, n_items, R, D, s); });
+        // CLS row in front: image families add its position row; the video family with one (levjepa)
+        // gives it no position (reference src/jepa.cpp:865-880)
+        if (e.cls_token)
+            kt.run("cls", [&] { launch_cls_rows(w.x, m->cls_token, w.video ? nullptr : m->pos_embed, n_items, R, D, s); });
     }
     if (trace) launch_copy_f32(w.x, trace, rows * D, s);
+    // block-causal attention (levjepa): temporal slots of gh*gw patch rows after the prefix rows
+    const int64_t slot_rows = e.attn_mode == "block_causal" ? (int64_t) (w.height / e.patch_size) * (w.width / e.patch_size) : 0;
+    const int n_prefix = (int) w.prefix;
     for (int l = 0; l < e.n_layer; l++) {
         const dev_layer & L = m->layers[(size_t) l];
         // attention half
@@ -289,11 +295,15 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
         w.actA.fmt = L.out.act();
         if (w.actA.fmt == A_Q8_0) {
             // the attention epilogue writes the out-projection's q8_0 input directly
-            kt.run("attention", [&] { launch_attention(w.Q, w.Kt, w.Vt, w.actA, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), s); });
+            kt.run("attention", [&] {
+                launch_attention(w.Q, w.Kt, w.Vt, w.actA, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
+            });
         } else {
             act_view o;
             o.fmt = A_F32; o.q = w.attn; o.ld = D;
-            kt.run("attention", [&] { launch_attention(w.Q, w.Kt, w.Vt, o, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), s); });
+            kt.run("attention", [&] {
+                launch_attention(w.Q, w.Kt, w.Vt, o, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
+            });
             kt.run("quantize", [&] { launch_rownorm_quant(w.attn, rows, D, nullptr, nullptr, 0.0f, false, w.actA, s); }, "attn");
         }
         {
@@ -353,7 +363,7 @@ bool check_supported(const jepa_model * m) {
         jepa_log("jepa: jepa_encode: only the gelu_erf activation is implemented on this path\n");
         return false;
     }
-    if (e.attn_mode != "full") {
+    if (e.attn_mode != "full" && !(e.attn_mode == "block_causal" && is_video_family(m->hp.family))) {
         jepa_log("jepa: jepa_encode: attn_mode '%s' is not implemented on this path\n", e.attn_mode.c_str());
         return false;
     }

@@ -56,8 +56,11 @@ void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w
 
 // Flash attention over (items*H) heads into `out` [item*R][H*hd]: A_F32 (f32 rows in out.q) or
 // A_Q8_0 (the next linear's q8_0 activation: int8 codes in out.q, f16 d per 32 in out.d).
+// tokens_per_slot > 0 applies the block-causal mask: n_prefix leading rows read every key, a patch row
+// reads the patch keys of its own and earlier temporal slots (tokens_per_slot rows each) and no prefix
+// key. tokens_per_slot = 0: full attention.
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items, int n_head,
-                      int hd, int64_t R, int64_t R_pad, float scale, hipStream_t s);
+                      int hd, int64_t R, int64_t R_pad, float scale, int n_prefix, int64_t tokens_per_slot, hipStream_t s);
 
 // Patch rows from NCTHW input: rows [items*Np][C*tub*P*P] in f16 (half_out) or f32.
 void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_items, int C, int T, int H, int W,

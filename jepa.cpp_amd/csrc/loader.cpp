@@ -130,6 +130,13 @@ bool hparams_from_gguf(const gguf::file & f, hparams & hp, std::vector<std::pair
         jepa_log("jepa: unknown jepa.enc.attn_mode '%s' (expected full | block_causal)\n", e.attn_mode.c_str());
         return false;
     }
+    // only the video encoder graph builds the mask; an image family would run unmasked, which is
+    // what the key exists to prevent (reference tests/test-errors.cpp:259-262)
+    if (e.attn_mode == "block_causal" && !is_video_family(hp.family)) {
+        jepa_log("jepa: jepa.enc.attn_mode 'block_causal' is only defined for the video families (family '%s')\n",
+                 hp.family_str.c_str());
+        return false;
+    }
     e.has_proj = r.has("jepa.enc.proj_act");
     if (!kv_range("jepa.enc.n_registers", nreg, 0, JEPA_LIMIT_N_TOKENS)) return false;
     e.n_registers = (int) nreg;
@@ -298,7 +305,7 @@ struct loader {
 
 }  // namespace
 
-bool is_video_family(family_id f) { return f == FAM_VJEPA2 || f == FAM_VJEPA2_1; }
+bool is_video_family(family_id f) { return f == FAM_VJEPA2 || f == FAM_VJEPA2_1 || f == FAM_LEVJEPA; }
 bool is_image_family(family_id f) { return f == FAM_IJEPA || f == FAM_HFVIT || f == FAM_LEWM || f == FAM_HJEPA; }
 
 static void model_free_device(jepa_model * m) {

@@ -99,7 +99,7 @@ def lib() -> C.CDLL:
         "jepa_amd_rownorm": (C.c_int, [C.c_int, vp, i64, i64, vp, vp, C.c_float, C.c_int, C.c_int, vp]),
         "jepa_amd_matmul": (C.c_int, [C.c_int, C.c_int, vp, i64, i64, vp, vp, i64, vp, C.c_int, C.POINTER(C.c_double)]),
         "jepa_amd_matmul_gelu": (C.c_int, [C.c_int, C.c_int, vp, i64, i64, vp, vp, i64, C.c_int, vp, C.c_int, C.POINTER(C.c_double)]),
-        "jepa_amd_attention": (C.c_int, [C.c_int, vp, i64, i64, C.c_int, vp, vp, C.c_int, vp]),
+        "jepa_amd_attention": (C.c_int, [C.c_int, vp, i64, i64, C.c_int, vp, vp, C.c_int, i64, C.c_int, vp]),
         "jepa_amd_mfma_probe": (C.c_int, [C.c_int, vp, vp, vp]),
         "jepa_amd_copy": (C.c_int, [C.c_int, vp, vp, i64, C.c_int, C.POINTER(C.c_double)]),
         "jepa_amd_gemm_tile": (C.c_int, [C.c_int]),

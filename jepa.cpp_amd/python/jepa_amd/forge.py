@@ -22,7 +22,7 @@ from .gguf import (FTYPE, GGML_F16, GGML_F32, GGML_Q4_0, GGML_Q4_K, GGML_Q8_0, G
 @dataclass(frozen=True)
 class EncoderConfig:
     name: str
-    family: str            # hfvit | vjepa2 | vjepa2_1
+    family: str            # hfvit | vjepa2 | vjepa2_1 | levjepa
     embed_dim: int
     n_layer: int
     n_head: int
@@ -40,6 +40,7 @@ class EncoderConfig:
     image_patch_embed: bool = False
     layer_scale: bool = False
     ln_random: bool = False
+    attn_mode: str = "full"  # full | block_causal (levjepa)
     seed: int = 1234
 
 
@@ -58,6 +59,11 @@ CONFIGS = {
                                  img_size=256, n_frames=16, ftype="q8_0", rope_layout="tiled"),
     "vitl16_q4_k": EncoderConfig("vjepa2-vitl16-256-synthetic", "vjepa2", 1024, 24, 16, 4096, patch=16, tubelet=2,
                                  img_size=256, n_frames=16, ftype="q4_k", rope_layout="tiled"),
+    # LeVJEPA ViT-L/16 224x224, 16 frames, tubelet 1 (16 x 196 patch tokens + CLS = 3137 rows), block-causal
+    # attention, tiled RoPE with an identity row for the CLS
+    "levjepa_vitl16_q8_0": EncoderConfig("levjepa-vitl16-224-synthetic", "levjepa", 1024, 24, 16, 4096, patch=16,
+                                         tubelet=1, img_size=224, n_frames=16, cls_token=True, ftype="q8_0",
+                                         rope_layout="tiled", attn_mode="block_causal"),
     # V-JEPA 2 ViT-g/16 256x256, 64 frames (8192 tokens)
     "vitg16_q8_0": EncoderConfig("vjepa2-vitg16-256-synthetic", "vjepa2", 1408, 40, 22, 6144, patch=16, tubelet=2,
                                  img_size=256, n_frames=64, ftype="q8_0", rope_layout="tiled"),
@@ -75,6 +81,9 @@ def tiny(family: str, ftype: str, **kw) -> EncoderConfig:
         base = EncoderConfig("tiny-vjepa2_1", "vjepa2_1", 128, 2, 2, 512, patch=16, tubelet=2, img_size=64,
                              n_frames=4, ftype=ftype, rope_layout="interleaved", rope_interpolate=True,
                              rope_ref_grid=16, modality_embed=True, image_patch_embed=True)
+    elif family == "levjepa":
+        base = EncoderConfig("tiny-levjepa", "levjepa", 128, 2, 2, 512, patch=16, tubelet=1, img_size=64, n_frames=4,
+                             cls_token=True, ftype=ftype, rope_layout="tiled", attn_mode="block_causal")
     else:
         raise ValueError(family)
     return replace(base, **kw)
@@ -94,7 +103,7 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     """Write the synthetic GGUF for `cfg` to `path` (returns path)."""
     rng = np.random.default_rng(cfg.seed)
     D, F = cfg.embed_dim, cfg.ffn_dim
-    video = cfg.family in ("vjepa2", "vjepa2_1")
+    video = cfg.family in ("vjepa2", "vjepa2_1", "levjepa")
     w = GGUFWriter()
     w.add("general.architecture", "jepa")
     w.add("general.name", cfg.name)
@@ -126,6 +135,8 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     w.add("jepa.enc.modality_embed", cfg.modality_embed)
     w.add("jepa.enc.image_patch_embed", cfg.image_patch_embed)
     w.add("jepa.enc.layer_scale", cfg.layer_scale)
+    if cfg.attn_mode != "full":
+        w.add("jepa.enc.attn_mode", cfg.attn_mode)
     w.add("jepa.pre.mean", [0.485, 0.456, 0.406])
     w.add("jepa.pre.std", [0.229, 0.224, 0.225])
     w.add("jepa.pre.resize_short", cfg.img_size)

@@ -613,8 +613,19 @@ void or_rope_apply(float * x, int64_t n_tok, int n_head, int hd, const float * c
  * attention: ggml_flash_attn_ext on the CPU tiled path: Q f32, K/V f16 tiles widened to f32,
  * scores/softmax/accumulator f32 (docs/ggml-notes.md:48-58). Softmax written two-pass here.
  * ---------------------------------------------------------------------------------------------- */
+void or_block_causal_mask(int gt, int gh, int gw, int n_prefix, float * out) {
+    const int64_t tpf = (int64_t) gh * gw, np = n_prefix, N = np + (int64_t) gt * tpf;
+    for (int64_t i = 0; i < N; i++)
+        for (int64_t j = 0; j < N; j++) {
+            int open;
+            if (i < np) open = 1;                                   /* prefix rows read the whole clip */
+            else open = j >= np && (j - np) / tpf <= (i - np) / tpf; /* own slot or earlier, no prefix */
+            out[i * N + j] = open ? 0.0f : -INFINITY;
+        }
+}
+
 void or_attention(const float * q, const float * k, const float * v, int64_t n_q, int64_t n_kv,
-                  int n_head, int hd, float scale, int kv_f16, float * out, int n_threads) {
+                  int n_head, int hd, float scale, int kv_f16, const float * mask, float * out, int n_threads) {
     const int64_t row = (int64_t) n_head * hd;
     for (int h = 0; h < n_head; h++) {
         float * kh = (float *) malloc(sizeof(float) * n_kv * hd);
@@ -635,10 +646,15 @@ void or_attention(const float * q, const float * k, const float * v, int64_t n_q
                 float mx = -INFINITY;
                 for (int64_t j = 0; j < n_kv; j++) {
                     sc[j] = dot_f32_8acc(qi, kh + j * hd, hd) * scale;
+                    if (mask) sc[j] = sc[j] + mask[i * n_kv + j];
                     if (sc[j] > mx) mx = sc[j];
                 }
                 float sum = 0.0f;
                 for (int d = 0; d < hd; d++) acc[d] = 0.0f;
+                if (mx == -INFINITY) {   /* no visible key */
+                    for (int d = 0; d < hd; d++) out[i * row + h * hd + d] = 0.0f;
+                    continue;
+                }
                 for (int64_t j = 0; j < n_kv; j++) {
                     const float p = expf(sc[j] - mx);
                     sum += p;
@@ -803,7 +819,7 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
     if (gg_open(path, &f)) return -1;
     int64_t ret = -1;
     const char * fam = gg_str(&f, "jepa.family", "");
-    const int video = !strcmp(fam, "vjepa2") || !strcmp(fam, "vjepa2_1");
+    const int video = !strcmp(fam, "vjepa2") || !strcmp(fam, "vjepa2_1") || !strcmp(fam, "levjepa");
     const int image = !strcmp(fam, "hfvit") || !strcmp(fam, "ijepa") || !strcmp(fam, "lewm");
     const int D = (int) gg_int(&f, "jepa.enc.embed_dim", 0), L = (int) gg_int(&f, "jepa.enc.n_layer", 0);
     const int H = (int) gg_int(&f, "jepa.enc.n_head", 0), F = (int) gg_int(&f, "jepa.enc.ffn_dim", 0);
@@ -833,7 +849,10 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
     if (height % P || width % P || T % tub) { fprintf(stderr, "oracle: shape not encodable\n"); gg_close(&f); return -1; }
     const int GT = T / tub, GH = height / P, GW = width / P;
     const int64_t Np = (int64_t) GT * GH * GW;
-    const int64_t R = Np + (image && cls ? 1 : 0);
+    const int np = cls ? 1 : 0;                 /* CLS row in front (hfvit; levjepa: the video family with one) */
+    const int64_t R = Np + np;
+    const int block_causal = !strcmp(gg_str(&f, "jepa.enc.attn_mode", "full"), "block_causal");
+    if (block_causal && !video) { fprintf(stderr, "oracle: block_causal needs a video family\n"); gg_close(&f); return -1; }
     const int64_t K = (int64_t) C * tub * P * P;
     if (out_cap < (int64_t) n_items * R * D) { fprintf(stderr, "oracle: output too small\n"); gg_close(&f); return -1; }
 
@@ -845,8 +864,15 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
         rp.variant = !strcmp(gg_str(&f, "jepa.enc.rope_freq_layout", ""), "interleaved") ? 1 : 0;
         rp.interpolate = (int) gg_int(&f, "jepa.enc.rope_interpolate", 0);
         rp.train_grid_h = rp.train_grid_w = (int) gg_int(&f, "jepa.enc.rope_ref_grid", 0);
-        rope_c = (float *) malloc(sizeof(float) * Np * hd); rope_s = (float *) malloc(sizeof(float) * Np * hd);
-        or_rope_tables(&rp, NULL, Np, rope_c, rope_s, 1);
+        /* the prefix rows carry no position: identity rows (cos 1, sin 0), src/jepa.cpp:960-966 */
+        rope_c = (float *) malloc(sizeof(float) * R * hd); rope_s = (float *) malloc(sizeof(float) * R * hd);
+        for (int64_t i = 0; i < (int64_t) np * hd; i++) { rope_c[i] = 1.0f; rope_s[i] = 0.0f; }
+        or_rope_tables(&rp, NULL, Np, rope_c + (int64_t) np * hd, rope_s + (int64_t) np * hd, 1);
+    }
+    float * mask = NULL;
+    if (block_causal) {
+        mask = (float *) malloc(sizeof(float) * R * R);
+        or_block_causal_mask(GT, GH, GW, np, mask);
     }
 
     float * rows = (float *) malloc(sizeof(float) * Np * K);
@@ -879,12 +905,12 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
             if (!mod) goto done;
             for (int64_t r = 0; r < Np; r++) for (int d = 0; d < D; d++) xp[r * D + d] = xp[r * D + d] + mod[d];
         }
+        if (cls) {   /* after the patch embedding, no position information (src/jepa.cpp:865-880) */
+            const float * ct = gg_vec(&f, "enc.cls_token");
+            if (!ct) goto done;
+            memcpy(x, ct, sizeof(float) * D);
+        }
         if (image) {
-            if (cls) {
-                const float * ct = gg_vec(&f, "enc.cls_token");
-                if (!ct) goto done;
-                memcpy(x, ct, sizeof(float) * D);
-            }
             const float * pos = gg_vec(&f, "enc.pos_embed");
             if (pos) {
                 const gg_tensor * pt = gg_tensor_find(&f, "enc.pos_embed");
@@ -912,7 +938,7 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
                 or_rope_apply(q, R, H, hd, rope_c, rope_s);
                 or_rope_apply(kk, R, H, hd, rope_c, rope_s);
             }
-            or_attention(q, kk, vv, R, R, H, hd, 1.0f / sqrtf((float) hd), kv_f16, att, n_threads);
+            or_attention(q, kk, vv, R, R, H, hd, 1.0f / sqrtf((float) hd), kv_f16, mask, att, n_threads);
             if (linear(&f, TN(n1, "attn_out.weight"), TN(n2, "attn_out.bias"), att, R, D, D, o, n_threads)) goto done;
             const float * ls1 = gg_vec(&f, TN(a1, "ls1"));
             for (int64_t i = 0; i < R * D; i++) x[i] = x[i] + (ls1 ? o[i] * ls1[i % D] : o[i]);
@@ -931,7 +957,7 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
     ret = R;
 done:
     free(rows); free(x); free(h); free(qkv); free(q); free(kk); free(vv); free(att); free(o); free(ff); free(chw);
-    free(rope_c); free(rope_s);
+    free(rope_c); free(rope_s); free(mask);
     gg_close(&f);
     return ret;
 }

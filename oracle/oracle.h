@@ -78,10 +78,17 @@ void or_rope_tables(const or_rope_params * p, const int32_t * ids, int64_t n_row
 /* x [n_tok, n_head, head_dim] in place: x*C + swap(x)*S' with the signed table */
 void or_rope_apply(float * x, int64_t n_tok, int n_head, int head_dim, const float * cos_t, const float * sin_t);
 
-/* softmax(q k^T * scale) v per head. q f32 [n_q, n_head*hd] rows, k/v [n_kv, n_head*hd]; when
- * kv_f16 the K/V values are rounded to f16 first (ggml_cast). Output [n_q, n_head*hd]. */
+/* softmax(q k^T * scale + mask) v per head. q f32 [n_q, n_head*hd] rows, k/v [n_kv, n_head*hd]; when
+ * kv_f16 the K/V values are rounded to f16 first (ggml_cast). mask (optional): additive [n_q][n_kv]
+ * (0 / -inf), the flash_attn_ext mask argument; a row with no visible key gives zeros. Output
+ * [n_q, n_head*hd]. */
 void or_attention(const float * q, const float * k, const float * v, int64_t n_q, int64_t n_kv,
-                  int n_head, int hd, float scale, int kv_f16, float * out, int n_threads);
+                  int n_head, int hd, float scale, int kv_f16, const float * mask, float * out, int n_threads);
+
+/* LeVJEPA block-causal mask [N][N], N = n_prefix + gt*gh*gw (src/jepa.cpp:827-844): 0 where query i
+ * sees key j, -inf elsewhere. Prefix rows see every key; a patch query sees the patch keys of its own
+ * and earlier temporal slots and no prefix key. */
+void or_block_causal_mask(int gt, int gh, int gw, int n_prefix, float * out);
 
 /* Encoder forward of a GGUF file on NCTHW input (what jepa_encode returns).
  * trace (optional): [n_items][n_layer + 1][rows][D] residual stream after the patch embedding /

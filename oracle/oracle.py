@@ -54,8 +54,10 @@ def lib() -> C.CDLL:
         L.or_rope_tables.restype = None
         L.or_rope_apply.argtypes = [vp, i64, C.c_int, C.c_int, vp, vp]
         L.or_rope_apply.restype = None
-        L.or_attention.argtypes = [vp, vp, vp, i64, i64, C.c_int, C.c_int, C.c_float, C.c_int, vp, C.c_int]
+        L.or_attention.argtypes = [vp, vp, vp, i64, i64, C.c_int, C.c_int, C.c_float, C.c_int, vp, vp, C.c_int]
         L.or_attention.restype = None
+        L.or_block_causal_mask.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, vp]
+        L.or_block_causal_mask.restype = None
         L.or_encode_file.argtypes = [C.c_char_p, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64,
                                      vp, i64, C.c_int, C.c_int]
         L.or_encode_file.restype = i64
@@ -156,7 +158,7 @@ def rope_apply(x, cos_t, sin_t):
     return x
 
 
-def attention(q, k, v, n_head, scale=None, kv_f16=True):
+def attention(q, k, v, n_head, scale=None, kv_f16=True, mask=None):
     q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)
     v = np.ascontiguousarray(v, np.float32)
@@ -164,7 +166,20 @@ def attention(q, k, v, n_head, scale=None, kv_f16=True):
     hd = row // n_head
     out = np.zeros_like(q)
     sc = scale if scale is not None else 1.0 / np.sqrt(hd)
-    lib().or_attention(_p(q), _p(k), _p(v), n_q, k.shape[0], n_head, hd, sc, 1 if kv_f16 else 0, _p(out), threads())
+    mp = None
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, np.float32)
+        assert mask.shape == (n_q, k.shape[0])
+        mp = _p(mask)
+    lib().or_attention(_p(q), _p(k), _p(v), n_q, k.shape[0], n_head, hd, sc, 1 if kv_f16 else 0, mp, _p(out), threads())
+    return out
+
+
+def block_causal_mask(gt, gh, gw, n_prefix):
+    """[N][N] float32 additive mask (0 visible / -inf), N = n_prefix + gt*gh*gw"""
+    n = n_prefix + gt * gh * gw
+    out = np.zeros((n, n), np.float32)
+    lib().or_block_causal_mask(gt, gh, gw, n_prefix, _p(out))
     return out
 
 

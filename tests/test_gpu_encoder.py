@@ -55,7 +55,7 @@ def _case(jlib, oracle, models_dir, cfg, n_batch, n_frames, size, trace=True):
     m = jlib.Model(path)
     ctx = jlib.Context(m)
     x = inputs.make_input(n_batch, n_frames, size, size, seed=1234)
-    video = cfg.family in ("vjepa2", "vjepa2_1")
+    video = cfg.family in ("vjepa2", "vjepa2_1", "levjepa")
     rows = m.token_grid(n_frames if video else 1, size, size)
     n_items = n_batch if video else n_batch * n_frames
     if trace:
@@ -67,7 +67,10 @@ def _case(jlib, oracle, models_dir, cfg, n_batch, n_frames, size, trace=True):
 
 
 TINY = [("hfvit", "f16", 2, 1, 64), ("hfvit", "q8_0", 1, 2, 64), ("vjepa2", "q8_0", 1, 4, 64), ("vjepa2", "q4_k", 1, 4, 64),
-        ("vjepa2", "q4_0", 2, 4, 64), ("vjepa2", "f16", 1, 4, 64), ("vjepa2_1", "q8_0", 2, 1, 64), ("vjepa2_1", "q8_0", 1, 4, 64)]
+        ("vjepa2", "q4_0", 2, 4, 64), ("vjepa2", "f16", 1, 4, 64), ("vjepa2_1", "q8_0", 2, 1, 64), ("vjepa2_1", "q8_0", 1, 4, 64),
+        # LeVJEPA: CLS + block-causal mask; 65 rows (one query block), and 8 x 64 + 1 = 513 rows (five query
+        # blocks whose temporal slots straddle key tiles), two clips in one call
+        ("levjepa", "q8_0", 1, 4, 64), ("levjepa", "f16", 2, 8, 128), ("levjepa", "q4_k", 1, 4, 64)]
 
 
 @pytest.mark.parametrize("family,ftype,n_batch,n_frames,size", TINY)
@@ -130,6 +133,16 @@ def test_vitl16_16f_full(jlib, oracle, models_dir, name):
     check_parity(got, want, gtr, wtr, floor, label=name)
     if name == "vitl16_q8_0":
         assert cos_rows(got, want).mean() >= 0.9999   # the 0.9999 cosine bar for q8_0 holds outright
+
+
+def test_levjepa_vitl16_16f_q8_0_full(jlib, oracle, models_dir):
+    """LeVJEPA ViT-L/16, 16 frames 224x224, tubelet 1: 16 x 196 patch rows + CLS = 3137 rows, block-causal
+    attention (53.1 % of the score matrix visible), 24 layers; CLS pooled."""
+    cfg = forge.CONFIGS["levjepa_vitl16_q8_0"]
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 1, 16, 224)
+    assert got.shape == (3137, 1024)
+    floor = _floor(oracle, forge.cached_model(cfg, models_dir), x, 1, 3137, 1024, m.n_layer, want, wtr)
+    check_parity(got, want, gtr, wtr, floor, label="levjepa_vitl16_q8_0")
 
 
 def test_encode_errors(jlib, models_dir):

@@ -291,8 +291,8 @@ def test_gemm_tile_hook_rejects_unknown(jlib):
     assert jlib.lib().jepa_amd_gemm_tile(-1) == 0
 
 
-def _attention_ref(qkv, n_items, n_tok, H, rope=None):
-    """double-precision softmax(q k^T / 8) v per head, K/V rounded to f16 like ggml_cast"""
+def _attention_ref(qkv, n_items, n_tok, H, rope=None, mask=None):
+    """double-precision softmax(q k^T / 8 + mask) v per head, K/V rounded to f16 like ggml_cast"""
     D = H * 64
     out = np.zeros((n_items * n_tok, D))
     for it in range(n_items):
@@ -308,6 +308,8 @@ def _attention_ref(qkv, n_items, n_tok, H, rope=None):
             k = k.astype(np.float16).astype(np.float64)
             v = v.astype(np.float16).astype(np.float64)
             sc = q @ k.T / 8.0
+            if mask is not None:
+                sc = sc + mask
             sc -= sc.max(1, keepdims=True)
             p = np.exp(sc)
             p /= p.sum(1, keepdims=True)
@@ -335,7 +337,7 @@ def test_attention(jlib, oracle, n_items, n_tok, H, rope):
     out = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
     dq = dev(qkv)
     r = jlib.lib().jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, rc.data_ptr() if rope else None,
-                                      rs.data_ptr() if rope else None, 0, out.data_ptr())
+                                      rs.data_ptr() if rope else None, 0, 0, 0, out.data_ptr())
     assert r == 0, jlib.error_text()
     got = host(out).astype(np.float64)
     ref = _attention_ref(qkv, n_items, n_tok, H, (c.astype(np.float64), s.astype(np.float64)) if rope else None)
@@ -343,6 +345,39 @@ def test_attention(jlib, oracle, n_items, n_tok, H, rope):
     cos = (got * ref).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(ref, axis=1))
     assert rel <= 1e-2, rel
     assert cos.min() >= 0.9999, cos.min()
+
+
+# block-causal (LeVJEPA) shapes (n_items, gt, gh, gw, n_prefix, H): the reference's mask KAT shape (65
+# rows), 513 rows (five query blocks; slots of 64 rows against tiles of 64 keys shifted by the CLS),
+# slots of 35 rows with no prefix, and the 16 x 224^2 clip (3137 rows, slots of 196)
+MASK_CASES = [(1, 4, 4, 4, 1, 2), (2, 8, 8, 8, 1, 2), (1, 3, 5, 7, 0, 2), (1, 16, 14, 14, 1, 1)]
+
+
+@pytest.mark.parametrize("n_items,gt,gh,gw,n_prefix,H", MASK_CASES)
+def test_attention_block_causal(jlib, oracle, n_items, gt, gh, gw, n_prefix, H):
+    """The kernel's block-causal mask (per-query key ranges, skipped tiles and blocks) against a double
+    softmax over the oracle's [N][N] mask, and the q8_0 epilogue against the separate quantizer."""
+    n_tok = n_prefix + gt * gh * gw
+    rng = np.random.default_rng(n_tok * 7 + H)
+    D = H * 64
+    qkv = (rng.standard_normal((n_items * n_tok, 3 * D)) * 1.5).astype(np.float32)
+    mask = oracle.block_causal_mask(gt, gh, gw, n_prefix).astype(np.float64)
+    dq = dev(qkv)
+    out = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
+    oq = torch.zeros((n_items * n_tok, D // 32 * 34), dtype=torch.uint8, device="cuda")
+    L = jlib.lib()
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, n_prefix, gh * gw, 0, out.data_ptr()) == 0, \
+        jlib.error_text()
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, n_prefix, gh * gw, gguf.GGML_Q8_0,
+                                oq.data_ptr()) == 0
+    got = host(out).astype(np.float64)
+    ref = _attention_ref(qkv, n_items, n_tok, H, None, mask)
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    cos = (got * ref).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(ref, axis=1))
+    assert rel <= 1e-2, rel
+    assert cos.min() >= 0.9999, cos.min()
+    want = oracle.quantize_act(oracle.OR_Q8_0, host(out))
+    np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))
 
 
 @pytest.mark.parametrize("n_items,n_tok,H", [(1, 2048, 4), (2, 197, 6), (1, 65, 2)])
@@ -356,7 +391,7 @@ def test_attention_fused_q8_0_equals_separate_quantizer(jlib, oracle, n_items, n
     o32 = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
     oq = torch.zeros((n_items * n_tok, D // 32 * 34), dtype=torch.uint8, device="cuda")
     L = jlib.lib()
-    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, 0, o32.data_ptr()) == 0
-    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, gguf.GGML_Q8_0, oq.data_ptr()) == 0
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, 0, 0, 0, o32.data_ptr()) == 0
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, 0, 0, gguf.GGML_Q8_0, oq.data_ptr()) == 0
     want = oracle.quantize_act(oracle.OR_Q8_0, host(o32))
     np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))

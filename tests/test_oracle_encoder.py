@@ -58,7 +58,7 @@ def forward64(path, x):
     fam = kv["jepa.family"]
     D, L, H, P = kv["jepa.enc.embed_dim"], kv["jepa.enc.n_layer"], kv["jepa.enc.n_head"], kv["jepa.enc.patch_size"]
     hd, eps = D // H, float(kv["jepa.enc.ln_eps"])
-    video = fam in ("vjepa2", "vjepa2_1")
+    video = fam in ("vjepa2", "vjepa2_1", "levjepa")
     B, Cc, Tt, Hh, Ww = x.shape
     tub = kv["jepa.enc.tubelet_size"] if video else 1
     items = []
@@ -87,6 +87,18 @@ def forward64(path, x):
             rope = _rope_tables64(grid, hd, 0 if kv["jepa.enc.rope_freq_layout"] == "tiled" else 1,
                                   bool(kv.get("jepa.enc.rope_interpolate")), (ref, ref), float(kv["jepa.enc.rope_theta"]))
         n = h.shape[0]
+        npre = n - rows.shape[0]                  # CLS rows in front of the patch rows
+        if rope is not None and npre:             # the CLS is not rotated (identity rows)
+            rope = (np.vstack([np.ones((npre, hd)), rope[0]]), np.vstack([np.zeros((npre, hd)), rope[1]]))
+        mask = np.zeros((n, n))
+        if kv.get("jepa.enc.attn_mode") == "block_causal":
+            # LeVJEPA (docs/gguf-schema.md, levjepa note): key j visible to query i iff frame(i) >= frame(j);
+            # the CLS row is open, the CLS column closed to the patch queries
+            tpf = grid[1] * grid[2]
+            frame = np.concatenate([np.full(npre, -1), np.arange(n - npre) // tpf])
+            vis = (frame[:, None] >= frame[None, :]) & (frame[None, :] >= 0)
+            vis[:npre] = True
+            mask[~vis] = -np.inf
         for i in range(L):
             p = f"enc.blk.{i}."
             a = _ln(h, T(p + "ln1.weight"), T(p + "ln1.bias"), eps)
@@ -98,7 +110,7 @@ def forward64(path, x):
             v = v.astype(np.float32).astype(np.float16).astype(np.float64)
             att = np.zeros((n, H, hd))
             for hh in range(H):
-                s = q[:, hh] @ k[:, hh].T / math.sqrt(hd)
+                s = q[:, hh] @ k[:, hh].T / math.sqrt(hd) + mask
                 pr = np.exp(s - s.max(1, keepdims=True))
                 att[:, hh] = (pr / pr.sum(1, keepdims=True)) @ v[:, hh]
             o = att.reshape(n, D) @ T(p + "attn_out.weight").T + T(p + "attn_out.bias")
@@ -116,7 +128,7 @@ def forward64(path, x):
 
 
 @pytest.mark.parametrize("family,kw", [("hfvit", {}), ("hfvit", {"layer_scale": True}), ("vjepa2", {}),
-                                       ("vjepa2_1", {})])
+                                       ("vjepa2_1", {}), ("levjepa", {})])
 def test_oracle_encoder_matches_float64_forward(family, kw, tmp_path):
     cfg = forge.tiny(family, "f32", ln_random=True, **kw)
     path = forge.cached_model(cfg, str(tmp_path))

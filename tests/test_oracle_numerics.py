@@ -263,3 +263,49 @@ def test_attention_against_float64():
         p = np.exp(s - s.max(1, keepdims=True))
         ref[:, sl] = (p / p.sum(1, keepdims=True)) @ vh
     assert np.abs(out - ref).max() <= 2e-5 * np.abs(ref).max()
+
+
+# ------------------------------------------------------------------------------------ block-causal mask
+@pytest.mark.parametrize("gt,gh,gw,npre", [(4, 4, 4, 1), (3, 5, 7, 0), (2, 2, 3, 2)])
+def test_block_causal_mask_rule(oracle, gt, gh, gw, npre):
+    """Every entry against the rule of the reference's mask test (tests/test-ops.cpp:271-290): prefix
+    rows see everything; a patch query sees a patch key of its own or an earlier temporal slot and
+    never a prefix key; closed entries are -inf."""
+    m = oracle.block_causal_mask(gt, gh, gw, npre)
+    tpf = gh * gw
+    n = npre + gt * tpf
+    i, j = np.meshgrid(np.arange(n), np.arange(n), indexing="ij")
+    want = (i < npre) | ((j >= npre) & ((j - npre) // tpf <= (i - npre) // tpf))
+    assert m.shape == (n, n)
+    assert np.array_equal(m == 0.0, want)
+    assert np.all(np.isneginf(m[~want]))
+
+
+def test_block_causal_mask_levjepa_density(oracle):
+    """16 x 14 x 14 + CLS = 3137 rows: 53.1 % of the entries are open (docs/gguf-schema.md, levjepa note)."""
+    m = oracle.block_causal_mask(16, 14, 14, 1)
+    assert m.shape == (3137, 3137)
+    assert round(100.0 * float((m == 0.0).mean()), 1) == 53.1
+
+
+def test_masked_attention_matches_visible_key_softmax(oracle):
+    """or_attention with the additive mask equals softmax over the visible keys only (double reference),
+    and a row with no visible key gives zeros."""
+    rng = np.random.default_rng(3)
+    n, H, hd = 65, 2, 64
+    q = rng.standard_normal((n, H * hd)).astype(np.float32)
+    k = rng.standard_normal((n, H * hd)).astype(np.float32)
+    v = rng.standard_normal((n, H * hd)).astype(np.float32)
+    m = oracle.block_causal_mask(4, 4, 4, 1)
+    m[5] = -np.inf                                   # a row with nothing visible
+    got = oracle.attention(q, k, v, H, kv_f16=False, mask=m)
+    for h in range(H):
+        sl = slice(h * hd, (h + 1) * hd)
+        s = q[:, sl].astype(np.float64) @ k[:, sl].astype(np.float64).T / 8.0 + m
+        with np.errstate(invalid="ignore"):
+            p = np.exp(s - s.max(1, keepdims=True))
+        p[5] = 0.0
+        den = p.sum(1, keepdims=True)
+        ref = np.where(den > 0, p @ v[:, sl].astype(np.float64) / np.where(den > 0, den, 1), 0.0)
+        assert np.abs(got[:, sl] - ref).max() < 1e-5
+    assert np.all(got[5] == 0.0)
