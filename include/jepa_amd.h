@@ -79,6 +79,15 @@ int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64
                        const float * rope_c_dev, const float * rope_s_dev, int n_prefix, int64_t tokens_per_slot,
                        int out_type, void * out_dev);
 
+/* jepa_preprocess_frames_rgb_ex on the device: n_frames RGB8 HWC frames of h x w, contiguous in device
+ * memory ([n_frames][h][w][3]), are resized (uint8 antialias), centre-cropped and normalised into
+ * out_dev, NCTHW f32 [3][n_frames][crop][crop] (N = 1), bit-identical to the host function. The clip
+ * then goes to jepa_amd_encode_device without a host round trip, and only uint8 frames cross PCIe.
+ * out_cap is out_dev's size in floats; out_h / out_w receive the crop. Returns 0, or -1 with the
+ * reason in jepa_error_text(). Replaces the host half of reference src/preprocess.cpp:233-300. */
+int jepa_amd_preprocess_frames_device(int device, const jepa_preprocess_params * p, const uint8_t * frames_dev, int n_frames, int h,
+                                      int w, float * out_dev, int64_t out_cap, int * out_h, int * out_w);
+
 /* One v_mfma_f32_32x32x16_f16 on host matrices a [32][16], b [16][32] -> d [32][32] (row-major),
  * written back through the accumulator layout the GEMM epilogues assume. */
 int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * d);

@@ -2,6 +2,7 @@
 #include "../../include/jepa_amd.h"
 #include "model.h"
 #include "kernels.h"
+#include "preprocess.h"
 
 #include <cstring>
 #include <vector>
@@ -322,4 +323,27 @@ extern "C" int jepa_amd_copy(int device, const float * src, float * dst, int64_t
     if (ms) *ms = t / reps;
     hipEventDestroy(e0); hipEventDestroy(e1);
     return rc;
+}
+
+extern "C" int jepa_amd_preprocess_frames_device(int device, const jepa_preprocess_params * p, const uint8_t * frames, int n_frames, int h,
+                                                 int w, float * out, int64_t out_cap, int * out_h, int * out_w) {
+    if (!p || !frames || !out || n_frames <= 0 || h <= 0 || w <= 0) return -1;
+    pre_plan g;
+    if (!pre_plan_for(p, h, w, g)) return -1;
+    const int64_t need = (int64_t) 3 * n_frames * g.crop * g.crop;
+    if (out_cap < need) {
+        jepa_log("jepa: jepa_amd_preprocess_frames_device: output holds %lld floats, %lld needed\n", (long long) out_cap, (long long) need);
+        return -1;
+    }
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    void * scratch = d.alloc(preprocess_scratch_bytes(p, g, n_frames, h, w));
+    if (!scratch) return -1;
+    if (!launch_preprocess(p, g, frames, n_frames, h, w, out, scratch, d.s)) {
+        jepa_log("jepa: jepa_amd_preprocess_frames_device: launch failed\n");
+        return -1;
+    }
+    if (out_h) *out_h = g.crop;
+    if (out_w) *out_w = g.crop;
+    return d.finish();
 }

@@ -20,13 +20,7 @@ int nope(const char * fn) {
 
 extern "C" {
 
-float * jepa_preprocess_image_file(const jepa_model *, const char *, int *, int *) { NOPE_PTR("jepa_preprocess_image_file"); }
-float * jepa_preprocess_image_rgb(const jepa_model *, const uint8_t *, int, int, int *, int *) { NOPE_PTR("jepa_preprocess_image_rgb"); }
-float * jepa_preprocess_frames_rgb(const jepa_model *, const uint8_t * const *, int, int, int, int *, int *) { NOPE_PTR("jepa_preprocess_frames_rgb"); }
-float * jepa_preprocess_image_rgb_ex(const jepa_preprocess_params *, const uint8_t *, int, int, int *, int *) { NOPE_PTR("jepa_preprocess_image_rgb_ex"); }
-float * jepa_preprocess_frames_rgb_ex(const jepa_preprocess_params *, const uint8_t * const *, int, int, int, int *, int *) { NOPE_PTR("jepa_preprocess_frames_rgb_ex"); }
-uint8_t * jepa_load_image_rgb(const char *, int *, int *) { NOPE_PTR("jepa_load_image_rgb"); }
-void jepa_resize_antialias_u8(const uint8_t *, int, int, int, uint8_t *, int, int, int) { nope("jepa_resize_antialias_u8"); }
+
 
 int jepa_lewm_project(jepa_context *, const jepa_output *, jepa_output *) { NOPE_INT("jepa_lewm_project"); }
 int jepa_lewm_project_rows(jepa_context *, const float *, int, jepa_output *) { NOPE_INT("jepa_lewm_project_rows"); }

@@ -82,6 +82,15 @@ def lib() -> C.CDLL:
         "jepa_device_name": (cp, [C.c_int]),
         "jepa_device_description": (cp, [C.c_int]),
         "jepa_preprocess_default_params": (PreprocessParams, [vp]),
+        "jepa_preprocess_frames_rgb_ex": (C.POINTER(C.c_float), [C.POINTER(PreprocessParams), C.POINTER(C.c_void_p), C.c_int, C.c_int,
+                                                                 C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "jepa_preprocess_image_rgb_ex": (C.POINTER(C.c_float), [C.POINTER(PreprocessParams), vp, C.c_int, C.c_int,
+                                                                C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "jepa_preprocess_image_file": (C.POINTER(C.c_float), [vp, cp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "jepa_load_image_rgb": (C.POINTER(C.c_uint8), [cp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "jepa_resize_antialias_u8": (None, [vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, C.c_int, C.c_int]),
+        "jepa_amd_preprocess_frames_device": (C.c_int, [C.c_int, C.POINTER(PreprocessParams), vp, C.c_int, C.c_int, C.c_int, vp, i64,
+                                                        C.POINTER(C.c_int), C.POINTER(C.c_int)]),
         "jepa_pool_mean": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
         "jepa_pool_cls": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
         "jepa_softmax": (None, [vp, C.c_int, vp]),
@@ -218,3 +227,43 @@ class Context:
             self.close()
         except Exception:
             pass
+
+
+# ------------------------------------------------------------------------------------------------
+# preprocessing helpers (host functions of include/jepa.h; numpy in, numpy out)
+# ------------------------------------------------------------------------------------------------
+def resize_u8(img: np.ndarray, out_h: int, out_w: int, resample: int = 0) -> np.ndarray:
+    """jepa_resize_antialias_u8 on an HWC uint8 array"""
+    img = np.ascontiguousarray(img, dtype=np.uint8)
+    h, w, c = img.shape
+    out = np.zeros((out_h, out_w, c), np.uint8)
+    lib().jepa_resize_antialias_u8(img.ctypes.data, h, w, c, out.ctypes.data, out_h, out_w, resample)
+    return out
+
+
+def preprocess_frames(params: PreprocessParams, frames) -> np.ndarray:
+    """jepa_preprocess_frames_rgb_ex on a list of equal HWC uint8 frames -> [3][T][crop][crop] float32"""
+    frames = [np.ascontiguousarray(f, dtype=np.uint8) for f in frames]
+    h, w, _ = frames[0].shape
+    ptrs = (C.c_void_p * len(frames))(*[f.ctypes.data for f in frames])
+    oh, ow = C.c_int(0), C.c_int(0)
+    L = lib()
+    r = L.jepa_preprocess_frames_rgb_ex(C.byref(params), ptrs, len(frames), h, w, C.byref(oh), C.byref(ow))
+    if not r:
+        raise RuntimeError(f"jepa_preprocess_frames_rgb_ex failed: {error_text().strip()}")
+    n = 3 * len(frames) * oh.value * ow.value
+    out = np.ctypeslib.as_array(r, shape=(n,)).copy().reshape(3, len(frames), oh.value, ow.value)
+    L.jepa_free(C.cast(r, C.c_void_p))
+    return out
+
+
+def load_image(path: str) -> np.ndarray:
+    """jepa_load_image_rgb -> HWC uint8"""
+    h, w = C.c_int(0), C.c_int(0)
+    L = lib()
+    r = L.jepa_load_image_rgb(path.encode(), C.byref(h), C.byref(w))
+    if not r:
+        raise RuntimeError(f"jepa_load_image_rgb({path}) failed: {error_text().strip()}")
+    out = np.ctypeslib.as_array(r, shape=(h.value * w.value * 3,)).copy().reshape(h.value, w.value, 3)
+    L.jepa_free(C.cast(r, C.c_void_p))
+    return out

@@ -395,3 +395,36 @@ def test_attention_fused_q8_0_equals_separate_quantizer(jlib, oracle, n_items, n
     assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, 0, 0, gguf.GGML_Q8_0, oq.data_ptr()) == 0
     want = oracle.quantize_act(oracle.OR_Q8_0, host(o32))
     np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))
+
+
+# ------------------------------------------------------------------------------------------------ ingest
+def _pre_params(jlib, resize_short=224, crop=224, resample=0, mode=0, fused=True):
+    p = jlib.PreprocessParams()
+    for c, (m, sd) in enumerate(zip((0.485, 0.456, 0.406), (0.229, 0.224, 0.225))):
+        p.mean[c], p.std[c] = m, sd
+    p.resize_short, p.crop, p.resample, p.resize_mode, p.rescale, p.fused_norm = resize_short, crop, resample, mode, 1.0 / 255.0, fused
+    return p
+
+
+@pytest.mark.parametrize("hw,kw", [((300, 400), {}), ((400, 300), dict(resample=1)), ((256, 256), dict(resize_short=256, crop=256)),
+                                   ((180, 320), dict(mode=1, resize_short=224)), ((200, 260), dict(crop=320, fused=False)),
+                                   ((1080, 1920), dict(resample=1))])
+def test_preprocess_device_equals_host(jlib, hw, kw):
+    """jepa_amd_preprocess_frames_device (uint8 frames on the device -> NCTHW floats) equals the host
+    jepa_preprocess_frames_rgb_ex bit for bit: down / up / identity resizes, bicubic, squash, a crop
+    larger than the image (zero padding), the unfused normalisation, a 1080p frame."""
+    rng = np.random.default_rng(hw[0] + hw[1])
+    T = 3
+    frames = rng.integers(0, 256, (T, hw[0], hw[1], 3), dtype=np.uint8)
+    p = _pre_params(jlib, **kw)
+    want = jlib.preprocess_frames(p, list(frames))
+    d = torch.from_numpy(frames).cuda()
+    out = torch.zeros(want.size, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    oh, ow = C.c_int(0), C.c_int(0)
+    rc = jlib.lib().jepa_amd_preprocess_frames_device(0, C.byref(p), d.data_ptr(), T, hw[0], hw[1], out.data_ptr(), out.numel(),
+                                                     C.byref(oh), C.byref(ow))
+    assert rc == 0, jlib.error_text()
+    assert (oh.value, ow.value) == want.shape[2:]
+    got = host(out).reshape(want.shape)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{int((got != want).sum())} values differ"
