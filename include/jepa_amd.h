@@ -88,6 +88,14 @@ int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64
 int jepa_amd_preprocess_frames_device(int device, const jepa_preprocess_params * p, const uint8_t * frames_dev, int n_frames, int h,
                                       int w, float * out_dev, int64_t out_cap, int * out_h, int * out_w);
 
+/* Split-K of the q8_0 / q4_0 GEMMs (two workgroups per output tile, one per K half, the second to
+ * finish adding the first's partial sums): jepa_amd_gemm_split forces it off (1), on where the shape
+ * allows (2) or back to the automatic choice (-1) for later launches; jepa_amd_gemm_split_of returns
+ * the halves a GEMM of this weight type and shape runs in with the residual or plain f32 epilogue
+ * (the choice depends on n_out and n_in only; the other epilogues do not split). */
+int jepa_amd_gemm_split(int split);
+int jepa_amd_gemm_split_of(int wtype, int64_t n_out, int64_t n_in);
+
 /* One v_mfma_f32_32x32x16_f16 on host matrices a [32][16], b [16][32] -> d [32][32] (row-major),
  * written back through the accumulator layout the GEMM epilogues assume. */
 int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * d);

@@ -47,6 +47,16 @@ struct dev_scope {
     }
 };
 
+// split-K scratch for n_rows-row GEMMs, counters zeroed
+bool alloc_split(dev_scope & d, gemm_split_ws & sw, int64_t n_rows) {
+    gemm_split_ws_size(n_rows, &sw.part_floats, &sw.cnt_n);
+    sw.part = (float *) d.alloc((size_t) sw.part_floats * 4);
+    sw.cnt = (int *) d.alloc((size_t) sw.cnt_n * 4);
+    if (!sw.part || !sw.cnt) return false;
+    launch_fill_zero(sw.cnt, (size_t) sw.cnt_n * 4, d.s);
+    return true;
+}
+
 bool alloc_act(dev_scope & d, act_view & a, int fmt, int64_t M, int64_t K) {
     a.fmt = fmt;
     a.ld = K;
@@ -189,15 +199,17 @@ extern "C" int jepa_amd_matmul(int device, int wtype, const void * w, int64_t n_
     act_view a;
     if (!alloc_act(d, a, L.act(), n_rows, n_in)) return -1;
     launch_rownorm_quant(x, n_rows, n_in, nullptr, nullptr, 0.0f, false, a, d.s);
+    gemm_split_ws sw;
+    if (!alloc_split(d, sw, n_rows)) return -1;
     gemm_epi ep;
     ep.kind = EPI_F32;
     ep.y = y; ep.ldy = n_out; ep.rin = n_rows; ep.rout = n_rows; ep.pre = 0;
     hipEvent_t e0, e1;
     hipEventCreate(&e0); hipEventCreate(&e1);
     if (reps < 1) reps = 1;
-    launch_gemm(L, a, n_rows, ep, d.s);   // warm-up (and the result when reps == 1)
+    launch_gemm(L, a, n_rows, ep, d.s, &sw);   // warm-up (and the result when reps == 1)
     hipEventRecord(e0, d.s);
-    for (int i = 0; i < reps; i++) launch_gemm(L, a, n_rows, ep, d.s);
+    for (int i = 0; i < reps; i++) launch_gemm(L, a, n_rows, ep, d.s, &sw);
     hipEventRecord(e1, d.s);
     const int rc = d.finish();
     float ms = 0;
@@ -240,9 +252,11 @@ extern "C" int jepa_amd_matmul_gelu(int device, int wtype, const void * w, int64
     hipEvent_t e0, e1;
     hipEventCreate(&e0); hipEventCreate(&e1);
     if (reps < 1) reps = 1;
-    launch_gemm(L, a, n_rows, ep, d.s);   // warm-up (and the result when reps == 1)
+    gemm_split_ws sw;
+    if (!alloc_split(d, sw, n_rows)) return -1;
+    launch_gemm(L, a, n_rows, ep, d.s, &sw);   // warm-up (and the result when reps == 1)
     hipEventRecord(e0, d.s);
-    for (int i = 1; i < reps; i++) launch_gemm(L, a, n_rows, ep, d.s);
+    for (int i = 1; i < reps; i++) launch_gemm(L, a, n_rows, ep, d.s, &sw);
     hipEventRecord(e1, d.s);
     if (out_type == T_Q8_0 || out_type == T_Q8_K) launch_pack_act_blocks(o, n_rows, n_out, out, d.s);
     const int rc = d.finish();
@@ -251,6 +265,13 @@ extern "C" int jepa_amd_matmul_gelu(int device, int wtype, const void * w, int64
     if (gemm_ms) *gemm_ms = reps > 1 ? ms / (reps - 1) : 0.0;
     hipEventDestroy(e0); hipEventDestroy(e1);
     return rc;
+}
+
+extern "C" int jepa_amd_gemm_split(int split) { return gemm_force_split(split); }
+
+extern "C" int jepa_amd_gemm_split_of(int wtype, int64_t n_out, int64_t n_in) {
+    const int wf = wtype == T_Q8_0 || wtype == T_Q4_0 ? W_Q32 : wtype == T_Q4_K ? W_Q4K : wtype == T_F16 ? W_F16 : W_F32;
+    return gemm_split_for(wf, n_out, n_in);
 }
 
 extern "C" int jepa_amd_gemm_tile(int index) {

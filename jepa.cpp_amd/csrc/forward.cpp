@@ -37,6 +37,7 @@ struct fwd_workspace {
     void * Q = nullptr, * Kt = nullptr, * Vt = nullptr;
     float * attn = nullptr, * ff = nullptr, * out = nullptr;
     float * rope_c = nullptr, * rope_s = nullptr;
+    gemm_split_ws split;         // split-K GEMM scratch (counters zeroed once, left zero by every launch)
     // graph
     hipGraphExec_t exec = nullptr;
     const float * g_in = nullptr; float * g_out = nullptr;
@@ -178,6 +179,10 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
         dalloc(*w, &w->Vt, (size_t) n_items * H * w->R_pad * hd * 2) && dalloc(*w, (void **) &w->attn, (size_t) rows * D * 4) &&
         dalloc(*w, (void **) &w->ff, (size_t) rows * F * 4) && dalloc(*w, (void **) &w->out, (size_t) rows * D * 4);
     if (!ok) { ctx->ws.reset(); return false; }
+    gemm_split_ws_size(rows, &w->split.part_floats, &w->split.cnt_n);
+    if (!dalloc(*w, (void **) &w->split.part, (size_t) w->split.part_floats * 4) ||
+        !dalloc(*w, (void **) &w->split.cnt, (size_t) w->split.cnt_n * 4)) { ctx->ws.reset(); return false; }
+    launch_fill_zero(w->split.cnt, (size_t) w->split.cnt_n * 4, ctx->stream);
     // Q/K/V^T padding rows are read by the attention kernel: zero them once (never written again)
     launch_fill_zero(w->Q, (size_t) n_items * H * w->R_pad * hd * 2, ctx->stream);
     launch_fill_zero(w->Kt, (size_t) n_items * H * w->R_pad * hd * 2, ctx->stream);
@@ -269,7 +274,7 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
         ep.rin = w.Np; ep.rout = R; ep.pre = w.prefix;
         if (w.video && e.modality_embed) ep.addvec = w.image_path ? m->mod_img : m->mod_video;
         if (!w.video && m->pos_embed) ep.addrows = m->pos_embed;
-        kt.run("patch_embed", [&] { launch_gemm(pe, pa, n_items * w.Np, ep, s); });
+        kt.run("patch_embed", [&] { launch_gemm(pe, pa, n_items * w.Np, ep, s, &w.split); });
         // CLS row in front: image families add its position row; the video family with one (levjepa)
         // gives it no position (reference src/jepa.cpp:865-880)
         if (e.cls_token)
@@ -290,7 +295,7 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
             ep.q = w.Q; ep.k = w.Kt; ep.vt = w.Vt;
             ep.rope_c = w.rope_c; ep.rope_s = w.rope_s;
             ep.n_head = H; ep.hd = hd; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
-            kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s); }, "qkv");
+            kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
         }
         w.actA.fmt = L.out.act();
         if (w.actA.fmt == A_Q8_0) {
@@ -309,7 +314,7 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
         {
             gemm_epi ep;
             ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls1;
-            kt.run(gemm_class(L.out), [&] { launch_gemm(L.out, w.actA, rows, ep, s); }, "out");
+            kt.run(gemm_class(L.out), [&] { launch_gemm(L.out, w.actA, rows, ep, s, &w.split); }, "out");
         }
         // MLP half
         w.actA.fmt = L.up.act();
@@ -325,14 +330,14 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
             }
             else if (mfma && w.actB.fmt == A_F16) { ep.kind = EPI_GELU_F16; ep.oh = w.actB.q; }
             else { ep.kind = EPI_GELU_F32; ep.y = w.ff; }
-            kt.run(gemm_class(L.up), [&] { launch_gemm(L.up, w.actA, rows, ep, s); }, "up");
+            kt.run(gemm_class(L.up), [&] { launch_gemm(L.up, w.actA, rows, ep, s, &w.split); }, "up");
             if (ep.kind == EPI_GELU_F32)
                 kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, w.actB, s); }, "ff");
         }
         {
             gemm_epi ep;
             ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls2;
-            kt.run(gemm_class(L.down), [&] { launch_gemm(L.down, w.actB, rows, ep, s); }, "down");
+            kt.run(gemm_class(L.down), [&] { launch_gemm(L.down, w.actB, rows, ep, s, &w.split); }, "down");
         }
         if (trace) launch_copy_f32(w.x, trace + (int64_t) (l + 1) * rows * D, rows * D, s);
     }

@@ -38,6 +38,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef int i4v __attribute__((ext_vector_type(4)));
 typedef int i16v __attribute__((ext_vector_type(16)));
+typedef unsigned int u4v __attribute__((ext_vector_type(4)));
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
 #define MFMA8(a, b, c) __builtin_amdgcn_mfma_f32_32x32x8f16((a), (b), (c), 0, 0, 0)
@@ -56,6 +57,9 @@ struct kargs {
     int64_t M, N, K;
     int tn, tm;              // workgroup tiles along N and M
     int xa, xb;              // tiles per XCD block along N and M (0: plain order)
+    int split;               // K halves computed by separate workgroups (1 or 2; q8_0 / q4_0 only)
+    float * part;            // split: raw accumulators of every workgroup [split][tiles][BN*BM]
+    int * cnt;               // split: arrivals per tile (0 between launches)
     gemm_epi ep;
 };
 
@@ -244,19 +248,29 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // Workgroups are dealt to the 8 XCDs round-robin (workgroup w runs on XCD w % 8). Each XCD gets one
     // block of xa x xb tiles, chosen on the host so that the weight and activation rows the XCD's L2
     // has to fetch (xa BN + xb BM rows per K-column) are fewest.
+    // split-K (residual and plain epilogues only; elsewhere it folds away): workgroups
+    // [s * tiles, (s + 1) * tiles) compute K half s of every tile
+    constexpr bool SPLITTABLE = (WF == W_Q32 || WF == W_Q4K) && (EPI == EPI_RESID || EPI == EPI_F32);
+    const int split = SPLITTABLE ? a.split : 1;
+    const int ntile = a.tn * a.tm;
+    const int sp = split > 1 ? (int) blockIdx.x / ntile : 0;
+    const int bid = (int) blockIdx.x - sp * ntile;
     int64_t tni, tmi;
     if (a.xa > 0) {
-        const int x = (int) (blockIdx.x & 7), slot = (int) (blockIdx.x >> 3);
+        const int x = bid & 7, slot = bid >> 3;
         const int nbn = a.tn / a.xa;
         tni = (int64_t) (x % nbn) * a.xa + slot / a.xb;
         tmi = (int64_t) (x / nbn) * a.xb + slot % a.xb;
     } else {
-        tni = blockIdx.x / a.tm;
-        tmi = blockIdx.x - tni * a.tm;
+        tni = bid / a.tm;
+        tmi = bid - tni * a.tm;
     }
     const int64_t n0 = tni * BN, m0 = tmi * T::BM;
     const int64_t K = a.K, M = a.M, KB = K >> 5;
-    const int64_t nst = (K + KC - 1) / KC;            // q8_0 / q4_0: the last stage may hold 64 columns
+    // stages of this workgroup (q8_0 / q4_0: the last stage may hold 64 columns; a split has whole
+    // stages per half) and the K-stage its addresses start at
+    const int64_t nst = split > 1 ? K / KC / split : (K + KC - 1) / KC;
+    const int64_t kst0 = (int64_t) sp * nst;
     const int64_t rowbytes = K * ESZ;
 
     // buffer resources rebased at the tile's first weight row and first token, so that every copy's
@@ -285,7 +299,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     static_assert((8 * NW) % 16 == 0, "copy rows of a wave must agree modulo 16");
     auto issue_tile = [&](int64_t st, int64_t sa, int i) {
         unsigned char * base = smem + (int) (st % NST) * T::STAGE;
-        const int64_t k0 = sa * KC;
+        const int64_t k0 = (sa + kst0) * KC;
         const int c = lds_slot(8 * wave + (lane >> 3), lane & 7);
         const uint32_t soff = (uint32_t) (k0 * ESZ);
         const uint32_t cb = 16 * ((k0 * ESZ + 128 > rowbytes) ? (c & 3) : c);
@@ -300,7 +314,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // another wave's copy (the same bytes to the same place).
     [[maybe_unused]] auto issue_scales = [&](int64_t st, int64_t sa, int p) {
         unsigned char * base = smem + (int) (st % NST) * T::STAGE;
-        const uint32_t kb0 = (uint32_t) ((sa * KC) >> 5);
+        const uint32_t kb0 = (uint32_t) (((sa + kst0) * KC) >> 5);
         const uint32_t kbo = (kb0 + 2 < KB) ? 2 * (lane & 1) : 0;
         int L = wave + NW * p;
         if (L >= T::ROWS / 32) L = wave % (T::ROWS / 32);
@@ -321,8 +335,10 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     auto issue_xsb = [&](int64_t st) {
         if constexpr (WF == W_Q4K) {
             if ((st & 3) == 0) {
-                const uint32_t sb = (uint32_t) (st >> 2);
-                unsigned char * xb = smem + NST * T::STAGE + (int) (sb & 1) * T::XSB;
+                // buffer by this workgroup's super-block count, data of K super-block sb (a split
+                // starts at a super-block boundary)
+                const uint32_t sb = (uint32_t) ((st + kst0) >> 2);
+                unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 2) & 1) * T::XSB;
                 constexpr int N1 = BN / 64, N2 = BN / 32, N3 = T::BM / 64, N4 = T::BM / 32;
                 for (int L = wave; L < N1 + N2 + N3 + N4; L += NW) {
                     if (L < N1) {
@@ -628,7 +644,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
 
     // q8_0 / q4_0 with K % 128 == 64 end in a half stage, peeled off the loop so that the loop body
     // has one path (the accumulators then stay in place across iterations)
-    const int64_t nfull = WF == W_Q32 ? K / KC : nst;
+    const int64_t nfull = WF == W_Q32 ? (split > 1 ? nst : K / KC) : nst;
     if constexpr (WF == W_Q32) {
         q32_main(nfull);
     } else if constexpr (PIPE16) {
@@ -690,6 +706,49 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             for (int j = 0; j < TJ; j++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[i][j][r] = __fsub_rn(acc[i][j][r], accm[i][j][r]);
+    }
+
+    if constexpr (SPLITTABLE) {
+        if (split > 1) {
+            // Publish this half's accumulators; of the two workgroups of a tile, the second to arrive
+            // adds the other's (a + b == b + a, so the result does not depend on which one that is)
+            // and runs the epilogue, the first leaves. Nothing waits on another workgroup.
+            // The partials bypass the XCD-private L2s (cache policy sc1, what agent-scope atomic loads
+            // and stores use), so no L2 write-back or invalidation is needed: once this wave's stores
+            // have completed (vmcnt(0)) they are visible to every XCD, and the arrival counter is an
+            // agent-coherent atomic.
+            constexpr int TT = TI * TJ, SC1 = 16;
+            const int64_t tile_floats = (int64_t) BN * T::BM;
+            const brsrc rmine = make_brsrc(a.part + ((int64_t) sp * ntile + bid) * tile_floats, tile_floats * 4);
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f16v & v = acc[t / TJ][t % TJ];
+                    const u4v b = {__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
+                                   __float_as_uint(v[4 * q + 3])};
+                    __builtin_amdgcn_raw_buffer_store_b128(b, rmine, ((t * 4 + q) * T::NT + tid) * 16, 0, SC1);
+                }
+            __builtin_amdgcn_s_waitcnt(0x0f70);    // vmcnt(0): this wave's partial has been written
+            __syncthreads();
+            int * flag = (int *) smem;              // the stage buffers are free (all copies landed)
+            if (tid == 0) flag[0] = atomicAdd(a.cnt + bid, 1);
+            __syncthreads();
+            if (flag[0] == 0) return;               // first of the pair
+            if (tid == 0) __hip_atomic_store(a.cnt + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next launch
+            const brsrc rother = make_brsrc(a.part + ((int64_t) (1 - sp) * ntile + bid) * tile_floats, tile_floats * 4);
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const u4v o = __builtin_amdgcn_raw_buffer_load_b128(rother, ((t * 4 + q) * T::NT + tid) * 16, 0, SC1);
+                    f16v & v = acc[t / TJ][t % TJ];
+                    v[4 * q] = __fadd_rn(v[4 * q], __uint_as_float(o.x)); v[4 * q + 1] = __fadd_rn(v[4 * q + 1], __uint_as_float(o.y));
+                    v[4 * q + 2] = __fadd_rn(v[4 * q + 2], __uint_as_float(o.z)); v[4 * q + 3] = __fadd_rn(v[4 * q + 3], __uint_as_float(o.w));
+                }
+                __builtin_amdgcn_sched_barrier(0);   // one tile's loads in flight at a time (registers)
+            }
+        }
     }
 
     if constexpr (EPI == EPI_GELU_Q8_K) {
@@ -936,6 +995,8 @@ constexpr tile_cfg k_tiles[] = {{4, 2, 2, 2}, {2, 4, 3, 1}, {2, 4, 2, 1}, {4, 2,
 constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66, 0.8};
 
 std::atomic<int> g_force_tile{-1};
+std::atomic<int> g_force_split{-1};
+constexpr int64_t SPLIT_MAX_N = 1024;
 
 int cu_count() {
     static std::atomic<int> cache[64];
@@ -952,7 +1013,7 @@ int cu_count() {
 // The tile with the least estimated time: whole waves of workgroups over the CUs (one workgroup per
 // CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N; q4_K
 // skips the 256x128 tile (its three accumulator sets do not fit 256 VGPRs with two waves per SIMD).
-int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0) {
+int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
     const int f = g_force_tile.load();
     const int nt = (int) (sizeof(k_tiles) / sizeof(k_tiles[0]));
     const auto bn_of = [](int c) { return 32 * k_tiles[c].wn * k_tiles[c].ti; };
@@ -964,7 +1025,7 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0) {
         const int64_t bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
         if (N % bn || (need_bn && bn != need_bn)) continue;
         if (wf == W_Q4K && c == 0) continue;
-        const int64_t t = (N / bn) * ((M + bm - 1) / bm);
+        const int64_t t = (N / bn) * ((M + bm - 1) / bm) * split;
         const double waves = (double) ((t + cus - 1) / cus);
         const double cost = waves * (double) (bn * bm) / k_tile_eff[c];
         if (cost < best) { best = cost; b = c; }
@@ -974,7 +1035,7 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0) {
 
 template <int WF, int EPI>
 void launch_tiles(int c, const kargs & a, hipStream_t s) {
-    const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm);
+    const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm * (a.split > 1 ? a.split : 1));
     if constexpr (EPI == EPI_GELU_Q8_K) {   // 256-wide tiles only (pick_tile keeps to them)
         if (c == 6) k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a);
         if constexpr (WF != W_Q4K)   // q4_K never takes the 256x128 tile
@@ -993,8 +1054,11 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
 }
 
 template <int WF>
-void dispatch_mfma(kargs a, hipStream_t s) {
-    const int c = pick_tile(WF, a.N, a.M, a.ep.kind == EPI_GELU_Q8_K ? 256 : 0);
+void dispatch_mfma(kargs a, hipStream_t s, const gemm_split_ws * sw) {
+    // split-K runs with the residual and plain epilogues (the N <= 1024 GEMMs of an encoder block)
+    a.split = sw && sw->part && sw->cnt && (a.ep.kind == EPI_RESID || a.ep.kind == EPI_F32) ? gemm_split_for(WF, a.N, a.K) : 1;
+    a.part = nullptr; a.cnt = nullptr;
+    const int c = pick_tile(WF, a.N, a.M, a.ep.kind == EPI_GELU_Q8_K ? 256 : 0, a.split);
     if (c < 0) {
         jepa_log("jepa: internal error: no 256-wide GEMM tile for the q8_K epilogue (N = %lld)\n", (long long) a.N);
         return;
@@ -1002,6 +1066,14 @@ void dispatch_mfma(kargs a, hipStream_t s) {
     const int bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
     a.tn = (int) (a.N / bn);
     a.tm = (int) ((a.M + bm - 1) / bm);
+    if (a.split > 1) {
+        const int64_t tiles = (int64_t) a.tn * a.tm;
+        if (tiles * bn * bm * a.split > sw->part_floats || tiles > sw->cnt_n) {
+            jepa_log("jepa: internal error: split-K scratch too small for %lld tiles\n", (long long) tiles);
+            return;
+        }
+        a.part = sw->part; a.cnt = sw->cnt;
+    }
     // XCD blocks: eight xa x xb blocks tiling the tn x tm grid, least rows per block
     a.xa = a.xb = 0;
     const int64_t ntile = (int64_t) a.tn * a.tm;
@@ -1027,7 +1099,26 @@ void dispatch_mfma(kargs a, hipStream_t s) {
 
 }  // namespace
 
-void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm_epi & ep, hipStream_t s) {
+int gemm_split_for(int wf, int64_t N, int64_t K) {
+    // q8_0 / q4_0 GEMMs with N <= 1024 cannot fill 256 CUs with tiles big enough to run well
+    // (2048 tokens x 1024 outputs is 64 tiles of 256x128); two workgroups per tile, one per K half,
+    // each of whole 128-column stages. The partial-sum exchange costs a few microseconds, which pays
+    // off from K = 2048 (fc2: 43.6 -> 37.4 us) but not at K = 1024 (out-proj: 18 -> 21 us).
+    // q4_K: each half starts at a super-block (256 columns) and spans whole 4-stage super-blocks
+    if (!(wf == W_Q32 && K % 256 == 0) && !(wf == W_Q4K && K % 512 == 0)) return 1;
+    const int f = g_force_split.load();
+    if (f >= 1) return f >= 2 ? 2 : 1;
+    return N <= SPLIT_MAX_N && K >= 2048 ? 2 : 1;
+}
+
+void gemm_split_ws_size(int64_t max_rows, int64_t * part_floats, int64_t * cnt_n) {
+    // tiles x BN x BM <= (rows rounded up to 128) x N for every tile, two halves; tiles <= that / 64^2
+    const int64_t rows = (max_rows + 127) / 128 * 128;
+    *part_floats = 2 * rows * SPLIT_MAX_N;
+    *cnt_n = (rows / 64) * (SPLIT_MAX_N / 64) + 64;
+}
+
+void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm_epi & ep, hipStream_t s, const gemm_split_ws * sw) {
     kargs a{};
     a.A = (const _Float16 *) W.w;
     a.Ad = (const uint16_t *) W.wd;
@@ -1051,10 +1142,15 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
         return;
     }
     switch (W.fmt) {
-        case W_F16: dispatch_mfma<W_F16>(a, s); break;
-        case W_Q32: dispatch_mfma<W_Q32>(a, s); break;
-        case W_Q4K: dispatch_mfma<W_Q4K>(a, s); break;
+        case W_F16: dispatch_mfma<W_F16>(a, s, nullptr); break;
+        case W_Q32: dispatch_mfma<W_Q32>(a, s, sw); break;
+        case W_Q4K: dispatch_mfma<W_Q4K>(a, s, sw); break;
     }
+}
+
+int gemm_force_split(int split) {
+    g_force_split.store(split < 1 ? -1 : split > 2 ? 2 : split);
+    return 0;
 }
 
 int gemm_force_tile(int index) {

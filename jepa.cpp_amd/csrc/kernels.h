@@ -46,8 +46,22 @@ struct gemm_epi {
 
 struct dev_linear;
 
-// Y = X W^T (+ epilogue). M = rows of X.
-void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm_epi & ep, hipStream_t s);
+// Scratch of the split-K GEMMs (q8_0 / q4_0 weights with N <= 1024: two workgroups per output tile,
+// one per K half): the raw accumulators of both halves and one arrival counter per tile, which must
+// be zero before the first launch (every launch leaves them zero). Sizes from gemm_split_ws_size.
+struct gemm_split_ws {
+    float * part = nullptr;
+    int * cnt = nullptr;
+    int64_t part_floats = 0, cnt_n = 0;
+};
+void gemm_split_ws_size(int64_t max_rows, int64_t * part_floats, int64_t * cnt_n);
+
+// Y = X W^T (+ epilogue). M = rows of X. Without split scratch every tile is one workgroup.
+void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm_epi & ep, hipStream_t s,
+                 const gemm_split_ws * sw = nullptr);
+// K halves the GEMM of this weight format and shape runs in (1 or 2); depends on N and K only, so
+// that the summation order of an output never depends on the number of rows
+int gemm_split_for(int wf, int64_t N, int64_t K);
 
 // LayerNorm (ggml_norm + affine) of x [M][D] written in `out` format; w/b may be null (no affine).
 // out.fmt A_F32 writes f32 rows into out.q. When normalize == false the rows are only quantized.
@@ -77,6 +91,8 @@ void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, voi
 // force the MFMA GEMM onto workgroup tile `index` (0..5) for every later launch whose N it divides;
 // -1 restores the automatic choice. Returns -1 for an index past the table.
 int gemm_force_tile(int index);
+// force the split-K choice: 1 off, 2 on where the shape allows it, -1 automatic
+int gemm_force_split(int split);
 void launch_qkv_split(const float * qkv, int64_t M, int64_t N, const gemm_epi & ep, hipStream_t s);
 void launch_dequant_rows(int gtype, const void * raw, int64_t n_rows, int64_t n_cols, float * y, hipStream_t s);
 void launch_pack_act_blocks(const act_view & a, int64_t M, int64_t K, void * blocks, hipStream_t s);

@@ -112,6 +112,8 @@ def lib() -> C.CDLL:
         "jepa_amd_mfma_probe": (C.c_int, [C.c_int, vp, vp, vp]),
         "jepa_amd_copy": (C.c_int, [C.c_int, vp, vp, i64, C.c_int, C.POINTER(C.c_double)]),
         "jepa_amd_gemm_tile": (C.c_int, [C.c_int]),
+        "jepa_amd_gemm_split": (C.c_int, [C.c_int]),
+        "jepa_amd_gemm_split_of": (C.c_int, [C.c_int, i64, i64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

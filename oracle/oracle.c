@@ -388,6 +388,11 @@ float or_vec_dot(int wtype, int64_t n, const void * wrow, const void * arow) {
  * quantized encoder. */
 static int g_reverse_blocks = 0;
 void or_set_reverse_block_order(int on) { g_reverse_blocks = on; }
+/* The blocks (q8_0 / q4_0) or super-blocks (q4_K) in k_split equal consecutive ranges, each summed in
+ * its own chain from 0 (q4_K: main and mins chains, then their difference), the range results added
+ * in order (a GEMM that gives each K range to its own worker). 1: one chain. */
+static int g_k_split = 1;
+void or_set_k_split(int s) { g_k_split = s < 1 ? 1 : s; }
 
 int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
                const float * x, int64_t n_rows, const float * bias, float * y, int n_threads) {
@@ -488,7 +493,26 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
             const int8_t * a = qa + m * n_in;
             const int8_t * q = qw + o * n_in;
             float s = 0.0f, sm = 0.0f;
-            if (wtype == OR_Q4_K) {
+            if (wtype == OR_Q4_K && g_k_split > 1 && nb % g_k_split == 0) {
+                /* each K range gives its own main and mins chains and their difference; the range
+                   results are added in order */
+                const int64_t per = nb / g_k_split;
+                for (int p = 0; p < g_k_split; p++) {
+                    float sp = 0.0f, smp = 0.0f;
+                    for (int64_t b = p * per; b < (p + 1) * per; b++) {
+                        int32_t isum = 0, msum = 0;
+                        for (int j = 0; j < 8; j++) {
+                            int32_t si = 0;
+                            for (int l = 0; l < 32; l++) si += (int32_t) q[b * QK_K + 32 * j + l] * (int32_t) a[b * QK_K + 32 * j + l];
+                            isum += scw[(o * nb + b) * 8 + j] * si;
+                            msum += mw[(o * nb + b) * 8 + j] * bsa[(m * nb + b) * 8 + j];
+                        }
+                        sp  = fmaf(dw[o * nb + b] * da[m * nb + b], (float) isum, sp);
+                        smp = fmaf(dmw[o * nb + b] * da[m * nb + b], (float) msum, smp);
+                    }
+                    s = p == 0 ? sp - smp : s + (sp - smp);
+                }
+            } else if (wtype == OR_Q4_K) {
                 for (int64_t bb = 0; bb < nb; bb++) {
                     const int64_t b = g_reverse_blocks ? nb - 1 - bb : bb;
                     int32_t isum = 0, msum = 0;
@@ -502,6 +526,17 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
                     sm = fmaf(dmw[o * nb + b] * da[m * nb + b], (float) msum, sm);
                 }
                 s = s - sm;
+            } else if (g_k_split > 1 && nb % g_k_split == 0) {
+                const int64_t per = nb / g_k_split;
+                for (int p = 0; p < g_k_split; p++) {
+                    float sp = 0.0f;
+                    for (int64_t b = p * per; b < (p + 1) * per; b++) {
+                        int32_t si = 0;
+                        for (int l = 0; l < 32; l++) si += (int32_t) q[b * 32 + l] * (int32_t) a[b * 32 + l];
+                        sp = fmaf((float) si, dw[o * nb + b] * da[m * nb + b], sp);
+                    }
+                    s = p == 0 ? sp : s + sp;
+                }
             } else {
                 for (int64_t bb = 0; bb < nb; bb++) {
                     const int64_t b = g_reverse_blocks ? nb - 1 - bb : bb;

@@ -59,6 +59,7 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
 
 /* 1: sum the per-block terms of quantized dots from the last K-block to the first (see oracle.c) */
 void or_set_reverse_block_order(int on);
+void or_set_k_split(int s);
 
 void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, const float * b,
                    float eps, float * y);

@@ -66,6 +66,8 @@ def lib() -> C.CDLL:
             getattr(L, fn).restype = None
         L.or_set_reverse_block_order.argtypes = [C.c_int]
         L.or_set_reverse_block_order.restype = None
+        L.or_set_k_split.argtypes = [C.c_int]
+        L.or_set_k_split.restype = None
         _lib = L
     return _lib
 
@@ -247,3 +249,8 @@ def gelu_erf_array(x: np.ndarray) -> np.ndarray:
 
 def set_reverse_block_order(on: bool) -> None:
     lib().or_set_reverse_block_order(1 if on else 0)
+
+
+def set_k_split(s: int) -> None:
+    """q8_0 / q4_0 dots: sum the blocks in s consecutive K ranges, one chain each, then add the chains"""
+    lib().or_set_k_split(int(s))

@@ -114,6 +114,16 @@ def test_layer_norm(jlib, oracle, out_type):
         assert frac < 1e-3, f"{frac:.2e} of the bytes differ"
 
 
+def _mul_mat_as_gpu(jlib, oracle, gtype, raw, n_out, n_in, x, bias, split=None):
+    """the oracle's mul_mat with the K split the GPU uses for this shape (q8_0 / q4_0 with N <= 1024 run
+    as two K halves whose sums are added; one chain otherwise)"""
+    oracle.set_k_split(split if split is not None else jlib.lib().jepa_amd_gemm_split_of(gtype, n_out, n_in))
+    try:
+        return oracle.mul_mat(gtype, raw, n_out, n_in, x, bias)
+    finally:
+        oracle.set_k_split(1)
+
+
 C2_SHAPES = [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)]
 
 
@@ -130,7 +140,7 @@ def test_matmul_vs_oracle(jlib, oracle, gtype, shape):
     x = rng.standard_normal((M, n_in)).astype(np.float32)
     bias = (rng.standard_normal(n_out) * 0.02).astype(np.float32)
     raw = gguf.quantize(gtype, w)
-    want = oracle.mul_mat(gtype, raw, n_out, n_in, x, bias)
+    want = _mul_mat_as_gpu(jlib, oracle, gtype, raw, n_out, n_in, x, bias)
     dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
     y = torch.zeros((M, n_out), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
@@ -153,7 +163,7 @@ def test_matmul_full_m2048_q8_0(jlib, oracle):
     w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
     x = rng.standard_normal((M, n_in)).astype(np.float32)
     raw = gguf.quantize(gguf.GGML_Q8_0, w)
-    want = oracle.mul_mat(gguf.GGML_Q8_0, raw, n_out, n_in, x, None)
+    want = _mul_mat_as_gpu(jlib, oracle, gguf.GGML_Q8_0, raw, n_out, n_in, x, None)
     dw, dx = dev(raw.reshape(-1)), dev(x)
     y = torch.zeros((M, n_out), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
@@ -188,7 +198,7 @@ def test_matmul_gelu_epilogue(jlib, oracle, gtype, out_type):
     bias = (rng.standard_normal(n_out) * 0.1).astype(np.float32)
     bias[256:512] = 0.0
     raw = w.astype(np.float16).view(np.uint8) if gtype == gguf.GGML_F16 else gguf.quantize(gtype, w)
-    pre = oracle.mul_mat(gtype, raw, n_out, n_in, x, bias)
+    pre = _mul_mat_as_gpu(jlib, oracle, gtype, raw, n_out, n_in, x, bias)
     ref = oracle.gelu_erf_array(pre)
     dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
     if out_type == gguf.GGML_F32:
@@ -247,6 +257,40 @@ def test_gelu_epilogue_every_f16_input(jlib, oracle):
     assert np.array_equal(got[x == 0], want[x == 0]) and np.all(got[x >= 6] == x[x >= 6])
 
 
+@pytest.mark.parametrize("gtype", [gguf.GGML_Q8_0, gguf.GGML_Q4_0, gguf.GGML_Q4_K])
+@pytest.mark.parametrize("shape,M", [((1024, 4096), 2048), ((1024, 1024), 389), ((256, 512), 64)])
+def test_matmul_split_k(jlib, oracle, gtype, shape, M):
+    """Split-K (two workgroups per tile, one per K half; the second to finish adds the first's partial
+    sums and runs the epilogue): forced on and off, each bit-exact with the oracle summing the same K
+    ranges (q4_K: whole super-blocks per half), over three launches in a row (the arrival counters
+    must come back to zero); on a ragged M."""
+    n_out, n_in = shape
+    rng = np.random.default_rng(n_out + n_in + M + gtype)
+    w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    bias = (rng.standard_normal(n_out) * 0.02).astype(np.float32)
+    raw = gguf.quantize(gtype, w)
+    dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
+    L = jlib.lib()
+    got = {}
+    for split in (1, 2):
+        y = torch.full((M, n_out), float("nan"), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        assert L.jepa_amd_gemm_split(split) == 0
+        try:
+            rc = L.jepa_amd_matmul(0, gtype, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, y.data_ptr(), 3, None)
+        finally:
+            L.jepa_amd_gemm_split(-1)
+        assert rc == 0, jlib.error_text()
+        got[split] = host(y)
+        want = _mul_mat_as_gpu(jlib, oracle, gtype, raw, n_out, n_in, x, bias, split=split)
+        diff = np.argwhere(got[split].view(np.uint32) != want.view(np.uint32))
+        assert diff.size == 0, f"split {split}: {len(diff)} outputs differ, first {diff[:4].tolist()}"
+    assert L.jepa_amd_gemm_split_of(gtype, n_out, n_in) == (2 if n_in >= 2048 else 1)
+    # the two orders agree to rounding
+    assert np.abs(got[1] - got[2]).max() <= 1e-5 * np.abs(got[1]).max()
+
+
 # workgroup tiles of the MFMA GEMM (weight rows x tokens), by index
 TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64), 6: (256, 64)}
 
@@ -267,7 +311,7 @@ def test_matmul_every_tile(jlib, oracle, gtype, tile):
         raw = w.astype(np.float16).view(np.uint8)
     else:
         raw = gguf.quantize(gtype, w)
-    want = oracle.mul_mat(gtype, raw, n_out, n_in, x, bias)
+    want = _mul_mat_as_gpu(jlib, oracle, gtype, raw, n_out, n_in, x, bias)
     dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
     y = torch.zeros((M, n_out), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
