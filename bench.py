@@ -123,6 +123,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-q4k", action="store_true", help="skip the q4_K line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--configs", default="",
+                    help="also time these encoder configurations (comma list: vits16_f16, vitb16_2_1_q8_0, "
+                         "vitg16_q8_0, levjepa_vitl16_q8_0)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the library's plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -181,6 +184,23 @@ def main():
             q4["gemm_roofline"] = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                                    "frac": round(ach / PEAK_INT8_TOPS, 4)}
         extra["q4_k"] = q4
+    # the other encoder configurations: (batch, frames, size) of one step and what one item is
+    shapes = {"vits16_f16": (1, 1, 224, "images"), "vitb16_2_1_q8_0": (8, 1, 384, "images"),
+              "vitg16_q8_0": (1, 64, 256, "clips"), "levjepa_vitl16_q8_0": (1, 16, 224, "clips")}
+    for name in [c for c in args.configs.split(",") if c]:
+        if name not in shapes:
+            log(f"bench: unknown configuration {name}")
+            continue
+        b, t, sz, unit = shapes[name]
+        pc = make_model(name)
+        xc = inputs.make_input(b, t, sz, sz, seed=1234)
+        log(f"bench: timing {name}")
+        st = max(3, min(args.steps, 20))
+        rc = time_forward(pc, xc, st, max(2, min(args.warmup, 3)), kernel_pass=False)
+        extra.setdefault("configs", {})[name] = {
+            "value": round(b * st / rc["elapsed_s"], 3), "unit": f"{unit}/s", "items_per_step": b,
+            "tokens_per_item": rc["rows"], "ms_per_step": round(rc["elapsed_s"] / st * 1e3, 4),
+            "p50_ms": round(float(np.median(rc["device_ms"])), 4), "steps": st}
     if args.copy_mib > 0:
         # a copy of known size: FETCH_SIZE / WRITE_SIZE of k_copy_f32 calibrate the counters
         import ctypes as C

@@ -145,6 +145,24 @@ def test_levjepa_vitl16_16f_q8_0_full(jlib, oracle, models_dir):
     check_parity(got, want, gtr, wtr, floor, label="levjepa_vitl16_q8_0")
 
 
+def test_vitg16_64f_q8_0_first_blocks(jlib, oracle, models_dir):
+    """V-JEPA 2 ViT-g/16, 64 frames 256x256 = 8192 tokens, D 1408, 22 heads, MLP 6144, 40 layers: the
+    whole forward runs on the GPU (finite output of the right shape); the residual stream after the
+    patch embedding and after each of the first two blocks is checked against the oracle (all 40
+    blocks of the oracle at 8192 tokens would take tens of minutes on the host)."""
+    cfg = forge.CONFIGS["vitg16_q8_0"]
+    path = forge.cached_model(cfg, models_dir)
+    m = jlib.Model(path)
+    ctx = jlib.Context(m)
+    x = inputs.make_input(1, 64, 256, 256, seed=1234)
+    rows = m.token_grid(64, 256, 256)
+    assert rows == 8192 and m.dim == 1408 and m.n_layer == 40
+    got, gtr = ctx.encode_trace(x, 1, rows)
+    assert got.shape == (8192, 1408) and np.isfinite(got).all()
+    _, wtr = oracle.encode(path, x, 1, rows, m.dim, n_layers=2, trace=True)
+    check_parity(gtr[:, 2], wtr[:, 2], gtr[:, :3], wtr[:, :3], label="vitg16_q8_0 (first two blocks)")
+
+
 def test_encode_errors(jlib, models_dir):
     cfg = forge.tiny("vjepa2", "q8_0")
     m = jlib.Model(forge.cached_model(cfg, models_dir))
