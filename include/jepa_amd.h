@@ -22,6 +22,13 @@ extern "C" {
 int64_t jepa_amd_encode_device(jepa_context * ctx, const float * in_dev, int n_batch, int n_chans, int n_frames,
                                int height, int width, float * out_dev, int64_t out_cap_floats);
 
+/* jepa_head_ex on device-resident encoder rows: x_dev [n_tokens][embed_dim] float32 on the model's
+ * device; pooled_dev [embed_dim] and logits_dev [n_classes] (device, either may be NULL) receive
+ * the pooled token and the classifier logits. Replaces the tensor_set / tensor_get of reference
+ * src/jepa.cpp:1093-1110 with device data. Returns n_classes, or -1 with the reason in
+ * jepa_error_text(). last_compute_ms covers the head's kernels. */
+int jepa_amd_head_device(jepa_context * ctx, const float * x_dev, int64_t n_tokens, float * pooled_dev, float * logits_dev);
+
 /* jepa_encode that also returns the residual stream after the patch embedding and after every
  * block (before the final norm): trace [n_items][n_layer + 1][rows][dim] on the host. For per-layer
  * parity checks; runs without graph replay. */

@@ -74,6 +74,11 @@ extern "C" int64_t jepa_amd_encode_device(jepa_context * ctx, const float * in_d
     return encode_device(ctx, in_dev, n_batch, n_chans, n_frames, height, width, out_dev, out_cap, nullptr, 0);
 }
 
+extern "C" int jepa_amd_head_device(jepa_context * ctx, const float * x_dev, int64_t n_tokens, float * pooled_dev, float * logits_dev) {
+    if (!ctx || !x_dev) return -1;
+    return head_device(ctx, x_dev, n_tokens, pooled_dev, logits_dev);
+}
+
 extern "C" int64_t jepa_amd_encode_trace(jepa_context * ctx, const jepa_input * in, float * out, int64_t out_cap, float * trace,
                                          int64_t trace_cap) {
     if (!ctx || !in || !in->data || !out || !trace) return -1;

@@ -9,8 +9,7 @@
 //              down GEMM + bias (* ls2) + residual into x
 //   final LN -> f32 output rows
 // The whole sequence for one input shape is captured once into a hipGraph and replayed.
-#include "model.h"
-#include "kernels.h"
+#include "forward.h"
 #include "rope3d.h"
 
 #include <algorithm>
@@ -20,37 +19,6 @@
 
 #define HIP_OK(expr) \
     do { hipError_t e_ = (expr); if (e_ != hipSuccess) { jepa_log("jepa: %s failed: %s\n", #expr, hipGetErrorString(e_)); return false; } } while (0)
-
-struct fwd_workspace {
-    // shape the buffers and the captured graph were made for
-    int n_items = 0, n_chans = 0, n_frames = 0, height = 0, width = 0;
-    int64_t R = 0, Np = 0, R_pad = 0, K = 0, prefix = 0;
-    bool image_path = false, video = false;
-    int tubelet = 1;
-    const jepa_model * model = nullptr;
-    // buffers
-    std::vector<void *> allocs;
-    void * clip = nullptr;       // f32 input (host-input path)
-    void * patches = nullptr;    // f16 or f32 patch rows
-    float * x = nullptr;         // residual stream
-    act_view actA, actB;         // GEMM inputs (LN outputs / attention output codes; up-GEMM output codes)
-    void * Q = nullptr, * Kt = nullptr, * Vt = nullptr;
-    float * attn = nullptr, * ff = nullptr, * out = nullptr;
-    float * rope_c = nullptr, * rope_s = nullptr;
-    gemm_split_ws split;         // split-K GEMM scratch (counters zeroed once, left zero by every launch)
-    // graph
-    hipGraphExec_t exec = nullptr;
-    const float * g_in = nullptr; float * g_out = nullptr;
-    bool graph_ok = false;
-
-    void release() {
-        if (exec) { hipGraphExecDestroy(exec); exec = nullptr; }
-        for (void * p : allocs) hipFree(p);
-        allocs.clear();
-        graph_ok = false;
-    }
-    ~fwd_workspace() { release(); }
-};
 
 jepa_context::jepa_context() = default;
 
@@ -112,9 +80,7 @@ int64_t encode_rows(const jepa_model * m, int n_batch, int n_frames, int height,
     return 0;
 }
 
-namespace {
-
-bool dalloc(fwd_workspace & w, void ** p, size_t bytes) {
+bool ws_alloc(fwd_workspace & w, void ** p, size_t bytes) {
     *p = nullptr;
     if (bytes == 0) bytes = 256;
     if (hipMalloc(p, bytes) != hipSuccess) {
@@ -125,12 +91,104 @@ bool dalloc(fwd_workspace & w, void ** p, size_t bytes) {
     return true;
 }
 
-bool alloc_act(fwd_workspace & w, act_view & a, int64_t rows, int64_t K) {
+static bool alloc_act(fwd_workspace & w, act_view & a, int64_t rows, int64_t K) {
     a.ld = K;
-    return dalloc(w, &a.q, (size_t) rows * K * 4) &&   // f32 worst case (A_F32)
-           dalloc(w, &a.d, (size_t) rows * std::max<int64_t>(K / 32 * 2, K / 256 * 4) + 16) &&
-           dalloc(w, &a.bsum, (size_t) rows * (K / 16) * 2 + 16);
+    return ws_alloc(w, &a.q, (size_t) rows * K * 4) &&   // f32 worst case (A_F32)
+           ws_alloc(w, &a.d, (size_t) rows * std::max<int64_t>(K / 32 * 2, K / 256 * 4) + 16) &&
+           ws_alloc(w, &a.bsum, (size_t) rows * (K / 16) * 2 + 16);
 }
+
+bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, int64_t F, int H, int hd, hipStream_t s) {
+    w.R = R;
+    w.R_pad = (R + 127) / 128 * 128;
+    const int64_t rows = n_items * R, qkv = n_items * H * w.R_pad * hd * 2;
+    const bool ok = ws_alloc(w, (void **) &w.x, (size_t) rows * D * 4) && alloc_act(w, w.actA, rows, D) && alloc_act(w, w.actB, rows, F) &&
+                    ws_alloc(w, &w.Q, (size_t) qkv) && ws_alloc(w, &w.Kt, (size_t) qkv) && ws_alloc(w, &w.Vt, (size_t) qkv) &&
+                    ws_alloc(w, (void **) &w.attn, (size_t) rows * D * 4) && ws_alloc(w, (void **) &w.ff, (size_t) rows * F * 4) &&
+                    ws_alloc(w, (void **) &w.out, (size_t) rows * D * 4);
+    if (!ok) return false;
+    gemm_split_ws_size(rows, &w.split.part_floats, &w.split.cnt_n);
+    if (!ws_alloc(w, (void **) &w.split.part, (size_t) w.split.part_floats * 4) ||
+        !ws_alloc(w, (void **) &w.split.cnt, (size_t) w.split.cnt_n * 4)) return false;
+    launch_fill_zero(w.split.cnt, (size_t) w.split.cnt_n * 4, s);
+    // Q/K/V^T padding rows are read by the attention kernel: zero them once (never written again)
+    launch_fill_zero(w.Q, (size_t) qkv, s);
+    launch_fill_zero(w.Kt, (size_t) qkv, s);
+    launch_fill_zero(w.Vt, (size_t) qkv, s);
+    return true;
+}
+
+const char * gemm_class(const dev_linear & W) {
+    switch (W.fmt) { case W_F16: return "gemm_f16"; case W_Q32: return "gemm_q8"; case W_Q4K: return "gemm_q4k"; default: return "gemm_f32"; }
+}
+
+void enqueue_mlp(const dev_linear & up, const dev_linear & down, const float * ln_w, const float * ln_b, float eps, const float * ls,
+                 float * x, int64_t rows, int64_t D, fwd_workspace & w, hipStream_t s, ktimer & kt) {
+    const int64_t F = up.n_out;
+    w.actA.fmt = up.act();
+    kt.run("layernorm", [&] { launch_rownorm_quant(x, rows, D, ln_w, ln_b, eps, true, w.actA, s); });
+    w.actB.fmt = down.act();
+    {
+        gemm_epi ep;
+        ep.ldy = F;
+        const bool mfma = up.fmt != W_F32;
+        if (mfma && w.actB.fmt == A_Q8_0) { ep.kind = EPI_GELU_Q8_0; ep.oq = w.actB.q; ep.od = w.actB.d; }
+        else if (mfma && w.actB.fmt == A_Q8_K && F % 256 == 0) {
+            ep.kind = EPI_GELU_Q8_K; ep.oh = w.actB.q; ep.od = w.actB.d; ep.ob = w.actB.bsum;
+        }
+        else if (mfma && w.actB.fmt == A_F16) { ep.kind = EPI_GELU_F16; ep.oh = w.actB.q; }
+        else { ep.kind = EPI_GELU_F32; ep.y = w.ff; }
+        kt.run(gemm_class(up), [&] { launch_gemm(up, w.actA, rows, ep, s, &w.split); }, "up");
+        if (ep.kind == EPI_GELU_F32)
+            kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, w.actB, s); }, "ff");
+    }
+    {
+        gemm_epi ep;
+        ep.kind = EPI_RESID; ep.y = x; ep.ldy = D; ep.ls = ls;
+        kt.run(gemm_class(down), [&] { launch_gemm(down, w.actB, rows, ep, s, &w.split); }, "down");
+    }
+}
+
+void enqueue_block(const jepa_model * m, const dev_layer & L, fwd_workspace & w, int64_t n_items, int64_t R, const float * rope_c,
+                   const float * rope_s, int n_prefix, int64_t slot_rows, hipStream_t s, ktimer & kt) {
+    const enc_hparams & e = m->hp.enc;
+    const int64_t D = e.embed_dim, rows = n_items * R;
+    const int H = e.n_head, hd = e.head_dim();
+    // attention half
+    w.actA.fmt = L.qkv.act();
+    kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln1_w, L.ln1_b, e.ln_eps, true, w.actA, s); });
+    {
+        gemm_epi ep;
+        ep.kind = EPI_QKV;
+        ep.q = w.Q; ep.k = w.Kt; ep.vt = w.Vt;
+        ep.rope_c = rope_c; ep.rope_s = rope_s;
+        ep.n_head = H; ep.hd = hd; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
+        kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
+    }
+    w.actA.fmt = L.out.act();
+    if (w.actA.fmt == A_Q8_0) {
+        // the attention epilogue writes the out-projection's q8_0 input directly
+        kt.run("attention", [&] {
+            launch_attention(w.Q, w.Kt, w.Vt, w.actA, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
+        });
+    } else {
+        act_view o;
+        o.fmt = A_F32; o.q = w.attn; o.ld = D;
+        kt.run("attention", [&] {
+            launch_attention(w.Q, w.Kt, w.Vt, o, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
+        });
+        kt.run("quantize", [&] { launch_rownorm_quant(w.attn, rows, D, nullptr, nullptr, 0.0f, false, w.actA, s); }, "attn");
+    }
+    {
+        gemm_epi ep;
+        ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls1;
+        kt.run(gemm_class(L.out), [&] { launch_gemm(L.out, w.actA, rows, ep, s, &w.split); }, "out");
+    }
+    // MLP half
+    enqueue_mlp(L.up, L.down, L.ln2_w, L.ln2_b, e.ln_eps, L.ls2, w.x, rows, D, w, s, kt);
+}
+
+namespace {
 
 // bytes the workspace needs for n items of R rows (the $JEPA_MAX_GRAPH_MIB guard)
 double workspace_bytes(const jepa_model * m, int64_t n_items, int64_t R, int64_t Np, int64_t K) {
@@ -167,26 +225,12 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
         w->prefix = e.cls_token ? 1 : 0;
         w->K = (int64_t) e.in_chans * P * P;
     }
-    w->R = w->Np + w->prefix;
-    w->R_pad = (w->R + 127) / 128 * 128;
-    const int64_t rows = (int64_t) n_items * w->R, D = e.embed_dim, F = e.ffn_dim, H = e.n_head, hd = e.head_dim();
+    const int64_t D = e.embed_dim, F = e.ffn_dim, H = e.n_head, hd = e.head_dim();
     const dev_linear & pe = w->image_path ? m->patch_img : m->patch;
-    const bool ok =
-        dalloc(*w, &w->clip, (size_t) n_items * n_chans * (w->video ? n_frames : 1) * height * width * 4) &&
-        dalloc(*w, &w->patches, (size_t) n_items * w->Np * w->K * (pe.fmt == W_F32 ? 4 : 2)) &&
-        dalloc(*w, (void **) &w->x, (size_t) rows * D * 4) && alloc_act(*w, w->actA, rows, D) && alloc_act(*w, w->actB, rows, F) &&
-        dalloc(*w, &w->Q, (size_t) n_items * H * w->R_pad * hd * 2) && dalloc(*w, &w->Kt, (size_t) n_items * H * w->R_pad * hd * 2) &&
-        dalloc(*w, &w->Vt, (size_t) n_items * H * w->R_pad * hd * 2) && dalloc(*w, (void **) &w->attn, (size_t) rows * D * 4) &&
-        dalloc(*w, (void **) &w->ff, (size_t) rows * F * 4) && dalloc(*w, (void **) &w->out, (size_t) rows * D * 4);
+    const bool ok = ws_alloc(*w, &w->clip, (size_t) n_items * n_chans * (w->video ? n_frames : 1) * height * width * 4) &&
+                    ws_alloc(*w, &w->patches, (size_t) n_items * w->Np * w->K * (pe.fmt == W_F32 ? 4 : 2)) &&
+                    ws_alloc_blocks(*w, n_items, w->Np + w->prefix, D, F, (int) H, (int) hd, ctx->stream);
     if (!ok) { ctx->ws.reset(); return false; }
-    gemm_split_ws_size(rows, &w->split.part_floats, &w->split.cnt_n);
-    if (!dalloc(*w, (void **) &w->split.part, (size_t) w->split.part_floats * 4) ||
-        !dalloc(*w, (void **) &w->split.cnt, (size_t) w->split.cnt_n * 4)) { ctx->ws.reset(); return false; }
-    launch_fill_zero(w->split.cnt, (size_t) w->split.cnt_n * 4, ctx->stream);
-    // Q/K/V^T padding rows are read by the attention kernel: zero them once (never written again)
-    launch_fill_zero(w->Q, (size_t) n_items * H * w->R_pad * hd * 2, ctx->stream);
-    launch_fill_zero(w->Kt, (size_t) n_items * H * w->R_pad * hd * 2, ctx->stream);
-    launch_fill_zero(w->Vt, (size_t) n_items * H * w->R_pad * hd * 2, ctx->stream);
     if (w->video) {
         rope3d_params rp;
         rp.grid_t = w->n_frames / w->tubelet; rp.grid_h = height / P; rp.grid_w = width / P;
@@ -201,7 +245,7 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
             c.insert(c.begin(), (size_t) w->prefix * hd, 1.0f);
             s.insert(s.begin(), (size_t) w->prefix * hd, 0.0f);
         }
-        if (!dalloc(*w, (void **) &w->rope_c, c.size() * 4) || !dalloc(*w, (void **) &w->rope_s, s.size() * 4)) { ctx->ws.reset(); return false; }
+        if (!ws_alloc(*w, (void **) &w->rope_c, c.size() * 4) || !ws_alloc(*w, (void **) &w->rope_s, s.size() * 4)) { ctx->ws.reset(); return false; }
         if (hipMemcpy(w->rope_c, c.data(), c.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemcpy(w->rope_s, s.data(), s.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
             jepa_log("jepa: RoPE table upload failed\n");
@@ -213,50 +257,13 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
     return true;
 }
 
-struct ktimer {   // optional per-kernel-class event timing (jepa_amd_context_set_kernel_timing)
-    jepa_context * ctx;
-    struct rec { std::string name, detail; hipEvent_t a, b; };
-    std::vector<rec> evs;
-    // the launch counts under `name` and, when given, also under "name.detail" (e.g. gemm_q8.qkv)
-    template <typename F> void run(const char * name, F && f, const char * detail = nullptr) {
-        if (!ctx->kernel_timing) { f(); return; }
-        hipEvent_t a, b;
-        hipEventCreate(&a); hipEventCreate(&b);
-        hipEventRecord(a, ctx->stream);
-        f();
-        hipEventRecord(b, ctx->stream);
-        evs.push_back({name, detail ? std::string(name) + "." + detail : std::string(), a, b});
-    }
-    void collect() {
-        for (auto & e : evs) {
-            hipEventSynchronize(e.b);
-            float ms = 0;
-            hipEventElapsedTime(&ms, e.a, e.b);
-            for (const std::string * k : {&e.name, &e.detail}) {
-                if (k->empty()) continue;
-                auto & st = ctx->kstats[*k];
-                st.first += 1;
-                st.second += ms;
-            }
-            hipEventDestroy(e.a);
-            hipEventDestroy(e.b);
-        }
-        evs.clear();
-    }
-};
-
-const char * gemm_class(const dev_linear & W) {
-    switch (W.fmt) { case W_F16: return "gemm_f16"; case W_Q32: return "gemm_q8"; case W_Q4K: return "gemm_q4k"; default: return "gemm_f32"; }
-}
-
 // Enqueue the forward of the workspace's shape on ctx->stream. in: NCTHW f32 of n_items; out: [rows][D].
 void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * trace, ktimer & kt) {
     const jepa_model * m = ctx->model;
     const enc_hparams & e = m->hp.enc;
     fwd_workspace & w = *ctx->ws;
     hipStream_t s = ctx->stream;
-    const int64_t n_items = w.n_items, R = w.R, D = e.embed_dim, F = e.ffn_dim, rows = n_items * R;
-    const int H = e.n_head, hd = e.head_dim();
+    const int64_t n_items = w.n_items, R = w.R, D = e.embed_dim, rows = n_items * R;
     const dev_linear & pe = w.image_path ? m->patch_img : m->patch;
 
     kt.run("patchify", [&] {
@@ -285,60 +292,7 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
     const int64_t slot_rows = e.attn_mode == "block_causal" ? (int64_t) (w.height / e.patch_size) * (w.width / e.patch_size) : 0;
     const int n_prefix = (int) w.prefix;
     for (int l = 0; l < e.n_layer; l++) {
-        const dev_layer & L = m->layers[(size_t) l];
-        // attention half
-        w.actA.fmt = L.qkv.act();
-        kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln1_w, L.ln1_b, e.ln_eps, true, w.actA, s); });
-        {
-            gemm_epi ep;
-            ep.kind = EPI_QKV;
-            ep.q = w.Q; ep.k = w.Kt; ep.vt = w.Vt;
-            ep.rope_c = w.rope_c; ep.rope_s = w.rope_s;
-            ep.n_head = H; ep.hd = hd; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
-            kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
-        }
-        w.actA.fmt = L.out.act();
-        if (w.actA.fmt == A_Q8_0) {
-            // the attention epilogue writes the out-projection's q8_0 input directly
-            kt.run("attention", [&] {
-                launch_attention(w.Q, w.Kt, w.Vt, w.actA, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
-            });
-        } else {
-            act_view o;
-            o.fmt = A_F32; o.q = w.attn; o.ld = D;
-            kt.run("attention", [&] {
-                launch_attention(w.Q, w.Kt, w.Vt, o, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
-            });
-            kt.run("quantize", [&] { launch_rownorm_quant(w.attn, rows, D, nullptr, nullptr, 0.0f, false, w.actA, s); }, "attn");
-        }
-        {
-            gemm_epi ep;
-            ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls1;
-            kt.run(gemm_class(L.out), [&] { launch_gemm(L.out, w.actA, rows, ep, s, &w.split); }, "out");
-        }
-        // MLP half
-        w.actA.fmt = L.up.act();
-        kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln2_w, L.ln2_b, e.ln_eps, true, w.actA, s); });
-        w.actB.fmt = L.down.act();
-        {
-            gemm_epi ep;
-            ep.ldy = F;
-            const bool mfma = L.up.fmt != W_F32;
-            if (mfma && w.actB.fmt == A_Q8_0) { ep.kind = EPI_GELU_Q8_0; ep.oq = w.actB.q; ep.od = w.actB.d; }
-            else if (mfma && w.actB.fmt == A_Q8_K && F % 256 == 0) {
-                ep.kind = EPI_GELU_Q8_K; ep.oh = w.actB.q; ep.od = w.actB.d; ep.ob = w.actB.bsum;
-            }
-            else if (mfma && w.actB.fmt == A_F16) { ep.kind = EPI_GELU_F16; ep.oh = w.actB.q; }
-            else { ep.kind = EPI_GELU_F32; ep.y = w.ff; }
-            kt.run(gemm_class(L.up), [&] { launch_gemm(L.up, w.actA, rows, ep, s, &w.split); }, "up");
-            if (ep.kind == EPI_GELU_F32)
-                kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, w.actB, s); }, "ff");
-        }
-        {
-            gemm_epi ep;
-            ep.kind = EPI_RESID; ep.y = w.x; ep.ldy = D; ep.ls = L.ls2;
-            kt.run(gemm_class(L.down), [&] { launch_gemm(L.down, w.actB, rows, ep, s, &w.split); }, "down");
-        }
+        enqueue_block(m, m->layers[(size_t) l], w, n_items, R, w.rope_c, w.rope_s, n_prefix, slot_rows, s, kt);
         if (trace) launch_copy_f32(w.x, trace + (int64_t) (l + 1) * rows * D, rows * D, s);
     }
     act_view o;

@@ -76,6 +76,13 @@ void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items, int n_head,
                       int hd, int64_t R, int64_t R_pad, float scale, int n_prefix, int64_t tokens_per_slot, hipStream_t s);
 
+// Single-query attention of the attentive-pool head: y = softmax(q . K^T * scale) V + q0 per head
+// (hd 64), q / q0 / y [n_head * hd], K / V f32 rows [N][ld]. `part` holds pool_attention_part_floats
+// floats of per-chunk partial results. Returns false (logged) on an unsupported shape.
+int64_t pool_attention_part_floats(int64_t N, int n_head);
+bool launch_pool_attention(const float * q, const float * K, const float * V, int64_t N, int64_t ld, int n_head, int hd, float scale,
+                           const float * q0, float * y, float * part, int64_t part_floats, hipStream_t s);
+
 // Patch rows from NCTHW input: rows [items*Np][C*tub*P*P] in f16 (half_out) or f32.
 void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_items, int C, int T, int H, int W,
                      int P, int tub, bool video, hipStream_t s);

@@ -7,6 +7,7 @@
 #include "model.h"
 #include "kernels.h"
 
+#include <algorithm>
 #include <cinttypes>
 #include <cmath>
 #include <cstdarg>
@@ -162,7 +163,10 @@ bool hparams_from_gguf(const gguf::file & f, hparams & hp, std::vector<std::pair
         hp.n_classes = (int) r.geti("jepa.head.n_classes", 0);
         const gguf::value * lv = f.find("jepa.head.labels");
         if (lv && lv->type == gguf::ARR && lv->arr_type == gguf::STR) hp.labels = lv->as;
-        if (!kv_range("jepa.head.n_classes", hp.n_classes, 0, JEPA_LIMIT_N_TOKENS)) return false;
+        hp.n_pool_layers = (int) r.geti("jepa.head.n_pool_layers", 0);
+        if (!kv_range("jepa.head.n_classes", hp.n_classes, 0, JEPA_LIMIT_N_TOKENS) ||
+            !kv_range("jepa.head.n_pool_layers", hp.n_pool_layers, 0, JEPA_LIMIT_N_LAYER) ||
+            !kv_range("jepa.head.labels length", (int64_t) hp.labels.size(), 0, JEPA_LIMIT_N_TOKENS)) return false;
     }
     pre_hparams & pre = hp.pre;
     r.farr("jepa.pre.mean", pre.mean, 3);
@@ -213,21 +217,26 @@ struct loader {
         return true;
     }
 
-    bool to_staging(const gguf::tensor_info & t) {
+    // the tensor's bytes into device staging, followed by pad_bytes of zeros (zero rows: d = 0 in
+    // every quantized block format, so they dequantize to 0)
+    bool to_staging(const gguf::tensor_info & t, size_t pad_bytes = 0) {
         if (!read(t)) return false;
-        if (staging_size < t.nbytes) {
+        const size_t need = t.nbytes + pad_bytes;
+        if (staging_size < need) {
             if (staging) hipFree(staging);
             staging = nullptr;
             staging_size = 0;
-            if (hipMalloc(&staging, t.nbytes) != hipSuccess) { jepa_log("jepa: hipMalloc(staging) failed\n"); return false; }
-            staging_size = t.nbytes;
+            if (hipMalloc(&staging, need) != hipSuccess) { jepa_log("jepa: hipMalloc(staging) failed\n"); return false; }
+            staging_size = need;
         }
         return hipMemcpyAsync(staging, host.data(), t.nbytes, hipMemcpyHostToDevice, s) == hipSuccess &&
+               (pad_bytes == 0 || hipMemsetAsync((char *) staging + t.nbytes, 0, pad_bytes, s) == hipSuccess) &&
                hipStreamSynchronize(s) == hipSuccess;
     }
 
     // an f32 vector of exactly n values (norms, biases, tokens, tables) - src/jepa-gguf.cpp:675-701
-    bool vec(const std::string & name, int64_t n, float ** out, bool required = false) {
+    // (n_alloc > n: the device copy is n_alloc values, the tail zero)
+    bool vec(const std::string & name, int64_t n, float ** out, bool required = false, int64_t n_alloc = 0) {
         const gguf::tensor_info * t = f.tensor(name);
         if (!t) {
             if (required) { jepa_log("jepa: required tensor '%s' missing from %s\n", name.c_str(), m->path.c_str()); return false; }
@@ -244,13 +253,24 @@ struct loader {
             return false;
         }
         if (!read(*t)) return false;
-        float * d = (float *) dalloc(t->nbytes);
-        if (!d || hipMemcpy(d, host.data(), t->nbytes, hipMemcpyHostToDevice) != hipSuccess) return false;
+        const size_t bytes = std::max<size_t>(t->nbytes, (size_t) n_alloc * 4);
+        float * d = (float *) dalloc(bytes);
+        if (!d || (bytes > t->nbytes && hipMemset(d, 0, bytes) != hipSuccess) ||
+            hipMemcpy(d, host.data(), t->nbytes, hipMemcpyHostToDevice) != hipSuccess) return false;
         *out = d;
         return true;
     }
 
-    bool linear(const std::string & wname, const std::string & bname, int64_t n_in, int64_t n_out, dev_linear & L, bool required) {
+    // rows (ne[1]) of a 2-D tensor, 0 when it is absent
+    int64_t rows_of(const std::string & name) const {
+        const gguf::tensor_info * t = f.tensor(name);
+        return t ? t->ne[1] : 0;
+    }
+
+    // pad_out: the device matrix gets n_out rounded up to 128 rows (zero weights and bias), for the
+    // linears whose output count the file chooses freely (the classifier); L.n_valid keeps n_out
+    bool linear(const std::string & wname, const std::string & bname, int64_t n_in, int64_t n_out, dev_linear & L, bool required,
+                bool pad_out = false) {
         const gguf::tensor_info * t = f.tensor(wname);
         if (!t) {
             if (required) { jepa_log("jepa: required tensor '%s' missing from %s\n", wname.c_str(), m->path.c_str()); return false; }
@@ -261,7 +281,10 @@ struct loader {
                      wname.c_str(), t->ne[0], t->ne[1], n_in, n_out);
             return false;
         }
-        L.gtype = t->type; L.n_in = n_in; L.n_out = n_out;
+        const int64_t n_file = n_out;
+        if (pad_out) n_out = (n_out + 127) / 128 * 128;
+        const size_t pad_bytes = (size_t) (n_out - n_file) * (t->nbytes / (size_t) n_file);
+        L.gtype = t->type; L.n_in = n_in; L.n_out = n_out; L.n_valid = n_file;
         switch (t->type) {
             case T_F32: L.fmt = W_F32; break;
             case T_F16: L.fmt = W_F16; break;
@@ -281,10 +304,10 @@ struct loader {
             jepa_log("jepa: tensor %s: %" PRId64 " outputs is not a multiple of 4\n", wname.c_str(), n_out);
             return false;
         }
-        if (!to_staging(*t)) return false;
+        if (!to_staging(*t, pad_bytes)) return false;
         if (L.fmt == W_F32 || L.fmt == W_F16) {
-            L.w = dalloc(t->nbytes);
-            if (!L.w || hipMemcpyAsync(L.w, staging, t->nbytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
+            L.w = dalloc(t->nbytes + pad_bytes);
+            if (!L.w || hipMemcpyAsync(L.w, staging, t->nbytes + pad_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
         } else {
             L.w = dalloc((size_t) n_in * n_out * (L.fmt == W_Q32 ? 1 : 2));
             if (!L.w) return false;
@@ -299,7 +322,24 @@ struct loader {
             launch_repack(t->type, staging, n_out, n_in, L.w, L.wd, L.wmin, s);
         }
         if (hipStreamSynchronize(s) != hipSuccess) { jepa_log("jepa: weight upload of %s failed\n", wname.c_str()); return false; }
-        return vec(bname, n_out, &L.bias);
+        return vec(bname, n_file, &L.bias, false, n_out);
+    }
+
+    // one pre-LN block "<p>ln1.weight" ... (src/jepa-gguf.cpp:236-252 names) of FFN width F (0: the
+    // ffn_up tensor's row count)
+    bool block(const std::string & p, int64_t D, int64_t F, dev_layer & Ly) {
+        if (!f.tensor(p + "ln1.weight") || !f.tensor(p + "ln2.weight") || !f.tensor(p + "attn_out.weight") || !f.tensor(p + "ffn_up.weight") ||
+            !f.tensor(p + "ffn_down.weight") || !f.tensor(p + "attn_qkv.weight")) {
+            jepa_log("jepa: block %s* is incomplete: needs ln1/ln2/attn_out/ffn_up/ffn_down and attn_qkv\n", p.c_str());
+            return false;
+        }
+        if (F <= 0) F = rows_of(p + "ffn_up.weight");
+        return vec(p + "ln1.weight", D, &Ly.ln1_w) && vec(p + "ln1.bias", D, &Ly.ln1_b) && vec(p + "ln2.weight", D, &Ly.ln2_w) &&
+               vec(p + "ln2.bias", D, &Ly.ln2_b) && vec(p + "ls1", D, &Ly.ls1) && vec(p + "ls2", D, &Ly.ls2) &&
+               linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * D, Ly.qkv, true) &&
+               linear(p + "attn_out.weight", p + "attn_out.bias", D, D, Ly.out, true) &&
+               linear(p + "ffn_up.weight", p + "ffn_up.bias", D, F, Ly.up, true) &&
+               linear(p + "ffn_down.weight", p + "ffn_down.bias", F, D, Ly.down, true);
     }
 };
 
@@ -395,25 +435,29 @@ extern "C" jepa_model * jepa_model_load_ex(const char * path, const jepa_model_p
         }
         if (ok && !e.qkv_fused) { jepa_log("jepa: separate attn_q/k/v weights are not implemented on this path (qkv_fused = false)\n"); ok = false; }
         m->layers.resize((size_t) e.n_layer);
-        for (int i = 0; i < e.n_layer && ok; i++) {
-            const std::string p = "enc.blk." + std::to_string(i) + ".";
-            dev_layer & Ly = m->layers[(size_t) i];
-            if (!f.tensor(p + "ln1.weight") || !f.tensor(p + "ln2.weight") || !f.tensor(p + "attn_out.weight") || !f.tensor(p + "ffn_up.weight") ||
-                !f.tensor(p + "ffn_down.weight") || !f.tensor(p + "attn_qkv.weight")) {
-                jepa_log("jepa: block %d is incomplete (enc.blk.%d.*): needs ln1/ln2/attn_out/ffn_up/ffn_down and attn_qkv\n", i, i);
-                ok = false;
-                break;
-            }
-            ok = L.vec(p + "ln1.weight", D, &Ly.ln1_w) && L.vec(p + "ln1.bias", D, &Ly.ln1_b) &&
-                 L.vec(p + "ln2.weight", D, &Ly.ln2_w) && L.vec(p + "ln2.bias", D, &Ly.ln2_b) &&
-                 L.vec(p + "ls1", D, &Ly.ls1) && L.vec(p + "ls2", D, &Ly.ls2) &&
-                 L.linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * D, Ly.qkv, true) &&
-                 L.linear(p + "attn_out.weight", p + "attn_out.bias", D, D, Ly.out, true) &&
-                 L.linear(p + "ffn_up.weight", p + "ffn_up.bias", D, e.ffn_dim, Ly.up, true) &&
-                 L.linear(p + "ffn_down.weight", p + "ffn_down.bias", e.ffn_dim, D, Ly.down, true);
-        }
+        for (int i = 0; i < e.n_layer && ok; i++) ok = L.block("enc.blk." + std::to_string(i) + ".", D, e.ffn_dim, m->layers[(size_t) i]);
         if (ok && e.modality_embed && video && !m->mod_video) {
             jepa_log("jepa: jepa.enc.modality_embed is set but enc.mod_embed_video is missing\n");
+            ok = false;
+        }
+    }
+    if (ok && encoder && m->hp.head_kind == "attentive_pool") {
+        // src/jepa-gguf.cpp:1070-1090: every head tensor is required, shapes checked against D
+        dev_head & h = m->head;
+        h.blocks.resize((size_t) m->hp.n_pool_layers);
+        for (int i = 0; i < m->hp.n_pool_layers && ok; i++) ok = L.block("head.blk." + std::to_string(i) + ".", D, 0, h.blocks[(size_t) i]);
+        const int64_t Fx = L.rows_of("head.xattn.ffn_up.weight"), C = L.rows_of("head.cls.weight");
+        ok = ok && L.vec("head.query", D, &h.query, true) && L.vec("head.xattn.ln_kv.weight", D, &h.ln_kv_w, true) &&
+             L.vec("head.xattn.ln_kv.bias", D, &h.ln_kv_b, true) && L.vec("head.xattn.ln2.weight", D, &h.ln2_w, true) &&
+             L.vec("head.xattn.ln2.bias", D, &h.ln2_b, true) &&
+             L.linear("head.xattn.q.weight", "head.xattn.q.bias", D, D, h.q, true) &&
+             L.linear("head.xattn.k.weight", "head.xattn.k.bias", D, D, h.k, true) &&
+             L.linear("head.xattn.v.weight", "head.xattn.v.bias", D, D, h.v, true) &&
+             L.linear("head.xattn.ffn_up.weight", "head.xattn.ffn_up.bias", D, Fx, h.up, true) &&
+             L.linear("head.xattn.ffn_down.weight", "head.xattn.ffn_down.bias", Fx, D, h.down, true) &&
+             L.linear("head.cls.weight", "head.cls.bias", D, C, h.cls, true, true);
+        if (ok && m->hp.n_classes > 0 && C != m->hp.n_classes) {
+            jepa_log("jepa: head.cls.weight has %" PRId64 " rows, jepa.head.n_classes is %d\n", C, m->hp.n_classes);
             ok = false;
         }
     }

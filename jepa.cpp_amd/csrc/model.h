@@ -68,7 +68,7 @@ struct hparams {
     pre_hparams pre;
     bool has_pred = false, has_head = false;
     std::string pred_kind, head_kind;
-    int n_classes = 0;
+    int n_classes = 0, n_pool_layers = 0;
     std::vector<std::string> labels;
 };
 
@@ -83,6 +83,7 @@ struct dev_linear {
     int      gtype = -1;          // ggml type in the file
     int      fmt = W_F32;
     int64_t  n_out = 0, n_in = 0;
+    int64_t  n_valid = 0;         // outputs in the file (n_out is rounded up to 128 for the head's linears)
     void *   w = nullptr;         // [n_out][n_in]: f32 (W_F32), int8 (W_Q32) or f16 (W_F16, W_Q4K)
     void *   wd = nullptr;        // W_Q32: f16 d [n_out][n_in/32]; W_Q4K: u32 (f16 d | f16 dmin << 16) [n_in/256][n_out]
     void *   wmin = nullptr;      // W_Q4K: f16 mins [n_out][n_in/256][16] (m_{k/2}, k = 0..15)
@@ -96,6 +97,14 @@ struct dev_layer {
     float * ln1_w = nullptr, * ln1_b = nullptr, * ln2_w = nullptr, * ln2_b = nullptr;
     float * ls1 = nullptr, * ls2 = nullptr;
     dev_linear qkv, out, up, down;
+};
+
+// attentive-pool head (reference src/jepa.cpp:1026-1075, tensors docs/gguf-schema.md:121-137)
+struct dev_head {
+    std::vector<dev_layer> blocks;   // head.blk.{i}
+    float * query = nullptr;         // [D] raw query token
+    float * ln_kv_w = nullptr, * ln_kv_b = nullptr, * ln2_w = nullptr, * ln2_b = nullptr;
+    dev_linear q, k, v, up, down, cls;   // cls: n_out rounded up to 128, n_valid = n_classes
 };
 
 struct jepa_model {
@@ -112,6 +121,7 @@ struct jepa_model {
     float * mod_img = nullptr, * mod_video = nullptr;
     float * norm_w = nullptr, * norm_b = nullptr;
     std::vector<dev_layer> layers;
+    dev_head head;                   // loaded when jepa.head.kind = attentive_pool
     std::vector<void *> allocations;   // every device allocation, freed with the model
 };
 
@@ -130,6 +140,7 @@ struct jepa_context {
     bool prec_f32 = true;
     bool use_graph = true;           // capture the forward into a hipGraph and replay it
     std::unique_ptr<fwd_workspace> ws;
+    std::unique_ptr<fwd_workspace> hws;   // jepa_head's buffers, made for the last token count
     void * io_in = nullptr, * io_out = nullptr;   // device copies of jepa_encode's host input / output
     size_t io_in_cap = 0, io_out_cap = 0;
     // per-kernel timing (jepa_amd_context_set_kernel_timing)
@@ -171,3 +182,6 @@ int64_t encode_device(jepa_context * ctx, const float * in_dev, int n_batch, int
 int64_t encode_rows(const jepa_model * m, int n_batch, int n_frames, int height, int width, int64_t * n_items);
 // jepa_encode's path: host input -> device -> forward -> host output rows. Returns rows per item or -1.
 int64_t encode_host(jepa_context * ctx, const jepa_input * in, float * out_host, int64_t out_cap);
+// Attentive-pool head on device-resident encoder rows x_dev [n_tokens][D] f32: pooled_dev [D] and
+// logits_dev [n_classes] (device, either may be null). Returns n_classes or -1. Records last_compute_ms.
+int head_device(jepa_context * ctx, const float * x_dev, int64_t n_tokens, float * pooled_dev, float * logits_dev);

@@ -24,8 +24,6 @@ extern "C" {
 
 int jepa_lewm_project(jepa_context *, const jepa_output *, jepa_output *) { NOPE_INT("jepa_lewm_project"); }
 int jepa_lewm_project_rows(jepa_context *, const float *, int, jepa_output *) { NOPE_INT("jepa_lewm_project_rows"); }
-int jepa_head(jepa_context *, const jepa_output *, jepa_output *) { NOPE_INT("jepa_head"); }
-int jepa_head_ex(jepa_context *, const jepa_output *, jepa_output *, jepa_output *) { NOPE_INT("jepa_head_ex"); }
 int jepa_predict(jepa_context *, const jepa_output *, const int32_t *, int, const int32_t *, int, jepa_output *) { NOPE_INT("jepa_predict"); }
 int jepa_predict_ex(jepa_context *, const jepa_output *, const int32_t *, int, const int32_t *, int, int, jepa_output *) { NOPE_INT("jepa_predict_ex"); }
 int jepa_predict_mod(jepa_context *, const jepa_output *, const int32_t *, int, const int32_t *, int, int, int, jepa_output *) { NOPE_INT("jepa_predict_mod"); }

@@ -96,6 +96,11 @@ def lib() -> C.CDLL:
         "jepa_softmax": (None, [vp, C.c_int, vp]),
         "jepa_top_k": (C.c_int, [vp, C.c_int, C.c_int, vp]),
         "jepa_head": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
+        "jepa_head_ex": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output), C.POINTER(Output)]),
+        "jepa_model_has_head": (C.c_bool, [vp]),
+        "jepa_model_n_classes": (C.c_int, [vp]),
+        "jepa_model_label": (cp, [vp, C.c_int]),
+        "jepa_amd_head_device": (C.c_int, [vp, vp, i64, vp, vp]),
         # jepa_amd.h
         "jepa_amd_encode_device": (i64, [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64]),
         "jepa_amd_encode_trace": (i64, [vp, C.POINTER(Input), vp, i64, vp, i64]),
@@ -147,6 +152,12 @@ class Model:
             raise RuntimeError(f"jepa_model_load_ex({path}) failed: {error_text().strip()}")
         self.dim = L.jepa_model_embed_dim(self.ptr)
         self.n_layer = L.jepa_model_n_layer(self.ptr)
+        self.has_head = bool(L.jepa_model_has_head(self.ptr))
+        self.n_classes = int(L.jepa_model_n_classes(self.ptr))
+
+    def label(self, i: int):
+        r = lib().jepa_model_label(self.ptr, i)
+        return None if r is None else r.decode()
 
     def token_grid(self, n_frames, h, w) -> int:
         return int(lib().jepa_token_grid(self.ptr, n_frames, h, w, None, None, None))
@@ -183,6 +194,26 @@ class Context:
         y = np.ctypeslib.as_array(out.data, shape=(out.n_tokens, out.dim)).copy()
         L.jepa_free(C.cast(out.data, C.c_void_p))
         return y
+
+    def head(self, rows: np.ndarray, pooled: bool = True, logits: bool = True):
+        """Attentive-pool head on encoder rows [N, dim] (jepa_head_ex) -> (pooled [dim] | None, logits | None)."""
+        L = lib()
+        rows = np.ascontiguousarray(rows, dtype=np.float32)
+        enc = Output(C.cast(rows.ctypes.data, C.POINTER(C.c_float)), rows.shape[0], rows.shape[1])
+        po, lo = Output(), Output()
+        L.jepa_error_reset()
+        check(L.jepa_head_ex(self.ptr, C.byref(enc), C.byref(po) if pooled else None, C.byref(lo) if logits else None), "jepa_head_ex")
+        res = []
+        for want, o in ((pooled, po), (logits, lo)):
+            if not want:
+                res.append(None)
+                continue
+            res.append(np.ctypeslib.as_array(o.data, shape=(o.dim,)).copy())
+            L.jepa_free(C.cast(o.data, C.c_void_p))
+        return tuple(res)
+
+    def head_device(self, x_ptr: int, n_tokens: int, pooled_ptr: int, logits_ptr: int) -> int:
+        return check(lib().jepa_amd_head_device(self.ptr, x_ptr, n_tokens, pooled_ptr, logits_ptr), "jepa_amd_head_device")
 
     def encode_trace(self, x: np.ndarray, n_items: int, rows: int):
         L = lib()

@@ -41,6 +41,8 @@ class EncoderConfig:
     layer_scale: bool = False
     ln_random: bool = False
     attn_mode: str = "full"  # full | block_causal (levjepa)
+    n_classes: int = 0       # > 0: attentive-pool classifier head (video families)
+    n_pool_layers: int = 0   # self-attention blocks of the head, run before the cross-attention
     seed: int = 1234
 
 
@@ -65,6 +67,11 @@ CONFIGS = {
                                          tubelet=1, img_size=224, n_frames=16, cls_token=True, ftype="q8_0",
                                          rope_layout="tiled", attn_mode="block_causal"),
     # V-JEPA 2 ViT-g/16 256x256, 64 frames (8192 tokens)
+    # V-JEPA 2 ViT-L/16 256x256 16-frame classifier: the encoder plus the SSv2 attentive-pool head
+    # (3 pooler blocks over the 2048 tokens, cross-attention, 174 classes)
+    "vitl16_ssv2_q8_0": EncoderConfig("vjepa2-vitl16-256-ssv2-synthetic", "vjepa2", 1024, 24, 16, 4096, patch=16,
+                                      tubelet=2, img_size=256, n_frames=16, ftype="q8_0", rope_layout="tiled",
+                                      n_classes=174, n_pool_layers=3),
     "vitg16_q8_0": EncoderConfig("vjepa2-vitg16-256-synthetic", "vjepa2", 1408, 40, 22, 6144, patch=16, tubelet=2,
                                  img_size=256, n_frames=64, ftype="q8_0", rope_layout="tiled"),
 }
@@ -137,6 +144,11 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     w.add("jepa.enc.layer_scale", cfg.layer_scale)
     if cfg.attn_mode != "full":
         w.add("jepa.enc.attn_mode", cfg.attn_mode)
+    if cfg.n_classes > 0:
+        w.add("jepa.head.kind", "attentive_pool")
+        w.add("jepa.head.n_classes", cfg.n_classes)
+        w.add("jepa.head.n_pool_layers", cfg.n_pool_layers)
+        w.add("jepa.head.labels", [f"class {i}" for i in range(cfg.n_classes)])
     w.add("jepa.pre.mean", [0.485, 0.456, 0.406])
     w.add("jepa.pre.std", [0.229, 0.224, 0.225])
     w.add("jepa.pre.resize_short", cfg.img_size)
@@ -180,8 +192,7 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     if not video:
         n_tok = (cfg.img_size // cfg.patch) ** 2 + (1 if cfg.cls_token else 0)
         w.add_tensor("enc.pos_embed", GGML_F32, (D, n_tok), normal(n_tok, D))
-    for i in range(cfg.n_layer):
-        p = f"enc.blk.{i}."
+    def block(p):
         ln(p + "ln1")
         mat(p + "attn_qkv.weight", 3 * D, D, _block_type(cfg, D))
         vec(p + "attn_qkv.bias", 3 * D)
@@ -195,7 +206,27 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
         if cfg.layer_scale:
             vec(p + "ls1", D, std=0.1)
             vec(p + "ls2", D, std=0.1)
+
+    for i in range(cfg.n_layer):
+        block(f"enc.blk.{i}.")
     ln("enc.norm")
+    if cfg.n_classes > 0:
+        # head tensors (docs/gguf-schema.md:121-137); every head matrix takes the file type
+        # (tools/jepa-quantize.cpp:105-116: head.blk.*, head.xattn.*, head.cls.)
+        for i in range(cfg.n_pool_layers):
+            block(f"head.blk.{i}.")
+        w.add_tensor("head.query", GGML_F32, (D, 1), normal(1, D, std=1.0))
+        ln("head.xattn.ln_kv")
+        for n in ("q", "k", "v"):
+            mat(f"head.xattn.{n}.weight", D, D, _block_type(cfg, D))
+            vec(f"head.xattn.{n}.bias", D)
+        ln("head.xattn.ln2")
+        mat("head.xattn.ffn_up.weight", F, D, _block_type(cfg, D))
+        vec("head.xattn.ffn_up.bias", F)
+        mat("head.xattn.ffn_down.weight", D, F, _block_type(cfg, F))
+        vec("head.xattn.ffn_down.bias", D)
+        mat("head.cls.weight", cfg.n_classes, D, _block_type(cfg, D))
+        vec("head.cls.bias", cfg.n_classes)
     os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
     w.write(path)
     return path

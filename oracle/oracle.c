@@ -847,6 +847,57 @@ static void patchify(const float * cthw, int C, int T, int H, int W, int P, int 
             }
 }
 
+/* One pre-LN block on x [R][D] in place (src/jepa.cpp:444-471), tensors "<pre>ln1.weight" etc.:
+ * x += out(attn(rope(qkv(LN1 x)))) [* ls1]; x += down(gelu(up(LN2 x))) [* ls2]. rope_c null: no
+ * rotation; mask (optional): additive [R][R]. The block's FFN width is read from its ffn_up tensor. */
+static int block_fwd(const gg_file * f, const char * pre, float * x, int64_t R, int D, int H, const float * rope_c,
+                     const float * rope_s, const float * mask, int kv_f16, float eps, int n_threads) {
+    char n1[128], n2[128];
+#define TN(buf, s) (snprintf(buf, sizeof(buf), "%s%s", pre, s), buf)
+    const gg_tensor * up = gg_tensor_find(f, TN(n1, "ffn_up.weight"));
+    if (!up) { fprintf(stderr, "oracle: missing %s\n", n1); return -1; }
+    const int64_t F = up->ne[1];
+    const int hd = D / H;
+    int rc = -1;
+    float * h = (float *) malloc(sizeof(float) * R * D);
+    float * qkv = (float *) malloc(sizeof(float) * R * 3 * D);
+    float * q = (float *) malloc(sizeof(float) * R * D), * kk = (float *) malloc(sizeof(float) * R * D), * vv = (float *) malloc(sizeof(float) * R * D);
+    float * att = (float *) malloc(sizeof(float) * R * D);
+    float * o = (float *) malloc(sizeof(float) * R * D);
+    float * ff = (float *) malloc(sizeof(float) * R * F);
+    or_layer_norm(x, R, D, gg_vec(f, TN(n1, "ln1.weight")), gg_vec(f, TN(n2, "ln1.bias")), eps, h);
+    if (linear(f, TN(n1, "attn_qkv.weight"), TN(n2, "attn_qkv.bias"), h, R, D, 3 * D, qkv, n_threads)) goto out;
+    for (int64_t r = 0; r < R; r++) {
+        memcpy(q + r * D, qkv + r * 3 * D, sizeof(float) * D);
+        memcpy(kk + r * D, qkv + r * 3 * D + D, sizeof(float) * D);
+        memcpy(vv + r * D, qkv + r * 3 * D + 2 * D, sizeof(float) * D);
+    }
+    if (rope_c) {   /* q and k rotated before the 1/sqrt(d) scale (src/jepa.cpp:880-882) */
+        or_rope_apply(q, R, H, hd, rope_c, rope_s);
+        or_rope_apply(kk, R, H, hd, rope_c, rope_s);
+    }
+    or_attention(q, kk, vv, R, R, H, hd, 1.0f / sqrtf((float) hd), kv_f16, mask, att, n_threads);
+    if (linear(f, TN(n1, "attn_out.weight"), TN(n2, "attn_out.bias"), att, R, D, D, o, n_threads)) goto out;
+    {
+        const float * ls1 = gg_vec(f, TN(n1, "ls1"));
+        for (int64_t i = 0; i < R * D; i++) x[i] = x[i] + (ls1 ? o[i] * ls1[i % D] : o[i]);
+    }
+    or_layer_norm(x, R, D, gg_vec(f, TN(n1, "ln2.weight")), gg_vec(f, TN(n2, "ln2.bias")), eps, h);
+    if (linear(f, TN(n1, "ffn_up.weight"), TN(n2, "ffn_up.bias"), h, R, D, F, ff, n_threads)) goto out;
+#pragma omp parallel for num_threads(n_threads)
+    for (int64_t i = 0; i < R * F; i++) ff[i] = or_gelu_erf(ff[i]);
+    if (linear(f, TN(n1, "ffn_down.weight"), TN(n2, "ffn_down.bias"), ff, R, F, D, o, n_threads)) goto out;
+    {
+        const float * ls2 = gg_vec(f, TN(n1, "ls2"));
+        for (int64_t i = 0; i < R * D; i++) x[i] = x[i] + (ls2 ? o[i] * ls2[i % D] : o[i]);
+    }
+#undef TN
+    rc = 0;
+out:
+    free(h); free(qkv); free(q); free(kk); free(vv); free(att); free(o); free(ff);
+    return rc;
+}
+
 int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_chans, int n_frames,
                        int height, int width, float * out, int64_t out_cap, float * trace, int64_t trace_cap,
                        int n_layers_limit, int n_threads) {
@@ -857,7 +908,7 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
     const int video = !strcmp(fam, "vjepa2") || !strcmp(fam, "vjepa2_1") || !strcmp(fam, "levjepa");
     const int image = !strcmp(fam, "hfvit") || !strcmp(fam, "ijepa") || !strcmp(fam, "lewm");
     const int D = (int) gg_int(&f, "jepa.enc.embed_dim", 0), L = (int) gg_int(&f, "jepa.enc.n_layer", 0);
-    const int H = (int) gg_int(&f, "jepa.enc.n_head", 0), F = (int) gg_int(&f, "jepa.enc.ffn_dim", 0);
+    const int H = (int) gg_int(&f, "jepa.enc.n_head", 0);
     const int P = (int) gg_int(&f, "jepa.enc.patch_size", 16), C = (int) gg_int(&f, "jepa.enc.in_chans", 3);
     const int cls = (int) gg_int(&f, "jepa.enc.cls_token", 0), n_reg = (int) gg_int(&f, "jepa.enc.n_registers", 0);
     const float eps = (float) gg_flt(&f, "jepa.enc.ln_eps", 1e-6);
@@ -912,12 +963,6 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
 
     float * rows = (float *) malloc(sizeof(float) * Np * K);
     float * x = (float *) malloc(sizeof(float) * R * D);
-    float * h = (float *) malloc(sizeof(float) * R * D);
-    float * qkv = (float *) malloc(sizeof(float) * R * 3 * D);
-    float * q = (float *) malloc(sizeof(float) * R * D), * kk = (float *) malloc(sizeof(float) * R * D), * vv = (float *) malloc(sizeof(float) * R * D);
-    float * att = (float *) malloc(sizeof(float) * R * D);
-    float * o = (float *) malloc(sizeof(float) * R * D);
-    float * ff = (float *) malloc(sizeof(float) * R * F);
     float * chw = (float *) malloc(sizeof(float) * C * height * width * (video ? T : 1));
     const int64_t plane = (int64_t) height * width;
 
@@ -959,40 +1004,73 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
             memcpy(trace + off, x, sizeof(float) * R * D);
         }
         for (int l = 0; l < n_layers; l++) {
-            char n1[96], n2[96];
-#define TN(buf, s) (snprintf(buf, sizeof(buf), "enc.blk.%d.%s", l, s), buf)
-            char a1[96], a2[96];
-            or_layer_norm(x, R, D, gg_vec(&f, TN(a1, "ln1.weight")), gg_vec(&f, TN(a2, "ln1.bias")), eps, h);
-            if (linear(&f, TN(n1, "attn_qkv.weight"), TN(n2, "attn_qkv.bias"), h, R, D, 3 * D, qkv, n_threads)) goto done;
-            for (int64_t r = 0; r < R; r++) {
-                memcpy(q + r * D, qkv + r * 3 * D, sizeof(float) * D);
-                memcpy(kk + r * D, qkv + r * 3 * D + D, sizeof(float) * D);
-                memcpy(vv + r * D, qkv + r * 3 * D + 2 * D, sizeof(float) * D);
-            }
-            if (video) {   /* q and k rotated before the 1/sqrt(d) scale (src/jepa.cpp:880-882) */
-                or_rope_apply(q, R, H, hd, rope_c, rope_s);
-                or_rope_apply(kk, R, H, hd, rope_c, rope_s);
-            }
-            or_attention(q, kk, vv, R, R, H, hd, 1.0f / sqrtf((float) hd), kv_f16, mask, att, n_threads);
-            if (linear(&f, TN(n1, "attn_out.weight"), TN(n2, "attn_out.bias"), att, R, D, D, o, n_threads)) goto done;
-            const float * ls1 = gg_vec(&f, TN(a1, "ls1"));
-            for (int64_t i = 0; i < R * D; i++) x[i] = x[i] + (ls1 ? o[i] * ls1[i % D] : o[i]);
-            or_layer_norm(x, R, D, gg_vec(&f, TN(a1, "ln2.weight")), gg_vec(&f, TN(a2, "ln2.bias")), eps, h);
-            if (linear(&f, TN(n1, "ffn_up.weight"), TN(n2, "ffn_up.bias"), h, R, D, F, ff, n_threads)) goto done;
-#pragma omp parallel for num_threads(n_threads)
-            for (int64_t i = 0; i < R * F; i++) ff[i] = or_gelu_erf(ff[i]);
-            if (linear(&f, TN(n1, "ffn_down.weight"), TN(n2, "ffn_down.bias"), ff, R, F, D, o, n_threads)) goto done;
-            const float * ls2 = gg_vec(&f, TN(a1, "ls2"));
-            for (int64_t i = 0; i < R * D; i++) x[i] = x[i] + (ls2 ? o[i] * ls2[i % D] : o[i]);
-#undef TN
+            char pre[64];
+            snprintf(pre, sizeof(pre), "enc.blk.%d.", l);
+            if (block_fwd(&f, pre, x, R, D, H, video ? rope_c : NULL, rope_s, mask, kv_f16, eps, n_threads)) goto done;
             if (trace) memcpy(trace + (((int64_t) it * (n_layers + 1)) + l + 1) * R * D, x, sizeof(float) * R * D);
         }
         or_layer_norm(x, R, D, gg_vec(&f, "enc.norm.weight"), gg_vec(&f, "enc.norm.bias"), eps, out + (int64_t) it * R * D);
     }
     ret = R;
 done:
-    free(rows); free(x); free(h); free(qkv); free(q); free(kk); free(vv); free(att); free(o); free(ff); free(chw);
+    free(rows); free(x); free(chw);
     free(rope_c); free(rope_s); free(mask);
+    gg_close(&f);
+    return ret;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * attentive-pool head (src/jepa.cpp:1026-1075): n_pool_layers self-attention blocks without RoPE on
+ * the encoder rows, then one learned query cross-attends to LN_kv of them (no output projection);
+ * y = q0 + attn; y += ffn_down(gelu(ffn_up(LN2 y))); logits = cls(y). The cross-attention K/V stay
+ * f32 (kv_type F32 on the CPU, src/jepa.cpp:1053-1058); the blocks use the encoder's K/V rule.
+ * ---------------------------------------------------------------------------------------------- */
+int64_t or_head_file(const char * path, const float * x_in, int64_t N, float * pooled, float * logits, int64_t logits_cap,
+                     int n_threads) {
+    gg_file f;
+    if (gg_open(path, &f)) return -1;
+    int64_t ret = -1;
+    const int D = (int) gg_int(&f, "jepa.enc.embed_dim", 0), H = (int) gg_int(&f, "jepa.enc.n_head", 0);
+    const int n_pool = (int) gg_int(&f, "jepa.head.n_pool_layers", 0);
+    const float eps = (float) gg_flt(&f, "jepa.enc.ln_eps", 1e-6);
+    const int kv_f16 = gg_int(&f, "general.file_type", 0) != 0;
+    const int hd = H > 0 ? D / H : 0;
+    float * x = NULL, * kv = NULL, * k = NULL, * v = NULL, * q = NULL, * y = NULL, * h = NULL, * ff = NULL, * o = NULL;
+    if (strcmp(gg_str(&f, "jepa.head.kind", "none"), "attentive_pool") != 0 || D <= 0 || H <= 0 || N <= 0) {
+        fprintf(stderr, "oracle: no attentive-pool head\n"); goto done;
+    }
+    const gg_tensor * up = gg_tensor_find(&f, "head.xattn.ffn_up.weight");
+    const gg_tensor * cls = gg_tensor_find(&f, "head.cls.weight");
+    const float * q0 = gg_vec(&f, "head.query");
+    if (!up || !cls || !q0) { fprintf(stderr, "oracle: head tensors missing\n"); goto done; }
+    const int64_t F = up->ne[1], C = cls->ne[1];
+    if (C > logits_cap) { fprintf(stderr, "oracle: logits buffer too small\n"); goto done; }
+    x = (float *) malloc(sizeof(float) * N * D); kv = (float *) malloc(sizeof(float) * N * D);
+    k = (float *) malloc(sizeof(float) * N * D); v = (float *) malloc(sizeof(float) * N * D);
+    q = (float *) malloc(sizeof(float) * D); y = (float *) malloc(sizeof(float) * D); h = (float *) malloc(sizeof(float) * D);
+    o = (float *) malloc(sizeof(float) * D); ff = (float *) malloc(sizeof(float) * F);
+    memcpy(x, x_in, sizeof(float) * N * D);
+    for (int l = 0; l < n_pool; l++) {
+        char pre[64];
+        snprintf(pre, sizeof(pre), "head.blk.%d.", l);
+        if (block_fwd(&f, pre, x, N, D, H, NULL, NULL, NULL, kv_f16, eps, n_threads)) goto done;
+    }
+    or_layer_norm(x, N, D, gg_vec(&f, "head.xattn.ln_kv.weight"), gg_vec(&f, "head.xattn.ln_kv.bias"), eps, kv);
+    if (linear(&f, "head.xattn.q.weight", "head.xattn.q.bias", q0, 1, D, D, q, n_threads) ||
+        linear(&f, "head.xattn.k.weight", "head.xattn.k.bias", kv, N, D, D, k, n_threads) ||
+        linear(&f, "head.xattn.v.weight", "head.xattn.v.bias", kv, N, D, D, v, n_threads)) goto done;
+    or_attention(q, k, v, 1, N, H, hd, 1.0f / sqrtf((float) hd), 0, NULL, o, n_threads);
+    for (int d = 0; d < D; d++) y[d] = o[d] + q0[d];   /* residual on the raw query */
+    or_layer_norm(y, 1, D, gg_vec(&f, "head.xattn.ln2.weight"), gg_vec(&f, "head.xattn.ln2.bias"), eps, h);
+    if (linear(&f, "head.xattn.ffn_up.weight", "head.xattn.ffn_up.bias", h, 1, D, F, ff, n_threads)) goto done;
+    for (int64_t i = 0; i < F; i++) ff[i] = or_gelu_erf(ff[i]);
+    if (linear(&f, "head.xattn.ffn_down.weight", "head.xattn.ffn_down.bias", ff, 1, F, D, o, n_threads)) goto done;
+    for (int d = 0; d < D; d++) y[d] = y[d] + o[d];
+    if (pooled) memcpy(pooled, y, sizeof(float) * D);
+    if (logits && linear(&f, "head.cls.weight", "head.cls.bias", y, 1, D, C, logits, n_threads)) goto done;
+    ret = C;
+done:
+    free(x); free(kv); free(k); free(v); free(q); free(y); free(h); free(o); free(ff);
     gg_close(&f);
     return ret;
 }

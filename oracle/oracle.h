@@ -99,6 +99,11 @@ int64_t or_encode_file(const char * gguf_path, const float * in, int n_batch, in
                        int height, int width, float * out, int64_t out_cap_floats,
                        float * trace, int64_t trace_cap_floats, int n_layers_limit, int n_threads);
 
+/* Attentive-pool head of a GGUF file on encoder rows x [N][D] (what jepa_head_ex returns): pooled
+ * [D] and logits [n_classes] (either may be NULL). Returns n_classes, or -1 on error. */
+int64_t or_head_file(const char * gguf_path, const float * x, int64_t n_tokens, float * pooled, float * logits,
+                     int64_t logits_cap, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

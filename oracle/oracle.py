@@ -61,6 +61,8 @@ def lib() -> C.CDLL:
         L.or_encode_file.argtypes = [C.c_char_p, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64,
                                      vp, i64, C.c_int, C.c_int]
         L.or_encode_file.restype = i64
+        L.or_head_file.argtypes = [C.c_char_p, vp, i64, vp, vp, i64, C.c_int]
+        L.or_head_file.restype = i64
         for fn in ("or_fp32_to_fp16_row", "or_fp16_to_fp32_row"):
             getattr(L, fn).argtypes = [vp, vp, i64]
             getattr(L, fn).restype = None
@@ -207,6 +209,17 @@ def _encode(path, x, rows, dim, n_layers, trace, items):
     if tr is not None:
         tr = tr.reshape(items, n_layers + 1, rows, dim)
     return out, tr
+
+
+def head(path: str, x: np.ndarray, n_classes: int):
+    """Oracle attentive-pool head on encoder rows x [N, D]. Returns (pooled [D], logits [n_classes])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    pooled = np.zeros(x.shape[1], dtype=np.float32)
+    logits = np.zeros(max(n_classes, 1), dtype=np.float32)
+    r = lib().or_head_file(path.encode(), _p(x), x.shape[0], _p(pooled), _p(logits), logits.size, threads())
+    if r < 0:
+        raise RuntimeError("oracle head failed")
+    return pooled, logits[:r]
 
 
 def encode(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, n_layers: int = 0, trace: bool = False):

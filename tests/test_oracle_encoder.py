@@ -50,6 +50,63 @@ def _rot(x, C, S):
     return x * C + sw * S
 
 
+def _block64(T, has, p, h, D, H, rope, mask, kv_f16):
+    """One pre-LN block (reference src/jepa.cpp:444-471) in float64."""
+    n, hd = h.shape[0], D // H
+    a = _ln(h, T(p + "ln1.weight"), T(p + "ln1.bias"), 1e-6)
+    qkv = a @ T(p + "attn_qkv.weight").T + T(p + "attn_qkv.bias")
+    q, k, v = (qkv[:, j * D:(j + 1) * D].reshape(n, H, hd) for j in range(3))
+    if rope is not None:
+        q, k = _rot(q, rope[0][:, None], rope[1][:, None]), _rot(k, rope[0][:, None], rope[1][:, None])
+    if kv_f16:
+        k = k.astype(np.float32).astype(np.float16).astype(np.float64)
+        v = v.astype(np.float32).astype(np.float16).astype(np.float64)
+    att = np.zeros((n, H, hd))
+    for hh in range(H):
+        s = q[:, hh] @ k[:, hh].T / math.sqrt(hd) + (0 if mask is None else mask)
+        pr = np.exp(s - s.max(1, keepdims=True))
+        att[:, hh] = (pr / pr.sum(1, keepdims=True)) @ v[:, hh]
+    o = att.reshape(n, D) @ T(p + "attn_out.weight").T + T(p + "attn_out.bias")
+    if has(p + "ls1"):
+        o = o * T(p + "ls1")
+    h = h + o
+    f = _ln(h, T(p + "ln2.weight"), T(p + "ln2.bias"), 1e-6) @ T(p + "ffn_up.weight").T + T(p + "ffn_up.bias")
+    f = _gelu(f) @ T(p + "ffn_down.weight").T + T(p + "ffn_down.bias")
+    if has(p + "ls2"):
+        f = f * T(p + "ls2")
+    return h + f
+
+
+def head64(path, rows):
+    """The attentive-pool head (reference src/jepa.cpp:1026-1075) in float64 on encoder rows [N, D]:
+    pooler blocks without RoPE, one query cross-attending to LN_kv(x) with no output projection, the
+    residual on the raw query, LN2 + MLP, then the classifier. Returns (pooled, logits)."""
+    g = gguf.read_gguf(path)
+    kv = g.kv
+    T = lambda n: g.tensor_f32(n).astype(np.float64)
+    has = lambda n: n in g.tensors
+    D, H = kv["jepa.enc.embed_dim"], kv["jepa.enc.n_head"]
+    hd = D // H
+    x = rows.astype(np.float64)
+    for i in range(kv["jepa.head.n_pool_layers"]):
+        x = _block64(T, has, f"head.blk.{i}.", x, D, H, None, None, kv["general.file_type"] != 0)
+    q0 = T("head.query").reshape(D)
+    kvn = _ln(x, T("head.xattn.ln_kv.weight"), T("head.xattn.ln_kv.bias"), 1e-6)
+    q = (q0 @ T("head.xattn.q.weight").T + T("head.xattn.q.bias")).reshape(H, hd)
+    k = (kvn @ T("head.xattn.k.weight").T + T("head.xattn.k.bias")).reshape(-1, H, hd)
+    v = (kvn @ T("head.xattn.v.weight").T + T("head.xattn.v.bias")).reshape(-1, H, hd)
+    o = np.zeros((H, hd))
+    for hh in range(H):
+        s = k[:, hh] @ q[hh] / math.sqrt(hd)
+        pr = np.exp(s - s.max())
+        o[hh] = (pr / pr.sum()) @ v[:, hh]
+    y = o.reshape(D) + q0
+    f = _ln(y, T("head.xattn.ln2.weight"), T("head.xattn.ln2.bias"), 1e-6) @ T("head.xattn.ffn_up.weight").T
+    f = _gelu(f + T("head.xattn.ffn_up.bias")) @ T("head.xattn.ffn_down.weight").T + T("head.xattn.ffn_down.bias")
+    y = y + f
+    return y, y @ T("head.cls.weight").T + T("head.cls.bias")
+
+
 def forward64(path, x):
     g = gguf.read_gguf(path)
     kv = g.kv
@@ -59,6 +116,7 @@ def forward64(path, x):
     D, L, H, P = kv["jepa.enc.embed_dim"], kv["jepa.enc.n_layer"], kv["jepa.enc.n_head"], kv["jepa.enc.patch_size"]
     hd, eps = D // H, float(kv["jepa.enc.ln_eps"])
     video = fam in ("vjepa2", "vjepa2_1", "levjepa")
+    kv_f16 = kv["general.file_type"] != 0      # the CPU's K/V type rule (reference src/jepa.cpp:531-535)
     B, Cc, Tt, Hh, Ww = x.shape
     tub = kv["jepa.enc.tubelet_size"] if video else 1
     items = []
@@ -100,28 +158,7 @@ def forward64(path, x):
             vis[:npre] = True
             mask[~vis] = -np.inf
         for i in range(L):
-            p = f"enc.blk.{i}."
-            a = _ln(h, T(p + "ln1.weight"), T(p + "ln1.bias"), eps)
-            qkv = a @ T(p + "attn_qkv.weight").T + T(p + "attn_qkv.bias")
-            q, k, v = (qkv[:, j * D:(j + 1) * D].reshape(n, H, hd) for j in range(3))
-            if rope is not None:
-                q, k = _rot(q, rope[0][:, None], rope[1][:, None]), _rot(k, rope[0][:, None], rope[1][:, None])
-            k = k.astype(np.float32).astype(np.float16).astype(np.float64)
-            v = v.astype(np.float32).astype(np.float16).astype(np.float64)
-            att = np.zeros((n, H, hd))
-            for hh in range(H):
-                s = q[:, hh] @ k[:, hh].T / math.sqrt(hd) + mask
-                pr = np.exp(s - s.max(1, keepdims=True))
-                att[:, hh] = (pr / pr.sum(1, keepdims=True)) @ v[:, hh]
-            o = att.reshape(n, D) @ T(p + "attn_out.weight").T + T(p + "attn_out.bias")
-            if has(p + "ls1"):
-                o = o * T(p + "ls1")
-            h = h + o
-            f = _ln(h, T(p + "ln2.weight"), T(p + "ln2.bias"), eps) @ T(p + "ffn_up.weight").T + T(p + "ffn_up.bias")
-            f = _gelu(f) @ T(p + "ffn_down.weight").T + T(p + "ffn_down.bias")
-            if has(p + "ls2"):
-                f = f * T(p + "ls2")
-            h = h + f
+            h = _block64(T, has, f"enc.blk.{i}.", h, D, H, rope, mask, kv_f16)
         streams.append(h)
         outs.append(_ln(h, T("enc.norm.weight"), T("enc.norm.bias"), eps))
     return np.concatenate(outs), np.stack(streams), outs[0].shape[0], len(outs)
@@ -141,6 +178,19 @@ def test_oracle_encoder_matches_float64_forward(family, kw, tmp_path):
     # final LayerNorm output: rows with a small residual (the CLS row) have their rounding scaled up
     err = np.abs(got - want).max() / np.abs(want).max()
     assert err < 5e-4, err
+
+
+def test_oracle_head_matches_float64_head(tmp_path):
+    """The oracle's attentive-pool head against the float64 restatement above, on a tiny f32 model with
+    two pooler blocks and 10 classes; random LayerNorm affines so that ln_kv / ln2 count."""
+    cfg = forge.tiny("vjepa2", "f32", ln_random=True, n_classes=10, n_pool_layers=2)
+    path = forge.cached_model(cfg, str(tmp_path))
+    rows = np.random.default_rng(5).standard_normal((40, cfg.embed_dim)).astype(np.float32)
+    want_p, want_l = head64(path, rows)
+    got_p, got_l = O.head(path, rows, cfg.n_classes)
+    assert got_l.shape == (10,)
+    assert np.abs(got_p - want_p).max() / np.abs(want_p).max() < 2e-5
+    assert np.abs(got_l - want_l).max() / np.abs(want_l).max() < 1e-4
 
 
 def test_oracle_items_are_independent(tmp_path):
