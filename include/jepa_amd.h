@@ -74,15 +74,15 @@ int jepa_amd_matmul(int device, int wtype, const void * w_dev, int64_t n_out, in
 int jepa_amd_matmul_gelu(int device, int wtype, const void * w_dev, int64_t n_out, int64_t n_in, const float * bias_dev,
                          const float * x_dev, int64_t n_rows, int out_type, void * out_dev, int reps, double * gemm_ms);
 
-/* Attention of one block from its fused qkv rows: qkv_dev f32 [n_items*n_tok][3*n_head*64] (rows
- * [q | k | v], head-major), optional RoPE tables rope_c/rope_s [n_tok][64] (signed sine). Runs the QKV
- * epilogue's split/RoPE/f16 cast and the attention kernel. tokens_per_slot > 0 applies the LeVJEPA
- * block-causal mask (reference src/jepa.cpp:827-844): the n_prefix leading rows read every key, a patch
- * row reads the patch keys of its own and earlier temporal slots of tokens_per_slot rows, and no
- * prefix key; 0 is full attention. out_type 0 (f32): out_dev f32 [n_items*n_tok][n_head*64]; 8 (q8_0):
- * out_dev ggml q8_0 blocks of those rows, as the attention kernel's fused epilogue quantizes them for
- * the out-projection. */
-int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64_t n_tok, int n_head,
+/* Attention of one block from its fused qkv rows: qkv_dev f32 [n_items*n_tok][3*n_head*hd] (rows
+ * [q | k | v], head-major), head width hd 64 or 32, optional RoPE tables rope_c/rope_s [n_tok][hd]
+ * (signed sine). Runs the QKV epilogue's split/RoPE/f16 cast and the attention kernel. tokens_per_slot
+ * > 0 applies the LeVJEPA block-causal mask (reference src/jepa.cpp:827-844): the n_prefix leading
+ * rows read every key, a patch row reads the patch keys of its own and earlier temporal slots of
+ * tokens_per_slot rows, and no prefix key; 0 is full attention. out_type 0 (f32): out_dev f32
+ * [n_items*n_tok][n_head*hd]; 8 (q8_0): out_dev ggml q8_0 blocks of those rows, as the attention
+ * kernel's fused epilogue quantizes them for the out-projection. */
+int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64_t n_tok, int n_head, int hd,
                        const float * rope_c_dev, const float * rope_s_dev, int n_prefix, int64_t tokens_per_slot,
                        int out_type, void * out_dev);
 

@@ -4,6 +4,7 @@
 #include "kernels.h"
 #include "preprocess.h"
 
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -284,16 +285,18 @@ extern "C" int jepa_amd_gemm_tile(int index) {
     return 0;
 }
 
-extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items, int64_t n_tok, int n_head, const float * rope_c,
-                                  const float * rope_s, int n_prefix, int64_t tokens_per_slot, int out_type, void * out) {
+extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items, int64_t n_tok, int n_head, int hd,
+                                  const float * rope_c, const float * rope_s, int n_prefix, int64_t tokens_per_slot, int out_type,
+                                  void * out) {
     if (!qkv || !out || n_items <= 0 || n_tok <= 0 || n_head <= 0 || n_prefix < 0 || tokens_per_slot < 0 ||
         n_tok > 0x40000000) return -1;
+    if (hd != 64 && hd != 32) { jepa_log("jepa: jepa_amd_attention: head width %d (64 or 32)\n", hd); return -1; }
     if (out_type != T_F32 && out_type != T_Q8_0) { jepa_log("jepa: jepa_amd_attention: output type %d\n", out_type); return -1; }
     dev_scope d(device);
     if (!d.ok) return -1;
-    const int hd = 64;
+    const int hds = 64;   // stored head width
     const int64_t R_pad = (n_tok + 127) / 128 * 128;
-    const size_t bytes = (size_t) n_items * n_head * R_pad * hd * 2;
+    const size_t bytes = (size_t) n_items * n_head * R_pad * hds * 2;
     void * q = d.alloc(bytes), * k = d.alloc(bytes), * vt = d.alloc(bytes);
     if (!q || !k || !vt) return -1;
     launch_fill_zero(q, bytes, d.s);
@@ -302,7 +305,7 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
     gemm_epi ep;
     ep.kind = EPI_QKV;
     ep.q = q; ep.k = k; ep.vt = vt; ep.rope_c = rope_c; ep.rope_s = rope_s;
-    ep.n_head = n_head; ep.hd = hd; ep.D = n_head * hd; ep.R = n_tok; ep.R_pad = R_pad;
+    ep.n_head = n_head; ep.hd = hd; ep.hds = hds; ep.D = n_head * hd; ep.R = n_tok; ep.R_pad = R_pad;
     launch_qkv_split(qkv, n_items * n_tok, (int64_t) 3 * n_head * hd, ep, d.s);
     act_view o;
     const int64_t rows = n_items * n_tok, D = (int64_t) n_head * hd;
@@ -314,7 +317,7 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
         o.d = d.alloc((size_t) rows * (D / 32) * 2);
         if (!o.q || !o.d) return -1;
     }
-    launch_attention(q, k, vt, o, n_items, n_head, hd, n_tok, R_pad, 0.125f, n_prefix, tokens_per_slot, d.s);
+    launch_attention(q, k, vt, o, n_items, n_head, hd, n_tok, R_pad, 1.0f / sqrtf((float) hd), n_prefix, tokens_per_slot, d.s);
     if (out_type == T_Q8_0) launch_pack_act_blocks(o, rows, D, out, d.s);
     return d.finish();
 }

@@ -69,11 +69,13 @@ __device__ __forceinline__ int2 key_range(int q, int R, int np, int tpf) {
     return make_int2(np, min(R, np + ((q - np) / tpf + 1) * tpf));
 }
 
-// OUT: A_F32 writes O f32 [item*R][H*64]; A_Q8_0 writes the q8_0 activation of the next linear
-// (int8 codes [item*R][H*64] + f16 d per 32), the same values the separate quantizer would produce.
+// OUT: A_F32 writes O f32 [item*R][H*HDO]; A_Q8_0 writes the q8_0 activation of the next linear
+// (int8 codes [item*R][H*HDO] + f16 d per 32), the same values the separate quantizer would produce.
+// HDO: the heads' real width, 64, or 32 for heads stored 64 wide with a zero upper half (their
+// second Q.K^T dim pair and second P.V row block are skipped: both are zero).
 // np / tpf select the block-causal mask (tpf = 0: none); key tiles that no query of the workgroup
 // sees are not visited, 32-key blocks that no query of a wave sees are skipped by that wave.
-template <int OUT>
+template <int OUT, int HDO>
 __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
                                                       const _Float16 * __restrict__ Vt, void * __restrict__ O,
                                                       void * __restrict__ Od, int n_head, int64_t R, int64_t R_pad,
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
             if (kb0 + 32 <= lo_min || kb0 >= hi_max) continue;     // no query of this wave sees them
             f16v S = zero;
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) S = MFMA16(lds_chunk(sK, 32 * kb + l32, 2 * kk + g), qv[kk], S);
+            for (int kk = 0; kk < HDO / 16; kk++) S = MFMA16(lds_chunk(sK, 32 * kb + l32, 2 * kk + g), qv[kk], S);
             if (kb0 < lo_max || kb0 + 32 > hi_min) {                 // keys past R or outside a lane's range
                 const int key0 = kb0 + 4 * g;
 #pragma unroll
@@ -188,7 +190,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
                 for (int e = 0; e < 8; e++) pb[e] = (_Float16) p[8 * kk2 + e];
                 const int ch = 4 * kb + 2 * kk2 + g;
                 acc0 = MFMA16(lds_chunk(sV, l32, ch), pb, acc0);
-                acc1 = MFMA16(lds_chunk(sV, 32 + l32, ch), pb, acc1);
+                if constexpr (HDO == 64) acc1 = MFMA16(lds_chunk(sV, 32 + l32, ch), pb, acc1);
             }
         }
     }
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     float o0[16], o1[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) { o0[r] = acc0[r] * inv; o1[r] = acc1[r] * inv; }
-    const int64_t DD = (int64_t) n_head * HD;
+    const int64_t DD = (int64_t) n_head * HDO;
     if constexpr (OUT == A_Q8_0) {
         // dims 0-31 (acc0) and 32-63 (acc1) are one q8_0 block each, split over lanes l32 and l32+32
         float am0 = 0.0f, am1 = 0.0f;
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
         am1 = halves_max(am1);
         if (q >= R) return;
         const float id0 = am0 != 0.0f ? 127.0f / am0 : 0.0f, id1 = am1 != 0.0f ? 127.0f / am1 : 0.0f;
-        int8_t * crow = (int8_t *) O + (item * R + q) * DD + h * HD;
+        int8_t * crow = (int8_t *) O + (item * R + q) * DD + h * HDO;
 #pragma unroll
         for (int qq = 0; qq < 4; qq++) {
             uint32_t w0 = 0, w1 = 0;
@@ -244,21 +246,22 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
             }
             const int d = 8 * qq + 4 * g;
             *(uint32_t *) (crow + d) = w0;
-            *(uint32_t *) (crow + 32 + d) = w1;
+            if constexpr (HDO == 64) *(uint32_t *) (crow + 32 + d) = w1;
         }
         if (g == 0) {
-            uint16_t * drow = (uint16_t *) Od + (item * R + q) * (DD / 32) + h * 2;
+            uint16_t * drow = (uint16_t *) Od + (item * R + q) * (DD / 32) + h * (HDO / 32);
             drow[0] = f2hbits(am0 / 127.0f);
-            drow[1] = f2hbits(am1 / 127.0f);
+            if constexpr (HDO == 64) drow[1] = f2hbits(am1 / 127.0f);
         }
     } else {
         if (q >= R) return;
-        float * orow = (float *) O + (item * R + q) * DD + h * HD;
+        float * orow = (float *) O + (item * R + q) * DD + h * HDO;
 #pragma unroll
         for (int qq = 0; qq < 4; qq++) {
             const int d = 8 * qq + 4 * g;
             *(float4 *) (orow + d) = make_float4(o0[4 * qq], o0[4 * qq + 1], o0[4 * qq + 2], o0[4 * qq + 3]);
-            *(float4 *) (orow + 32 + d) = make_float4(o1[4 * qq], o1[4 * qq + 1], o1[4 * qq + 2], o1[4 * qq + 3]);
+            if constexpr (HDO == 64)
+                *(float4 *) (orow + 32 + d) = make_float4(o1[4 * qq], o1[4 * qq + 1], o1[4 * qq + 2], o1[4 * qq + 3]);
         }
     }
 }
@@ -268,14 +271,16 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items,
                       int n_head, int hd, int64_t R, int64_t R_pad, float scale, int n_prefix, int64_t tokens_per_slot,
                       hipStream_t s) {
-    (void) hd;   // only 64 (checked by the caller)
+    // hd: 64, or 32 (stored 64 wide; checked by the callers)
     const float c = scale * 1.4426950408889634f;   // exp(x*scale) = exp2(x*scale*log2(e))
     const int tpf = (int) tokens_per_slot;
     dim3 grid((unsigned) ((R + QB - 1) / QB), (unsigned) (n_items * n_head));
-    if (out.fmt == A_Q8_0)
-        k_attn_hd64<A_Q8_0><<<grid, 512, 0, s>>>((const _Float16 *) q, (const _Float16 *) k, (const _Float16 *) vt, out.q,
-                                                  out.d, n_head, R, R_pad, c, n_prefix, tpf);
-    else
-        k_attn_hd64<A_F32><<<grid, 512, 0, s>>>((const _Float16 *) q, (const _Float16 *) k, (const _Float16 *) vt, out.q,
-                                                 nullptr, n_head, R, R_pad, c, n_prefix, tpf);
+    const _Float16 * Q = (const _Float16 *) q, * K = (const _Float16 *) k, * V = (const _Float16 *) vt;
+    if (out.fmt == A_Q8_0) {
+        if (hd == 32) k_attn_hd64<A_Q8_0, 32><<<grid, 512, 0, s>>>(Q, K, V, out.q, out.d, n_head, R, R_pad, c, n_prefix, tpf);
+        else k_attn_hd64<A_Q8_0, 64><<<grid, 512, 0, s>>>(Q, K, V, out.q, out.d, n_head, R, R_pad, c, n_prefix, tpf);
+    } else {
+        if (hd == 32) k_attn_hd64<A_F32, 32><<<grid, 512, 0, s>>>(Q, K, V, out.q, nullptr, n_head, R, R_pad, c, n_prefix, tpf);
+        else k_attn_hd64<A_F32, 64><<<grid, 512, 0, s>>>(Q, K, V, out.q, nullptr, n_head, R, R_pad, c, n_prefix, tpf);
+    }
 }

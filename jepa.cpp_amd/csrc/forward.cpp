@@ -91,18 +91,18 @@ bool ws_alloc(fwd_workspace & w, void ** p, size_t bytes) {
     return true;
 }
 
-static bool alloc_act(fwd_workspace & w, act_view & a, int64_t rows, int64_t K) {
+bool ws_alloc_act(fwd_workspace & w, act_view & a, int64_t rows, int64_t K) {
     a.ld = K;
     return ws_alloc(w, &a.q, (size_t) rows * K * 4) &&   // f32 worst case (A_F32)
            ws_alloc(w, &a.d, (size_t) rows * std::max<int64_t>(K / 32 * 2, K / 256 * 4) + 16) &&
            ws_alloc(w, &a.bsum, (size_t) rows * (K / 16) * 2 + 16);
 }
 
-bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, int64_t F, int H, int hd, hipStream_t s) {
+bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, int64_t F, int H, int hds, hipStream_t s) {
     w.R = R;
     w.R_pad = (R + 127) / 128 * 128;
-    const int64_t rows = n_items * R, qkv = n_items * H * w.R_pad * hd * 2;
-    const bool ok = ws_alloc(w, (void **) &w.x, (size_t) rows * D * 4) && alloc_act(w, w.actA, rows, D) && alloc_act(w, w.actB, rows, F) &&
+    const int64_t rows = n_items * R, qkv = n_items * H * w.R_pad * hds * 2;
+    const bool ok = ws_alloc(w, (void **) &w.x, (size_t) rows * D * 4) && ws_alloc_act(w, w.actA, rows, D) && ws_alloc_act(w, w.actB, rows, F) &&
                     ws_alloc(w, &w.Q, (size_t) qkv) && ws_alloc(w, &w.Kt, (size_t) qkv) && ws_alloc(w, &w.Vt, (size_t) qkv) &&
                     ws_alloc(w, (void **) &w.attn, (size_t) rows * D * 4) && ws_alloc(w, (void **) &w.ff, (size_t) rows * F * 4) &&
                     ws_alloc(w, (void **) &w.out, (size_t) rows * D * 4);
@@ -118,51 +118,56 @@ bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, i
     return true;
 }
 
+blk_shape enc_blk_shape(const jepa_model * m) {
+    const enc_hparams & e = m->hp.enc;
+    blk_shape b;
+    b.D = e.embed_dim; b.H = e.n_head; b.hd = e.head_dim(); b.hds = std::max(b.hd, 64); b.eps = e.ln_eps;
+    return b;
+}
+
 const char * gemm_class(const dev_linear & W) {
     switch (W.fmt) { case W_F16: return "gemm_f16"; case W_Q32: return "gemm_q8"; case W_Q4K: return "gemm_q4k"; default: return "gemm_f32"; }
 }
 
+void enqueue_gemm_gelu(const dev_linear & W, const act_view & x, int64_t rows, act_view & out, fwd_workspace & w, hipStream_t s,
+                       ktimer & kt, const char * what) {
+    const int64_t F = W.n_out;
+    gemm_epi ep;
+    ep.ldy = F;
+    const bool mfma = W.fmt != W_F32;
+    if (mfma && out.fmt == A_Q8_0) { ep.kind = EPI_GELU_Q8_0; ep.oq = out.q; ep.od = out.d; }
+    else if (mfma && out.fmt == A_Q8_K && F % 256 == 0) { ep.kind = EPI_GELU_Q8_K; ep.oh = out.q; ep.od = out.d; ep.ob = out.bsum; }
+    else if (mfma && out.fmt == A_F16) { ep.kind = EPI_GELU_F16; ep.oh = out.q; }
+    else { ep.kind = EPI_GELU_F32; ep.y = w.ff; }
+    kt.run(gemm_class(W), [&] { launch_gemm(W, x, rows, ep, s, &w.split); }, what);
+    if (ep.kind == EPI_GELU_F32)
+        kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, out, s); }, "ff");
+}
+
 void enqueue_mlp(const dev_linear & up, const dev_linear & down, const float * ln_w, const float * ln_b, float eps, const float * ls,
                  float * x, int64_t rows, int64_t D, fwd_workspace & w, hipStream_t s, ktimer & kt) {
-    const int64_t F = up.n_out;
     w.actA.fmt = up.act();
     kt.run("layernorm", [&] { launch_rownorm_quant(x, rows, D, ln_w, ln_b, eps, true, w.actA, s); });
     w.actB.fmt = down.act();
-    {
-        gemm_epi ep;
-        ep.ldy = F;
-        const bool mfma = up.fmt != W_F32;
-        if (mfma && w.actB.fmt == A_Q8_0) { ep.kind = EPI_GELU_Q8_0; ep.oq = w.actB.q; ep.od = w.actB.d; }
-        else if (mfma && w.actB.fmt == A_Q8_K && F % 256 == 0) {
-            ep.kind = EPI_GELU_Q8_K; ep.oh = w.actB.q; ep.od = w.actB.d; ep.ob = w.actB.bsum;
-        }
-        else if (mfma && w.actB.fmt == A_F16) { ep.kind = EPI_GELU_F16; ep.oh = w.actB.q; }
-        else { ep.kind = EPI_GELU_F32; ep.y = w.ff; }
-        kt.run(gemm_class(up), [&] { launch_gemm(up, w.actA, rows, ep, s, &w.split); }, "up");
-        if (ep.kind == EPI_GELU_F32)
-            kt.run("quantize", [&] { launch_rownorm_quant(w.ff, rows, F, nullptr, nullptr, 0.0f, false, w.actB, s); }, "ff");
-    }
-    {
-        gemm_epi ep;
-        ep.kind = EPI_RESID; ep.y = x; ep.ldy = D; ep.ls = ls;
-        kt.run(gemm_class(down), [&] { launch_gemm(down, w.actB, rows, ep, s, &w.split); }, "down");
-    }
+    enqueue_gemm_gelu(up, w.actA, rows, w.actB, w, s, kt, "up");
+    gemm_epi ep;
+    ep.kind = EPI_RESID; ep.y = x; ep.ldy = D; ep.ls = ls;
+    kt.run(gemm_class(down), [&] { launch_gemm(down, w.actB, rows, ep, s, &w.split); }, "down");
 }
 
-void enqueue_block(const jepa_model * m, const dev_layer & L, fwd_workspace & w, int64_t n_items, int64_t R, const float * rope_c,
+void enqueue_block(const blk_shape & b, const dev_layer & L, fwd_workspace & w, int64_t n_items, int64_t R, const float * rope_c,
                    const float * rope_s, int n_prefix, int64_t slot_rows, hipStream_t s, ktimer & kt) {
-    const enc_hparams & e = m->hp.enc;
-    const int64_t D = e.embed_dim, rows = n_items * R;
-    const int H = e.n_head, hd = e.head_dim();
+    const int64_t D = b.D, rows = n_items * R;
+    const int H = b.H, hd = b.hd;
     // attention half
     w.actA.fmt = L.qkv.act();
-    kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln1_w, L.ln1_b, e.ln_eps, true, w.actA, s); });
+    kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln1_w, L.ln1_b, b.eps, true, w.actA, s); });
     {
         gemm_epi ep;
         ep.kind = EPI_QKV;
         ep.q = w.Q; ep.k = w.Kt; ep.vt = w.Vt;
         ep.rope_c = rope_c; ep.rope_s = rope_s;
-        ep.n_head = H; ep.hd = hd; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
+        ep.n_head = H; ep.hd = hd; ep.hds = b.hds; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
         kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
     }
     w.actA.fmt = L.out.act();
@@ -185,7 +190,7 @@ void enqueue_block(const jepa_model * m, const dev_layer & L, fwd_workspace & w,
         kt.run(gemm_class(L.out), [&] { launch_gemm(L.out, w.actA, rows, ep, s, &w.split); }, "out");
     }
     // MLP half
-    enqueue_mlp(L.up, L.down, L.ln2_w, L.ln2_b, e.ln_eps, L.ls2, w.x, rows, D, w, s, kt);
+    enqueue_mlp(L.up, L.down, L.ln2_w, L.ln2_b, b.eps, L.ls2, w.x, rows, D, w, s, kt);
 }
 
 namespace {
@@ -229,7 +234,7 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
     const dev_linear & pe = w->image_path ? m->patch_img : m->patch;
     const bool ok = ws_alloc(*w, &w->clip, (size_t) n_items * n_chans * (w->video ? n_frames : 1) * height * width * 4) &&
                     ws_alloc(*w, &w->patches, (size_t) n_items * w->Np * w->K * (pe.fmt == W_F32 ? 4 : 2)) &&
-                    ws_alloc_blocks(*w, n_items, w->Np + w->prefix, D, F, (int) H, (int) hd, ctx->stream);
+                    ws_alloc_blocks(*w, n_items, w->Np + w->prefix, D, F, (int) H, enc_blk_shape(m).hds, ctx->stream);
     if (!ok) { ctx->ws.reset(); return false; }
     if (w->video) {
         rope3d_params rp;
@@ -291,8 +296,9 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
     // block-causal attention (levjepa): temporal slots of gh*gw patch rows after the prefix rows
     const int64_t slot_rows = e.attn_mode == "block_causal" ? (int64_t) (w.height / e.patch_size) * (w.width / e.patch_size) : 0;
     const int n_prefix = (int) w.prefix;
+    const blk_shape bs = enc_blk_shape(m);
     for (int l = 0; l < e.n_layer; l++) {
-        enqueue_block(m, m->layers[(size_t) l], w, n_items, R, w.rope_c, w.rope_s, n_prefix, slot_rows, s, kt);
+        enqueue_block(bs, m->layers[(size_t) l], w, n_items, R, w.rope_c, w.rope_s, n_prefix, slot_rows, s, kt);
         if (trace) launch_copy_f32(w.x, trace + (int64_t) (l + 1) * rows * D, rows * D, s);
     }
     act_view o;

@@ -27,6 +27,10 @@ struct fwd_workspace {
     // attentive-pool head (head.cpp): query projection, pooled token, padded logits, pool partials
     float * hq = nullptr, * hy = nullptr, * hlog = nullptr, * hpart = nullptr;
     int64_t hpart_n = 0;
+    // masked predictor (predict.cpp): context rows in, target rows out, context embedding input codes
+    int n_ctx = 0, n_tgt = 0;
+    float * pin = nullptr, * pout = nullptr;
+    act_view actC;
     // graph
     hipGraphExec_t exec = nullptr;
     const float * g_in = nullptr; float * g_out = nullptr;
@@ -73,12 +77,28 @@ struct ktimer {   // optional per-kernel-class event timing (jepa_amd_context_se
     }
 };
 
+// shape of a transformer block: width, heads, head width, stored head width of Q / K / V^T (64 for
+// 32-wide heads, see gemm_epi::hds), LayerNorm epsilon
+struct blk_shape {
+    int64_t D = 0;
+    int H = 0, hd = 0, hds = 0;
+    float eps = 1e-6f;
+};
+blk_shape enc_blk_shape(const jepa_model * m);
+
 const char * gemm_class(const dev_linear & W);
 // a device buffer owned by the workspace (freed with it); logs and returns false on failure
 bool ws_alloc(fwd_workspace & w, void ** p, size_t bytes);
+// GEMM input buffers of `rows` rows of K values in any activation format
+bool ws_alloc_act(fwd_workspace & w, act_view & a, int64_t rows, int64_t K);
 // the residual-stream / block buffers of n_items x R rows: x, actA (D), actB (F), Q / K / V^T
-// (zero-padded to R_pad), attn, ff, out and the split-K scratch, for blocks of width D, FFN F
-bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, int64_t F, int H, int hd, hipStream_t s);
+// (H heads stored hds wide, zero-padded to R_pad rows), attn, ff, out and the split-K scratch, for
+// blocks of width D, FFN F
+bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, int64_t F, int H, int hds, hipStream_t s);
+// out = codes of gelu(x W^T + b) in the input format of the linear that consumes them (`out.fmt`),
+// through the GEMM's fused GELU + quantize epilogue (or f32 + the quantizer: w.ff holds rows x n_out)
+void enqueue_gemm_gelu(const dev_linear & W, const act_view & x, int64_t rows, act_view & out, fwd_workspace & w, hipStream_t s,
+                       ktimer & kt, const char * what);
 // MLP half of a block on the residual rows x [rows][D] (any f32 stream of the workspace's row count or
 // fewer): x += down(gelu(up(LN(x)))) [* ls], through w.actA / w.actB / w.ff
 void enqueue_mlp(const dev_linear & up, const dev_linear & down, const float * ln_w, const float * ln_b, float eps, const float * ls,
@@ -86,5 +106,5 @@ void enqueue_mlp(const dev_linear & up, const dev_linear & down, const float * l
 // One pre-LN transformer block on the workspace's residual stream w.x [n_items * R][D]
 // (reference src/jepa.cpp:444-471): x += out(attn(rope(qkv(LN1 x)))) [* ls1]; x += down(gelu(up(LN2 x))) [* ls2].
 // rope_c / rope_s null: no rotation; slot_rows > 0: block-causal attention after n_prefix rows.
-void enqueue_block(const jepa_model * m, const dev_layer & L, fwd_workspace & w, int64_t n_items, int64_t R, const float * rope_c,
+void enqueue_block(const blk_shape & b, const dev_layer & L, fwd_workspace & w, int64_t n_items, int64_t R, const float * rope_c,
                    const float * rope_s, int n_prefix, int64_t slot_rows, hipStream_t s, ktimer & kt);

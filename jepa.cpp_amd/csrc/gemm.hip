@@ -145,7 +145,7 @@ __device__ __forceinline__ void epi4(const kargs & a, int64_t m, int64_t n, floa
         h4 v = {(_Float16) gelu_erf(t[0]), (_Float16) gelu_erf(t[1]), (_Float16) gelu_erf(t[2]), (_Float16) gelu_erf(t[3])};
         *(h4 *) o = v;
     } else if constexpr (EPI == EPI_QKV) {
-        const int D = ep.D, hd = ep.hd;
+        const int D = ep.D, hd = ep.hd, hds = ep.hds ? ep.hds : hd;
         const int which = (int) (n / D);
         const int nn = (int) (n - (int64_t) which * D);
         const int h = nn / hd, d0 = nn - h * hd;
@@ -166,10 +166,10 @@ __device__ __forceinline__ void epi4(const kargs & a, int64_t m, int64_t n, floa
             }
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
             h4 v = {(_Float16) o[0], (_Float16) o[1], (_Float16) o[2], (_Float16) o[3]};
-            _Float16 * dst = (_Float16 *) (which == 0 ? ep.q : ep.k) + (head * ep.R_pad + tok) * hd + d0;
+            _Float16 * dst = (_Float16 *) (which == 0 ? ep.q : ep.k) + (head * ep.R_pad + tok) * hds + d0;
             *(h4 *) dst = v;
         } else {
-            _Float16 * vt = (_Float16 *) ep.vt + head * hd * ep.R_pad;
+            _Float16 * vt = (_Float16 *) ep.vt + head * hds * ep.R_pad;
             const int p = perm16(tok);
             for (int e = 0; e < 4; e++) vt[(int64_t) (d0 + e) * ep.R_pad + p] = (_Float16) t[e];
         }
@@ -884,7 +884,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 // the tile's 32 features lie in one head of one of Q, K, V (D and hd are multiples of 32):
                 // head and offset are wave-uniform, the token is one 32-bit division per lane
                 const gemm_epi & ep = a.ep;
-                const int hd = ep.hd;
+                const int hd = ep.hd, hds = ep.hds ? ep.hds : hd;
                 const int nbi = __builtin_amdgcn_readfirstlane((int) nb);
                 const int which = nbi / ep.D, nn = nbi - which * ep.D;
                 const int h = nn / hd, dbase = nn - h * hd + 4 * g;
@@ -901,7 +901,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                     for (int e = 0; e < 4; e++) t[4 * q + e] = a.bias ? __fadd_rn(acc[i][j][4 * q + e], bb[e]) : acc[i][j][4 * q + e];
                 }
                 if (which < 2) {
-                    _Float16 * dst = (_Float16 *) (which == 0 ? ep.q : ep.k) + (head * ep.R_pad + tok) * hd + dbase;
+                    _Float16 * dst = (_Float16 *) (which == 0 ? ep.q : ep.k) + (head * ep.R_pad + tok) * hds + dbase;
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         float o[4] = {t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]};
@@ -918,7 +918,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                         *(h4 *) (dst + 8 * q) = v;
                     }
                 } else {
-                    _Float16 * vt = (_Float16 *) ep.vt + (head * hd + dbase) * ep.R_pad + perm16(tok);
+                    _Float16 * vt = (_Float16 *) ep.vt + (head * hds + dbase) * ep.R_pad + perm16(tok);
 #pragma unroll
                     for (int q = 0; q < 4; q++)
 #pragma unroll
@@ -1130,6 +1130,7 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
     a.M = M; a.N = W.n_out; a.K = W.n_in;
     a.ep = ep;
     if (M <= 0) return;
+    if (a.ep.kind == EPI_F32 && a.ep.rin <= 0) { a.ep.rin = M; a.ep.rout = M; a.ep.pre = 0; }   // identity row map
     if (W.fmt == W_F32) {
         dim3 grid((unsigned) ((a.N + 63) / 64), (unsigned) ((M + 63) / 64));
         switch (ep.kind) {

@@ -59,7 +59,7 @@ bool ensure_head_workspace(jepa_context * ctx, int64_t N) {
     for (const dev_layer & L : h.blocks) F = std::max<int64_t>(F, L.up.n_out);
     const int64_t D = e.embed_dim;
     w->hpart_n = pool_attention_part_floats(N, e.n_head);
-    const bool ok = ws_alloc_blocks(*w, 1, N, D, F, e.n_head, e.head_dim(), ctx->stream) && ws_alloc(*w, (void **) &w->hq, (size_t) D * 4) &&
+    const bool ok = ws_alloc_blocks(*w, 1, N, D, F, e.n_head, enc_blk_shape(m).hds, ctx->stream) && ws_alloc(*w, (void **) &w->hq, (size_t) D * 4) &&
                     ws_alloc(*w, (void **) &w->hy, (size_t) D * 4) && ws_alloc(*w, (void **) &w->hlog, (size_t) h.cls.n_out * 4) &&
                     ws_alloc(*w, (void **) &w->hpart, (size_t) w->hpart_n * 4);
     if (!ok || hipStreamSynchronize(ctx->stream) != hipSuccess) { ctx->hws.reset(); return false; }
@@ -88,7 +88,8 @@ int head_run(jepa_context * ctx, int64_t N, bool with_logits) {
     ktimer kt{ctx};
     bool ok = true;
     hipEventRecord(ctx->ev0, s);
-    for (const dev_layer & L : h.blocks) enqueue_block(m, L, w, 1, N, nullptr, nullptr, 0, 0, s, kt);
+    const blk_shape bs = enc_blk_shape(m);
+    for (const dev_layer & L : h.blocks) enqueue_block(bs, L, w, 1, N, nullptr, nullptr, 0, 0, s, kt);
     // cross-attention: K and V from LN_kv(x) (one set of codes when both weights take the same input format)
     float * Kf = w.attn, * Vf = w.out;
     w.actA.fmt = h.k.act();

@@ -32,7 +32,7 @@ enum epi_kind {
 struct gemm_epi {
     int kind = EPI_F32;
     float * y = nullptr; int64_t ldy = 0;
-    int64_t rin = 0, rout = 0, pre = 0;     // EPI_F32 row map: row = (m/rin)*rout + pre + m%rin
+    int64_t rin = 0, rout = 0, pre = 0;     // EPI_F32 row map: row = (m/rin)*rout + pre + m%rin (rin 0: row = m)
     const float * addvec = nullptr;
     const float * addrows = nullptr;
     const float * ls = nullptr;
@@ -41,6 +41,8 @@ struct gemm_epi {
     void * q = nullptr; void * k = nullptr; void * vt = nullptr;
     const float * rope_c = nullptr; const float * rope_s = nullptr;
     int n_head = 0, hd = 0, D = 0;
+    int hds = 0;                            // stored head width of Q / K / V^T (0: hd); 64 for hd 32 heads,
+                                            // whose upper 32 dims stay zero
     int64_t R = 0, R_pad = 0;
 };
 
@@ -68,7 +70,8 @@ int gemm_split_for(int wf, int64_t N, int64_t K);
 void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w, const float * b, float eps,
                           bool normalize, const act_view & out, hipStream_t s);
 
-// Flash attention over (items*H) heads into `out` [item*R][H*hd]: A_F32 (f32 rows in out.q) or
+// Flash attention over (items*H) heads into `out` [item*R][H*hd]: hd 64, or hd 32 with Q / K / V^T
+// stored 64 wide (zero upper half, gemm_epi::hds). A_F32 (f32 rows in out.q) or
 // A_Q8_0 (the next linear's q8_0 activation: int8 codes in out.q, f16 d per 32 in out.d).
 // tokens_per_slot > 0 applies the block-causal mask: n_prefix leading rows read every key, a patch row
 // reads the patch keys of its own and earlier temporal slots (tokens_per_slot rows each) and no prefix

@@ -157,6 +157,36 @@ bool hparams_from_gguf(const gguf::file & f, hparams & hp, std::vector<std::pair
     }
     hp.has_pred = r.has("jepa.pred.kind") && r.gets("jepa.pred.kind", "none") != "none";
     hp.pred_kind = r.gets("jepa.pred.kind", "");
+    if (hp.has_pred) {
+        // src/jepa-gguf.cpp:379-440
+        pred_hparams & p = hp.pred;
+        p.kind = hp.pred_kind;
+        const int64_t ped = r.geti("jepa.pred.embed_dim", 0), pnl = r.geti("jepa.pred.n_layer", 0), pnh = r.geti("jepa.pred.n_head", 0);
+        const int64_t pff = r.geti("jepa.pred.ffn_dim", 0), phd = r.geti("jepa.pred.head_dim", 0), pnm = r.geti("jepa.pred.n_mask_tokens", 0);
+        const int64_t pod = r.geti("jepa.pred.out_dim", e.embed_dim), pgs = r.geti("jepa.pred.grid_size", 0);
+        const int64_t prg = r.geti("jepa.pred.rope_ref_grid", 0);
+        if (!kv_range("jepa.pred.embed_dim", ped, 1, JEPA_LIMIT_EMBED_DIM) || !kv_range("jepa.pred.n_layer", pnl, 1, JEPA_LIMIT_N_LAYER) ||
+            !kv_range("jepa.pred.n_head", pnh, 1, JEPA_LIMIT_N_HEAD) || !kv_range("jepa.pred.ffn_dim", pff, 1, JEPA_LIMIT_FFN_DIM) ||
+            !kv_range("jepa.pred.out_dim", pod, 1, JEPA_LIMIT_FFN_DIM) || !kv_range("jepa.pred.head_dim", phd, 0, JEPA_LIMIT_EMBED_DIM) ||
+            !kv_range("jepa.pred.n_mask_tokens", pnm, 0, JEPA_LIMIT_N_TOKENS) ||
+            !kv_range("jepa.pred.grid_size", pgs, 0, JEPA_LIMIT_IMG_SIZE) || !kv_range("jepa.pred.rope_ref_grid", prg, 0, JEPA_LIMIT_IMG_SIZE))
+            return false;
+        p.embed_dim = (int) ped; p.n_layer = (int) pnl; p.n_head = (int) pnh; p.ffn_dim = (int) pff; p.head_dim = (int) phd;
+        p.n_mask_tokens = (int) pnm; p.out_dim = (int) pod; p.grid_size = (int) pgs; p.rope_ref_grid = (int) prg;
+        p.rope_freq_layout = r.gets("jepa.pred.rope_freq_layout", "");
+        p.rope_interpolate = r.getb("jepa.pred.rope_interpolate", false);
+        p.modality_embed = r.getb("jepa.pred.modality_embed", false);
+        if (!act_from_string(r.gets("jepa.pred.act", "gelu_erf"), p.act)) return false;
+        if (p.head_dim == 0 && p.embed_dim % p.n_head != 0) {
+            jepa_log("jepa: jepa.pred.embed_dim %d is not divisible by jepa.pred.n_head %d and there is no jepa.pred.head_dim\n",
+                     p.embed_dim, p.n_head);
+            return false;
+        }
+        if (p.rope_interpolate && p.rope_ref_grid <= 0) {
+            jepa_log("jepa: jepa.pred.rope_interpolate is set but jepa.pred.rope_ref_grid is %d\n", p.rope_ref_grid);
+            return false;
+        }
+    }
     hp.head_kind = r.gets("jepa.head.kind", "none");
     hp.has_head = hp.head_kind != "none" && !hp.head_kind.empty();
     if (hp.has_head) {
@@ -327,7 +357,8 @@ struct loader {
 
     // one pre-LN block "<p>ln1.weight" ... (src/jepa-gguf.cpp:236-252 names) of FFN width F (0: the
     // ffn_up tensor's row count)
-    bool block(const std::string & p, int64_t D, int64_t F, dev_layer & Ly) {
+    bool block(const std::string & p, int64_t D, int64_t F, dev_layer & Ly, int64_t inner = 0) {
+        if (inner <= 0) inner = D;   // attention width n_head * head_dim
         if (!f.tensor(p + "ln1.weight") || !f.tensor(p + "ln2.weight") || !f.tensor(p + "attn_out.weight") || !f.tensor(p + "ffn_up.weight") ||
             !f.tensor(p + "ffn_down.weight") || !f.tensor(p + "attn_qkv.weight")) {
             jepa_log("jepa: block %s* is incomplete: needs ln1/ln2/attn_out/ffn_up/ffn_down and attn_qkv\n", p.c_str());
@@ -336,8 +367,8 @@ struct loader {
         if (F <= 0) F = rows_of(p + "ffn_up.weight");
         return vec(p + "ln1.weight", D, &Ly.ln1_w) && vec(p + "ln1.bias", D, &Ly.ln1_b) && vec(p + "ln2.weight", D, &Ly.ln2_w) &&
                vec(p + "ln2.bias", D, &Ly.ln2_b) && vec(p + "ls1", D, &Ly.ls1) && vec(p + "ls2", D, &Ly.ls2) &&
-               linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * D, Ly.qkv, true) &&
-               linear(p + "attn_out.weight", p + "attn_out.bias", D, D, Ly.out, true) &&
+               linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * inner, Ly.qkv, true) &&
+               linear(p + "attn_out.weight", p + "attn_out.bias", inner, D, Ly.out, true) &&
                linear(p + "ffn_up.weight", p + "ffn_up.bias", D, F, Ly.up, true) &&
                linear(p + "ffn_down.weight", p + "ffn_down.bias", F, D, Ly.down, true);
     }
@@ -439,6 +470,36 @@ extern "C" jepa_model * jepa_model_load_ex(const char * path, const jepa_model_p
         if (ok && e.modality_embed && video && !m->mod_video) {
             jepa_log("jepa: jepa.enc.modality_embed is set but enc.mod_embed_video is missing\n");
             ok = false;
+        }
+    }
+    if (ok && encoder && m->hp.has_pred && m->hp.pred.kind == "masked") {
+        // src/jepa-gguf.cpp:990-1066: blocks, norm, mask tokens, embed (linear or 2-layer MLP), proj
+        const pred_hparams & p = m->hp.pred;
+        dev_pred & pr = m->pred;
+        const int64_t Dp = p.embed_dim;
+        pr.blocks.resize((size_t) p.n_layer);
+        for (int i = 0; i < p.n_layer && ok; i++) ok = L.block("pred.blk." + std::to_string(i) + ".", Dp, p.ffn_dim, pr.blocks[(size_t) i],
+                          (int64_t) p.n_head * p.head_dim_eff());
+        const gguf::tensor_info * mt = f.tensor("pred.mask_tokens");
+        if (ok && (!mt || mt->ne[0] != Dp || mt->ne[1] < 1 || mt->ne[2] != 1 || mt->ne[3] != 1)) {
+            jepa_log("jepa: pred.mask_tokens is missing or not [%" PRId64 ", n] f32\n", Dp);
+            ok = false;
+        }
+        if (ok && p.n_mask_tokens > mt->ne[1]) {
+            jepa_log("jepa: jepa.pred.n_mask_tokens is %d but pred.mask_tokens holds %" PRId64 " rows\n", p.n_mask_tokens, mt->ne[1]);
+            ok = false;
+        }
+        if (ok) pr.n_mask_rows = mt->ne[1];
+        ok = ok && L.vec("pred.mask_tokens", -1, &pr.mask_tokens, true) && L.vec("pred.norm.weight", Dp, &pr.norm_w, true) &&
+             L.vec("pred.norm.bias", Dp, &pr.norm_b) && L.vec("pred.mod_embed_video", Dp, &pr.mod_video) &&
+             L.vec("pred.mod_embed_img", Dp, &pr.mod_img) &&
+             L.linear("pred.proj.weight", "pred.proj.bias", Dp, p.out_dim, pr.proj, true);
+        if (ok && f.tensor("pred.embed.0.weight")) {
+            const int64_t hid = L.rows_of("pred.embed.0.weight");
+            ok = L.linear("pred.embed.0.weight", "pred.embed.0.bias", D, hid, pr.embed0, true) &&
+                 L.linear("pred.embed.2.weight", "pred.embed.2.bias", hid, Dp, pr.embed2, true);
+        } else if (ok) {
+            ok = L.linear("pred.embed.weight", "pred.embed.bias", D, Dp, pr.embed, true);
         }
     }
     if (ok && encoder && m->hp.head_kind == "attentive_pool") {

@@ -60,6 +60,17 @@ struct pre_hparams {
     float rescale = 1.0f / 255.0f;
 };
 
+// jepa.pred.* of the masked predictor (reference src/jepa-internal.h:142-173, src/jepa-gguf.cpp:379-440)
+struct pred_hparams {
+    std::string kind;              // masked | ac | lewm
+    int   embed_dim = 0, n_layer = 0, n_head = 0, ffn_dim = 0, head_dim = 0;
+    int   n_mask_tokens = 0, out_dim = 0, grid_size = 0, rope_ref_grid = 0;
+    std::string rope_freq_layout;
+    bool  rope_interpolate = false, modality_embed = false;
+    act_id act = ACT_GELU_ERF;
+    int head_dim_eff() const { return head_dim > 0 ? head_dim : (n_head > 0 ? embed_dim / n_head : 0); }
+};
+
 struct hparams {
     std::string arch, name, family_str, modality;
     uint32_t file_type = 0;
@@ -68,6 +79,7 @@ struct hparams {
     pre_hparams pre;
     bool has_pred = false, has_head = false;
     std::string pred_kind, head_kind;
+    pred_hparams pred;
     int n_classes = 0, n_pool_layers = 0;
     std::vector<std::string> labels;
 };
@@ -107,6 +119,18 @@ struct dev_head {
     dev_linear q, k, v, up, down, cls;   // cls: n_out rounded up to 128, n_valid = n_classes
 };
 
+// masked predictor (reference src/predictor.cpp:56-133)
+struct dev_pred {
+    dev_linear embed;                // pred.embed: encoder width -> predictor width
+    dev_linear embed0, embed2;       // or the 2-layer MLP pred.embed.0 / .2 (V-JEPA 2.1 ViT-g/G)
+    float * mask_tokens = nullptr;   // [n_mask_rows][Dp]
+    int64_t n_mask_rows = 0;
+    float * mod_video = nullptr, * mod_img = nullptr;
+    float * norm_w = nullptr, * norm_b = nullptr;
+    std::vector<dev_layer> blocks;   // pred.blk.{i}
+    dev_linear proj;                 // pred.proj: predictor width -> out_dim
+};
+
 struct jepa_model {
     std::string path;
     hparams hp;
@@ -122,6 +146,7 @@ struct jepa_model {
     float * norm_w = nullptr, * norm_b = nullptr;
     std::vector<dev_layer> layers;
     dev_head head;                   // loaded when jepa.head.kind = attentive_pool
+    dev_pred pred;                   // loaded when jepa.pred.kind = masked
     std::vector<void *> allocations;   // every device allocation, freed with the model
 };
 
@@ -141,6 +166,7 @@ struct jepa_context {
     bool use_graph = true;           // capture the forward into a hipGraph and replay it
     std::unique_ptr<fwd_workspace> ws;
     std::unique_ptr<fwd_workspace> hws;   // jepa_head's buffers, made for the last token count
+    std::unique_ptr<fwd_workspace> pws;   // jepa_predict's buffers, made for the last context + target count
     void * io_in = nullptr, * io_out = nullptr;   // device copies of jepa_encode's host input / output
     size_t io_in_cap = 0, io_out_cap = 0;
     // per-kernel timing (jepa_amd_context_set_kernel_timing)

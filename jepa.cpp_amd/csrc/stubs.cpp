@@ -24,9 +24,6 @@ extern "C" {
 
 int jepa_lewm_project(jepa_context *, const jepa_output *, jepa_output *) { NOPE_INT("jepa_lewm_project"); }
 int jepa_lewm_project_rows(jepa_context *, const float *, int, jepa_output *) { NOPE_INT("jepa_lewm_project_rows"); }
-int jepa_predict(jepa_context *, const jepa_output *, const int32_t *, int, const int32_t *, int, jepa_output *) { NOPE_INT("jepa_predict"); }
-int jepa_predict_ex(jepa_context *, const jepa_output *, const int32_t *, int, const int32_t *, int, int, jepa_output *) { NOPE_INT("jepa_predict_ex"); }
-int jepa_predict_mod(jepa_context *, const jepa_output *, const int32_t *, int, const int32_t *, int, int, int, jepa_output *) { NOPE_INT("jepa_predict_mod"); }
 
 int jepa_lewm_n_frames(const jepa_model *) { return 0; }
 int jepa_lewm_action_dim(const jepa_model *) { return 0; }

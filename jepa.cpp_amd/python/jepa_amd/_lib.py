@@ -101,6 +101,10 @@ def lib() -> C.CDLL:
         "jepa_model_n_classes": (C.c_int, [vp]),
         "jepa_model_label": (cp, [vp, C.c_int]),
         "jepa_amd_head_device": (C.c_int, [vp, vp, i64, vp, vp]),
+        "jepa_model_has_predictor": (C.c_bool, [vp]),
+        "jepa_predict": (C.c_int, [vp, C.POINTER(Output), vp, C.c_int, vp, C.c_int, C.POINTER(Output)]),
+        "jepa_predict_ex": (C.c_int, [vp, C.POINTER(Output), vp, C.c_int, vp, C.c_int, C.c_int, C.POINTER(Output)]),
+        "jepa_predict_mod": (C.c_int, [vp, C.POINTER(Output), vp, C.c_int, vp, C.c_int, C.c_int, C.c_int, C.POINTER(Output)]),
         # jepa_amd.h
         "jepa_amd_encode_device": (i64, [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, i64]),
         "jepa_amd_encode_trace": (i64, [vp, C.POINTER(Input), vp, i64, vp, i64]),
@@ -113,7 +117,7 @@ def lib() -> C.CDLL:
         "jepa_amd_rownorm": (C.c_int, [C.c_int, vp, i64, i64, vp, vp, C.c_float, C.c_int, C.c_int, vp]),
         "jepa_amd_matmul": (C.c_int, [C.c_int, C.c_int, vp, i64, i64, vp, vp, i64, vp, C.c_int, C.POINTER(C.c_double)]),
         "jepa_amd_matmul_gelu": (C.c_int, [C.c_int, C.c_int, vp, i64, i64, vp, vp, i64, C.c_int, vp, C.c_int, C.POINTER(C.c_double)]),
-        "jepa_amd_attention": (C.c_int, [C.c_int, vp, i64, i64, C.c_int, vp, vp, C.c_int, i64, C.c_int, vp]),
+        "jepa_amd_attention": (C.c_int, [C.c_int, vp, i64, i64, C.c_int, C.c_int, vp, vp, C.c_int, i64, C.c_int, vp]),
         "jepa_amd_mfma_probe": (C.c_int, [C.c_int, vp, vp, vp]),
         "jepa_amd_copy": (C.c_int, [C.c_int, vp, vp, i64, C.c_int, C.POINTER(C.c_double)]),
         "jepa_amd_gemm_tile": (C.c_int, [C.c_int]),
@@ -153,6 +157,7 @@ class Model:
         self.dim = L.jepa_model_embed_dim(self.ptr)
         self.n_layer = L.jepa_model_n_layer(self.ptr)
         self.has_head = bool(L.jepa_model_has_head(self.ptr))
+        self.has_predictor = bool(L.jepa_model_has_predictor(self.ptr))
         self.n_classes = int(L.jepa_model_n_classes(self.ptr))
 
     def label(self, i: int):
@@ -211,6 +216,22 @@ class Context:
             res.append(np.ctypeslib.as_array(o.data, shape=(o.dim,)).copy())
             L.jepa_free(C.cast(o.data, C.c_void_p))
         return tuple(res)
+
+    def predict(self, enc: np.ndarray, ctx_ids, tgt_ids, mask_index: int = 1, modality: int = 1) -> np.ndarray:
+        """Masked predictor (jepa_predict_mod): encoder rows [N, dim], context / target token ids."""
+        L = lib()
+        enc = np.ascontiguousarray(enc, dtype=np.float32)
+        e = Output(C.cast(enc.ctypes.data, C.POINTER(C.c_float)), enc.shape[0], enc.shape[1])
+        ci = None if ctx_ids is None else np.ascontiguousarray(ctx_ids, dtype=np.int32)
+        ti = None if tgt_ids is None else np.ascontiguousarray(tgt_ids, dtype=np.int32)
+        out = Output()
+        L.jepa_error_reset()
+        check(L.jepa_predict_mod(self.ptr, C.byref(e), None if ci is None else ci.ctypes.data, 0 if ci is None else len(ci),
+                                 None if ti is None else ti.ctypes.data, 0 if ti is None else len(ti), mask_index, modality,
+                                 C.byref(out)), "jepa_predict_mod")
+        y = np.ctypeslib.as_array(out.data, shape=(out.n_tokens, out.dim)).copy()
+        L.jepa_free(C.cast(out.data, C.c_void_p))
+        return y
 
     def head_device(self, x_ptr: int, n_tokens: int, pooled_ptr: int, logits_ptr: int) -> int:
         return check(lib().jepa_amd_head_device(self.ptr, x_ptr, n_tokens, pooled_ptr, logits_ptr), "jepa_amd_head_device")

@@ -43,6 +43,13 @@ class EncoderConfig:
     attn_mode: str = "full"  # full | block_causal (levjepa)
     n_classes: int = 0       # > 0: attentive-pool classifier head (video families)
     n_pool_layers: int = 0   # self-attention blocks of the head, run before the cross-attention
+    pred_dim: int = 0        # > 0: masked predictor of this width (heads of 32, V-JEPA 2 / 2.1)
+    pred_layers: int = 0
+    pred_ffn: int = 0
+    pred_mask_tokens: int = 10
+    pred_mlp_embed: bool = False   # pred.embed.0 / .2 two-layer embedding (V-JEPA 2.1 ViT-g/G)
+    pred_grid: int = 0             # jepa.pred.grid_size (0: the encoder's img_size / patch)
+    w_std: float = 0.02            # standard deviation of the matmul weights
     seed: int = 1234
 
 
@@ -72,6 +79,10 @@ CONFIGS = {
     "vitl16_ssv2_q8_0": EncoderConfig("vjepa2-vitl16-256-ssv2-synthetic", "vjepa2", 1024, 24, 16, 4096, patch=16,
                                       tubelet=2, img_size=256, n_frames=16, ftype="q8_0", rope_layout="tiled",
                                       n_classes=174, n_pool_layers=3),
+    # V-JEPA 2 ViT-L/16 with its masked predictor (384 wide, 12 blocks, 12 heads of 32, 10 mask tokens)
+    "vitl16_pred_q8_0": EncoderConfig("vjepa2-vitl16-256-predictor-synthetic", "vjepa2", 1024, 24, 16, 4096, patch=16,
+                                      tubelet=2, img_size=256, n_frames=16, ftype="q8_0", rope_layout="tiled",
+                                      pred_dim=384, pred_layers=12, pred_ffn=1536),
     "vitg16_q8_0": EncoderConfig("vjepa2-vitg16-256-synthetic", "vjepa2", 1408, 40, 22, 6144, patch=16, tubelet=2,
                                  img_size=256, n_frames=64, ftype="q8_0", rope_layout="tiled"),
 }
@@ -144,6 +155,20 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     w.add("jepa.enc.layer_scale", cfg.layer_scale)
     if cfg.attn_mode != "full":
         w.add("jepa.enc.attn_mode", cfg.attn_mode)
+    if cfg.pred_dim > 0:
+        w.add("jepa.pred.kind", "masked")
+        w.add("jepa.pred.embed_dim", cfg.pred_dim)
+        w.add("jepa.pred.n_layer", cfg.pred_layers)
+        w.add("jepa.pred.n_head", cfg.pred_dim // 32)
+        w.add("jepa.pred.ffn_dim", cfg.pred_ffn)
+        w.add("jepa.pred.n_mask_tokens", cfg.pred_mask_tokens)
+        w.add("jepa.pred.out_dim", D)
+        w.add("jepa.pred.rope_freq_layout", cfg.rope_layout)
+        w.add("jepa.pred.act", "gelu_erf")
+        if cfg.pred_grid:
+            w.add("jepa.pred.grid_size", cfg.pred_grid)
+        if cfg.modality_embed:
+            w.add("jepa.pred.modality_embed", True)
     if cfg.n_classes > 0:
         w.add("jepa.head.kind", "attentive_pool")
         w.add("jepa.head.n_classes", cfg.n_classes)
@@ -160,20 +185,20 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
         return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
     def mat(name, n_out, n_in, gtype):
-        x = normal(n_out, n_in)
+        x = normal(n_out, n_in, std=cfg.w_std)
         w.add_tensor(name, gtype, (n_in, n_out), quantize(gtype, x))
 
     def vec(name, n, value=None, std=0.02):
         x = np.full(n, value, dtype=np.float32) if value is not None else normal(n, std=std)
         w.add_tensor(name, GGML_F32, (n,), x)
 
-    def ln(prefix):
+    def ln(prefix, n=D):
         if cfg.ln_random:
-            w.add_tensor(prefix + ".weight", GGML_F32, (D,), (1.0 + normal(D, std=0.1)).astype(np.float32))
-            vec(prefix + ".bias", D, std=0.1)
+            w.add_tensor(prefix + ".weight", GGML_F32, (n,), (1.0 + normal(n, std=0.1)).astype(np.float32))
+            vec(prefix + ".bias", n, std=0.1)
         else:
-            vec(prefix + ".weight", D, 1.0)
-            vec(prefix + ".bias", D, 0.0)
+            vec(prefix + ".weight", n, 1.0)
+            vec(prefix + ".bias", n, 0.0)
 
     patch_type = GGML_F16 if video else GGML_F32
     if cfg.ftype == "f32":
@@ -192,13 +217,13 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     if not video:
         n_tok = (cfg.img_size // cfg.patch) ** 2 + (1 if cfg.cls_token else 0)
         w.add_tensor("enc.pos_embed", GGML_F32, (D, n_tok), normal(n_tok, D))
-    def block(p):
-        ln(p + "ln1")
+    def block(p, D=D, F=F):
+        ln(p + "ln1", D)
         mat(p + "attn_qkv.weight", 3 * D, D, _block_type(cfg, D))
         vec(p + "attn_qkv.bias", 3 * D)
         mat(p + "attn_out.weight", D, D, _block_type(cfg, D))
         vec(p + "attn_out.bias", D)
-        ln(p + "ln2")
+        ln(p + "ln2", D)
         mat(p + "ffn_up.weight", F, D, _block_type(cfg, D))
         vec(p + "ffn_up.bias", F)
         mat(p + "ffn_down.weight", D, F, _block_type(cfg, F))
@@ -210,6 +235,27 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     for i in range(cfg.n_layer):
         block(f"enc.blk.{i}.")
     ln("enc.norm")
+    if cfg.pred_dim > 0:
+        # masked predictor tensors (src/jepa-gguf.cpp:990-1066); pred.embed* / pred.proj / the blocks take
+        # the file type (tools/jepa-quantize.cpp:105-116), mask tokens and modality vectors stay f32
+        Dp = cfg.pred_dim
+        if cfg.pred_mlp_embed:
+            mat("pred.embed.0.weight", 4 * Dp, D, _block_type(cfg, D))
+            vec("pred.embed.0.bias", 4 * Dp)
+            mat("pred.embed.2.weight", Dp, 4 * Dp, _block_type(cfg, 4 * Dp))
+            vec("pred.embed.2.bias", Dp)
+        else:
+            mat("pred.embed.weight", Dp, D, _block_type(cfg, D))
+            vec("pred.embed.bias", Dp)
+        w.add_tensor("pred.mask_tokens", GGML_F32, (Dp, cfg.pred_mask_tokens), normal(cfg.pred_mask_tokens, Dp, std=1.0))
+        if cfg.modality_embed:
+            vec("pred.mod_embed_img", Dp, std=0.5)
+            vec("pred.mod_embed_video", Dp, std=0.5)
+        for i in range(cfg.pred_layers):
+            block(f"pred.blk.{i}.", Dp, cfg.pred_ffn)
+        ln("pred.norm", Dp)
+        mat("pred.proj.weight", D, Dp, _block_type(cfg, Dp))
+        vec("pred.proj.bias", D)
     if cfg.n_classes > 0:
         # head tensors (docs/gguf-schema.md:121-137); every head matrix takes the file type
         # (tools/jepa-quantize.cpp:105-116: head.blk.*, head.xattn.*, head.cls.)

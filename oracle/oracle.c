@@ -659,6 +659,11 @@ void or_block_causal_mask(int gt, int gh, int gw, int n_prefix, float * out) {
         }
 }
 
+/* 1: with f16 K/V, also round q and the softmax weights p to f16 before their products (what an f16
+ * matrix-core attention does: ggml's CUDA kernels, its CPU per-row path for q, the GPU kernel here) */
+static int g_attn_f16 = 0;
+void or_set_attn_f16(int on) { g_attn_f16 = on; }
+
 void or_attention(const float * q, const float * k, const float * v, int64_t n_q, int64_t n_kv,
                   int n_head, int hd, float scale, int kv_f16, const float * mask, float * out, int n_threads) {
     const int64_t row = (int64_t) n_head * hd;
@@ -678,6 +683,11 @@ void or_attention(const float * q, const float * k, const float * v, int64_t n_q
 #pragma omp for schedule(static)
             for (int64_t i = 0; i < n_q; i++) {
                 const float * qi = q + i * row + h * hd;
+                float q16[1024];
+                if (g_attn_f16 && kv_f16) {
+                    for (int d = 0; d < hd; d++) q16[d] = or_fp16_to_fp32(or_fp32_to_fp16(qi[d]));
+                    qi = q16;
+                }
                 float mx = -INFINITY;
                 for (int64_t j = 0; j < n_kv; j++) {
                     sc[j] = dot_f32_8acc(qi, kh + j * hd, hd) * scale;
@@ -693,8 +703,9 @@ void or_attention(const float * q, const float * k, const float * v, int64_t n_q
                 for (int64_t j = 0; j < n_kv; j++) {
                     const float p = expf(sc[j] - mx);
                     sum += p;
+                    const float pv = (g_attn_f16 && kv_f16) ? or_fp16_to_fp32(or_fp32_to_fp16(p)) : p;
                     const float * vj = vh + j * hd;
-                    for (int d = 0; d < hd; d++) acc[d] = fmaf(p, vj[d], acc[d]);
+                    for (int d = 0; d < hd; d++) acc[d] = fmaf(pv, vj[d], acc[d]);
                 }
                 const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
                 for (int d = 0; d < hd; d++) out[i * row + h * hd + d] = acc[d] * inv;
@@ -1071,6 +1082,100 @@ int64_t or_head_file(const char * path, const float * x_in, int64_t N, float * p
     ret = C;
 done:
     free(x); free(kv); free(k); free(v); free(q); free(y); free(h); free(o); free(ff);
+    gg_close(&f);
+    return ret;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * masked predictor (src/predictor.cpp:23-285): context rows (gathered at the context ids) through
+ * pred.embed (or the 2-layer MLP pred.embed.0 / .2), mask token row mask_index % n_mask for every
+ * target, + the modality vector (2.1), 3-D RoPE from the token ids on the predictor grid, the pred.blk
+ * blocks, pred.norm, and pred.proj of the target rows. LayerNorm epsilon: the encoder's.
+ * modality: 1 video, 2 image (resolved by the caller).
+ * ---------------------------------------------------------------------------------------------- */
+int64_t or_predict_file(const char * path, const float * enc, int64_t n_tok, const int32_t * ctx_ids, int n_ctx,
+                        const int32_t * tgt_ids, int n_tgt, int mask_index, int modality, float * out, int64_t out_cap,
+                        int n_threads) {
+    gg_file f;
+    if (gg_open(path, &f)) return -1;
+    int64_t ret = -1;
+    const int De = (int) gg_int(&f, "jepa.enc.embed_dim", 0);
+    const int Dp = (int) gg_int(&f, "jepa.pred.embed_dim", 0), L = (int) gg_int(&f, "jepa.pred.n_layer", 0);
+    const int H = (int) gg_int(&f, "jepa.pred.n_head", 0);
+    const int hd0 = (int) gg_int(&f, "jepa.pred.head_dim", 0), hd = hd0 > 0 ? hd0 : (H > 0 ? Dp / H : 0);
+    const int out_dim = (int) gg_int(&f, "jepa.pred.out_dim", De);
+    const float eps = (float) gg_flt(&f, "jepa.enc.ln_eps", 1e-6);
+    const int kv_f16 = gg_int(&f, "general.file_type", 0) != 0;
+    const int64_t N = (int64_t) n_ctx + n_tgt;
+    float * x = NULL, * rc = NULL, * rs = NULL, * rows = NULL, * hid = NULL, * h = NULL;
+    int32_t * ids = NULL;
+    if (strcmp(gg_str(&f, "jepa.pred.kind", "none"), "masked") != 0 || Dp <= 0 || H <= 0 || hd * H != Dp || n_tgt <= 0 || n_ctx < 0) {
+        fprintf(stderr, "oracle: no masked predictor / bad shape\n"); goto done;
+    }
+    if ((int64_t) n_tgt * out_dim > out_cap) { fprintf(stderr, "oracle: output too small\n"); goto done; }
+    ids = (int32_t *) malloc(sizeof(int32_t) * N);
+    int64_t max_id = 0;
+    for (int i = 0; i < n_ctx; i++) { ids[i] = ctx_ids ? ctx_ids[i] : i; if (ids[i] < 0 || ids[i] >= n_tok) { fprintf(stderr, "oracle: bad context id\n"); goto done; } }
+    for (int i = 0; i < n_tgt; i++) { ids[n_ctx + i] = tgt_ids ? tgt_ids[i] : i; if (ids[n_ctx + i] < 0) { fprintf(stderr, "oracle: bad target id\n"); goto done; } }
+    for (int64_t i = 0; i < N; i++) if (ids[i] > max_id) max_id = ids[i];
+    x = (float *) malloc(sizeof(float) * N * Dp);
+    /* 1. context rows */
+    if (n_ctx > 0) {
+        rows = (float *) malloc(sizeof(float) * n_ctx * De);
+        for (int i = 0; i < n_ctx; i++) memcpy(rows + (int64_t) i * De, enc + (int64_t) ids[i] * De, sizeof(float) * De);
+        const gg_tensor * e0 = gg_tensor_find(&f, "pred.embed.0.weight");
+        if (e0) {
+            const int64_t nh = e0->ne[1];
+            hid = (float *) malloc(sizeof(float) * n_ctx * nh);
+            if (linear(&f, "pred.embed.0.weight", "pred.embed.0.bias", rows, n_ctx, De, nh, hid, n_threads)) goto done;
+            for (int64_t i = 0; i < n_ctx * nh; i++) hid[i] = or_gelu_erf(hid[i]);
+            if (linear(&f, "pred.embed.2.weight", "pred.embed.2.bias", hid, n_ctx, nh, Dp, x, n_threads)) goto done;
+        } else if (linear(&f, "pred.embed.weight", "pred.embed.bias", rows, n_ctx, De, Dp, x, n_threads)) goto done;
+    }
+    /* 2. mask token rows */
+    {
+        const gg_tensor * mt = gg_tensor_find(&f, "pred.mask_tokens");
+        if (!mt || mt->type != OR_F32 || mt->ne[0] != Dp) { fprintf(stderr, "oracle: pred.mask_tokens\n"); goto done; }
+        const int64_t nm0 = gg_int(&f, "jepa.pred.n_mask_tokens", 0), n_mask = nm0 > 0 ? nm0 : mt->ne[1];
+        int64_t idx = n_mask > 0 ? mask_index % n_mask : 0;
+        if (idx < 0) idx += n_mask;
+        const float * row = (const float *) gg_data(&f, mt) + idx * Dp;
+        for (int i = 0; i < n_tgt; i++) memcpy(x + ((int64_t) n_ctx + i) * Dp, row, sizeof(float) * Dp);
+    }
+    /* 3. modality vector on every row */
+    if (gg_int(&f, "jepa.pred.modality_embed", 0)) {
+        const float * mod = gg_vec(&f, modality == 2 ? "pred.mod_embed_img" : "pred.mod_embed_video");
+        if (!mod) { fprintf(stderr, "oracle: modality vector missing\n"); goto done; }
+        for (int64_t r = 0; r < N; r++) for (int d = 0; d < Dp; d++) x[r * Dp + d] = x[r * Dp + d] + mod[d];
+    }
+    /* 4. RoPE tables from the ids (src/predictor.cpp:23-49) */
+    {
+        or_rope_params rp;
+        const int gs = (int) gg_int(&f, "jepa.pred.grid_size", 0);
+        const int grid = gs > 0 ? gs : (int) (gg_int(&f, "jepa.enc.img_size", 224) / gg_int(&f, "jepa.enc.patch_size", 16));
+        rp.grid_h = rp.grid_w = grid;
+        rp.grid_t = (int) (max_id / ((int64_t) grid * grid)) + 1;
+        rp.head_dim = hd;
+        rp.theta = (float) gg_flt(&f, "jepa.enc.rope_theta", 10000.0);
+        rp.interpolate = (int) gg_int(&f, "jepa.pred.rope_interpolate", 0);
+        rp.train_grid_h = rp.train_grid_w = (int) gg_int(&f, "jepa.pred.rope_ref_grid", 0);
+        const char * lay = gg_str(&f, "jepa.pred.rope_freq_layout", "");
+        rp.variant = lay[0] ? !strcmp(lay, "interleaved") : !strcmp(gg_str(&f, "jepa.family", ""), "vjepa2_1");
+        rc = (float *) malloc(sizeof(float) * N * hd);
+        rs = (float *) malloc(sizeof(float) * N * hd);
+        or_rope_tables(&rp, ids, N, rc, rs, 1);
+    }
+    for (int l = 0; l < L; l++) {
+        char pre[64];
+        snprintf(pre, sizeof(pre), "pred.blk.%d.", l);
+        if (block_fwd(&f, pre, x, N, Dp, H, rc, rs, NULL, kv_f16, eps, n_threads)) goto done;
+    }
+    h = (float *) malloc(sizeof(float) * n_tgt * Dp);
+    or_layer_norm(x + (int64_t) n_ctx * Dp, n_tgt, Dp, gg_vec(&f, "pred.norm.weight"), gg_vec(&f, "pred.norm.bias"), eps, h);
+    if (linear(&f, "pred.proj.weight", "pred.proj.bias", h, n_tgt, Dp, out_dim, out, n_threads)) goto done;
+    ret = out_dim;
+done:
+    free(x); free(rc); free(rs); free(rows); free(hid); free(h); free(ids);
     gg_close(&f);
     return ret;
 }

@@ -60,6 +60,8 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
 /* 1: sum the per-block terms of quantized dots from the last K-block to the first (see oracle.c) */
 void or_set_reverse_block_order(int on);
 void or_set_k_split(int s);
+/* 1: with f16 K/V, round q and the softmax weights to f16 too (an f16 matrix-core attention) */
+void or_set_attn_f16(int on);
 
 void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, const float * b,
                    float eps, float * y);
@@ -103,6 +105,13 @@ int64_t or_encode_file(const char * gguf_path, const float * in, int n_batch, in
  * [D] and logits [n_classes] (either may be NULL). Returns n_classes, or -1 on error. */
 int64_t or_head_file(const char * gguf_path, const float * x, int64_t n_tokens, float * pooled, float * logits,
                      int64_t logits_cap, int n_threads);
+
+/* Masked predictor of a GGUF file (what jepa_predict_mod returns): encoder rows enc [n_tok][enc_dim],
+ * context ids (NULL: 0..n_ctx-1, rows of enc) and target ids (NULL: 0..n_tgt-1), modality 1 video /
+ * 2 image. out [n_tgt][out_dim]. Returns out_dim, or -1. */
+int64_t or_predict_file(const char * gguf_path, const float * enc, int64_t n_tok, const int32_t * ctx_ids, int n_ctx,
+                        const int32_t * tgt_ids, int n_tgt, int mask_index, int modality, float * out, int64_t out_cap,
+                        int n_threads);
 
 #ifdef __cplusplus
 }

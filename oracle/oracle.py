@@ -63,6 +63,8 @@ def lib() -> C.CDLL:
         L.or_encode_file.restype = i64
         L.or_head_file.argtypes = [C.c_char_p, vp, i64, vp, vp, i64, C.c_int]
         L.or_head_file.restype = i64
+        L.or_predict_file.argtypes = [C.c_char_p, vp, i64, vp, C.c_int, vp, C.c_int, C.c_int, C.c_int, vp, i64, C.c_int]
+        L.or_predict_file.restype = i64
         for fn in ("or_fp32_to_fp16_row", "or_fp16_to_fp32_row"):
             getattr(L, fn).argtypes = [vp, vp, i64]
             getattr(L, fn).restype = None
@@ -70,6 +72,8 @@ def lib() -> C.CDLL:
         L.or_set_reverse_block_order.restype = None
         L.or_set_k_split.argtypes = [C.c_int]
         L.or_set_k_split.restype = None
+        L.or_set_attn_f16.argtypes = [C.c_int]
+        L.or_set_attn_f16.restype = None
         _lib = L
     return _lib
 
@@ -222,6 +226,19 @@ def head(path: str, x: np.ndarray, n_classes: int):
     return pooled, logits[:r]
 
 
+def predict(path: str, enc: np.ndarray, ctx_ids, tgt_ids, out_dim: int, mask_index: int = 1, modality: int = 1):
+    """Oracle masked predictor: enc [n_tok, enc_dim], int id lists -> [len(tgt_ids), out_dim]."""
+    enc = np.ascontiguousarray(enc, dtype=np.float32)
+    ci = np.ascontiguousarray(ctx_ids, dtype=np.int32)
+    ti = np.ascontiguousarray(tgt_ids, dtype=np.int32)
+    out = np.zeros((len(ti), out_dim), dtype=np.float32)
+    r = lib().or_predict_file(path.encode(), _p(enc), enc.shape[0], _p(ci) if len(ci) else None, len(ci), _p(ti), len(ti),
+                              mask_index, modality, _p(out), out.size, threads())
+    if r < 0:
+        raise RuntimeError("oracle predict failed")
+    return out
+
+
 def encode(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, n_layers: int = 0, trace: bool = False):
     """Oracle forward with an explicit item count (video: n_batch; image: n_batch * n_frames)."""
     return _encode(path, np.ascontiguousarray(x, dtype=np.float32), rows, dim, n_layers, trace, n_items)
@@ -267,3 +284,8 @@ def set_reverse_block_order(on: bool) -> None:
 def set_k_split(s: int) -> None:
     """q8_0 / q4_0 dots: sum the blocks in s consecutive K ranges, one chain each, then add the chains"""
     lib().or_set_k_split(int(s))
+
+
+def set_attn_f16(on: bool) -> None:
+    """Round q and the softmax weights to f16 in attentions with f16 K/V (an f16 matrix-core kernel)."""
+    lib().or_set_attn_f16(1 if on else 0)

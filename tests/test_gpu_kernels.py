@@ -335,29 +335,29 @@ def test_gemm_tile_hook_rejects_unknown(jlib):
     assert jlib.lib().jepa_amd_gemm_tile(-1) == 0
 
 
-def _attention_ref(qkv, n_items, n_tok, H, rope=None, mask=None):
-    """double-precision softmax(q k^T / 8 + mask) v per head, K/V rounded to f16 like ggml_cast"""
-    D = H * 64
+def _attention_ref(qkv, n_items, n_tok, H, rope=None, mask=None, hd=64):
+    """double-precision softmax(q k^T / sqrt(hd) + mask) v per head, K/V rounded to f16 like ggml_cast"""
+    D = H * hd
     out = np.zeros((n_items * n_tok, D))
     for it in range(n_items):
         blk = qkv[it * n_tok:(it + 1) * n_tok].astype(np.float64)
         for h in range(H):
-            q = blk[:, h * 64:(h + 1) * 64]
-            k = blk[:, D + h * 64:D + (h + 1) * 64]
-            v = blk[:, 2 * D + h * 64:2 * D + (h + 1) * 64]
+            q = blk[:, h * hd:(h + 1) * hd]
+            k = blk[:, D + h * hd:D + (h + 1) * hd]
+            v = blk[:, 2 * D + h * hd:2 * D + (h + 1) * hd]
             if rope is not None:
                 c, s = rope
-                q = q * c + q[:, np.arange(64) ^ 1] * s
-                k = k * c + k[:, np.arange(64) ^ 1] * s
+                q = q * c + q[:, np.arange(hd) ^ 1] * s
+                k = k * c + k[:, np.arange(hd) ^ 1] * s
             k = k.astype(np.float16).astype(np.float64)
             v = v.astype(np.float16).astype(np.float64)
-            sc = q @ k.T / 8.0
+            sc = q @ k.T / np.sqrt(hd)
             if mask is not None:
                 sc = sc + mask
             sc -= sc.max(1, keepdims=True)
             p = np.exp(sc)
             p /= p.sum(1, keepdims=True)
-            out[it * n_tok:(it + 1) * n_tok, h * 64:(h + 1) * 64] = p @ v
+            out[it * n_tok:(it + 1) * n_tok, h * hd:(h + 1) * hd] = p @ v
     return out
 
 
@@ -380,7 +380,7 @@ def test_attention(jlib, oracle, n_items, n_tok, H, rope):
         rc, rs = dev(c), dev(s)
     out = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
     dq = dev(qkv)
-    r = jlib.lib().jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, rc.data_ptr() if rope else None,
+    r = jlib.lib().jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 64, rc.data_ptr() if rope else None,
                                       rs.data_ptr() if rope else None, 0, 0, 0, out.data_ptr())
     assert r == 0, jlib.error_text()
     got = host(out).astype(np.float64)
@@ -389,6 +389,35 @@ def test_attention(jlib, oracle, n_items, n_tok, H, rope):
     cos = (got * ref).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(ref, axis=1))
     assert rel <= 1e-2, rel
     assert cos.min() >= 0.9999, cos.min()
+
+
+# head width 32 (the masked predictor's 12 x 32 heads): stored 64 wide with a zero upper half
+@pytest.mark.parametrize("n_items,n_tok,H,rope", [(1, 300, 12, True), (2, 65, 3, False), (1, 2048, 2, True)])
+def test_attention_hd32(jlib, oracle, n_items, n_tok, H, rope):
+    rng = np.random.default_rng(n_tok + 5 * H)
+    D = H * 32
+    qkv = (rng.standard_normal((n_items * n_tok, 3 * D)) * 1.5).astype(np.float32)
+    rc = rs = None
+    if rope:
+        ids = rng.integers(0, 8 * 16 * 16, n_tok).astype(np.int32)
+        c, s = oracle.rope_tables((8, 16, 16), 32, variant=0, ids=ids)
+        rc, rs = dev(c), dev(s)
+    out = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
+    oq = torch.zeros((n_items * n_tok, D // 32 * 34), dtype=torch.uint8, device="cuda")
+    dq = dev(qkv)
+    L = jlib.lib()
+    for ot, buf in ((0, out), (gguf.GGML_Q8_0, oq)):
+        r = L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 32, rc.data_ptr() if rope else None,
+                                 rs.data_ptr() if rope else None, 0, 0, ot, buf.data_ptr())
+        assert r == 0, jlib.error_text()
+    got = host(out).astype(np.float64)
+    ref = _attention_ref(qkv, n_items, n_tok, H, (c.astype(np.float64), s.astype(np.float64)) if rope else None, hd=32)
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    cos = (got * ref).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(ref, axis=1))
+    assert rel <= 1e-2, rel
+    assert cos.min() >= 0.9999, cos.min()
+    want = oracle.quantize_act(oracle.OR_Q8_0, host(out))
+    np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))
 
 
 # block-causal (LeVJEPA) shapes (n_items, gt, gh, gw, n_prefix, H): the reference's mask KAT shape (65
@@ -410,9 +439,9 @@ def test_attention_block_causal(jlib, oracle, n_items, gt, gh, gw, n_prefix, H):
     out = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
     oq = torch.zeros((n_items * n_tok, D // 32 * 34), dtype=torch.uint8, device="cuda")
     L = jlib.lib()
-    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, n_prefix, gh * gw, 0, out.data_ptr()) == 0, \
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 64, None, None, n_prefix, gh * gw, 0, out.data_ptr()) == 0, \
         jlib.error_text()
-    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, n_prefix, gh * gw, gguf.GGML_Q8_0,
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 64, None, None, n_prefix, gh * gw, gguf.GGML_Q8_0,
                                 oq.data_ptr()) == 0
     got = host(out).astype(np.float64)
     ref = _attention_ref(qkv, n_items, n_tok, H, None, mask)
@@ -435,8 +464,8 @@ def test_attention_fused_q8_0_equals_separate_quantizer(jlib, oracle, n_items, n
     o32 = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
     oq = torch.zeros((n_items * n_tok, D // 32 * 34), dtype=torch.uint8, device="cuda")
     L = jlib.lib()
-    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, 0, 0, 0, o32.data_ptr()) == 0
-    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, None, None, 0, 0, gguf.GGML_Q8_0, oq.data_ptr()) == 0
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 64, None, None, 0, 0, 0, o32.data_ptr()) == 0
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 64, None, None, 0, 0, gguf.GGML_Q8_0, oq.data_ptr()) == 0
     want = oracle.quantize_act(oracle.OR_Q8_0, host(o32))
     np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))
 

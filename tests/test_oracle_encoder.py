@@ -107,6 +107,39 @@ def head64(path, rows):
     return y, y @ T("head.cls.weight").T + T("head.cls.bias")
 
 
+def predict64(path, enc, ctx_ids, tgt_ids, mask_index=1, modality=1):
+    """The masked predictor (reference src/predictor.cpp:56-133) in float64: embed the context rows,
+    mask-token rows for the targets, modality vector, blocks with RoPE from the token ids on the
+    predictor grid, final norm and projection of the target rows."""
+    g = gguf.read_gguf(path)
+    kv = g.kv
+    T = lambda n: g.tensor_f32(n).astype(np.float64)
+    has = lambda n: n in g.tensors
+    Dp, H = kv["jepa.pred.embed_dim"], kv["jepa.pred.n_head"]
+    hd = Dp // H
+    ids = np.concatenate([np.asarray(ctx_ids, np.int64), np.asarray(tgt_ids, np.int64)])
+    rows = enc[np.asarray(ctx_ids, np.int64)].astype(np.float64)
+    if has("pred.embed.0.weight"):
+        h = _gelu(rows @ T("pred.embed.0.weight").T + T("pred.embed.0.bias"))
+        ctx = h @ T("pred.embed.2.weight").T + T("pred.embed.2.bias")
+    else:
+        ctx = rows @ T("pred.embed.weight").T + T("pred.embed.bias")
+    mt = T("pred.mask_tokens").reshape(-1, Dp)
+    n_mask = kv.get("jepa.pred.n_mask_tokens") or mt.shape[0]
+    x = np.vstack([ctx, np.repeat(mt[mask_index % n_mask][None], len(tgt_ids), 0)])
+    if kv.get("jepa.pred.modality_embed"):
+        x = x + T("pred.mod_embed_img" if modality == 2 else "pred.mod_embed_video")
+    grid = kv.get("jepa.pred.grid_size") or kv["jepa.enc.img_size"] // kv["jepa.enc.patch_size"]
+    gt = int(ids.max()) // (grid * grid) + 1
+    lay = kv.get("jepa.pred.rope_freq_layout") or ("interleaved" if kv["jepa.family"] == "vjepa2_1" else "tiled")
+    C, S = _rope_tables64((gt, grid, grid), hd, 0 if lay == "tiled" else 1, False, (0, 0), float(kv["jepa.enc.rope_theta"]))
+    rope = (C[ids], S[ids])
+    for i in range(kv["jepa.pred.n_layer"]):
+        x = _block64(T, has, f"pred.blk.{i}.", x, Dp, H, rope, None, kv["general.file_type"] != 0)
+    y = _ln(x[len(ctx_ids):], T("pred.norm.weight"), T("pred.norm.bias"), 1e-6)
+    return y @ T("pred.proj.weight").T + T("pred.proj.bias")
+
+
 def forward64(path, x):
     g = gguf.read_gguf(path)
     kv = g.kv
@@ -191,6 +224,27 @@ def test_oracle_head_matches_float64_head(tmp_path):
     assert got_l.shape == (10,)
     assert np.abs(got_p - want_p).max() / np.abs(want_p).max() < 2e-5
     assert np.abs(got_l - want_l).max() / np.abs(want_l).max() < 1e-4
+
+
+@pytest.mark.parametrize("family,kw", [("vjepa2", {}), ("vjepa2_1", {"pred_mlp_embed": True})])
+def test_oracle_predictor_matches_float64_predictor(family, kw, tmp_path):
+    """The oracle's masked predictor against the float64 restatement above on a tiny f32 model with
+    heads of 32 and weights large enough for position-dependent attention: context ids and target ids
+    interleaved over two temporal slices, mask index 3 of 10, the 2.1 modality vectors."""
+    cfg = forge.tiny(family, "f32", ln_random=True, pred_dim=128, pred_layers=2, pred_ffn=512, w_std=0.08, **kw)
+    path = forge.cached_model(cfg, str(tmp_path))
+    rng = np.random.default_rng(3)
+    enc = rng.standard_normal((32, cfg.embed_dim)).astype(np.float32)
+    perm = rng.permutation(32)
+    ctx, tgt = perm[:20], perm[20:]
+    for modality in ((1, 2) if family == "vjepa2_1" else (1,)):
+        want = predict64(path, enc, ctx, tgt, mask_index=3, modality=modality)
+        got = O.predict(path, enc, ctx, tgt, cfg.embed_dim, mask_index=3, modality=modality)
+        err = np.abs(got - want).max() / np.abs(want).max()
+        assert err < 2e-5, (modality, err)
+        # the targets differ from each other by more than the tolerance: the ids reach the output
+        spread = np.abs(want - want.mean(0)).max() / np.abs(want).max()
+        assert spread > 100 * 2e-5, spread
 
 
 def test_oracle_items_are_independent(tmp_path):
