@@ -103,6 +103,22 @@ int jepa_amd_preprocess_frames_device(int device, const jepa_preprocess_params *
 int jepa_amd_gemm_split(int split);
 int jepa_amd_gemm_split_of(int wtype, int64_t n_out, int64_t n_in);
 
+/* ---- GGUF quantizer ---------------------------------------------------------------------------
+ * The reference's jepa-quantize (tools/jepa-quantize.cpp) as a library call: in_path (an f32 / f16
+ * jepa GGUF, or a quantized one with allow_requant) -> out_path with the 2-D attention / FFN /
+ * projection / classifier weights re-typed to `type` ("f32", "f16", "q8_0", "q4_0", "q4_k"; f32
+ * widens every tensor), the same keep rule, per-tensor K-quant fallback to q4_0, metadata copied in
+ * order with general.file_type updated, GGUF v3 with 32-byte alignment. Tensors whose name contains
+ * one of the n_keep strings in `keep` keep their type. The block quantizers run on HIP device
+ * `device` (-1: 0) and are bit-exact with ggml's reference quantizers. verbose logs the plan.
+ * Returns 0, or -1 with the reason in jepa_error_text(). */
+int jepa_amd_quantize_file(const char * in_path, const char * out_path, const char * type, const char * const * keep, int n_keep,
+                           bool allow_requant, int device, bool verbose);
+
+/* f32 values on the device -> ggml blocks of gtype (8 q8_0, 2 q4_0, 12 q4_K) or f16 (1), bit-exact
+ * with ggml's reference quantizers (test hook of the quantizer kernels). n must be whole blocks. */
+int jepa_amd_quantize_rows(int device, int gtype, const float * x_dev, int64_t n, void * out_dev);
+
 /* One v_mfma_f32_32x32x16_f16 on host matrices a [32][16], b [16][32] -> d [32][32] (row-major),
  * written back through the accumulator layout the GEMM epilogues assume. */
 int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * d);

@@ -322,6 +322,17 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
     return d.finish();
 }
 
+extern "C" int jepa_amd_quantize_rows(int device, int gtype, const float * x, int64_t n, void * out) {
+    if (!x || !out || n < 0) return -1;
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    if (!launch_quantize_rows(gtype, x, n, out, d.s)) {
+        jepa_log("jepa: jepa_amd_quantize_rows: type %d with %lld values is not a quantizer target\n", gtype, (long long) n);
+        return -1;
+    }
+    return d.finish();
+}
+
 extern "C" int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * dd) {
     if (!a || !b || !dd) return -1;
     dev_scope d(device);

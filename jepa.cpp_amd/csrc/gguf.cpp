@@ -128,6 +128,7 @@ bool open(const std::string & path, file & out, std::string & err) {
     out.file_size = (uint64_t) fsz;
     uint64_t alignment = 32;
     for (uint64_t i = 0; i < n_kv; i++) {
+        const uint64_t kv_begin = r.pos;
         std::string key;
         uint32_t t = 0;
         if (!r.str(key) || !r.get(t)) { err = path + ": " + r.err; return false; }
@@ -154,6 +155,7 @@ bool open(const std::string & path, file & out, std::string & err) {
             alignment = (uint64_t) v.i;
         }
         out.kv.emplace_back(key, std::move(v));
+        out.kv_span.emplace_back(kv_begin, r.pos);
     }
     for (uint64_t i = 0; i < n_tensors; i++) {
         tensor_info ti;
@@ -181,6 +183,7 @@ bool open(const std::string & path, file & out, std::string & err) {
         out.tensors.push_back(std::move(ti));
     }
     const uint64_t data0 = (r.pos + alignment - 1) / alignment * alignment;
+    out.data_offset = data0;
     for (auto & t : out.tensors) {
         const uint64_t abs = data0 + t.offset;
         if (t.offset > (uint64_t) fsz || abs > (uint64_t) fsz || t.nbytes > (uint64_t) fsz - abs) {

@@ -39,8 +39,10 @@ struct tensor_info {
 struct file {
     std::string path;
     std::vector<std::pair<std::string, value>> kv;   // in file order
+    std::vector<std::pair<uint64_t, uint64_t>> kv_span;   // [begin, end) byte range of each kv pair in the file
     std::vector<tensor_info> tensors;
     uint64_t file_size = 0;
+    uint64_t data_offset = 0;                        // start of the tensor data section
 
     const value * find(const std::string & key) const;
     const tensor_info * tensor(const std::string & name) const;

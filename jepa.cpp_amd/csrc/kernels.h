@@ -93,6 +93,10 @@ void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_ite
 // prefix (CLS) rows: x[it*R + 0][n] = cls[n] (+ pos[n])
 void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D, hipStream_t s);
 
+// f32 values -> ggml blocks of dst_type (q8_0, q4_0, q4_K) or f16, bit-exact with ggml's reference
+// quantizers; n a multiple of the block size. Returns false for another type or a ragged n.
+bool launch_quantize_rows(int dst_type, const float * x, int64_t n, void * y, hipStream_t s);
+
 // weight expansion at load: raw ggml blocks (device) -> dev_linear operand arrays
 void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd,
                    void * wmin, hipStream_t s);

@@ -391,6 +391,8 @@ __global__ void k_dequant(int gtype, const uint8_t * __restrict__ raw, int64_t n
         y[id] = __fsub_rn(__fmul_rn(__fmul_rn(d, (float) s), (float) q), __fmul_rn(dmin, (float) m));
     } else if (gtype == T_F16) {
         y[id] = h2f(((const uint16_t *) raw)[id]);
+    } else if (gtype == T_BF16) {
+        y[id] = __uint_as_float((uint32_t) ((const uint16_t *) raw)[id] << 16);
     } else {
         y[id] = ((const float *) raw)[id];
     }

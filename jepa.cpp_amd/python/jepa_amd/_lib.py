@@ -102,6 +102,8 @@ def lib() -> C.CDLL:
         "jepa_model_label": (cp, [vp, C.c_int]),
         "jepa_amd_head_device": (C.c_int, [vp, vp, i64, vp, vp]),
         "jepa_model_has_predictor": (C.c_bool, [vp]),
+        "jepa_amd_quantize_file": (C.c_int, [cp, cp, cp, C.POINTER(cp), C.c_int, C.c_bool, C.c_int, C.c_bool]),
+        "jepa_amd_quantize_rows": (C.c_int, [C.c_int, C.c_int, vp, i64, vp]),
         "jepa_predict": (C.c_int, [vp, C.POINTER(Output), vp, C.c_int, vp, C.c_int, C.POINTER(Output)]),
         "jepa_predict_ex": (C.c_int, [vp, C.POINTER(Output), vp, C.c_int, vp, C.c_int, C.c_int, C.POINTER(Output)]),
         "jepa_predict_mod": (C.c_int, [vp, C.POINTER(Output), vp, C.c_int, vp, C.c_int, C.c_int, C.c_int, C.POINTER(Output)]),
@@ -321,3 +323,13 @@ def load_image(path: str) -> np.ndarray:
     out = np.ctypeslib.as_array(r, shape=(h.value * w.value * 3,)).copy().reshape(h.value, w.value, 3)
     L.jepa_free(C.cast(r, C.c_void_p))
     return out
+
+
+def quantize_file(in_path: str, out_path: str, qtype: str, keep=(), allow_requant: bool = False, device: int = 0,
+                  verbose: bool = False) -> None:
+    """jepa_amd_quantize_file: re-type the weights of a jepa GGUF (the reference's jepa-quantize)."""
+    L = lib()
+    arr = (C.c_char_p * max(len(keep), 1))(*[k.encode() for k in keep])
+    L.jepa_error_reset()
+    check(L.jepa_amd_quantize_file(in_path.encode(), out_path.encode(), qtype.encode(), arr, len(keep), allow_requant, device,
+                                   verbose), "jepa_amd_quantize_file")

@@ -9,8 +9,8 @@ rules"). Block layouts are ggml's (ggml-common.h):
   q4_0  {f16 d; u8 qs[16]}                        18 B / 32 values   x = d*(q-8), low nibbles = 0..15
   q4_K  {f16 d, dmin; u8 scales[12]; u8 qs[128]}  144 B / 256 values x = d*sc_j*q - dmin*m_j
 
-q8_0 and q4_0 use ggml's reference quantizer formulas (quantize_row_q8_0_ref / q4_0_ref); q4_K uses a
-per-sub-block min/max fit (not ggml's make_qkx2_quants search), which produces valid q4_K blocks.
+q8_0, q4_0 and q4_K use ggml's reference quantizers (quantize_row_q8_0_ref / q4_0_ref / q4_K_ref with
+its make_qkx2_quants search), restated in numpy.
 """
 from __future__ import annotations
 
@@ -84,32 +84,97 @@ def quantize_q4_0(x: np.ndarray) -> np.ndarray:
     return out.reshape(*lead, -1)
 
 
+def _make_qkx2(x, w, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20):
+    """ggml's make_qkx2_quants on rows of 32 (x, w: float32 [rows, 32]), vectorized over rows with the
+    sums taken sequentially in element order (float32 throughout). Returns (scale, the_min, L)."""
+    n = x.shape[1]
+    mn, mx = x[:, 0].copy(), x[:, 0].copy()
+    sum_w = w[:, 0].copy()
+    sum_x = (sum_w * x[:, 0]).astype(F32)
+    for i in range(1, n):
+        mn = np.where(x[:, i] < mn, x[:, i], mn)
+        mx = np.where(x[:, i] > mx, x[:, i], mx)
+        sum_w = (sum_w + w[:, i]).astype(F32)
+        sum_x = (sum_x + (w[:, i] * x[:, i]).astype(F32)).astype(F32)
+    mn = np.where(mn > 0, F32(0), mn).astype(F32)
+    flat = mx == mn
+    # (ggml updates `min` inside the search, and later candidates are formed against the updated value)
+    rng = np.where(flat, F32(1), (mx - mn).astype(F32)).astype(F32)
+    xm = (x - mn[:, None]).astype(F32)
+
+    def err(sc, m, L):
+        e = np.zeros(x.shape[0], F32)
+        for i in range(n):
+            diff = (((sc * L[:, i]).astype(F32) + m).astype(F32) - x[:, i]).astype(F32)
+            e = (e + (w[:, i] * (diff * diff).astype(F32)).astype(F32)).astype(F32)
+        return e
+
+    iscale = (F32(nmax) / rng).astype(F32)
+    scale = (F32(1) / iscale).astype(F32)
+    L = np.clip(np.rint((iscale[:, None] * xm).astype(F32)), 0, nmax).astype(F32)
+    best = err(scale, mn, L)
+    for step in range(nstep + 1):
+        rng = np.where(flat, F32(1), (mx - mn).astype(F32)).astype(F32)
+        xm = (x - mn[:, None]).astype(F32)
+        isc = (((F32(rmin) + (F32(rdelta) * F32(step)).astype(F32)).astype(F32) + F32(nmax)).astype(F32) / rng).astype(F32)
+        La = np.clip(np.rint((isc[:, None] * xm).astype(F32)), 0, nmax).astype(F32)
+        sum_l = np.zeros(x.shape[0], F32); sum_l2 = np.zeros(x.shape[0], F32); sum_xl = np.zeros(x.shape[0], F32)
+        for i in range(n):
+            wl = (w[:, i] * La[:, i]).astype(F32)
+            sum_l = (sum_l + wl).astype(F32)
+            sum_l2 = (sum_l2 + (wl * La[:, i]).astype(F32)).astype(F32)
+            sum_xl = (sum_xl + (wl * x[:, i]).astype(F32)).astype(F32)
+        D = ((sum_w * sum_l2).astype(F32) - (sum_l * sum_l).astype(F32)).astype(F32)
+        ok = D > 0
+        Ds = np.where(ok, D, F32(1)).astype(F32)
+        ts = ((((sum_w * sum_xl).astype(F32) - (sum_x * sum_l).astype(F32)).astype(F32)) / Ds).astype(F32)
+        tm = ((((sum_l2 * sum_x).astype(F32) - (sum_l * sum_xl).astype(F32)).astype(F32)) / Ds).astype(F32)
+        pos = tm > 0
+        with np.errstate(divide="ignore", invalid="ignore"):
+            ts = np.where(pos, (sum_xl / np.where(pos, sum_l2, F32(1))).astype(F32), ts).astype(F32)
+        tm = np.where(pos, F32(0), tm).astype(F32)
+        cur = err(ts, tm, La)
+        upd = ok & (cur < best)
+        L = np.where(upd[:, None], La, L)
+        best = np.where(upd, cur, best)
+        scale = np.where(upd, ts, scale).astype(F32)
+        mn = np.where(upd, tm, mn).astype(F32)
+    scale = np.where(flat, F32(0), scale).astype(F32)
+    L = np.where(flat[:, None], F32(0), L)
+    return scale, (-mn).astype(F32), L.astype(np.uint8)
+
+
 def quantize_q4_K(x: np.ndarray) -> np.ndarray:
-    """q4_K blocks from a per-sub-block min/max fit (see module docstring)."""
+    """ggml's quantize_row_q4_K_ref over the last axis (no importance matrix): per 32-value sub-block a
+    weighted make_qkx2_quants fit (weights sqrt(mean x^2) + |x|), 6-bit scales and mins against their
+    maxima, the values re-fitted to the quantized scale / min."""
     x = np.ascontiguousarray(x, dtype=F32)
     lead = x.shape[:-1]
     sb = x.reshape(-1, 8, 32)
-    mn = np.minimum(sb.min(axis=2), F32(0))
-    mx = sb.max(axis=2)
-    scales = ((mx - mn) / F32(15)).astype(F32)
-    mins = (-mn).astype(F32)
-    max_scale = np.maximum(scales.max(axis=1), F32(0))
-    max_min = np.maximum(mins.max(axis=1), F32(0))
+    nb = sb.shape[0]
+    flat = sb.reshape(-1, 32)
+    sum_x2 = np.zeros(flat.shape[0], F32)
+    for i in range(32):
+        sum_x2 = (sum_x2 + (flat[:, i] * flat[:, i]).astype(F32)).astype(F32)
+    av_x = np.sqrt((sum_x2 / F32(32)).astype(F32)).astype(F32)
+    w = (av_x[:, None] + np.abs(flat)).astype(F32)
+    sc, mi, L = _make_qkx2(flat, w)
+    scales, mins, L = sc.reshape(nb, 8), mi.reshape(nb, 8), L.reshape(nb, 8, 32)
+    max_scale = np.maximum(scales.max(axis=1), F32(0)).astype(F32)
+    max_min = np.maximum(mins.max(axis=1), F32(0)).astype(F32)
     with np.errstate(divide="ignore"):
         inv_s = np.where(max_scale > 0, F32(63) / np.where(max_scale > 0, max_scale, F32(1)), F32(0)).astype(F32)
         inv_m = np.where(max_min > 0, F32(63) / np.where(max_min > 0, max_min, F32(1)), F32(0)).astype(F32)
-    ls = np.clip(np.rint((inv_s[:, None] * scales).astype(F32)), 0, 63).astype(np.uint8)
-    lm = np.clip(np.rint((inv_m[:, None] * mins).astype(F32)), 0, 63).astype(np.uint8)
-    d16 = (max_scale / F32(63)).astype(np.float16)
-    dm16 = (max_min / F32(63)).astype(np.float16)
-    d = d16.astype(F32)
-    dmin = dm16.astype(F32)
-    dd = (d[:, None] * ls.astype(F32)).astype(F32)
-    dm = (dmin[:, None] * lm.astype(F32)).astype(F32)
+    # uint8_t ls = nearest_int(...); ls = MIN(63, ls): the int is truncated to a byte before the clamp
+    ls = np.minimum(np.rint((inv_s[:, None] * scales).astype(F32)).astype(np.int64) & 0xFF, 63).astype(np.uint8)
+    lm = np.minimum(np.rint((inv_m[:, None] * mins).astype(F32)).astype(np.int64) & 0xFF, 63).astype(np.uint8)
+    d16 = (max_scale / F32(63)).astype(F32).astype(np.float16)
+    dm16 = (max_min / F32(63)).astype(F32).astype(np.float16)
+    dd = (d16.astype(F32)[:, None] * ls.astype(F32)).astype(F32)
+    dm = (dm16.astype(F32)[:, None] * lm.astype(F32)).astype(F32)
     with np.errstate(divide="ignore", invalid="ignore"):
         qv = np.rint(((sb + dm[:, :, None]).astype(F32) / np.where(dd != 0, dd, F32(1))[:, :, None]).astype(F32))
-    q = np.where(dd[:, :, None] != 0, np.clip(qv, 0, 15), 0).astype(np.uint8).reshape(-1, 256)
-    nb = sb.shape[0]
+    q = np.where(dd[:, :, None] != 0, np.clip(qv, 0, 15), L).astype(np.uint8).reshape(-1, 256)
     scales12 = np.zeros((nb, 12), dtype=np.uint8)
     for j in range(8):
         if j < 4:

@@ -145,47 +145,136 @@ static inline int nearest_int(float v) {
     return (i & 0x007fffff) - 0x00400000;
 }
 
-/* q4_K writer (not ggml's make_qkx2_quants search: a plain per-sub-block min/max fit). The format it
- * produces is the ggml q4_K layout, which is all the dequantizer and the dot depend on. */
+/* 6-bit scale and min of sub-block j from the 12 packed q4_K scale bytes */
+static inline void q4k_scale_min(int j, const uint8_t * q, uint8_t * d, uint8_t * m) {
+    if (j < 4) { *d = q[j] & 63; *m = q[j + 4] & 63; }
+    else {
+        *d = (uint8_t) ((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t) ((q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4));
+    }
+}
+
+/* ggml's make_qkx2_quants (ggml-quants.c of the ggml the reference pins, 36da5713 / v0.22.0; the
+ * submodule is absent from the reference tree): an asymmetric 4-bit fit of n values with weights w.
+ * Start from the min/max grid, then try nstep + 1 scales iscale = (rmin + rdelta*is + nmax)/(max-min):
+ * for each, the weighted least-squares scale and min of the resulting levels (min clamped <= 0), kept
+ * when its weighted squared error beats the best so far. Returns the scale, *the_min = -min. Every sum
+ * runs sequentially in element order, in float32, as in ggml's scalar code. */
+static float make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L, float * the_min,
+                              uint8_t * Laux, float rmin, float rdelta, int nstep) {
+    float min = x[0], max = x[0];
+    float sum_w = weights[0], sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float w = weights[i];
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max == min) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        *the_min = -min;
+        return 0.0f;
+    }
+    float iscale = nmax / (max - min);
+    float scale = 1 / iscale;
+    float best_error = 0;
+    for (int i = 0; i < n; ++i) {
+        const int l = nearest_int(iscale * (x[i] - min));
+        L[i] = (uint8_t) (l < 0 ? 0 : l > nmax ? nmax : l);
+        const float diff = scale * L[i] + min - x[i];
+        best_error += weights[i] * (diff * diff);
+    }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * is + nmax) / (max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * (x[i] - min));
+            l = l < 0 ? 0 : l > nmax ? nmax : l;
+            Laux[i] = (uint8_t) l;
+            const float w = weights[i];
+            sum_l += w * l;
+            sum_l2 += w * l * l;
+            sum_xl += w * l * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = sum_xl / sum_l2;
+            }
+            float cur_error = 0;
+            for (int i = 0; i < n; ++i) {
+                const float diff = this_scale * Laux[i] + this_min - x[i];
+                cur_error += weights[i] * (diff * diff);
+            }
+            if (cur_error < best_error) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_error = cur_error;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    *the_min = -min;
+    return scale;
+}
+
+/* ggml quantize_row_q4_K_ref (same source as above): per 32-value sub-block, weights
+ * av_x + |x| with av_x = sqrt(mean x^2), make_qkx2_quants(32, 15, rmin -1, rdelta 0.1, 20 steps);
+ * the 8 scales and mins quantized to 6 bits against their maxima (d = max_scale/63, dmin =
+ * max_min/63, f16), packed into the 12 scale bytes; then every value re-fitted against its quantized
+ * scale and min (a sub-block whose quantized scale is 0 keeps the levels of the fit); nibbles hold
+ * values j..j+31 (low) and j+32..j+63 (high) of each 64. This is what ggml_quantize_chunk writes for a
+ * q4_K tensor without an importance matrix (tools/jepa-quantize.cpp:159-173). */
 void or_quantize_q4_K(const float * x, void * vb, int64_t n) {
     blk_q4_K * y = (blk_q4_K *) vb;
     for (int64_t i = 0; i < n / QK_K; i++) {
         const float * xb = x + i * QK_K;
-        float scales[8], mins[8], max_scale = 0.0f, max_min = 0.0f;
-        for (int j = 0; j < 8; j++) {
-            float mn = xb[32 * j], mx = xb[32 * j];
-            for (int l = 1; l < 32; l++) { mn = fminf(mn, xb[32 * j + l]); mx = fmaxf(mx, xb[32 * j + l]); }
-            if (mn > 0.0f) mn = 0.0f;
-            scales[j] = (mx - mn) / 15.0f;
-            mins[j] = -mn;
+        uint8_t L[QK_K], Laux[32];
+        float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < QK_K / 32; ++j) {
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; ++l) sum_x2 += xb[32 * j + l] * xb[32 * j + l];
+            const float av_x = sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(xb[32 * j + l]);
+            scales[j] = make_qkx2_quants(32, 15, xb + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.0f, 0.1f, 20);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
         }
         const float inv_scale = max_scale > 0 ? 63.0f / max_scale : 0.0f;
         const float inv_min = max_min > 0 ? 63.0f / max_min : 0.0f;
-        uint8_t ls[8], lm[8];
-        for (int j = 0; j < 8; j++) {
-            int a = nearest_int(inv_scale * scales[j]); ls[j] = (uint8_t) (a < 0 ? 0 : a > 63 ? 63 : a);
-            int b = nearest_int(inv_min * mins[j]);     lm[j] = (uint8_t) (b < 0 ? 0 : b > 63 ? 63 : b);
-        }
         memset(y[i].scales, 0, 12);
-        for (int j = 0; j < 8; j++) {
-            if (j < 4) { y[i].scales[j] = ls[j]; y[i].scales[j + 4] = lm[j]; }
-            else {
-                y[i].scales[j + 4] = (uint8_t) ((ls[j] & 0xF) | ((lm[j] & 0xF) << 4));
-                y[i].scales[j - 4] |= (uint8_t) ((ls[j] >> 4) << 6);
-                y[i].scales[j - 0] |= (uint8_t) ((lm[j] >> 4) << 6);
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t ls = (uint8_t) nearest_int(inv_scale * scales[j]);
+            uint8_t lm = (uint8_t) nearest_int(inv_min * mins[j]);
+            ls = ls < 63 ? ls : 63;
+            lm = lm < 63 ? lm : 63;
+            if (j < 4) {
+                y[i].scales[j] = ls;
+                y[i].scales[j + 4] = lm;
+            } else {
+                y[i].scales[j + 4] = (uint8_t) ((ls & 0xF) | ((lm & 0xF) << 4));
+                y[i].scales[j - 4] |= (uint8_t) ((ls >> 4) << 6);
+                y[i].scales[j - 0] |= (uint8_t) ((lm >> 4) << 6);
             }
         }
         y[i].d = or_fp32_to_fp16(max_scale / 63.0f);
         y[i].dmin = or_fp32_to_fp16(max_min / 63.0f);
-        const float d = or_fp16_to_fp32(y[i].d), dmin = or_fp16_to_fp32(y[i].dmin);
-        uint8_t L[QK_K];
-        for (int j = 0; j < 8; j++) {
-            const float dd = d * ls[j], dm = dmin * lm[j];
-            for (int l = 0; l < 32; l++) {
-                int q = dd != 0.0f ? nearest_int((xb[32 * j + l] + dm) / dd) : 0;
-                L[32 * j + l] = (uint8_t) (q < 0 ? 0 : q > 15 ? 15 : q);
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t sc, m;
+            q4k_scale_min(j, y[i].scales, &sc, &m);
+            const float d = or_fp16_to_fp32(y[i].d) * sc;
+            if (!d) continue;
+            const float dm = or_fp16_to_fp32(y[i].dmin) * m;
+            for (int ii = 0; ii < 32; ++ii) {
+                int l = nearest_int((xb[32 * j + ii] + dm) / d);
+                l = l < 0 ? 0 : l > 15 ? 15 : l;
+                L[32 * j + ii] = (uint8_t) l;
             }
         }
         for (int j = 0; j < QK_K; j += 64)
@@ -240,13 +329,6 @@ void or_quantize_q8_K_act(const float * x, void * vb, int64_t n) {
     }
 }
 
-static inline void q4k_scale_min(int j, const uint8_t * q, uint8_t * d, uint8_t * m) {
-    if (j < 4) { *d = q[j] & 63; *m = q[j + 4] & 63; }
-    else {
-        *d = (uint8_t) ((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
-        *m = (uint8_t) ((q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4));
-    }
-}
 
 void or_dequantize(int type, const void * vb, float * y, int64_t n) {
     switch (type) {
