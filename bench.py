@@ -97,6 +97,63 @@ def time_forward(path, x_host, steps, warmup, kernel_pass=True):
     return res
 
 
+def time_extra(name, steps):
+    """Device time of one call of a row next to the encoder, median over `steps` calls after one warm call."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    from jepa_amd import _lib, gguf
+    rng = np.random.default_rng(5)
+    if name in ("head", "predictor"):
+        path = make_model("vitl16_ssv2_q8_0" if name == "head" else "vitl16_pred_q8_0")
+        m = _lib.Model(path, device=0)
+        ctx = _lib.Context(m)
+        enc = rng.standard_normal((2048, 1024)).astype(np.float32)
+        ms = []
+        if name == "head":
+            x = torch.from_numpy(enc).cuda()
+            pooled = torch.zeros(1024, device="cuda")
+            logits = torch.zeros(m.n_classes, device="cuda")
+            torch.cuda.synchronize()
+            for i in range(steps + 1):
+                ctx.head_device(x.data_ptr(), 2048, pooled.data_ptr(), logits.data_ptr())
+                if i:
+                    ms.append(ctx.last_compute_ms)
+            n_bytes = 2 * 2048 * 1024 * 4
+            return {"workload": "V-JEPA 2 ViT-L SSv2 attentive-pool head: 3 pooler blocks over 2048 tokens, cross-attention, "
+                                "MLP, 174 classes, q8_0", "p50_ms": round(float(np.median(ms)), 4), "calls": steps,
+                    "pool_attention_bytes": n_bytes}
+        perm = rng.permutation(2048)
+        for i in range(steps + 1):
+            ctx.predict(enc, perm[:1024], perm[1024:])
+            if i:
+                ms.append(ctx.last_compute_ms)
+        return {"workload": "V-JEPA 2 ViT-L masked predictor: 12 blocks 384 wide, 12 heads of 32, 1024 context + 1024 "
+                            "target rows, q8_0", "p50_ms": round(float(np.median(ms)), 4), "calls": steps}
+    if name == "quantizer":
+        n = 64 << 20
+        x = (torch.randn(n, device="cuda") * 0.02).contiguous()
+        out = {}
+        for tname, gt in (("q8_0", gguf.GGML_Q8_0), ("q4_k", gguf.GGML_Q4_K)):
+            y = torch.empty(gguf.row_bytes(gt, n), dtype=torch.uint8, device="cuda")
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            _lib.lib().jepa_amd_quantize_rows(0, gt, x.data_ptr(), n, y.data_ptr())
+            torch.cuda.synchronize()
+            ms = []
+            for _ in range(max(3, steps // 4)):
+                ev0.record()
+                _lib.lib().jepa_amd_quantize_rows(0, gt, x.data_ptr(), n, y.data_ptr())
+                ev1.record()
+                torch.cuda.synchronize()
+                ms.append(ev0.elapsed_time(ev1))
+            t = float(np.median(ms))
+            out[tname] = {"ms_per_64Mi_values": round(t, 3), "Gvalues/s": round(n / (t * 1e-3) / 1e9, 2),
+                          "read_GB/s": round(n * 4 / (t * 1e-3) / 1e9, 1)}
+        return out
+    log(f"bench: unknown extra {name}")
+    return None
+
+
 def cpu_baseline(path, x_host):
     """The oracle on the host cores: patch embedding + 1 block and + 2 blocks of one clip."""
     from oracle import oracle as O
@@ -126,6 +183,10 @@ def main():
     ap.add_argument("--configs", default="",
                     help="also time these encoder configurations (comma list: vits16_f16, vitb16_2_1_q8_0, "
                          "vitg16_q8_0, levjepa_vitl16_q8_0)")
+    ap.add_argument("--extras", default="",
+                    help="also time the rows next to the encoder (comma list: head = ViT-L SSv2 attentive-pool head on "
+                         "2048 tokens; predictor = ViT-L masked predictor, 1024 context + 1024 target rows; quantizer = "
+                         "the q8_0 / q4_K block quantizers over 64 Mi weights)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the library's plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -201,6 +262,10 @@ def main():
             "value": round(b * st / rc["elapsed_s"], 3), "unit": f"{unit}/s", "items_per_step": b,
             "tokens_per_item": rc["rows"], "ms_per_step": round(rc["elapsed_s"] / st * 1e3, 4),
             "p50_ms": round(float(np.median(rc["device_ms"])), 4), "steps": st}
+    for name in [e for e in args.extras.split(",") if e]:
+        res = time_extra(name, max(5, min(args.steps, 20)))
+        if res is not None:
+            extra.setdefault("extras", {})[name] = res
     if args.copy_mib > 0:
         # a copy of known size: FETCH_SIZE / WRITE_SIZE of k_copy_f32 calibrate the counters
         import ctypes as C
