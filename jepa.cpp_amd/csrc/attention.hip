@@ -85,10 +85,17 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     const int l32 = lane & 31, g = lane >> 5;
     const int qg = wave & 3, kh = wave >> 2;            // query group, key half
     const int hw = wave & 3;                            // wave index inside its half (loads)
-    const int64_t head = blockIdx.y;
+    // XCD-aware order: workgroups go to the 8 XCDs round-robin by linear id, so linear id L runs on
+    // XCD L % 8. Renumber so that each XCD's share is a contiguous range of (head, query block): the
+    // query blocks of one head then share one XCD's L2 for that head's K / V^T instead of all eight
+    // fetching it (the identity when the grid is not a multiple of 8).
+    const uint32_t gx = gridDim.x, total = gridDim.x * gridDim.y, lin = blockIdx.x + gx * blockIdx.y;
+    const uint32_t rl = total % 8 == 0 ? (lin % 8) * (total / 8) + lin / 8 : lin;
+    const uint32_t qblk = rl % gx;
+    const int64_t head = rl / gx;
     const int64_t item = head / n_head;
     const int h = (int) (head - item * n_head);
-    const int64_t q0 = (int64_t) blockIdx.x * QB + qg * 32;
+    const int64_t q0 = (int64_t) qblk * QB + qg * 32;
 
     const _Float16 * Qh = Q + head * R_pad * HD;
     // buffer resources over this head's K rows and V^T rows (offsets below 4 GiB per head)
@@ -97,7 +104,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
 
     // key tiles of this workgroup: the union of its queries' key ranges (the first query has the
     // lowest bound, the last the highest; a prefix row among them reads everything)
-    const int qa = (int) blockIdx.x * QB, qz = min((int) R, qa + QB) - 1;
+    const int qa = (int) qblk * QB, qz = min((int) R, qa + QB) - 1;
     const int klo_wg = key_range(qa, (int) R, np, tpf).x;
     const int khi_wg = qa < np ? (int) R : key_range(qz, (int) R, np, tpf).y;
     const int tfirst = klo_wg / KT;
