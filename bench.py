@@ -182,7 +182,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--configs", default="",
                     help="also time these encoder configurations (comma list: vits16_f16, vitb16_2_1_q8_0, "
-                         "vitg16_q8_0, levjepa_vitl16_q8_0)")
+                         "vitg16_q8_0, levjepa_vitl16_q8_0, vitl16_q8_0 = the headline model with 4 clips per call)")
     ap.add_argument("--extras", default="",
                     help="also time the rows next to the encoder (comma list: head = ViT-L SSv2 attentive-pool head on "
                          "2048 tokens; predictor = ViT-L masked predictor, 1024 context + 1024 target rows; quantizer = "
@@ -247,7 +247,8 @@ def main():
         extra["q4_k"] = q4
     # the other encoder configurations: (batch, frames, size) of one step and what one item is
     shapes = {"vits16_f16": (1, 1, 224, "images"), "vitb16_2_1_q8_0": (8, 1, 384, "images"),
-              "vitg16_q8_0": (1, 64, 256, "clips"), "levjepa_vitl16_q8_0": (1, 16, 224, "clips")}
+              "vitg16_q8_0": (1, 64, 256, "clips"), "levjepa_vitl16_q8_0": (1, 16, 224, "clips"),
+              "vitl16_q8_0": (4, 16, 256, "clips")}   # the headline model, 4 clips per call (serving throughput)
     for name in [c for c in args.configs.split(",") if c]:
         if name not in shapes:
             log(f"bench: unknown configuration {name}")
