@@ -220,9 +220,19 @@ extern "C" int jepa_amd_quantize_file(const char * in_path, const char * out_pat
     }
     if (!have_ft || ftype_to_end) kv_out.push_back(ft_pair());
 
-    // ---- write ----------------------------------------------------------------------------------------
+    // ---- write (a file left half-written by a failure is removed) ------------------------------------
+    const int dev = device < 0 ? 0 : device;
+    int prev = 0;
+    hipGetDevice(&prev);
+    struct restore { int d; ~restore() { hipSetDevice(d); } } rs{prev};
+    if (hipSetDevice(dev) != hipSuccess) { jepa_log("jepa: jepa_amd_quantize_file: no HIP device %d\n", dev); return -1; }
     std::unique_ptr<FILE, int (*)(FILE *)> fout(fopen(out_path, "wb"), fclose);
     if (!fout) { jepa_log("jepa: cannot write '%s'\n", out_path); return -1; }
+    struct remove_on_failure {
+        const char * path;
+        bool keep = false;
+        ~remove_on_failure() { if (!keep) remove(path); }
+    } guard{out_path};
     writer w{fout.get()};
     w.bytes("GGUF", 4);
     w.put<uint32_t>(3);
@@ -241,11 +251,6 @@ extern "C" int jepa_amd_quantize_file(const char * in_path, const char * out_pat
     w.zeros((size_t) (pad32(pos) - pos));
 
     // ---- data: unchanged tensors copied, the others through f32 on the GPU ----------------------------
-    const int dev = device < 0 ? 0 : device;
-    int prev = 0;
-    hipGetDevice(&prev);
-    struct restore { int d; ~restore() { hipSetDevice(d); } } rs{prev};
-    if (hipSetDevice(dev) != hipSuccess) { jepa_log("jepa: jepa_amd_quantize_file: no HIP device %d\n", dev); return -1; }
     dev_buf d_src, d_f32, d_dst;
     std::vector<uint8_t> src, dst;
     int n_changed = 0;
@@ -279,5 +284,6 @@ extern "C" int jepa_amd_quantize_file(const char * in_path, const char * out_pat
     if (verbose)
         jepa_log("jepa-quantize: %s -> %s [%s]: %d tensors re-typed, %d K-quant fallbacks, general.file_type %u\n", in_path, out_path,
                  spec->name, n_changed, n_fallback, ftype);
+    guard.keep = true;
     return 0;
 }
