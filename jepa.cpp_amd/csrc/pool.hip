@@ -8,7 +8,8 @@
 //           16-wide slice of the dot product (one coalesced 256-byte row per four lanes), joined by
 //           two lane shuffles; the workgroup forms the chunk's max m, p = exp(s - m) and l = sum p.
 //           P V: lane = output dimension, wave w takes keys w, w + 4, ..., its 16 loads issued
-//           together; the four waves' sums are added in a fixed order; (m, l, acc[64]) go to `part`;
+//           together with the K loads; the four waves' sums are added in a fixed order; (m, l,
+//           acc[64]) go to `part`;
 //   pass 2: one workgroup per head merges its chunks (flash-decoding rescale by exp(m_c - M)): wave w
 //           takes chunks w, w + 4, ..., the four waves' sums are added in a fixed order, the result is
 //           divided by the total weight and q0 is added.
@@ -54,6 +55,15 @@ __global__ __launch_bounds__(NT) void k_pool_part(const float * __restrict__ q, 
             a += k4[i].w * sq[16 * pq + 4 * i + 3];
         }
     }
+    // P V operands, issued before the score reductions so that their latency overlaps them:
+    // lane = output dimension, wave wv takes keys wv, wv + 4, ..., wv + 60
+    const float * vc = V + t0 * ld + (int64_t) h * HD + lane;
+    float vv[CH / 4];
+#pragma unroll
+    for (int i = 0; i < CH / 4; i++) {
+        const int j = wv + 4 * i;
+        vv[i] = j < nc ? vc[(int64_t) j * ld] : 0.0f;
+    }
     a += __shfl_xor(a, 1, 64);
     a += __shfl_xor(a, 2, 64);
     const float s = kk < nc ? a * scale : -INFINITY;
@@ -66,14 +76,6 @@ __global__ __launch_bounds__(NT) void k_pool_part(const float * __restrict__ q, 
     const float lw = wave_sum(pq == 0 ? p : 0.0f);
     if (lane == 0) sred[1][wv] = lw;
     __syncthreads();
-    // P V: lane = output dimension, wave wv takes keys wv, wv + 4, ..., wv + 60
-    const float * vc = V + t0 * ld + (int64_t) h * HD + lane;
-    float vv[CH / 4];
-#pragma unroll
-    for (int i = 0; i < CH / 4; i++) {
-        const int j = wv + 4 * i;
-        vv[i] = j < nc ? vc[(int64_t) j * ld] : 0.0f;
-    }
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < CH / 4; i++) acc += sp[wv + 4 * i] * vv[i];
