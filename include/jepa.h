@@ -7,10 +7,13 @@
  * ctypes binding in python/src/jepa_cpp/_api.py) links against this library unchanged.
  *
  * What is implemented on the GPU: the ViT encoder forward of the image families (hfvit / ijepa /
- * lewm encoder part) and of the video families (vjepa2 / vjepa2_1), i.e. jepa_encode, plus the model
- * loader, introspection, device selection, pooling and diagnostics. Entry points that belong to
- * other subsystems of the reference (predictors, world models, planners, heads, image decoding)
- * are exported so that callers link, and return -1 / NULL / 0 with a message in jepa_error_text().
+ * lewm encoder part) and of the video families (vjepa2 / vjepa2_1 / levjepa), i.e. jepa_encode, the
+ * attentive-pool head (jepa_head, jepa_head_ex), the masked predictor (jepa_predict, _ex, _mod), the
+ * preprocessing entry points and image loading (PNG, PPM / PGM, baseline JPEG), plus the model
+ * loader, introspection, device selection, pooling and diagnostics. Entry points that belong to the
+ * other subsystems of the reference (LeWM and V-JEPA 2-AC world models, H-JEPA, planners, the LeWM
+ * projector) are exported so that callers link, and return -1 / NULL / 0 with a message in
+ * jepa_error_text().
  *
  * Conventions shared with the reference (include/jepa.h:612-647): a jepa_model is immutable after
  * load and may be shared; a jepa_context belongs to one thread; failures return -1 or NULL and the

@@ -123,6 +123,16 @@ int jepa_amd_quantize_rows(int device, int gtype, const float * x_dev, int64_t n
  * written back through the accumulator layout the GEMM epilogues assume. */
 int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * d);
 
+/* The 3-D RoPE tables this library uploads for an encoder (host only, no device work): [n_rows][head_dim]
+ * cos and sin rows for grid (grid_t, grid_h, grid_w), variant 0 (V-JEPA 2, tiled) or 1 (V-JEPA 2.1,
+ * interleaved), with the 2.1 interpolation to (train_h, train_w) when interpolate is set. ids (may
+ * be NULL: every token, T-major) selects rows of the grid. signed_sin = 1 gives the sine table with
+ * the rotation's sign on the even lanes, as the QKV epilogue reads it; 0 the plain sines. Replaces
+ * nothing in the reference: it exposes the tables of reference src/rope3d.cpp:9-134 to the tests
+ * that pin them against the reference's golden vectors. Returns 0, or -1 on a bad argument. */
+int jepa_amd_rope_tables(int head_dim, int grid_t, int grid_h, int grid_w, int variant, int interpolate, int train_h, int train_w,
+                         float theta, const int32_t * ids, int64_t n_rows, int signed_sin, float * cos_out, float * sin_out);
+
 /* Copy of n float32 values between device buffers (a plain copy kernel, for counter calibration). */
 int jepa_amd_copy(int device, const float * src_dev, float * dst_dev, int64_t n, int reps, double * ms);
 

@@ -3,6 +3,7 @@
 #include "model.h"
 #include "kernels.h"
 #include "preprocess.h"
+#include "rope3d.h"
 
 #include <cmath>
 #include <cstring>
@@ -386,4 +387,36 @@ extern "C" int jepa_amd_preprocess_frames_device(int device, const jepa_preproce
     if (out_h) *out_h = g.crop;
     if (out_w) *out_w = g.crop;
     return d.finish();
+}
+
+extern "C" int jepa_amd_rope_tables(int head_dim, int grid_t, int grid_h, int grid_w, int variant, int interpolate, int train_h,
+                                    int train_w, float theta, const int32_t * ids, int64_t n_rows, int signed_sin, float * cos_out,
+                                    float * sin_out) {
+    if (head_dim <= 0 || grid_t <= 0 || grid_h <= 0 || grid_w <= 0 || n_rows <= 0 || !cos_out || !sin_out || (variant != 0 && variant != 1)) {
+        jepa_log("jepa: jepa_amd_rope_tables: bad arguments (head_dim %d, grid %dx%dx%d, %lld rows, variant %d)\n", head_dim, grid_t,
+                 grid_h, grid_w, (long long) n_rows, variant);
+        return -1;
+    }
+    const int64_t n_grid = (int64_t) grid_t * grid_h * grid_w;
+    if (!ids && n_rows > n_grid) {
+        jepa_log("jepa: jepa_amd_rope_tables: %lld rows but the grid has %lld tokens\n", (long long) n_rows, (long long) n_grid);
+        return -1;
+    }
+    for (int64_t r = 0; ids && r < n_rows; r++)
+        if (ids[r] < 0 || ids[r] >= n_grid) {
+            jepa_log("jepa: jepa_amd_rope_tables: id %d is outside the %lld-token grid\n", ids[r], (long long) n_grid);
+            return -1;
+        }
+    rope3d_params p;
+    p.grid_t = grid_t; p.grid_h = grid_h; p.grid_w = grid_w;
+    p.head_dim = head_dim;
+    p.theta = theta;
+    p.interpolate = interpolate != 0;
+    p.train_grid_h = train_h; p.train_grid_w = train_w;
+    p.variant = variant;
+    std::vector<float> c, s;
+    rope3d_tables(p, ids, n_rows, c, s, signed_sin != 0);
+    memcpy(cos_out, c.data(), c.size() * sizeof(float));
+    memcpy(sin_out, s.data(), s.size() * sizeof(float));
+    return 0;
 }

@@ -1,9 +1,10 @@
 // api.cpp - the encoder-path entry points of include/jepa.h: diagnostics, devices, contexts,
 // jepa_encode, pooling, introspection, small host helpers.
 //
-// Behaviour follows reference src/jepa.cpp (error conventions 16-36, device parsing 107-132,
-// context knobs 178-254, encode dispatch and input checks 1183-1224, pooling 1229-1271, softmax /
-// top-k 1134-1156, token grid 1158-1181) and src/jepa-gguf.cpp:1122-1152 (introspection).
+// Behaviour follows the contracts of reference include/jepa.h and src/jepa.cpp (error conventions
+// 16-36, device parsing 107-132, context knobs 178-254, encode dispatch and input checks 1183-1224,
+// pooling 1229-1271, softmax / top-k 1128-1146, token grid 1158-1181) and src/jepa-gguf.cpp:1122-1152
+// (introspection).
 #include "model.h"
 
 #include <algorithm>
@@ -11,6 +12,7 @@
 #include <cctype>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -20,29 +22,51 @@
 #include <vector>
 
 // ---------------------------------------------------------------------------------------------
-// diagnostics (reference src/jepa.cpp:16-36)
+// diagnostics: the contract of include/jepa.h:596-610 (every message goes to stderr and into a
+// per-thread capture of bounded size that jepa_error_reset empties)
 // ---------------------------------------------------------------------------------------------
-static const size_t JEPA_ERROR_TEXT_MAX = 8192;
-static thread_local std::string g_error_text;
+namespace {
+// per-thread capture: a fixed buffer, so logging never allocates on the thread's behalf and a
+// runaway caller cannot grow it; once full, later text is dropped (stderr still gets all of it)
+struct capture_buffer {
+    static constexpr size_t cap = 8192;
+    char text[cap + 1] = {0};
+    size_t used = 0;
+    void clear() { used = 0; text[0] = 0; }
+    void add(const char * p, size_t n) {
+        const size_t take = std::min(n, cap - used);
+        memcpy(text + used, p, take);
+        used += take;
+        text[used] = 0;
+    }
+};
+thread_local capture_buffer t_capture;
+}  // namespace
 
 void jepa_log(const char * fmt, ...) {
-    va_list ap;
+    // format once (on the stack for the usual short line, on the heap for a long one), then hand the
+    // same bytes to stderr and to the capture
+    char small[512];
+    va_list ap, again;
     va_start(ap, fmt);
-    vfprintf(stderr, fmt, ap);
+    va_copy(again, ap);
+    const int n = vsnprintf(small, sizeof(small), fmt, ap);
     va_end(ap);
-    if (g_error_text.size() >= JEPA_ERROR_TEXT_MAX) return;
-    char buf[1024];
-    va_list ap2;
-    va_start(ap2, fmt);
-    const int n = vsnprintf(buf, sizeof(buf), fmt, ap2);
-    va_end(ap2);
-    if (n <= 0) return;
-    g_error_text.append(buf, std::min((size_t) n, sizeof(buf) - 1));
-    if (g_error_text.size() > JEPA_ERROR_TEXT_MAX) g_error_text.resize(JEPA_ERROR_TEXT_MAX);
+    if (n < 0) { va_end(again); return; }
+    const char * msg = small;
+    std::vector<char> big;
+    if ((size_t) n >= sizeof(small)) {
+        big.resize((size_t) n + 1);
+        vsnprintf(big.data(), big.size(), fmt, again);
+        msg = big.data();
+    }
+    va_end(again);
+    fwrite(msg, 1, (size_t) n, stderr);
+    t_capture.add(msg, (size_t) n);
 }
 
-extern "C" void jepa_error_reset(void) { g_error_text.clear(); }
-extern "C" const char * jepa_error_text(void) { return g_error_text.c_str(); }
+extern "C" void jepa_error_reset(void) { t_capture.clear(); }
+extern "C" const char * jepa_error_text(void) { return t_capture.text; }
 extern "C" const char * jepa_version(void) { return JEPA_VERSION; }
 
 // ---------------------------------------------------------------------------------------------
@@ -185,23 +209,37 @@ extern "C" bool jepa_context_mul_mat_prec_f32(const jepa_context * ctx) { return
 // ---------------------------------------------------------------------------------------------
 // jepa_encode (reference src/jepa.cpp:1183-1224)
 // ---------------------------------------------------------------------------------------------
+namespace {
+// The five extents are the only description of in->data: refuse a shape the model cannot take or
+// whose element count overflows a byte size, before anything indexes with it (logged refusal).
+bool input_acceptable(const jepa_model * m, const jepa_input * in) {
+    const int dims[5] = {in->n_batch, in->n_chans, in->n_frames, in->height, in->width};
+    if (in->n_chans != m->hp.enc.in_chans) {
+        jepa_log("jepa: the model takes %d-channel input; this input has %d channels\n", m->hp.enc.in_chans, in->n_chans);
+        return false;
+    }
+    uint64_t bytes = sizeof(float);
+    bool overflow = false;
+    for (int d : dims) {
+        if (d < 1) {
+            jepa_log("jepa: input shape [%d, %d, %d, %d, %d] has an empty extent\n", dims[0], dims[1], dims[2], dims[3], dims[4]);
+            return false;
+        }
+        overflow = overflow || __builtin_mul_overflow(bytes, (uint64_t) d, &bytes);
+    }
+    if (overflow || bytes > (uint64_t) PTRDIFF_MAX) {
+        jepa_log("jepa: input shape [%d, %d, %d, %d, %d] is larger than any buffer can be\n", dims[0], dims[1], dims[2], dims[3],
+                 dims[4]);
+        return false;
+    }
+    return true;
+}
+}  // namespace
+
 extern "C" int jepa_encode(jepa_context * ctx, const jepa_input * in, jepa_output * out) {
     if (!ctx || !in || !out || !in->data) return -1;
     const jepa_model * m = ctx->model;
-    if (in->n_chans != m->hp.enc.in_chans) {
-        jepa_log("jepa: input has %d channels, model expects %d\n", in->n_chans, m->hp.enc.in_chans);
-        return -1;
-    }
-    if (in->n_batch < 1 || in->n_frames < 1 || in->height < 1 || in->width < 1) {
-        jepa_log("jepa: bad input shape [%d, %d, %d, %d, %d]\n", in->n_batch, in->n_chans, in->n_frames, in->height, in->width);
-        return -1;
-    }
-    const double n_elems = (double) in->n_batch * in->n_chans * in->n_frames * in->height * in->width;
-    if (n_elems * sizeof(float) >= (double) SIZE_MAX) {
-        jepa_log("jepa: input shape [%d, %d, %d, %d, %d] describes %.3g floats, which cannot be a buffer\n", in->n_batch, in->n_chans,
-                 in->n_frames, in->height, in->width, n_elems);
-        return -1;
-    }
+    if (!input_acceptable(m, in)) return -1;
     out->data = nullptr; out->n_tokens = 0; out->dim = 0;
     int64_t n_items = 0;
     const int64_t R = encode_rows(m, in->n_batch, in->n_frames, in->height, in->width, &n_items);
@@ -250,67 +288,109 @@ extern "C" int64_t jepa_token_grid(const jepa_model * model, int n_frames, int h
 }
 
 // ---------------------------------------------------------------------------------------------
-// pooling (reference src/jepa.cpp:1229-1271), host side
+// pooling (contract: include/jepa.h:113-117; reference src/jepa.cpp:1229-1271), host side
 // ---------------------------------------------------------------------------------------------
-extern "C" int jepa_pool_mean(const jepa_model * model, const jepa_output * enc, jepa_output * out) {
-    if (!model || !enc || !out || !enc->data) return -1;
-    const int64_t skip = (model->hp.enc.cls_token ? 1 : 0) + model->hp.enc.n_registers;
-    const int64_t D = enc->dim, n = enc->n_tokens - skip;
-    if (D <= 0 || enc->n_tokens <= 0) {
-        jepa_log("jepa: jepa_pool_mean: encoder output is [%lld tokens, %lld dims]\n", (long long) enc->n_tokens, (long long) D);
-        return -1;
+namespace {
+// an encoder output the caller filled in: positive extents and data, else a logged refusal
+bool pool_input_ok(const char * fn, const jepa_output * enc) {
+    if (enc->dim > 0 && enc->n_tokens > 0) return true;
+    jepa_log("jepa: %s: encoder output is [%lld tokens, %lld dims]\n", fn, (long long) enc->n_tokens, (long long) enc->dim);
+    return false;
+}
+
+// one malloc'd row of D floats in out, or false
+bool pool_output(jepa_output * out, int64_t D) {
+    out->data = (float *) malloc((size_t) D * sizeof(float));
+    if (!out->data) {
+        out->n_tokens = out->dim = 0;
+        return false;
     }
-    if (n <= 0) return -1;
     out->n_tokens = 1;
     out->dim = D;
-    out->data = (float *) calloc((size_t) D, sizeof(float));
-    if (!out->data) return -1;
-    std::vector<double> acc((size_t) D, 0.0);
-    for (int64_t i = skip; i < enc->n_tokens; i++) {
-        const float * row = enc->data + i * D;
-        for (int64_t d = 0; d < D; d++) acc[(size_t) d] += row[d];
+    return true;
+}
+}  // namespace
+
+extern "C" int jepa_pool_mean(const jepa_model * model, const jepa_output * enc, jepa_output * out) {
+    if (!model || !enc || !out || !enc->data) return -1;
+    if (!pool_input_ok("jepa_pool_mean", enc)) return -1;
+    // the prefix rows (CLS, registers) are not patches and are left out of the mean
+    const int64_t prefix = (int64_t) (model->hp.enc.cls_token ? 1 : 0) + model->hp.enc.n_registers;
+    const int64_t rows = enc->n_tokens - prefix, D = enc->dim;
+    if (rows <= 0) return -1;
+    if (!pool_output(out, D)) return -1;
+    // columns in slabs that keep their double partial sums in cache; each sum runs over the rows in
+    // order, in double, and is divided once
+    constexpr int64_t SLAB = 512;
+    double part[SLAB];
+    const float * first = enc->data + prefix * D;
+    for (int64_t c0 = 0; c0 < D; c0 += SLAB) {
+        const int64_t w = std::min(SLAB, D - c0);
+        std::fill(part, part + w, 0.0);
+        for (int64_t r = 0; r < rows; r++) {
+            const float * src = first + r * D + c0;
+            for (int64_t c = 0; c < w; c++) part[c] += (double) src[c];
+        }
+        for (int64_t c = 0; c < w; c++) out->data[c0 + c] = (float) (part[c] / (double) rows);
     }
-    for (int64_t d = 0; d < D; d++) out->data[d] = (float) (acc[(size_t) d] / (double) n);
     return 0;
 }
 
 extern "C" int jepa_pool_cls(const jepa_model * model, const jepa_output * enc, jepa_output * out) {
     if (!model || !enc || !out || !enc->data) return -1;
-    if (!model->hp.enc.cls_token) { jepa_log("jepa: jepa_pool_cls: model has no CLS token\n"); return -1; }
-    if (enc->dim <= 0 || enc->n_tokens < 1) {
-        jepa_log("jepa: jepa_pool_cls: encoder output is [%lld tokens, %lld dims]\n", (long long) enc->n_tokens, (long long) enc->dim);
+    if (!model->hp.enc.cls_token) {
+        jepa_log("jepa: jepa_pool_cls: this model has no CLS token to pool\n");
         return -1;
     }
-    out->n_tokens = 1;
-    out->dim = enc->dim;
-    out->data = (float *) malloc((size_t) enc->dim * sizeof(float));
-    if (!out->data) return -1;
-    memcpy(out->data, enc->data, (size_t) enc->dim * sizeof(float));
+    if (!pool_input_ok("jepa_pool_cls", enc) || !pool_output(out, enc->dim)) return -1;
+    std::copy(enc->data, enc->data + enc->dim, out->data);   // row 0 is the CLS row
     return 0;
 }
 
 // ---------------------------------------------------------------------------------------------
-// host helpers (reference src/jepa.cpp:1134-1156)
+// host helpers for classifiers (contract: include/jepa.h:146-150)
 // ---------------------------------------------------------------------------------------------
 extern "C" void jepa_softmax(const float * logits, int n, float * probs) {
-    if (n <= 0 || !logits || !probs) return;
-    float mx = logits[0];
-    for (int i = 1; i < n; i++) mx = logits[i] > mx ? logits[i] : mx;
-    double sum = 0;
-    for (int i = 0; i < n; i++) { probs[i] = expf(logits[i] - mx); sum += probs[i]; }
-    const float inv = (float) (1.0 / (sum > 0 ? sum : 1.0));
-    for (int i = 0; i < n; i++) probs[i] *= inv;
+    if (!logits || !probs || n <= 0) return;
+    // shifted by the largest logit so that every exponent is <= 0; the normaliser is summed and
+    // applied in double
+    const float top = *std::max_element(logits, logits + n);
+    double total = 0.0;
+    for (int i = 0; i < n; i++) {
+        probs[i] = expf(logits[i] - top);
+        total += (double) probs[i];
+    }
+    const double scale = total > 0.0 ? 1.0 / total : 1.0;
+    for (int i = 0; i < n; i++) probs[i] = (float) ((double) probs[i] * scale);
 }
 
 extern "C" int jepa_top_k(const float * logits, int n, int k, int32_t * idx) {
-    if (n <= 0 || k <= 0 || !logits || !idx) return 0;
-    if (k > n) k = n;
-    std::vector<int32_t> order((size_t) n);
-    for (int i = 0; i < n; i++) order[(size_t) i] = i;
-    std::partial_sort(order.begin(), order.begin() + k, order.end(),
-                      [&](int32_t a, int32_t b) { return logits[a] != logits[b] ? logits[a] > logits[b] : a < b; });
-    for (int i = 0; i < k; i++) idx[i] = order[(size_t) i];
-    return k;
+    if (!logits || !idx || n <= 0 || k <= 0) return 0;
+    const int want = std::min(k, n);
+    // rank: larger logit first, the smaller index on a tie; NaN ranks below every number
+    auto before = [logits](int32_t a, int32_t b) {
+        const float x = logits[a], y = logits[b];
+        const bool xn = std::isnan(x), yn = std::isnan(y);
+        if (xn != yn) return yn;
+        if (!xn && x != y) return x > y;
+        return a < b;
+    };
+    // a bounded heap of the best `want` seen so far (its top is the weakest member)
+    std::vector<int32_t> heap;
+    heap.reserve((size_t) want);
+    for (int32_t i = 0; i < n; i++) {
+        if ((int) heap.size() < want) {
+            heap.push_back(i);
+            std::push_heap(heap.begin(), heap.end(), before);
+        } else if (before(i, heap.front())) {
+            std::pop_heap(heap.begin(), heap.end(), before);
+            heap.back() = i;
+            std::push_heap(heap.begin(), heap.end(), before);
+        }
+    }
+    std::sort_heap(heap.begin(), heap.end(), before);
+    std::copy(heap.begin(), heap.end(), idx);
+    return want;
 }
 
 extern "C" void jepa_free(void * p) { free(p); }

@@ -6,23 +6,19 @@
 //   q4_K weights x q8_K activations:         sum_sb (dw*da) * sum_j sc_j S_j  -  (dmin*da) * sum_j m_j bsum_j
 //   f16 weights x f16-rounded activations:   f32 accumulation of exact f16 products
 //
-// MFMA mapping (v_mfma_f32_32x32x16_f16, wave64). The integer codes of both operands are held as
-// f16 values, which are exact (|q| <= 945), so every MFMA product and every partial sum of a 32-deep
-// block is an exact integer in f32. Per 32-deep block and 32x32 output tile a wave issues:
-//   2 MFMAs  S  = A_blk . B_blk                       (the exact block sum S_b, already f32)
-//   1 MFMA   sc = dw (x) da                            (outer product of the two f16 scale vectors:
-//                                                       one non-zero K slot, so sc = dw*da exactly)
-//   16 VALU  acc = fma(S, sc, acc)                     (one rounding per block, like ggml's AVX2 fmadd)
-// so the per-block scale epilogue costs one VALU op per output element instead of three
-// (convert + scale product + fma), and the kernel is MFMA-bound rather than VALU-bound.
+// q8_0 / q4_0 (int8 codes in HBM and LDS), per 32-deep block b and 32x32 output tile:
+//   v_mfma_i32_32x32x32_i8   S  = A_b . B_b, started from the bits of 1.5 * 2^23 so that the int32
+//                               result read as a float is 12582912 + S exactly
+//   v_mfma_f32_32x32x8_f16   c  = dw_b (x) da_b (an outer product of the two f16 scale vectors; one
+//                               non-zero K slot, so every c = dw * da is exact)
+//   32 VALU                  acc = fma((12582912 + S) - 12582912, c, acc): one rounding per block
+// q4_K (f16 sc*q codes) and f16 weights run f16 MFMAs (v_mfma_f32_32x32x16_f16) over 64-column stages.
 //
-// Tiling: 256 threads = 4 waves in a 2x2 arrangement; block tile 128 (n) x 128 (m); each wave owns
-// 64 x 64 = 2 x 2 MFMA tiles with W rows on the MFMA "A" side, so a lane's 16 accumulators are
-// 4 groups of 4 consecutive output features of ONE token: RoPE pairs, 32-feature quantization
-// blocks and float4 stores all stay inside a lane (or a lane and its xor-32 partner).
-// K advances 64 per LDS stage (two 32-blocks); global loads of stage k+1 are issued before the
-// MFMAs of stage k. LDS rows are padded to 144 B so the 16-byte operand reads of 8 consecutive
-// rows hit disjoint banks.
+// Workgroups are eight waves (two per SIMD); a wave owns TI x TJ tiles of 32 x 32 with the weight
+// rows on the MFMA "A" side, so a lane's 16 accumulators are 4 groups of 4 consecutive output features
+// of one token (RoPE pairs, 32-feature quantization blocks and float4 stores stay inside a lane or a
+// lane and its xor-32 partner). Operand stages of 128 bytes per row are copied HBM -> LDS by buffer
+// loads with an LDS destination into an XOR-swizzled layout, several stages in flight.
 #include "kernels.h"
 #include "model.h"
 #include "lds_dma.h"
@@ -385,8 +381,10 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // Scale operands, read once per stage: the weight row's four f16 block scales, as they lie in LDS,
     // fill K-slots 0-3 (both lane groups); the token's scale of block blk alone fills K-slot blk of lane
     // group 0 (group 1 is zero), so the product picks dw_blk * da_blk.
-    // The 32 VALU ops per step (convert + fma) and the two MFMAs, which the SIMD does not overlap
-    // well, bound this path; everything else is hidden behind them:
+    // The 32 VALU ops per step (magic-offset subtraction + fma) and the two MFMAs bound this path:
+    // with two or more waves per SIMD the MFMA results and the VALU results share the register-file
+    // write bandwidth (about 32 dwords per cycle per SIMD, measured), so they mostly serialize.
+    // Everything else is meant to hide behind them:
     //  - software pipeline: operand chunks are read two steps ahead, the MFMAs of step u+1 are issued
     //    before the VALU work of step u, across stage boundaries;
     //  - the barrier that publishes stage st+1 sits two steps before the end of stage st, after the
@@ -425,7 +423,14 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         h4 SA[TI], SB[4][TJ];
         i16v S[2];
         f16v C[2];
-        const i16v izero = {};
+        // The int8 MFMA starts from 0x4B400000, the bits of 1.5 * 2^23: the int32 result M + S, read as
+        // a float, is exactly 12582912 + S for |S| < 2^22 (|S| <= 32 * 128 * 128 here), so one f32
+        // subtraction (a full-rate VALU op) gives float(S) exactly where v_cvt_f32_i32 runs at half rate.
+        i16v magic;
+#pragma unroll
+        for (int r = 0; r < 16; r++) magic[r] = 0x4B400000;
+        float neg_magic;   // in a VGPR: a VALU op with an SGPR operand issues at half rate here
+        asm("v_mov_b32 %0, 0xcb400000" : "=v"(neg_magic));
         auto ld_step = [&](const unsigned char * base, int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
             if (j == 0) A[blk][i] = lds_chunk<i4v>(base, 32 * (wn * TI + i) + l32, 2 * blk + g);
@@ -433,13 +438,16 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         };
         auto mma = [&](int u, const h4 (&sa)[TI], const h4 (&sb)[4][TJ]) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], izero);
+            S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], magic);
             C[u & 1] = MFMA8(sa[i], sb[blk][j], zero);
         };
         auto valu = [&](int u) {
             const int t = u % TT, i = t / TJ, j = t % TJ;
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float) S[u & 1][r], C[u & 1][r], acc[i][j][r]);
+            for (int r = 0; r < 16; r++) {
+                const float sf = __fadd_rn(__int_as_float(S[u & 1][r]), neg_magic);
+                acc[i][j][r] = fmaf(sf, C[u & 1][r], acc[i][j][r]);
+            }
         };
         // prologue: only stage 0 is copied before the first barrier (the waves would otherwise stall
         // behind NST-1 stages of copies before any compute); stages 1..NST-1 follow spread over the

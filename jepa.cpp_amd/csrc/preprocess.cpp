@@ -1,17 +1,20 @@
 // preprocess.cpp - host image / video preprocessing behind include/jepa.h (reference src/preprocess.cpp).
 //
-// jepa_resize_antialias_u8 is the uint8 antialiased resize that torchvision's resize(antialias=True)
-// runs on CPU (PyTorch's separable uint8 bilinear / bicubic kernel, Pillow's ImagingResample method),
-// which the reference reproduces (src/preprocess.cpp:1-10) and whose outputs these functions must equal
-// bit for bit:
-//   - separable: the horizontal pass first, rounded to uint8, then the vertical pass;
-//   - per output position, filter taps over the input window [center - support, center + support),
-//     support = (taps / 2) * max(scale, 1), the filter argument scaled by 1 / max(scale, 1)
-//     (triangle for bilinear, Keys cubic a = -0.5 for bicubic), weights normalised in double;
-//   - weights quantised to int16 with the largest precision whose largest weight still fits 15 bits;
-//     int32 accumulation from a rounding offset of 2^(precision-1), output clamp(acc >> precision).
-// Then the centre crop (zero padding when the image is smaller than the crop) and the mean / std
-// normalisation into NCTHW floats. The same tables drive the device version (preprocess.hip).
+// The resize is the uint8 antialiased resample that torchvision's resize(antialias=True) runs on
+// the CPU (PyTorch's separable uint8 kernel, which implements Pillow's ImagingResample), and whose
+// bytes the reference reproduces (src/preprocess.cpp:1-10). What that method fixes, and this file
+// therefore keeps:
+//   - the filter: triangle (bilinear, radius 1) or Keys' cubic with a = -0.5 (bicubic, radius 2),
+//     stretched by the downscale factor, evaluated in double at (input index - centre + 0.5) with
+//     centre = scale * (output index + 0.5), over the inputs whose rounded window
+//     [centre - radius, centre + radius) covers them; each output's weights divided by their sum;
+//   - int16 taps: the weights times 2^shift rounded half away from zero, shift the largest value
+//     (at most 22) at which the largest weight still rounds below 2^15 one step later;
+//   - integer accumulation from 2^(shift-1), result clamp(acc >> shift, 0, 255);
+//   - the horizontal pass first, its uint8 result fed to the vertical pass; a pass whose size does
+//     not change is skipped (its taps would be the identity).
+// The tables are compressed rows (resample_axis): every output keeps only its own taps, and the
+// device passes (preprocess.hip) read the same arrays.
 #include "model.h"
 #include "preprocess.h"
 
@@ -26,68 +29,119 @@
 
 namespace {
 
-double tri(double x) {
-    x = std::fabs(x);
-    return x < 1.0 ? 1.0 - x : 0.0;
+// the two antialias filters, each with its radius at scale 1
+struct aa_filter {
+    double radius;
+    double (*at)(double);
+};
+
+double triangle_at(double x) {
+    const double d = std::fabs(x);
+    return d < 1.0 ? 1.0 - d : 0.0;
 }
 
-// Keys cubic convolution kernel with a = -0.5, in the Horner form of its two pieces
-double keys_cubic(double x) {
-    const double a = -0.5;
-    x = std::fabs(x);
-    if (x < 1.0) return ((a + 2.0) * x - (a + 3.0)) * x * x + 1.0;
-    if (x < 2.0) return ((a * x - 5.0 * a) * x + 8.0 * a) * x - 4.0 * a;
-    return 0.0;
+// Keys (1981) cubic convolution, a = -0.5, in the nested form torch evaluates (the weights must be
+// the same doubles for the int16 rounding to agree): inner piece ((a+2)|x| - (a+3))|x|^2 + 1,
+// outer piece ((a|x| - 5a)|x| + 8a)|x| - 4a
+double keys_at(double x) {
+    constexpr double a = -0.5;
+    const double d = std::fabs(x);
+    if (d >= 2.0) return 0.0;
+    if (d >= 1.0) return ((a * d - 5.0 * a) * d + 8.0 * a) * d - 4.0 * a;
+    return ((a + 2.0) * d - (a + 3.0)) * d * d + 1.0;
+}
+
+// round half away from zero the way the method writes it, (int)(0.5 + |v|) with the sign put back
+int16_t round_tap(double v) {
+    const int mag = (int) (0.5 + std::fabs(v));
+    return (int16_t) (v < 0.0 ? -mag : mag);
+}
+
+uint8_t settle(int32_t acc, int shift) {
+    const int32_t v = acc >> shift;
+    return (uint8_t) std::min<int32_t>(255, std::max<int32_t>(0, v));
+}
+
+// horizontal pass: every row of `rows` (height h, n_in pixels of c channels) into n_out pixels
+void resample_rows(const resample_axis & ax, const uint8_t * src, int h, int c, uint8_t * dst) {
+    const int32_t half = ax.shift > 0 ? (int32_t) 1 << (ax.shift - 1) : 0;
+    std::vector<int32_t> acc((size_t) c);
+    for (int y = 0; y < h; y++) {
+        const uint8_t * in = src + (size_t) y * ax.n_in * c;
+        uint8_t * out = dst + (size_t) y * ax.n_out * c;
+        for (int o = 0; o < ax.n_out; o++) {
+            std::fill(acc.begin(), acc.end(), half);
+            const uint8_t * px = in + (size_t) ax.lo[(size_t) o] * c;
+            for (int32_t t = ax.beg[(size_t) o]; t < ax.beg[(size_t) o + 1]; t++, px += c) {
+                const int32_t tap = ax.taps[(size_t) t];
+                for (int ch = 0; ch < c; ch++) acc[(size_t) ch] += tap * (int32_t) px[ch];
+            }
+            for (int ch = 0; ch < c; ch++) out[(size_t) o * c + ch] = settle(acc[(size_t) ch], ax.shift);
+        }
+    }
+}
+
+// vertical pass: rows of `len` bytes, n_in of them, into n_out rows (whole rows scaled and summed)
+void resample_cols(const resample_axis & ax, const uint8_t * src, size_t len, uint8_t * dst) {
+    const int32_t half = ax.shift > 0 ? (int32_t) 1 << (ax.shift - 1) : 0;
+    std::vector<int32_t> acc(len);
+    for (int o = 0; o < ax.n_out; o++) {
+        std::fill(acc.begin(), acc.end(), half);
+        const uint8_t * row = src + (size_t) ax.lo[(size_t) o] * len;
+        for (int32_t t = ax.beg[(size_t) o]; t < ax.beg[(size_t) o + 1]; t++, row += len) {
+            const int32_t tap = ax.taps[(size_t) t];
+            for (size_t i = 0; i < len; i++) acc[i] += tap * (int32_t) row[i];
+        }
+        uint8_t * out = dst + (size_t) o * len;
+        for (size_t i = 0; i < len; i++) out[i] = settle(acc[i], ax.shift);
+    }
 }
 
 }  // namespace
 
-aa_taps aa_taps_for(int in_size, int out_size, int resample) {
-    aa_taps t;
-    if (in_size <= 0 || out_size <= 0) return t;
-    const int taps = resample == JEPA_RESAMPLE_BICUBIC ? 4 : 2;
-    double (*filt)(double) = resample == JEPA_RESAMPLE_BICUBIC ? keys_cubic : tri;
-    const double scale = (double) in_size / (double) out_size;
-    const double support = scale >= 1.0 ? (taps * 0.5) * scale : taps * 0.5;
-    const double fscale = scale >= 1.0 ? 1.0 / scale : 1.0;
-    t.ksize = (int) std::ceil(support) * 2 + 1;
-    t.first.assign((size_t) out_size, 0);
-    t.count.assign((size_t) out_size, 0);
-    std::vector<double> wd((size_t) out_size * t.ksize, 0.0);
-    double wmax = 0.0;
-    for (int i = 0; i < out_size; i++) {
-        const double center = scale * (i + 0.5);
-        const int64_t lo = std::max<int64_t>((int64_t) (center - support + 0.5), 0);
-        int64_t n = std::min<int64_t>((int64_t) (center + support + 0.5), in_size) - lo;
-        n = std::min<int64_t>(std::max<int64_t>(n, 0), t.ksize);
-        double * w = wd.data() + (size_t) i * t.ksize;
-        double sum = 0.0;
-        for (int64_t j = 0; j < n; j++) {
-            w[j] = filt((j + lo - center + 0.5) * fscale);
-            sum += w[j];
+resample_axis resample_axis_for(int n_in, int n_out, int resample) {
+    resample_axis ax;
+    if (n_in <= 0 || n_out <= 0) return ax;
+    ax.n_in = n_in;
+    ax.n_out = n_out;
+    const aa_filter f = resample == JEPA_RESAMPLE_BICUBIC ? aa_filter{2.0, keys_at} : aa_filter{1.0, triangle_at};
+    const double scale = (double) n_in / (double) n_out;
+    const double stretch = std::max(scale, 1.0);        // the filter widens only when shrinking
+    const double reach = f.radius * stretch;
+    const double step = 1.0 / stretch;
+    ax.lo.resize((size_t) n_out);
+    ax.beg.assign(1, 0);
+    std::vector<double> weight;
+    double peak = 0.0;
+    for (int o = 0; o < n_out; o++) {
+        const double centre = scale * (o + 0.5);
+        // inputs whose window rounds into [centre - reach, centre + reach), clipped to the image
+        const int first = std::max(0, (int) (centre - reach + 0.5));
+        const int end = std::min(n_in, (int) (centre + reach + 0.5));
+        const size_t row0 = weight.size();
+        double total = 0.0;
+        for (int x = first; x < end; x++) {
+            const double v = f.at((x - centre + 0.5) * step);
+            weight.push_back(v);
+            total += v;
         }
-        if (sum != 0.0)
-            for (int64_t j = 0; j < n; j++) {
-                w[j] /= sum;
-                wmax = std::max(wmax, w[j]);
+        if (total != 0.0)
+            for (size_t t = row0; t < weight.size(); t++) {
+                weight[t] /= total;
+                peak = std::max(peak, weight[t]);
             }
-        t.first[(size_t) i] = (int) lo;
-        t.count[(size_t) i] = (int) n;
+        ax.lo[(size_t) o] = first;
+        ax.beg.push_back((int32_t) weight.size());
     }
-    int prec = 0;
-    while (prec < 22 && (int) (0.5 + wmax * (double) (1 << (prec + 1))) < (1 << 15)) prec++;
-    t.precision = prec;
-    t.w.assign(wd.size(), 0);
-    for (size_t j = 0; j < wd.size(); j++) {
-        const double v = wd[j] * (double) (1 << prec);
-        t.w[j] = (int16_t) (v < 0 ? (int) (-0.5 + v) : (int) (0.5 + v));
-    }
-    return t;
-}
-
-static inline uint8_t clamp_shift(int32_t acc, int prec) {
-    const int32_t v = acc >> prec;
-    return (uint8_t) (v < 0 ? 0 : v > 255 ? 255 : v);
+    // shift: the first s in 0..21 whose next step would round the peak weight to 2^15 or more,
+    // else 22
+    ax.shift = 22;
+    for (int s = 0; s < 22; s++)
+        if ((int) (0.5 + peak * (double) (1 << (s + 1))) >= (1 << 15)) { ax.shift = s; break; }
+    ax.taps.resize(weight.size());
+    const double unit = (double) (1 << ax.shift);
+    for (size_t t = 0; t < weight.size(); t++) ax.taps[t] = round_tap(weight[t] * unit);
+    return ax;
 }
 
 extern "C" void jepa_resize_antialias_u8(const uint8_t * src, int h, int w, int c, uint8_t * dst, int out_h, int out_w, int resample) {
@@ -95,49 +149,24 @@ extern "C" void jepa_resize_antialias_u8(const uint8_t * src, int h, int w, int 
         jepa_log("jepa: jepa_resize_antialias_u8: %dx%dx%d -> %dx%d is not a resize\n", h, w, c, out_h, out_w);
         return;
     }
-    if (h == out_h && w == out_w) {
+    const bool across = out_w != w, down = out_h != h;
+    if (!across && !down) {
         memcpy(dst, src, (size_t) h * w * c);
         return;
     }
-    std::vector<uint8_t> mid;
-    const uint8_t * rows = src;
-    int rw = w;
-    if (out_w != w) {   // horizontal pass (into dst directly when there is no vertical one)
-        const aa_taps t = aa_taps_for(w, out_w, resample);
-        const int32_t bias = t.precision > 0 ? 1 << (t.precision - 1) : 0;
-        uint8_t * o = out_h == h ? dst : (mid.resize((size_t) h * out_w * c), mid.data());
-        for (int y = 0; y < h; y++) {
-            const uint8_t * in = src + (size_t) y * w * c;
-            uint8_t * orow = o + (size_t) y * out_w * c;
-            for (int x = 0; x < out_w; x++) {
-                const int16_t * k = t.w.data() + (size_t) x * t.ksize;
-                const uint8_t * p = in + (size_t) t.first[(size_t) x] * c;
-                for (int ch = 0; ch < c; ch++) {
-                    int32_t acc = bias;
-                    for (int j = 0; j < t.count[(size_t) x]; j++) acc += (int32_t) p[(size_t) j * c + ch] * k[j];
-                    orow[(size_t) x * c + ch] = clamp_shift(acc, t.precision);
-                }
-            }
+    // the horizontal result goes straight to dst when it is the last pass
+    std::vector<uint8_t> between;
+    const uint8_t * vin = src;
+    if (across) {
+        uint8_t * hout = dst;
+        if (down) {
+            between.resize((size_t) h * out_w * c);
+            hout = between.data();
         }
-        if (out_h == h) return;
-        rows = mid.data();
-        rw = out_w;
+        resample_rows(resample_axis_for(w, out_w, resample), src, h, c, hout);
+        vin = hout;
     }
-    const aa_taps t = aa_taps_for(h, out_h, resample);   // vertical pass
-    const int32_t bias = t.precision > 0 ? 1 << (t.precision - 1) : 0;
-    const size_t rowlen = (size_t) rw * c;
-    std::vector<int32_t> acc(rowlen);
-    for (int y = 0; y < out_h; y++) {
-        const int16_t * k = t.w.data() + (size_t) y * t.ksize;
-        std::fill(acc.begin(), acc.end(), bias);
-        for (int j = 0; j < t.count[(size_t) y]; j++) {
-            const uint8_t * r = rows + (size_t) (t.first[(size_t) y] + j) * rowlen;
-            const int32_t kj = k[j];
-            for (size_t i = 0; i < rowlen; i++) acc[i] += (int32_t) r[i] * kj;
-        }
-        uint8_t * orow = dst + (size_t) y * rowlen;
-        for (size_t i = 0; i < rowlen; i++) orow[i] = clamp_shift(acc[i], t.precision);
-    }
+    if (down) resample_cols(resample_axis_for(h, out_h, resample), vin, (size_t) out_w * c, dst);
 }
 
 // ------------------------------------------------------------------------------------------------

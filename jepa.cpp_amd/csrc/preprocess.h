@@ -11,14 +11,18 @@
 // ratio, not the file size, makes it large; reference src/preprocess.cpp:195-200)
 #define JEPA_PRE_MAX_PIXELS (64ll * 1024 * 1024)
 
-// quantised filter taps of one resize pass: output i reads inputs first[i] .. first[i] + count[i] - 1
-// with weights w[i * ksize + j] / 2^precision
-struct aa_taps {
-    int ksize = 0, precision = 0;
-    std::vector<int> first, count;
-    std::vector<int16_t> w;
+// One axis of a separable uint8 resize, as a compressed-row table: output o reads the inputs
+// lo[o], lo[o] + 1, ... with the integer taps taps[beg[o]] .. taps[beg[o + 1] - 1], accumulates
+// 2^(shift-1) + sum(tap * pixel) in int32 and keeps clamp(acc >> shift, 0, 255). The rows have
+// their own lengths (no padding), and the same arrays are uploaded for the device passes.
+struct resample_axis {
+    int n_in = 0, n_out = 0, shift = 0;
+    std::vector<int32_t> lo;      // [n_out]
+    std::vector<int32_t> beg;     // [n_out + 1]
+    std::vector<int16_t> taps;    // [beg[n_out]]
+    bool identity() const { return n_in == n_out; }
 };
-aa_taps aa_taps_for(int in_size, int out_size, int resample);
+resample_axis resample_axis_for(int n_in, int n_out, int resample);
 
 // geometry and normalisation of one preprocessing call
 struct pre_plan {

@@ -12,23 +12,25 @@
 
 namespace {
 
-struct dev_taps {
-    const int * first;
-    const int * count;
-    const int16_t * w;
-    int ksize, precision;
+// one resample_axis on the device: output o reads inputs lo[o] + t - beg[o] with taps[t],
+// beg[o] <= t < beg[o + 1]
+struct dev_axis {
+    const int32_t * lo;
+    const int32_t * beg;
+    const int16_t * taps;
+    int shift;
     int identity;   // size unchanged: the host skips this pass (a copy)
 };
 
-__device__ __forceinline__ uint8_t clamp_shift(int32_t acc, int prec) {
-    const int32_t v = acc >> prec;
+__device__ __forceinline__ uint8_t settle(int32_t acc, int shift) {
+    const int32_t v = acc >> shift;
     return (uint8_t) (v < 0 ? 0 : v > 255 ? 255 : v);
 }
 
 // mid[t][y][x][c] = horizontal pass of source row y at resized column x + ox, for the crop columns
 // that fall inside the resized image
 __global__ void k_resize_rows(const uint8_t * __restrict__ src, uint8_t * __restrict__ mid, int n, int h, int w, int crop, int ox,
-                              int rw, dev_taps ht) {
+                              int rw, dev_axis ha) {
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t total = (int64_t) n * h * crop;
     if (id >= total) return;
@@ -38,24 +40,22 @@ __global__ void k_resize_rows(const uint8_t * __restrict__ src, uint8_t * __rest
     uint8_t * o = mid + id * 3;
     if (sx < 0 || sx >= rw) return;                    // padding column, never read
     const uint8_t * row = src + ty * w * 3;
-    if (ht.identity) {
+    if (ha.identity) {
         o[0] = row[sx * 3]; o[1] = row[sx * 3 + 1]; o[2] = row[sx * 3 + 2];
         return;
     }
-    const int first = ht.first[sx], cnt = ht.count[sx];
-    const int16_t * k = ht.w + (int64_t) sx * ht.ksize;
-    const int32_t bias = ht.precision > 0 ? 1 << (ht.precision - 1) : 0;
-    int32_t a0 = bias, a1 = bias, a2 = bias;
-    const uint8_t * p = row + (int64_t) first * 3;
-    for (int j = 0; j < cnt; j++) {
-        const int32_t kj = k[j];
-        a0 += (int32_t) p[3 * j] * kj;
-        a1 += (int32_t) p[3 * j + 1] * kj;
-        a2 += (int32_t) p[3 * j + 2] * kj;
+    const int32_t half = ha.shift > 0 ? 1 << (ha.shift - 1) : 0;
+    int32_t a0 = half, a1 = half, a2 = half;
+    const uint8_t * p = row + (int64_t) ha.lo[sx] * 3;
+    for (int32_t t = ha.beg[sx], e = ha.beg[sx + 1]; t < e; t++, p += 3) {
+        const int32_t k = ha.taps[t];
+        a0 += (int32_t) p[0] * k;
+        a1 += (int32_t) p[1] * k;
+        a2 += (int32_t) p[2] * k;
     }
-    o[0] = clamp_shift(a0, ht.precision);
-    o[1] = clamp_shift(a1, ht.precision);
-    o[2] = clamp_shift(a2, ht.precision);
+    o[0] = settle(a0, ha.shift);
+    o[1] = settle(a1, ha.shift);
+    o[2] = settle(a2, ha.shift);
 }
 
 struct norm_params {
@@ -66,7 +66,7 @@ struct norm_params {
 // out[c][t][y][x] for crop pixel (y, x) of frame t: vertical pass over mid, zero outside the resized
 // image, then the normalisation
 __global__ void k_resize_cols_norm(const uint8_t * __restrict__ mid, float * __restrict__ out, int n, int h, int crop, int oy, int ox,
-                                   int rh, int rw, dev_taps vt, norm_params np) {
+                                   int rh, int rw, dev_axis va, norm_params np) {
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t plane = (int64_t) crop * crop;
     if (id >= (int64_t) n * plane) return;
@@ -77,24 +77,22 @@ __global__ void k_resize_cols_norm(const uint8_t * __restrict__ mid, float * __r
     uint8_t v[3] = {0, 0, 0};
     if (sy >= 0 && sy < rh && sx >= 0 && sx < rw) {
         const uint8_t * col = mid + ((int64_t) t * h * crop + x) * 3;   // row y of mid: + y * crop * 3
-        if (vt.identity) {
+        if (va.identity) {
             const uint8_t * p = col + (int64_t) sy * crop * 3;
             v[0] = p[0]; v[1] = p[1]; v[2] = p[2];
         } else {
-            const int first = vt.first[sy], cnt = vt.count[sy];
-            const int16_t * k = vt.w + (int64_t) sy * vt.ksize;
-            const int32_t bias = vt.precision > 0 ? 1 << (vt.precision - 1) : 0;
-            int32_t a0 = bias, a1 = bias, a2 = bias;
-            for (int j = 0; j < cnt; j++) {
-                const uint8_t * p = col + (int64_t) (first + j) * crop * 3;
-                const int32_t kj = k[j];
-                a0 += (int32_t) p[0] * kj;
-                a1 += (int32_t) p[1] * kj;
-                a2 += (int32_t) p[2] * kj;
+            const int32_t half = va.shift > 0 ? 1 << (va.shift - 1) : 0;
+            int32_t a0 = half, a1 = half, a2 = half;
+            const uint8_t * p = col + (int64_t) va.lo[sy] * crop * 3;
+            for (int32_t k = va.beg[sy], e = va.beg[sy + 1]; k < e; k++, p += (int64_t) crop * 3) {
+                const int32_t tap = va.taps[k];
+                a0 += (int32_t) p[0] * tap;
+                a1 += (int32_t) p[1] * tap;
+                a2 += (int32_t) p[2] * tap;
             }
-            v[0] = clamp_shift(a0, vt.precision);
-            v[1] = clamp_shift(a1, vt.precision);
-            v[2] = clamp_shift(a2, vt.precision);
+            v[0] = settle(a0, va.shift);
+            v[1] = settle(a1, va.shift);
+            v[2] = settle(a2, va.shift);
         }
     }
 #pragma unroll
@@ -104,22 +102,22 @@ __global__ void k_resize_cols_norm(const uint8_t * __restrict__ mid, float * __r
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t) 255; }
 
-size_t taps_bytes(const aa_taps & t) {
-    return align256(t.first.size() * 4) + align256(t.count.size() * 4) + align256(t.w.size() * 2);
+size_t axis_bytes(const resample_axis & ax) {
+    return align256(ax.lo.size() * 4) + align256(ax.beg.size() * 4) + align256(ax.taps.size() * 2);
 }
 
 }  // namespace
 
 size_t preprocess_scratch_bytes(const jepa_preprocess_params * p, const pre_plan & g, int n_frames, int h, int w) {
-    return taps_bytes(aa_taps_for(w, g.rw, p->resample)) + taps_bytes(aa_taps_for(h, g.rh, p->resample)) +
+    return axis_bytes(resample_axis_for(w, g.rw, p->resample)) + axis_bytes(resample_axis_for(h, g.rh, p->resample)) +
            align256((size_t) n_frames * h * g.crop * 3);
 }
 
 bool launch_preprocess(const jepa_preprocess_params * p, const pre_plan & g, const uint8_t * frames, int n_frames, int h, int w,
                        float * out, void * scratch, hipStream_t s) {
-    const aa_taps ht = aa_taps_for(w, g.rw, p->resample), vt = aa_taps_for(h, g.rh, p->resample);
-    // table blob: first / count / weights of both passes, 256-byte aligned pieces
-    std::vector<unsigned char> blob(taps_bytes(ht) + taps_bytes(vt), 0);
+    const resample_axis hx = resample_axis_for(w, g.rw, p->resample), vx = resample_axis_for(h, g.rh, p->resample);
+    // table blob: lo / beg / taps of both passes, 256-byte aligned pieces
+    std::vector<unsigned char> blob(axis_bytes(hx) + axis_bytes(vx), 0);
     unsigned char * dev = (unsigned char *) scratch;
     size_t off = 0;
     auto put = [&](const void * src, size_t bytes) -> const void * {
@@ -128,15 +126,16 @@ bool launch_preprocess(const jepa_preprocess_params * p, const pre_plan & g, con
         off += align256(bytes);
         return d;
     };
-    dev_taps dh, dv;
-    dh.first = (const int *) put(ht.first.data(), ht.first.size() * 4);
-    dh.count = (const int *) put(ht.count.data(), ht.count.size() * 4);
-    dh.w = (const int16_t *) put(ht.w.data(), ht.w.size() * 2);
-    dh.ksize = ht.ksize; dh.precision = ht.precision; dh.identity = g.rw == w;
-    dv.first = (const int *) put(vt.first.data(), vt.first.size() * 4);
-    dv.count = (const int *) put(vt.count.data(), vt.count.size() * 4);
-    dv.w = (const int16_t *) put(vt.w.data(), vt.w.size() * 2);
-    dv.ksize = vt.ksize; dv.precision = vt.precision; dv.identity = g.rh == h;
+    auto upload = [&](const resample_axis & ax, bool identity) {
+        dev_axis d;
+        d.lo = (const int32_t *) put(ax.lo.data(), ax.lo.size() * 4);
+        d.beg = (const int32_t *) put(ax.beg.data(), ax.beg.size() * 4);
+        d.taps = (const int16_t *) put(ax.taps.data(), ax.taps.size() * 2);
+        d.shift = ax.shift;
+        d.identity = identity ? 1 : 0;
+        return d;
+    };
+    const dev_axis dh = upload(hx, g.rw == w), dv = upload(vx, g.rh == h);
     uint8_t * mid = (uint8_t *) dev + off;
     if (hipMemcpyAsync(scratch, blob.data(), off, hipMemcpyHostToDevice, s) != hipSuccess) return false;
     norm_params np;

@@ -1,9 +1,10 @@
 // stubs.cpp - entry points of include/jepa.h outside the encoder path.
 //
-// The reference exports these for its predictors, world models, planners, the attentive-pool head,
-// the LeWM projector and host image decoding (reference include/jepa.h:69-103, 118-127, 142-145,
-// 161-523). They are exported here so that callers such as tools/jepa-bench.cpp link unchanged;
-// each one reports that it is not part of this library and returns its error value.
+// The reference exports these for its world models (LeWM, V-JEPA 2-AC), H-JEPA, planners and the
+// LeWM projector (reference include/jepa.h:69-103, 118-127, 161-523). They are exported here so that
+// callers such as tools/jepa-bench.cpp link unchanged; each one reports that it is not part of this
+// library and returns its error value. (The attentive-pool head, the masked predictor and image
+// decoding are implemented: head.cpp, predict.cpp, image_io.cpp.)
 #include "model.h"
 
 #include <cstring>

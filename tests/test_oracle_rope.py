@@ -93,3 +93,60 @@ def test_rope_apply_is_a_rotation_for_interleaved_pairs():
     nx = x[..., 0::2] ** 2 + x[..., 1::2] ** 2
     ny = y[..., 0::2] ** 2 + y[..., 1::2] ** 2
     np.testing.assert_allclose(ny, nx, rtol=1e-5, atol=1e-6)
+
+
+def _product_tables(case, ids, signed):
+    """The tables libjepa.so uploads (jepa_amd_rope_tables, host only)."""
+    import ctypes as C
+
+    from jepa_amd import _lib
+    L = _lib.lib()
+    L.jepa_amd_rope_tables.restype = C.c_int
+    L.jepa_amd_rope_tables.argtypes = [C.c_int] * 8 + [C.c_float, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
+    D, (gt, gh, gw) = case["hd"], case["grid"]
+    n = len(ids)
+    c = np.zeros((n, D), np.float32)
+    s = np.zeros((n, D), np.float32)
+    ids32 = np.ascontiguousarray(ids, dtype=np.int32)
+    rc = L.jepa_amd_rope_tables(D, gt, gh, gw, case["variant"], case["interp"], case["train"][0], case["train"][1], case["theta"],
+                                ids32.ctypes.data, n, 1 if signed else 0, c.ctypes.data, s.ctypes.data)
+    assert rc == 0
+    return c, s
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"{c['name']}-{c['tag']}")
+def test_product_rope_tables_golden(case):
+    """The product's own tables (csrc/rope3d.cpp), not only the oracle's: within 1e-5 of the reference
+    golden rows, bit-identical to the oracle's tables, and the rotation they drive reproduces the
+    golden output (reference tests/test-ops.cpp:151-245)."""
+    D, grid = case["hd"], case["grid"]
+    n_full = grid[0] * grid[1] * grid[2]
+    sub = case["n"] < n_full
+    ids = _load(f"{case['name']}_ids") if sub else np.arange(n_full, dtype=np.int32)
+    axes = _load(f"{case['name']}_{case['tag']}_axes")
+    rc, rs = _reference_tables(axes, grid, D, ids)
+    c_raw, s_raw = _product_tables(case, ids, signed=False)
+    assert max(np.abs(c_raw - rc).max(), np.abs(s_raw - rs).max()) < TOL
+    kw = dict(variant=case["variant"], interpolate=case["interp"], train=case["train"], theta=case["theta"])
+    oc, os_ = O.rope_tables(grid, D, ids=ids if sub else None, signed=True, **kw)
+    c_sgn, s_sgn = _product_tables(case, ids, signed=True)
+    np.testing.assert_array_equal(c_sgn.view(np.uint32), oc.view(np.uint32))
+    np.testing.assert_array_equal(s_sgn.view(np.uint32), os_.view(np.uint32))
+    x = _load(f"{case['name']}_x")
+    want = _load(f"{case['name']}_{case['tag']}_out")
+    got = O.rope_apply(np.repeat(x[:, None, :], 2, axis=1), c_sgn, s_sgn)
+    assert np.abs(got - want[:, None, :]).max() < TOL
+
+
+def test_product_rope_tables_refuse_bad_ids():
+    import ctypes as C
+
+    from jepa_amd import _lib
+    L = _lib.lib()
+    L.jepa_amd_rope_tables.restype = C.c_int
+    L.jepa_amd_rope_tables.argtypes = [C.c_int] * 8 + [C.c_float, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
+    c = np.zeros((1, 64), np.float32)
+    s = np.zeros((1, 64), np.float32)
+    bad = np.array([8], np.int32)      # a 2x2x2 grid has ids 0..7
+    assert L.jepa_amd_rope_tables(64, 2, 2, 2, 0, 0, 0, 0, 10000.0, bad.ctypes.data, 1, 1, c.ctypes.data, s.ctypes.data) == -1
+    assert L.jepa_amd_rope_tables(64, 2, 2, 2, 0, 0, 0, 0, 10000.0, None, 9, 1, c.ctypes.data, s.ctypes.data) == -1
