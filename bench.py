@@ -12,8 +12,11 @@ Also reported on the same JSON line:
                 launch on the library's stream during a second pass of K steps; HBM traffic per launch
                 from the committed rocprofv3 counter summary when present.
   q4_k          the same workload with q4_K weights.
-  cpu_baseline  the CPU oracle (a C restatement of ggml's CPU semantics, not ggml) on this host: one clip,
-                patch embedding + 1 and 2 blocks timed, extrapolated to 24 blocks.
+  configs       the other benchmark configurations measured by default: LeJEPA ViT-S/16 224^2 f16 (1 image,
+                CLS + learned positions) and V-JEPA 2.1 ViT-B/16 384^2 q8_0 (8 images per call, image path).
+  cpu_baseline  the CPU oracle (a C restatement of ggml's CPU semantics, not ggml) on this host's cores:
+                the whole 24-block clip, 1 warmup + 3 measured runs, mean (the reference's CPU protocol,
+                docs/benchmarks.md:41-53), with the host CPU model and core counts from lscpu.
 """
 import argparse
 import json
@@ -154,23 +157,45 @@ def time_extra(name, steps):
     return None
 
 
+def host_cpu():
+    """Model name, sockets and physical cores of this host (lscpu), for the CPU baseline's record."""
+    import subprocess
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {k.strip(): v.strip() for k, v in (ln.split(":", 1) for ln in out.splitlines() if ":" in ln)}
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        per = int(kv.get("Core(s) per socket", "0") or 0)
+        info = {"model": kv.get("Model name", ""), "sockets": sockets, "physical_cores": sockets * per,
+                "logical_cpus": int(kv.get("CPU(s)", "0") or 0)}
+    except Exception as e:          # lscpu missing: report what Python knows
+        info = {"model": "", "error": str(e)}
+    info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    return info
+
+
 def cpu_baseline(path, x_host):
-    """The oracle on the host cores: patch embedding + 1 block and + 2 blocks of one clip."""
+    """The oracle on the host cores, the reference's CPU protocol: one ViT-L/16 16f q8_0 clip through all
+    24 blocks, 1 warmup + 3 measured runs, mean. The thread count is the CPU share this process is given
+    ($OMP_NUM_THREADS, capped by its affinity), not the whole host."""
     from oracle import oracle as O
-    threads = int(os.environ.get("ORACLE_THREADS", min(16, os.cpu_count() or 1)))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    threads = int(os.environ.get("ORACLE_THREADS", min(share, len(os.sched_getaffinity(0)))))
     os.environ["ORACLE_THREADS"] = str(threads)
     O.build()
-    rows = N_TOK
-    t = {}
-    for nl in (1, 2):
+    runs = []
+    for i in range(4):
         t0 = time.perf_counter()
-        O.encode(path, x_host, 1, rows, D, n_layers=nl)
-        t[nl] = time.perf_counter() - t0
-    per_block = max(t[2] - t[1], 1e-9)
-    clip_s = t[1] + (L - 1) * per_block
-    return {"value": 1.0 / clip_s, "unit": "clips/s", "cores": threads, "kind": "port",
-            "sample": f"oracle (C restatement of ggml CPU semantics, OpenMP {threads} threads) on one ViT-L/16 16f q8_0 clip: "
-                      f"patch embed + 1 block = {t[1]:.2f} s, + 2 blocks = {t[2]:.2f} s, extrapolated to 24 blocks = {clip_s:.1f} s/clip"}
+        O.encode(path, x_host, 1, N_TOK, D)
+        runs.append(time.perf_counter() - t0)
+        log(f"bench: CPU baseline run {i} ({'warmup' if i == 0 else 'measured'}): {runs[-1]:.2f} s")
+    mean_s = sum(runs[1:]) / 3
+    return {"value": round(1.0 / mean_s, 5), "unit": "clips/s", "cores": threads, "kind": "port",
+            "ms_per_clip": round(mean_s * 1e3, 1), "runs_s": [round(t, 3) for t in runs], "host": host_cpu(),
+            "sample": f"oracle (C restatement of ggml's CPU semantics, not ggml; OpenMP, {threads} threads) on one whole "
+                      f"ViT-L/16 16f q8_0 clip (2048 tokens, 24 blocks): 1 warmup + 3 measured, mean {mean_s:.2f} s/clip",
+            "published_reference": "jepa-bench (ggml CPU) 794.1 ms/clip = 1.26 clips/s on a 96-core Threadripper PRO 7995WX at "
+                                   "32 threads (reference docs/benchmarks.md:103)"}
 
 
 def main():
@@ -180,9 +205,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-q4k", action="store_true", help="skip the q4_K line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--configs", default="",
-                    help="also time these encoder configurations (comma list: vits16_f16, vitb16_2_1_q8_0, "
-                         "vitg16_q8_0, levjepa_vitl16_q8_0, vitl16_q8_0 = the headline model with 4 clips per call)")
+    ap.add_argument("--configs", default="vits16_f16,vitb16_2_1_q8_0",
+                    help="also time these encoder configurations (comma list; default: vits16_f16, vitb16_2_1_q8_0; also "
+                         "vitg16_q8_0, levjepa_vitl16_q8_0, vitl16_q8_0 = the headline model with 4 clips per call; '' for none)")
     ap.add_argument("--extras", default="",
                     help="also time the rows next to the encoder (comma list: head = ViT-L SSv2 attentive-pool head on "
                          "2048 tokens; predictor = ViT-L masked predictor, 1024 context + 1024 target rows; quantizer = "

@@ -198,8 +198,7 @@ struct tiling {
     static constexpr int ESZ = WF == W_Q32 ? 1 : 2;          // bytes per code
     static constexpr int KC = 128 / ESZ;                      // K-columns per stage
     static constexpr int TILE = ROWS * 128;
-    static constexpr int SCAL = WF == W_Q32 ? ROWS * 8 : 0;
-    static constexpr int STAGE = TILE + SCAL;
+    static constexpr int STAGE = TILE;
     static constexpr int X_DW = 0, X_MIN = BN * 4, X_DA = X_MIN + BN * 32, X_BS = X_DA + BM * 4;
     static constexpr int XSB = WF == W_Q4K ? X_BS + BM * 32 : 0;
     // q4_K: the super-block buffer of sb+1 is filled while stage 4 sb + 5 - NST is computed, which must
@@ -210,8 +209,8 @@ struct tiling {
     static constexpr int NST = NST_FIT < NST_MAX ? NST_FIT : NST_MAX;
     static constexpr int LDS = NST * STAGE + 2 * XSB;
     static constexpr int LOADS = ROWS / 8 / NW;    // 1 KB tile loads per wave per stage
-    static constexpr int SL = WF == W_Q32 ? (ROWS / 32 + NW - 1) / NW : 0;   // scale copies per wave per stage
-    static constexpr int PARTS = LOADS + SL;       // copies per wave per stage (q4_K adds its own)
+    static constexpr int PARTS = LOADS;            // copies per wave per stage (q4_K adds its own)
+    static constexpr int SLD = WF == W_Q32 ? TI + TJ : 0;   // q8_0 / q4_0 scale loads per wave per stage
     static_assert(NST >= 2, "LDS too small for two stages");
     static_assert(BN % (8 * NW) == 0 && BN % 64 == 0 && BM % 64 == 0 && ROWS % (8 * NW) == 0, "load split");
     static_assert((NST - 2) * PARTS < 64, "vmcnt range");
@@ -304,28 +303,13 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         if (i < BN / (8 * NW)) dma_to_lds<16>(rA, (uint32_t) r * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
         else dma_to_lds<16>(rB, tok_row(r - BN) * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
     };
-    // q8_0 / q4_0 copy p (0 <= p < SL) of stage st: the four f16 block scales of 32 rows, two per lane
-    // (blocks past K, in a final half stage, repeat the stage's first pair). Every wave issues SL
-    // copies, so that the stage barrier can count them; a wave without a row group of its own repeats
-    // another wave's copy (the same bytes to the same place).
-    [[maybe_unused]] auto issue_scales = [&](int64_t st, int64_t sa, int p) {
-        unsigned char * base = smem + (int) (st % NST) * T::STAGE;
-        const uint32_t kb0 = (uint32_t) (((sa + kst0) * KC) >> 5);
-        const uint32_t kbo = (kb0 + 2 < KB) ? 2 * (lane & 1) : 0;
-        int L = wave + NW * p;
-        if (L >= T::ROWS / 32) L = wave % (T::ROWS / 32);
-        const int r = 32 * L + (lane >> 1);
-        if (32 * L < BN) dma_to_lds<4>(rAd, ((uint32_t) r * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
-        else dma_to_lds<4>(rBd, (tok_row(r - BN) * (uint32_t) KB + kbo) * 2, kb0 * 2, base + T::TILE + 256 * L);
-    };
     // q8_0 / q4_0 stages issue their PARTS copies one per compute step of the stage NST - 1 earlier
     // (spread, so that no wave stalls behind a burst of copies). Stages past the end copy the last
     // stage's data again into the buffer of the stage just finished, which no one reads any more:
     // the copies stay unconditional (a branch around them would split the software pipeline).
     [[maybe_unused]] auto issue_part = [&](int64_t st, int p) {
         const int64_t sa = st < nst ? st : nst - 1;
-        if (p < T::LOADS) issue_tile(st, sa, p);
-        else issue_scales(st, sa, p - T::LOADS);
+        issue_tile(st, sa, p);
     };
     // q4_K super-block data of super-block st / 4, copied with stage st when st % 4 == 0
     auto issue_xsb = [&](int64_t st) {
@@ -390,14 +374,32 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     //  - the barrier that publishes stage st+1 sits two steps before the end of stage st, after the
     //    wave's last LDS read of stage st, so the first reads of stage st+1 overlap the last steps;
     //  - each step issues one of the HBM->LDS copies of stage st + NST - 1 (spread, not a burst).
+    // Scale operands: a lane needs 8 bytes per stage, the four f16 block scales of its weight row and
+    // of its token row. They are not staged through LDS: bounds-checked buffer loads bring them into
+    // registers two stages ahead (the compiler cannot prove an LDS read unrelated to a pending LDS copy
+    // and waits for the youngest copy before it; a scale read at each stage's publication drained the
+    // whole copy pipeline). In a final half stage the loads read past the stage's two blocks into the
+    // next row, or as zero past the buffer; those words are never used.
     const uint32_t msk_lo = g == 0 ? 0x0000ffffu : 0u, msk_hi = g == 0 ? 0xffff0000u : 0u;
-    auto q32_scales = [&](const unsigned char * base, h4 (&sa)[TI], h4 (&sb)[4][TJ]) {
-        const unsigned char * scl = base + T::TILE;      // 8 B per row: f16 d of the stage's 4 blocks
+    typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+    [[maybe_unused]] auto load_scales = [&](int64_t st, u2v (&ra)[TI], u2v (&rb)[TJ]) {
+        const int64_t sa = st < nst ? st : nst - 1;
+        const uint32_t kb0 = (uint32_t) (((sa + kst0) * KC) >> 5);
 #pragma unroll
-        for (int i = 0; i < TI; i++) sa[i] = *(const h4 *) (scl + 8 * (32 * (wn * TI + i) + l32));
+        for (int i = 0; i < TI; i++)
+            ra[i] = __builtin_amdgcn_raw_buffer_load_b64(rAd, ((uint32_t) (32 * (wn * TI + i) + l32) * (uint32_t) KB + kb0) * 2, 0, 0);
+#pragma unroll
+        for (int j = 0; j < TJ; j++)
+            rb[j] = __builtin_amdgcn_raw_buffer_load_b64(rBd, (tok_row(32 * (wm * TJ + j) + l32) * (uint32_t) KB + kb0) * 2, 0, 0);
+    };
+    // the weight row's four block scales fill K-slots 0-3 (both lane groups); the token's scale of
+    // block blk alone fills K-slot blk of lane group 0 (group 1 is zero)
+    auto q32_scales = [&](const u2v (&ra)[TI], const u2v (&rb)[TJ], h4 (&sa)[TI], h4 (&sb)[4][TJ]) {
+#pragma unroll
+        for (int i = 0; i < TI; i++) sa[i] = __builtin_bit_cast(h4, ra[i]);
 #pragma unroll
         for (int j = 0; j < TJ; j++) {
-            const uint2 w = *(const uint2 *) (scl + 8 * (BN + 32 * (wm * TJ + j) + l32));
+            const uint2 w = make_uint2(rb[j].x, rb[j].y);
 #pragma unroll
             for (int blk = 0; blk < 4; blk++) {
                 const uint32_t msk = (blk & 1) ? msk_hi : msk_lo;
@@ -418,17 +420,25 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         constexpr int P1 = T::PARTS;
         // copies issued after the last copy of stage st+1 when stage st publishes it (step U-2, after
         // that step's copies): the NST-3 stages after it, and this body's copies so far
-        constexpr int NBAR = (NST - 3) * P1 + (U - 1) * P1 / U;
+        // Every body first issues its SLD scale loads (two stages ahead), then its copies. At the
+        // publication of stage st+1, the loads issued after stage st+1's last copy are at least the
+        // NST-3 bodies' copies in between, this body's scale loads and its copies up to step U-2
+        // (exactly that for st = 1; later bodies add older scale loads, which only tightens the wait).
+        constexpr int NBAR = (NST - 3) * P1 + T::SLD + (U - 1) * P1 / U;
         i4v A[4][TI], B[4][TJ];
         h4 SA[TI], SB[4][TJ];
+        u2v RS0A[TI], RS0B[TJ], RS1A[TI], RS1B[TJ];   // raw scales: stage st+2 (being loaded), st+1
         i16v S[2];
         f16v C[2];
-        // The int8 MFMA starts from 0x4B400000, the bits of 1.5 * 2^23: the int32 result M + S, read as
-        // a float, is exactly 12582912 + S for |S| < 2^22 (|S| <= 32 * 128 * 128 here), so one f32
-        // subtraction (a full-rate VALU op) gives float(S) exactly where v_cvt_f32_i32 runs at half rate.
+        // Tiles of at most two MFMA tiles per wave start the int8 MFMA from 0x4B400000, the bits of
+        // 1.5 * 2^23: the int32 result M + S, read as a float, is exactly 12582912 + S for |S| < 2^22
+        // (|S| <= 32 * 128 * 128 here), so one f32 subtraction gives float(S) exactly (measured ~7 %
+        // faster than v_cvt_f32_i32). Larger wave tiles cannot spare the 16 VGPRs the constant takes
+        // as an MFMA operand and convert with v_cvt_f32_i32.
+        constexpr bool MAGIC = TI * TJ <= 2;
         i16v magic;
 #pragma unroll
-        for (int r = 0; r < 16; r++) magic[r] = 0x4B400000;
+        for (int r = 0; r < 16; r++) magic[r] = MAGIC ? 0x4B400000 : 0;
         float neg_magic;   // in a VGPR: a VALU op with an SGPR operand issues at half rate here
         asm("v_mov_b32 %0, 0xcb400000" : "=v"(neg_magic));
         auto ld_step = [&](const unsigned char * base, int u) {
@@ -438,14 +448,15 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         };
         auto mma = [&](int u, const h4 (&sa)[TI], const h4 (&sb)[4][TJ]) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], magic);
+            if constexpr (MAGIC) S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], magic);
+            else S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], i16v{});
             C[u & 1] = MFMA8(sa[i], sb[blk][j], zero);
         };
         auto valu = [&](int u) {
             const int t = u % TT, i = t / TJ, j = t % TJ;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float sf = __fadd_rn(__int_as_float(S[u & 1][r]), neg_magic);
+                const float sf = MAGIC ? __fadd_rn(__int_as_float(S[u & 1][r]), neg_magic) : (float) S[u & 1][r];
                 acc[i][j][r] = fmaf(sf, C[u & 1][r], acc[i][j][r]);
             }
         };
@@ -453,10 +464,12 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         // behind NST-1 stages of copies before any compute); stages 1..NST-1 follow spread over the
         // steps of stage 0. Copies are unconditional, so that every barrier count is exact: stages
         // past the end copy the last stage again into buffers no stage uses.
+        load_scales(0, RS0A, RS0B);
+        load_scales(1, RS1A, RS1B);
 #pragma unroll
         for (int p = 0; p < T::PARTS; p++) issue_part(0, p);
         stage_barrier<0>();
-        q32_scales(smem, SA, SB);
+        q32_scales(RS0A, RS0B, SA, SB);
         ld_step(smem, 0);
         ld_step(smem, 1);
         mma(0, SA, SB);
@@ -472,6 +485,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
             const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
             h4 SAn[TI], SBn[4][TJ];
+            if constexpr (CROSS) load_scales(st + 2, RS0A, RS0B);
 #pragma unroll
             for (int u = 0; u < U; u++) {
 #pragma unroll
@@ -483,7 +497,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 if constexpr (CROSS) {
                     if (u == U - 2) {
                         stage_barrier<NB>();
-                        q32_scales(nbase, SAn, SBn);
+                        q32_scales(RS1A, RS1B, SAn, SBn);
                         ld_step(nbase, 0);
                     }
                     if (u == U - 1) ld_step(nbase, 1);
@@ -495,7 +509,9 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             }
             if constexpr (CROSS) {
 #pragma unroll
-                for (int i = 0; i < TI; i++) SA[i] = SAn[i];
+                for (int i = 0; i < TI; i++) { SA[i] = SAn[i]; RS1A[i] = RS0A[i]; }
+#pragma unroll
+                for (int j = 0; j < TJ; j++) RS1B[j] = RS0B[j];
 #pragma unroll
                 for (int blk = 0; blk < 4; blk++)
 #pragma unroll
@@ -511,7 +527,9 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         if (nfull < nst) {
             stage_barrier<0>();
             const unsigned char * base = smem + (int) (nfull % NST) * T::STAGE;
-            q32_scales(base, SA, SB);
+            // its scales: loaded into RS1 by the body that published the last full stage, or, with
+            // no full stage at all, by the prologue
+            q32_scales(RS1A, RS1B, SA, SB);
 #pragma unroll
             for (int u = 0; u < 2 * TT; u++) {
                 ld_step(base, u);

@@ -166,6 +166,25 @@ class Model:
         r = lib().jepa_model_label(self.ptr, i)
         return None if r is None else r.decode()
 
+    def _pool(self, fn, rows: np.ndarray) -> np.ndarray:
+        L = lib()
+        rows = np.ascontiguousarray(rows, dtype=np.float32)
+        enc = Output(C.cast(rows.ctypes.data, C.POINTER(C.c_float)), rows.shape[0], rows.shape[1])
+        out = Output()
+        L.jepa_error_reset()
+        check(fn(self.ptr, C.byref(enc), C.byref(out)), fn.__name__)
+        y = np.ctypeslib.as_array(out.data, shape=(out.dim,)).copy()
+        L.jepa_free(C.cast(out.data, C.c_void_p))
+        return y
+
+    def pool_mean(self, rows: np.ndarray) -> np.ndarray:
+        """jepa_pool_mean over one item's encoder rows [N, dim] (prefix rows left out)."""
+        return self._pool(lib().jepa_pool_mean, rows)
+
+    def pool_cls(self, rows: np.ndarray) -> np.ndarray:
+        """jepa_pool_cls: row 0 of one item's encoder rows (models with a CLS token)."""
+        return self._pool(lib().jepa_pool_cls, rows)
+
     def token_grid(self, n_frames, h, w) -> int:
         return int(lib().jepa_token_grid(self.ptr, n_frames, h, w, None, None, None))
 

@@ -117,6 +117,28 @@ def _block_type(cfg: EncoderConfig, n_in: int) -> int:
     return t
 
 
+def _device_q4_k():
+    """The library's own q4_K block quantizer on the GPU (jepa_amd_quantize_rows, byte-equal to the numpy
+    restatement), or None without a GPU. The numpy make_qkx2 search takes minutes on a ViT-L."""
+    try:
+        import torch
+        if not torch.cuda.is_available():
+            return None
+        from . import _lib
+        L = _lib.lib()
+    except Exception:
+        return None
+
+    def q(x: np.ndarray) -> np.ndarray:
+        xd = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32).reshape(-1)).cuda()
+        out = torch.empty(xd.numel() // 256 * 144, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        if L.jepa_amd_quantize_rows(0, GGML_Q4_K, xd.data_ptr(), xd.numel(), out.data_ptr()) != 0:
+            raise RuntimeError("jepa_amd_quantize_rows failed: " + _lib.error_text())
+        return out.cpu().numpy()
+    return q
+
+
 def write_model(cfg: EncoderConfig, path: str) -> str:
     """Write the synthetic GGUF for `cfg` to `path` (returns path)."""
     rng = np.random.default_rng(cfg.seed)
@@ -184,9 +206,14 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
     def normal(*shape, std=0.02):
         return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
+    dev_q4k = _device_q4_k() if cfg.ftype == "q4_k" and cfg.embed_dim >= 512 else None
+
     def mat(name, n_out, n_in, gtype):
         x = normal(n_out, n_in, std=cfg.w_std)
-        w.add_tensor(name, gtype, (n_in, n_out), quantize(gtype, x))
+        if gtype == GGML_Q4_K and dev_q4k is not None:
+            w.add_tensor(name, gtype, (n_in, n_out), dev_q4k(x))
+        else:
+            w.add_tensor(name, gtype, (n_in, n_out), quantize(gtype, x))
 
     def vec(name, n, value=None, std=0.02):
         x = np.full(n, value, dtype=np.float32) if value is not None else normal(n, std=std)

@@ -657,9 +657,38 @@ void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, 
     }
 }
 
+static int g_round;   /* rounding switches, see or_set_rounding below */
+
+/* the GPU epilogue's erf for z >= 0 (OR_ROUND_GELU): z*P(z^2) below 0.875, 1 - 2^Q(min(z, 4)) above,
+ * both evaluated and one selected, with the same coefficients and float operations */
+static float gpu_erf_nonneg(float z) {
+    const float s = z * z;
+    float p = -6.065624184e-04f;
+    p = fmaf(p, s, 5.004569888e-03f);
+    p = fmaf(p, s, -2.677160688e-02f);
+    p = fmaf(p, s, 1.128184572e-01f);
+    p = fmaf(p, s, -3.761247694e-01f);
+    p = fmaf(p, s, 1.128379107e+00f);
+    const float small = z * p;
+    const float zc = fminf(z, 4.0f);
+    float q = 3.032335662e-04f;
+    q = fmaf(q, zc, -4.579299595e-03f);
+    q = fmaf(q, zc, 3.277245909e-02f);
+    q = fmaf(q, zc, -1.513156891e-01f);
+    q = fmaf(q, zc, -9.177885652e-01f);
+    q = fmaf(q, zc, -1.627714038e+00f);
+    q = fmaf(q, zc, -9.482709720e-05f);
+    const float large = 1.0f - exp2f(q);
+    return z < 0.875f ? small : large;
+}
+
 /* ggml_vec_gelu_erf_f32 (docs/ggml-notes.md:291-292): 0.5*x*(1+erf(x/sqrt(2))) with libm erff */
 float or_gelu_erf(float x) {
     const float SQRT_2_INV = 0.70710678118654752440084436210484f;
+    if (g_round & 8) {
+        const float e = copysignf(gpu_erf_nonneg(fabsf(x) * SQRT_2_INV), x);
+        return (0.5f * x) * (1.0f + e);
+    }
     return 0.5f * x * (1.0f + erff(x * SQRT_2_INV));
 }
 
@@ -741,10 +770,21 @@ void or_block_causal_mask(int gt, int gh, int gw, int n_prefix, float * out) {
         }
 }
 
-/* 1: with f16 K/V, also round q and the softmax weights p to f16 before their products (what an f16
- * matrix-core attention does: ggml's CUDA kernels, its CPU per-row path for q, the GPU kernel here) */
-static int g_attn_f16 = 0;
-void or_set_attn_f16(int on) { g_attn_f16 = on; }
+/* Rounding switches: the oracle follows the reference's CPU arithmetic (tiled flash-attention path:
+ * q, scores, softmax and accumulator in f32, K/V rounded to f16; libm erff in GELU) unless a bit of
+ * g_round asks it to take one of the GPU kernels' roundings instead, so that the distance each one
+ * adds can be measured on its own:
+ *   OR_ROUND_Q16  (1): with f16 K/V, q is rounded to f16 before Q.K^T (the f16 matrix-core attention,
+ *                      and ggml's own per-row CPU path and CUDA kernels)
+ *   OR_ROUND_P16  (2): with f16 K/V, the softmax weights are rounded to f16 before P.V (the sum of the
+ *                      weights stays f32, as in the GPU kernel)
+ *   OR_ROUND_EXP2 (4): weights as 2^(s*c - m*c) with c = scale*log2(e) in float, s the raw dot and m
+ *                      the largest raw dot (the GPU kernel's exp2 form), instead of e^(s*scale - max)
+ *   OR_ROUND_GELU (8): erf from the GPU epilogue's branch-free polynomial pair instead of libm erff */
+static int g_round = 0;
+void or_set_rounding(int bits) { g_round = bits; }
+int or_get_rounding(void) { return g_round; }
+void or_set_attn_f16(int on) { g_round = on ? (g_round | 3) : (g_round & ~3); }
 
 void or_attention(const float * q, const float * k, const float * v, int64_t n_q, int64_t n_kv,
                   int n_head, int hd, float scale, int kv_f16, const float * mask, float * out, int n_threads) {
@@ -766,13 +806,16 @@ void or_attention(const float * q, const float * k, const float * v, int64_t n_q
             for (int64_t i = 0; i < n_q; i++) {
                 const float * qi = q + i * row + h * hd;
                 float q16[1024];
-                if (g_attn_f16 && kv_f16) {
+                if ((g_round & 1) && kv_f16) {
                     for (int d = 0; d < hd; d++) q16[d] = or_fp16_to_fp32(or_fp32_to_fp16(qi[d]));
                     qi = q16;
                 }
+                const int exp2_form = (g_round & 4) != 0;
+                const float c2 = scale * 1.4426950408889634f;
                 float mx = -INFINITY;
                 for (int64_t j = 0; j < n_kv; j++) {
-                    sc[j] = dot_f32_8acc(qi, kh + j * hd, hd) * scale;
+                    const float dot = dot_f32_8acc(qi, kh + j * hd, hd);
+                    sc[j] = exp2_form ? dot : dot * scale;
                     if (mask) sc[j] = sc[j] + mask[i * n_kv + j];
                     if (sc[j] > mx) mx = sc[j];
                 }
@@ -782,10 +825,11 @@ void or_attention(const float * q, const float * k, const float * v, int64_t n_q
                     for (int d = 0; d < hd; d++) out[i * row + h * hd + d] = 0.0f;
                     continue;
                 }
+                const float mc = mx * c2;
                 for (int64_t j = 0; j < n_kv; j++) {
-                    const float p = expf(sc[j] - mx);
+                    const float p = exp2_form ? exp2f(fmaf(sc[j], c2, -mc)) : expf(sc[j] - mx);
                     sum += p;
-                    const float pv = (g_attn_f16 && kv_f16) ? or_fp16_to_fp32(or_fp32_to_fp16(p)) : p;
+                    const float pv = ((g_round & 2) && kv_f16) ? or_fp16_to_fp32(or_fp32_to_fp16(p)) : p;
                     const float * vj = vh + j * hd;
                     for (int d = 0; d < hd; d++) acc[d] = fmaf(pv, vj[d], acc[d]);
                 }
@@ -991,6 +1035,14 @@ out:
     return rc;
 }
 
+/* Teacher forcing: when set, block l of item i starts from the residual stream the caller supplies
+ * (teacher [n_items][n_layers + 1][R][D], entry l = the input of block l, e.g. a GPU trace) instead of
+ * the oracle's own, so the trace's entry l + 1 is this oracle's block l applied to the caller's
+ * input: the error of each block alone, without what the earlier blocks passed on. */
+static const float * g_teacher = NULL;
+static int64_t g_teacher_n = 0;
+void or_set_teacher(const float * trace, int64_t n_floats) { g_teacher = trace; g_teacher_n = trace ? n_floats : 0; }
+
 int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_chans, int n_frames,
                        int height, int width, float * out, int64_t out_cap, float * trace, int64_t trace_cap,
                        int n_layers_limit, int n_threads) {
@@ -1099,6 +1151,11 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
         for (int l = 0; l < n_layers; l++) {
             char pre[64];
             snprintf(pre, sizeof(pre), "enc.blk.%d.", l);
+            if (g_teacher) {
+                const int64_t off = (((int64_t) it * (n_layers + 1)) + l) * R * D;
+                if (off + R * D > g_teacher_n) { fprintf(stderr, "oracle: teacher trace too small\n"); goto done; }
+                memcpy(x, g_teacher + off, sizeof(float) * R * D);
+            }
             if (block_fwd(&f, pre, x, R, D, H, video ? rope_c : NULL, rope_s, mask, kv_f16, eps, n_threads)) goto done;
             if (trace) memcpy(trace + (((int64_t) it * (n_layers + 1)) + l + 1) * R * D, x, sizeof(float) * R * D);
         }

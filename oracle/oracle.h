@@ -62,6 +62,11 @@ void or_set_reverse_block_order(int on);
 void or_set_k_split(int s);
 /* 1: with f16 K/V, round q and the softmax weights to f16 too (an f16 matrix-core attention) */
 void or_set_attn_f16(int on);
+/* rounding switches (bits: 1 f16 q, 2 f16 softmax weights, 4 exp2 form, 8 GPU erf polynomial) */
+void or_set_rounding(int bits);
+int  or_get_rounding(void);
+/* teacher forcing of the encoder: block l starts from trace entry l (NULL: off) */
+void or_set_teacher(const float * trace, int64_t n_floats);
 
 void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, const float * b,
                    float eps, float * y);

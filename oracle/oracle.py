@@ -74,6 +74,12 @@ def lib() -> C.CDLL:
         L.or_set_k_split.restype = None
         L.or_set_attn_f16.argtypes = [C.c_int]
         L.or_set_attn_f16.restype = None
+        L.or_set_rounding.argtypes = [C.c_int]
+        L.or_set_rounding.restype = None
+        L.or_get_rounding.argtypes = []
+        L.or_get_rounding.restype = C.c_int
+        L.or_set_teacher.argtypes = [C.c_void_p, C.c_int64]
+        L.or_set_teacher.restype = None
         _lib = L
     return _lib
 
@@ -289,3 +295,30 @@ def set_k_split(s: int) -> None:
 def set_attn_f16(on: bool) -> None:
     """Round q and the softmax weights to f16 in attentions with f16 K/V (an f16 matrix-core kernel)."""
     lib().or_set_attn_f16(1 if on else 0)
+
+
+# rounding switches (oracle.c): the GPU kernels' roundings, one bit each
+ROUND_Q16, ROUND_P16, ROUND_EXP2, ROUND_GELU = 1, 2, 4, 8
+ROUND_GPU = ROUND_Q16 | ROUND_P16 | ROUND_EXP2 | ROUND_GELU
+
+
+def set_rounding(bits: int) -> None:
+    """Take the GPU's rounding for the sources in `bits` (0: the reference's CPU arithmetic)."""
+    lib().or_set_rounding(int(bits))
+
+
+def get_rounding() -> int:
+    return int(lib().or_get_rounding())
+
+
+def encode_teacher(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, teacher: np.ndarray):
+    """Oracle forward in which block l starts from teacher[:, l] (teacher [n_items][L + 1][rows][dim],
+    e.g. the GPU's residual-stream trace): returns the oracle's trace, whose entry l + 1 is the
+    oracle's block l applied to the teacher's entry l (entry 0 is the oracle's own patch embedding)."""
+    t = np.ascontiguousarray(teacher, dtype=np.float32)
+    n_layers = t.shape[1] - 1
+    lib().or_set_teacher(_p(t), t.size)
+    try:
+        return _encode(path, np.ascontiguousarray(x, dtype=np.float32), rows, dim, n_layers, True, n_items)
+    finally:
+        lib().or_set_teacher(None, 0)

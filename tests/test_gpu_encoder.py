@@ -1,13 +1,9 @@
 """Encoder forward on the GPU (through the C ABI: jepa_model_load_ex / jepa_encode) against the CPU
 oracle's ggml-semantics restatement on the same synthetic GGUF and the same seeded inputs.
 
-Gates: per-token cosine >= 0.9999 (mean) and max relative error <= 1e-2 per layer on the residual
-stream. Quantized models have a floor under both numbers that no implementation can beat: a q8_0 /
-q8_K activation code flips when an input moves across a rounding boundary, and 24 layers amplify a
-last-bit difference into a visible one. The floor is measured live: the oracle against itself with
-the per-block float sums of its quantized dots taken in the opposite K order (ggml's own SIMD builds
-differ in exactly this). For quantized models the GPU must be within 1.5x of that floor, and inside
-the fixed gates wherever the floor itself is inside them.
+Gates: per-token cosine >= 0.9999 (mean) and max relative error <= 1e-2 on the residual stream after
+every layer. The full-size quantized benchmark models are in test_gpu_parity.py (teacher-forced per
+layer as well as end to end).
 """
 import numpy as np
 import pytest
@@ -26,25 +22,10 @@ def rel_max(a, b):
     return float(np.abs(a.astype(np.float64) - b).max() / np.abs(b).max())
 
 
-def _floor(oracle, path, x, n_items, rows, dim, n_layer, want, wtr):
-    """(cosine mean, per-layer rel_max) between two valid summation orders of the oracle"""
-    oracle.set_reverse_block_order(True)
-    try:
-        alt, atr = oracle.encode(path, x, n_items, rows, dim, n_layers=n_layer, trace=True)
-    finally:
-        oracle.set_reverse_block_order(False)
-    return cos_rows(alt, want).mean(), max(rel_max(atr[:, l], wtr[:, l]) for l in range(atr.shape[1]))
-
-
-def check_parity(got, want, gtr, wtr, floor=None, label=""):
+def check_parity(got, want, gtr, wtr, label=""):
     c = cos_rows(got, want)
     rl = [rel_max(gtr[:, l], wtr[:, l]) for l in range(gtr.shape[1])]
     cos_gate, rel_gate = 0.9999, 1e-2
-    if floor is not None:
-        fcos, frel = floor
-        cos_gate = min(cos_gate, 1.0 - 1.5 * (1.0 - fcos))
-        rel_gate = max(rel_gate, 1.5 * frel)
-        print(f"{label}: floor cos {fcos:.7f} rel {frel:.3e} -> gates cos >= {cos_gate:.7f}, rel <= {rel_gate:.3e}")
     print(f"{label}: token cosine mean {c.mean():.7f} min {c.min():.6f}, per-layer rel_max max {max(rl):.3e} (layer {int(np.argmax(rl))})")
     assert c.mean() >= cos_gate, (c.mean(), c.min())
     assert max(rl) <= rel_gate, (max(rl), int(np.argmax(rl)))
@@ -112,37 +93,6 @@ def test_vits16_f16_full(jlib, oracle, models_dir):
     got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, forge.CONFIGS["vits16_f16"], 1, 1, 224)
     assert got.shape == (197, 384)
     check_parity(got, want, gtr, wtr, label="vits16_f16")
-
-
-def test_vitb16_2_1_image_q8_0(jlib, oracle, models_dir):
-    """V-JEPA 2.1 ViT-B/16 384x384 image path (576 tokens), two images in one call."""
-    cfg = forge.CONFIGS["vitb16_2_1_q8_0"]
-    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 2, 1, 384)
-    assert got.shape == (2 * 576, 768)
-    floor = _floor(oracle, forge.cached_model(cfg, models_dir), x, 2, 576, 768, m.n_layer, want, wtr)
-    check_parity(got, want, gtr, wtr, floor, label="vitb16_2_1_q8_0")
-
-
-@pytest.mark.parametrize("name", ["vitl16_q8_0", "vitl16_q4_k"])
-def test_vitl16_16f_full(jlib, oracle, models_dir, name):
-    """V-JEPA 2 ViT-L/16, 16 frames 256x256 = 2048 tokens, 24 layers: the benchmark configuration."""
-    cfg = forge.CONFIGS[name]
-    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 1, 16, 256)
-    assert got.shape == (2048, 1024)
-    floor = _floor(oracle, forge.cached_model(cfg, models_dir), x, 1, 2048, 1024, m.n_layer, want, wtr)
-    check_parity(got, want, gtr, wtr, floor, label=name)
-    if name == "vitl16_q8_0":
-        assert cos_rows(got, want).mean() >= 0.9999   # the 0.9999 cosine bar for q8_0 holds outright
-
-
-def test_levjepa_vitl16_16f_q8_0_full(jlib, oracle, models_dir):
-    """LeVJEPA ViT-L/16, 16 frames 224x224, tubelet 1: 16 x 196 patch rows + CLS = 3137 rows, block-causal
-    attention (53.1 % of the score matrix visible), 24 layers; CLS pooled."""
-    cfg = forge.CONFIGS["levjepa_vitl16_q8_0"]
-    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 1, 16, 224)
-    assert got.shape == (3137, 1024)
-    floor = _floor(oracle, forge.cached_model(cfg, models_dir), x, 1, 3137, 1024, m.n_layer, want, wtr)
-    check_parity(got, want, gtr, wtr, floor, label="levjepa_vitl16_q8_0")
 
 
 def test_vitg16_64f_q8_0_first_blocks(jlib, oracle, models_dir):
