@@ -95,6 +95,18 @@ int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64
 int jepa_amd_preprocess_frames_device(int device, const jepa_preprocess_params * p, const uint8_t * frames_dev, int n_frames, int h,
                                       int w, float * out_dev, int64_t out_cap, int * out_h, int * out_w);
 
+/* jepa_amd_preprocess_frames_device without any allocation: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The tap tables and the horizontal-pass image live in a static
+ * device array of 32 MiB that every GPU the library runs on holds until the process ends; a call
+ * whose scratch would exceed it (about n_frames * h * crop * 3 bytes plus the tables) is refused
+ * with -1 and a message. Work is queued on `stream` (a hipStream_t of `device`; NULL: the null
+ * stream) and the call returns after it finished, with the same output, bit for bit, as
+ * jepa_amd_preprocess_frames_device. Calls on one GPU share that array: calls that overlap on one
+ * GPU (from several threads or streams) race and must be serialised by the caller. */
+int jepa_amd_preprocess_frames_device_noalloc(int device, const jepa_preprocess_params * p, const uint8_t * frames_dev, int n_frames,
+                                              int h, int w, float * out_dev, int64_t out_cap, int * out_h, int * out_w, void * stream);
+
 /* Split-K of the q8_0 / q4_0 GEMMs (two workgroups per output tile, one per K half, the second to
  * finish adding the first's partial sums): jepa_amd_gemm_split forces it off (1), on where the shape
  * allows (2) or back to the automatic choice (-1) for later launches; jepa_amd_gemm_split_of returns

@@ -389,6 +389,47 @@ extern "C" int jepa_amd_preprocess_frames_device(int device, const jepa_preproce
     return d.finish();
 }
 
+extern "C" int jepa_amd_preprocess_frames_device_noalloc(int device, const jepa_preprocess_params * p, const uint8_t * frames, int n_frames,
+                                                         int h, int w, float * out, int64_t out_cap, int * out_h, int * out_w, void * stream) {
+    if (!p || !frames || !out || n_frames <= 0 || h <= 0 || w <= 0) return -1;
+    pre_plan g;
+    if (!pre_plan_for(p, h, w, g)) return -1;
+    const int64_t need = (int64_t) 3 * n_frames * g.crop * g.crop;
+    if (out_cap < need) {
+        jepa_log("jepa: jepa_amd_preprocess_frames_device_noalloc: output holds %lld floats, %lld needed\n", (long long) out_cap,
+                 (long long) need);
+        return -1;
+    }
+    const size_t bytes = preprocess_scratch_bytes(p, g, n_frames, h, w);
+    if (bytes > PRE_NOALLOC_SCRATCH_BYTES) {
+        jepa_log("jepa: jepa_amd_preprocess_frames_device_noalloc: %d frames of %dx%d need %.1f MiB of scratch, over the %zu MiB "
+                 "this entry point has (use jepa_amd_preprocess_frames_device, or fewer frames per call)\n",
+                 n_frames, h, w, (double) bytes / 1048576.0, PRE_NOALLOC_SCRATCH_BYTES >> 20);
+        return -1;
+    }
+    if (!dev_check(device)) return -1;
+    int prev = 0;
+    hipGetDevice(&prev);
+    if (hipSetDevice(device) != hipSuccess) {
+        jepa_log("jepa: cannot use HIP device %d\n", device);
+        return -1;
+    }
+    int rc = -1;
+    void * scratch = preprocess_static_scratch(device);
+    if (scratch) {
+        hipStream_t s = (hipStream_t) stream;
+        if (!launch_preprocess(p, g, frames, n_frames, h, w, out, scratch, s)) {
+            jepa_log("jepa: jepa_amd_preprocess_frames_device_noalloc: launch failed: %s\n", hipGetErrorString(hipGetLastError()));
+        } else {
+            if (out_h) *out_h = g.crop;
+            if (out_w) *out_w = g.crop;
+            rc = 0;
+        }
+    }
+    hipSetDevice(prev);
+    return rc;
+}
+
 extern "C" int jepa_amd_rope_tables(int head_dim, int grid_t, int grid_h, int grid_w, int variant, int interpolate, int train_h,
                                     int train_w, float theta, const int32_t * ids, int64_t n_rows, int signed_sin, float * cos_out,
                                     float * sin_out) {

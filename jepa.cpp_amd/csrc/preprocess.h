@@ -47,3 +47,9 @@ inline float pre_normalize(const pre_plan & g, int c, uint8_t v) { return pre_no
 size_t preprocess_scratch_bytes(const jepa_preprocess_params * p, const pre_plan & g, int n_frames, int h, int w);
 bool launch_preprocess(const jepa_preprocess_params * p, const pre_plan & g, const uint8_t * frames, int n_frames, int h, int w,
                        float * out, void * scratch, hipStream_t s);
+
+// The allocation-free variant's scratch: a static device array of this size on every GPU the library
+// runs on (tap tables + the horizontal-pass image of all frames), and its device address on
+// `device` (looked up once per device with that device current; nullptr on failure).
+#define PRE_NOALLOC_SCRATCH_BYTES ((size_t) 32 << 20)
+void * preprocess_static_scratch(int device);

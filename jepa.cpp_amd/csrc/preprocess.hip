@@ -7,8 +7,10 @@
 // host rounds to uint8 between the passes too); the vertical pass computes the crop's pixels, applies
 // the zero padding of an undersized image and writes the normalised floats in NCTHW order.
 #include "preprocess.h"
+#include "common.h"
 
 #include <cstring>
+#include <mutex>
 
 namespace {
 
@@ -147,4 +149,34 @@ bool launch_preprocess(const jepa_preprocess_params * p, const pre_plan & g, con
     k_resize_cols_norm<<<(unsigned) ((n2 + 255) / 256), 256, 0, s>>>(mid, out, n_frames, h, g.crop, g.oy, g.ox, g.rh, g.rw, dv, np);
     // the blob must outlive the copy: wait for it here (pageable source)
     return hipStreamSynchronize(s) == hipSuccess;
+}
+
+// ---------------------------------------------------------------------------------------------------
+// The same preprocessing without any allocation: the tables and the horizontal-pass image live in a
+// file-scope device array. A host reference to `scratch` names a host-side stand-in, not device
+// memory; the device address of each GPU's copy comes from hipGetSymbolAddress with that GPU
+// current, and only that address is handed to copies and kernels.
+// ---------------------------------------------------------------------------------------------------
+namespace {
+__device__ __align__(256) unsigned char scratch[PRE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void * g_scratch_ptr[MAX_DEVICES] = {};
+}  // namespace
+
+void * preprocess_static_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void * ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            jepa_log("jepa: hipGetSymbolAddress(scratch) failed on device %d: %s\n", device, hipGetErrorString(e));
+            (void) hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[device] = ptr;
+    }
+    return g_scratch_ptr[device];
 }

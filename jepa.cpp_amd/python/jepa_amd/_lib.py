@@ -91,6 +91,8 @@ def lib() -> C.CDLL:
         "jepa_resize_antialias_u8": (None, [vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, C.c_int, C.c_int]),
         "jepa_amd_preprocess_frames_device": (C.c_int, [C.c_int, C.POINTER(PreprocessParams), vp, C.c_int, C.c_int, C.c_int, vp, i64,
                                                         C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        "jepa_amd_preprocess_frames_device_noalloc": (C.c_int, [C.c_int, C.POINTER(PreprocessParams), vp, C.c_int, C.c_int, C.c_int, vp,
+                                                                i64, C.POINTER(C.c_int), C.POINTER(C.c_int), vp]),
         "jepa_pool_mean": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
         "jepa_pool_cls": (C.c_int, [vp, C.POINTER(Output), C.POINTER(Output)]),
         "jepa_softmax": (None, [vp, C.c_int, vp]),
