@@ -27,6 +27,7 @@ struct dev_scope {
         ok = true;
     }
     void * alloc(size_t bytes) {
+        std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
         void * p = nullptr;
         if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) { jepa_log("jepa: hipMalloc(%zu) failed\n", bytes); return nullptr; }
         allocs.push_back(p);
@@ -43,6 +44,7 @@ struct dev_scope {
     }
     ~dev_scope() {
         if (s) hipStreamSynchronize(s);
+        std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
         for (void * p : allocs) hipFree(p);
         if (s) hipStreamDestroy(s);
         hipSetDevice(prev);
@@ -97,14 +99,15 @@ extern "C" int64_t jepa_amd_encode_trace(jepa_context * ctx, const jepa_input * 
     float * dout = (float *) d.alloc((size_t) n_items * R * D * 4);
     float * dtr = (float *) d.alloc((size_t) n_items * (L + 1) * R * D * 4);
     if (!din || !dout || !dtr) return -1;
-    if (hipMemcpy(din, in->data, n_in * 4, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    if (hipMemcpyAsync(din, in->data, n_in * 4, hipMemcpyHostToDevice, d.s) != hipSuccess || hipStreamSynchronize(d.s) != hipSuccess) return -1;
     const int64_t r = encode_device(ctx, din, in->n_batch, in->n_chans, in->n_frames, in->height, in->width, dout, n_items * R * D, dtr,
                                     n_items * (L + 1) * R * D);
     if (r < 0) return -1;
     // device trace is [layer][all rows]; the caller wants [item][layer][rows]
     std::vector<float> tmp((size_t) (L + 1) * n_items * R * D);
-    if (hipMemcpy(tmp.data(), dtr, tmp.size() * 4, hipMemcpyDeviceToHost) != hipSuccess ||
-        hipMemcpy(out, dout, (size_t) n_items * R * D * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    if (hipMemcpyAsync(tmp.data(), dtr, tmp.size() * 4, hipMemcpyDeviceToHost, d.s) != hipSuccess ||
+        hipMemcpyAsync(out, dout, (size_t) n_items * R * D * 4, hipMemcpyDeviceToHost, d.s) != hipSuccess ||
+        hipStreamSynchronize(d.s) != hipSuccess)
         return -1;
     for (int64_t it = 0; it < n_items; it++)
         for (int64_t l = 0; l <= L; l++)

@@ -65,6 +65,11 @@ void jepa_log(const char * fmt, ...) {
     t_capture.add(msg, (size_t) n);
 }
 
+std::recursive_mutex & jepa_hip_mutex() {
+    static std::recursive_mutex mu;
+    return mu;
+}
+
 extern "C" void jepa_error_reset(void) { t_capture.clear(); }
 extern "C" const char * jepa_error_text(void) { return t_capture.text; }
 extern "C" const char * jepa_version(void) { return JEPA_VERSION; }
@@ -174,6 +179,7 @@ extern "C" jepa_context * jepa_context_new(jepa_model * model, jepa_context_para
     ctx->n_threads = params.n_threads > 0 ? params.n_threads : (int) std::thread::hardware_concurrency();
     if (ctx->n_threads < 1) ctx->n_threads = 1;
     ctx->device = model->device;
+    std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
     if (hipSetDevice(ctx->device) != hipSuccess || hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&ctx->ev0) != hipSuccess || hipEventCreate(&ctx->ev1) != hipSuccess) {
         jepa_log("jepa: could not create a HIP stream / events on device %d\n", ctx->device);

@@ -3,6 +3,7 @@
 #include <cstdint>
 #include <cstddef>
 #include <string>
+#include <mutex>
 
 #ifndef JEPA_VERSION
 #define JEPA_VERSION "0.5.0-mi355x"
@@ -11,6 +12,13 @@
 // Diagnostics: every line goes to stderr and to a thread-local capture buffer (jepa_error_text),
 // the reference's contract (include/jepa.h:596-610, src/jepa.cpp:16-36).
 void jepa_log(const char * fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Serialises the library's device allocations and frees, model uploads and hipGraph captures across
+// threads. A stream capture fails when another thread allocates, frees or copies through the null
+// stream while it is open; contexts in different threads share one device, so every such call of
+// the library holds this lock. Kernel launches, graph replays and copies on a context's own
+// non-blocking stream do not need it.
+std::recursive_mutex & jepa_hip_mutex();
 
 // ggml_type ids as stored in GGUF tensor infos
 enum ggml_type_id : int {

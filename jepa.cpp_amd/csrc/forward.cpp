@@ -23,6 +23,7 @@
 jepa_context::jepa_context() = default;
 
 jepa_context::~jepa_context() {
+    std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
     hipSetDevice(device);
     ws.reset();
     if (io_in) hipFree(io_in);
@@ -251,8 +252,9 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
             s.insert(s.begin(), (size_t) w->prefix * hd, 0.0f);
         }
         if (!ws_alloc(*w, (void **) &w->rope_c, c.size() * 4) || !ws_alloc(*w, (void **) &w->rope_s, s.size() * 4)) { ctx->ws.reset(); return false; }
-        if (hipMemcpy(w->rope_c, c.data(), c.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemcpy(w->rope_s, s.data(), s.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        if (hipMemcpyAsync(w->rope_c, c.data(), c.size() * 4, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+            hipMemcpyAsync(w->rope_s, s.data(), s.size() * 4, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+            hipStreamSynchronize(ctx->stream) != hipSuccess) {
             jepa_log("jepa: RoPE table upload failed\n");
             ctx->ws.reset();
             return false;
@@ -385,7 +387,10 @@ int64_t encode_device(jepa_context * ctx, const float * in_dev, int n_batch, int
         const int nb = (int) std::min<int64_t>(bmax, n_items - base);
         // image families are laid out [items][C][1][H][W] for the patchify kernel (gathered below
         // when the caller's input has several frames per batch entry)
-        if (!ensure_workspace(ctx, nb, n_chans, video ? n_frames : 1, height, width)) return -1;
+        {
+            std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
+            if (!ensure_workspace(ctx, nb, n_chans, video ? n_frames : 1, height, width)) return -1;
+        }
         fwd_workspace & w = *ctx->ws;
         // image families: item `it` is the (b, t) slice; slices of one chunk must be contiguous in
         // memory for the patchify kernel, which indexes ((b*C + c)*T + f): pass the whole input and
@@ -417,6 +422,7 @@ int64_t encode_device(jepa_context * ctx, const float * in_dev, int n_batch, int
             enqueue_forward(ctx, src, dst, trace_dev, kt);
         } else {
             if (!w.graph_ok || w.g_in != src || w.g_out != dst) {
+                std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
                 if (w.exec) { hipGraphExecDestroy(w.exec); w.exec = nullptr; }
                 w.graph_ok = false;
                 hipGraph_t graph = nullptr;
@@ -470,6 +476,7 @@ int64_t encode_host(jepa_context * ctx, const jepa_input * in, float * out_host,
     if ((int64_t) n_out > out_cap) return -1;
     if (hipSetDevice(ctx->device) != hipSuccess) return -1;
     // persistent I/O buffers: stable pointers let the captured graph be replayed call after call
+    std::unique_lock<std::recursive_mutex> lk(jepa_hip_mutex());
     if (ctx->io_in_cap < n_in * 4) {
         if (ctx->io_in) hipFree(ctx->io_in);
         ctx->io_in = nullptr; ctx->io_in_cap = 0;
@@ -482,6 +489,7 @@ int64_t encode_host(jepa_context * ctx, const jepa_input * in, float * out_host,
         if (hipMalloc(&ctx->io_out, n_out * 4) != hipSuccess) { jepa_log("jepa: hipMalloc(output %.1f MiB) failed\n", n_out * 4 / 1048576.0); return -1; }
         ctx->io_out_cap = n_out * 4;
     }
+    lk.unlock();
     float * din = (float *) ctx->io_in, * dout = (float *) ctx->io_out;
     int64_t r = -1;
     if (hipMemcpyAsync(din, in->data, n_in * 4, hipMemcpyHostToDevice, ctx->stream) == hipSuccess) {

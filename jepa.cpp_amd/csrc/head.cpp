@@ -51,6 +51,7 @@ bool ensure_head_workspace(jepa_context * ctx, int64_t N) {
     const enc_hparams & e = m->hp.enc;
     fwd_workspace * w = ctx->hws.get();
     if (w && w->model == m && w->R == N) return true;
+    std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
     ctx->hws.reset(new fwd_workspace());
     w = ctx->hws.get();
     w->model = m;
@@ -176,8 +177,9 @@ extern "C" int jepa_head_ex(jepa_context * ctx, const jepa_output * enc, jepa_ou
     float * hp = nullptr, * hl = nullptr;
     if (pooled && !(hp = (float *) malloc((size_t) D * 4))) return -1;
     if (logits && !(hl = (float *) malloc((size_t) std::max(C, 1) * 4))) { free(hp); return -1; }
-    if ((hp && hipMemcpy(hp, w.hy, (size_t) D * 4, hipMemcpyDeviceToHost) != hipSuccess) ||
-        (hl && hipMemcpy(hl, w.hlog, (size_t) C * 4, hipMemcpyDeviceToHost) != hipSuccess)) {
+    if ((hp && hipMemcpyAsync(hp, w.hy, (size_t) D * 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess) ||
+        (hl && hipMemcpyAsync(hl, w.hlog, (size_t) C * 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess) ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
         jepa_log("jepa: output download failed\n");
         free(hp); free(hl);
         return -1;

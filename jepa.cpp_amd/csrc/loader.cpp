@@ -380,6 +380,7 @@ bool is_video_family(family_id f) { return f == FAM_VJEPA2 || f == FAM_VJEPA2_1 
 bool is_image_family(family_id f) { return f == FAM_IJEPA || f == FAM_HFVIT || f == FAM_LEWM || f == FAM_HJEPA; }
 
 static void model_free_device(jepa_model * m) {
+    std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
     int prev = 0;
     hipGetDevice(&prev);
     hipSetDevice(m->device);
@@ -434,6 +435,7 @@ extern "C" jepa_model * jepa_model_load_ex(const char * path, const jepa_model_p
     const int device = dev_resolve(mp.device);
     if (device < 0) return nullptr;
     m->device = device;
+    std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
     if (hipSetDevice(device) != hipSuccess) { jepa_log("jepa: hipSetDevice(%d) failed\n", device); return nullptr; }
     std::unique_ptr<FILE, int (*)(FILE *)> fp(fopen(path, "rb"), fclose);
     if (!fp) { jepa_log("jepa: cannot reopen %s for tensor data\n", path); return nullptr; }

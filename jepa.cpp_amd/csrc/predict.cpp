@@ -82,6 +82,7 @@ bool ensure_pred_workspace(jepa_context * ctx, int n_ctx, int n_tgt) {
     const pred_hparams & p = m->hp.pred;
     fwd_workspace * w = ctx->pws.get();
     if (w && w->model == m && w->n_ctx == n_ctx && w->n_tgt == n_tgt) return true;
+    std::lock_guard<std::recursive_mutex> lk(jepa_hip_mutex());
     ctx->pws.reset(new fwd_workspace());
     w = ctx->pws.get();
     w->model = m;
@@ -257,7 +258,8 @@ extern "C" int jepa_predict_mod(jepa_context * ctx, const jepa_output * enc, con
     if (n_context > 0) {
         std::vector<float> rows((size_t) n_context * De);
         for (int i = 0; i < n_context; i++) memcpy(rows.data() + (size_t) i * De, enc->data + (size_t) ids[(size_t) i] * De, (size_t) De * 4);
-        if (hipMemcpy(w.pin, rows.data(), rows.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        if (hipMemcpyAsync(w.pin, rows.data(), rows.size() * 4, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+            hipStreamSynchronize(ctx->stream) != hipSuccess) {
             jepa_log("jepa: input upload failed\n");
             return -1;
         }
@@ -266,7 +268,8 @@ extern "C" int jepa_predict_mod(jepa_context * ctx, const jepa_output * enc, con
     if (od < 0) return -1;
     float * data = (float *) malloc((size_t) n_target * od * 4);
     if (!data) return -1;
-    if (hipMemcpy(data, w.pout, (size_t) n_target * od * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+    if (hipMemcpyAsync(data, w.pout, (size_t) n_target * od * 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
         jepa_log("jepa: output download failed\n");
         free(data);
         return -1;
