@@ -186,7 +186,7 @@ bool make_linear(dev_scope & d, const char * who, int wtype, const void * w, int
         L.w = (void *) w;
         return true;
     }
-    L.w = d.alloc((size_t) n_out * n_in * (L.fmt == W_Q32 ? 1 : 2));
+    L.w = d.alloc(L.fmt == W_Q32 ? (size_t) n_out * n_in : (size_t) n_out * (n_in / 2) + (size_t) n_out * (n_in / 256) * 8);
     if (L.fmt == W_Q32) L.wd = d.alloc((size_t) n_out * (n_in / 32) * 2);
     else {
         L.wd = d.alloc((size_t) n_out * (n_in / 256) * 4);

@@ -7,12 +7,14 @@
 //   f16 weights x f16-rounded activations:   f32 accumulation of exact f16 products
 //
 // q8_0 / q4_0 (int8 codes in HBM and LDS), per 32-deep block b and 32x32 output tile:
-//   v_mfma_i32_32x32x32_i8   S  = A_b . B_b, started from the bits of 1.5 * 2^23 so that the int32
-//                               result read as a float is 12582912 + S exactly
+//   v_mfma_i32_32x32x32_i8   S  = A_b . B_b (with at most two MFMA tiles per wave started from the bits
+//                               of 1.5 * 2^23, so that the int32 result read as a float is 12582912 + S)
 //   v_mfma_f32_32x32x8_f16   c  = dw_b (x) da_b (an outer product of the two f16 scale vectors; one
 //                               non-zero K slot, so every c = dw * da is exact)
-//   32 VALU                  acc = fma((12582912 + S) - 12582912, c, acc): one rounding per block
-// q4_K (f16 sc*q codes) and f16 weights run f16 MFMAs (v_mfma_f32_32x32x16_f16) over 64-column stages.
+//   32 VALU                  acc = fma(float(S), c, acc): one rounding per block
+// q4_K (4-bit codes in HBM and LDS, unpacked in registers), per 256-deep super-block: int8 MFMAs sum
+// (sh q) . a and (sl q) . a over its eight sub-blocks (sc = 8 sh + sl), one float epilogue per super-block.
+// f16 weights run f16 MFMAs (v_mfma_f32_32x32x16_f16) over 64-column stages.
 //
 // Workgroups are eight waves (two per SIMD); a wave owns TI x TJ tiles of 32 x 32 with the weight
 // rows on the MFMA "A" side, so a lane's 16 accumulators are 4 groups of 4 consecutive output features
@@ -46,6 +48,7 @@ struct kargs {
     const _Float16 * A;      // [N][K] weight codes (or f16 / f32 weights)
     const uint16_t * Ad;     // W_Q32: f16 d [N][K/32]; W_Q4K: u32 (d | dmin << 16) [K/256][N]
     const _Float16 * Amin;   // W_Q4K: [N][K/256][16] sub-block mins, each twice
+    const uint8_t * Asc;     // W_Q4K: [N][K/256][8] 6-bit sub-block scales
     const _Float16 * B;      // [M][K] activation codes (or f16 / f32 activations)
     const void * Bd;         // A_Q8_0: f16 d [M][K/32]; A_Q8_K: f32 d [M][K/256]
     const _Float16 * Bsum;   // A_Q8_K: f16 bsums [M][K/16]
@@ -194,25 +197,31 @@ __device__ __forceinline__ void stage_barrier() {
 template <int WF, int WN, int WM, int TI, int TJ>
 struct tiling {
     static constexpr int NW = WN * WM, NT = 64 * NW;
-    static constexpr int BN = 32 * WN * TI, BM = 32 * WM * TJ, ROWS = BN + BM;
-    static constexpr int ESZ = WF == W_Q32 ? 1 : 2;          // bytes per code
+    static constexpr int BN = 32 * WN * TI, BM = 32 * WM * TJ;
+    // LDS rows of 128 B per stage: the weight rows (q4_K: two rows of 64 B of 4-bit codes share one),
+    // then the activation rows
+    static constexpr int AROWS = WF == W_Q4K ? BN / 2 : BN;
+    static constexpr int ROWS = AROWS + BM;
+    static constexpr int ESZ = WF == W_F16 ? 2 : 1;          // bytes per activation code
     static constexpr int KC = 128 / ESZ;                      // K-columns per stage
     static constexpr int TILE = ROWS * 128;
     static constexpr int STAGE = TILE;
-    static constexpr int X_DW = 0, X_MIN = BN * 4, X_DA = X_MIN + BN * 32, X_BS = X_DA + BM * 4;
+    // q4_K super-block data (one set per 256 K = two stages): per weight row (d | dmin << 16), the eight
+    // 6-bit sub-block scales as bytes and the 16 f16 mins; per token the q8_K d and the 16 f16 bsums.
+    // Three buffers: the set of super-block sb + 1 is copied while stage 2 sb + 3 - NST is computed,
+    // and every wave is then past the epilogue of sb - 2 (end of stage 2 sb - 3) when NST <= 4.
+    static constexpr int X_DW = 0, X_SC = BN * 4, X_MIN = X_SC + BN * 8, X_DA = X_MIN + BN * 32, X_BS = X_DA + BM * 4;
     static constexpr int XSB = WF == W_Q4K ? X_BS + BM * 32 : 0;
-    // q4_K: the super-block buffer of sb+1 is filled while stage 4 sb + 5 - NST is computed, which must
-    // come after the epilogue of sb-1 (end of stage 4 sb - 1) has been passed by every wave: NST <= 4
-    // in the pipelined loop, whose barrier sits inside a stage
+    static constexpr int NXSB = WF == W_Q4K ? 3 : 0;
     static constexpr int NST_MAX = WF == W_Q4K ? 4 : 6;
-    static constexpr int NST_FIT = (160 * 1024 - 2 * XSB) / STAGE;
+    static constexpr int NST_FIT = (160 * 1024 - NXSB * XSB) / STAGE;
     static constexpr int NST = NST_FIT < NST_MAX ? NST_FIT : NST_MAX;
-    static constexpr int LDS = NST * STAGE + 2 * XSB;
+    static constexpr int LDS = NST * STAGE + NXSB * XSB;
     static constexpr int LOADS = ROWS / 8 / NW;    // 1 KB tile loads per wave per stage
     static constexpr int PARTS = LOADS;            // copies per wave per stage (q4_K adds its own)
     static constexpr int SLD = WF == W_Q32 ? TI + TJ : 0;   // q8_0 / q4_0 scale loads per wave per stage
     static_assert(NST >= 2, "LDS too small for two stages");
-    static_assert(BN % (8 * NW) == 0 && BN % 64 == 0 && BM % 64 == 0 && ROWS % (8 * NW) == 0, "load split");
+    static_assert(AROWS % (8 * NW) == 0 && BN % 64 == 0 && BM % 64 == 0 && ROWS % (8 * NW) == 0, "load split");
     static_assert((NST - 2) * PARTS < 64, "vmcnt range");
 };
 
@@ -225,6 +234,25 @@ template <class V>
 __device__ __forceinline__ V lds_chunk(const unsigned char * base, int r, int c) {
     return *(const V *) (base + r * 128 + (lds_slot(r, c) << 4));
 }
+
+// LDS reads in inline asm, for data whose copy is known to have landed (by the stage barriers): the
+// compiler cannot tell their addresses from the HBM->LDS copies in flight and would wait for all of
+// those (vmcnt(0)) before an ordinary read. The caller waits for the results with lds_wait() and
+// passes each through lds_take() before its first use.
+__device__ __forceinline__ uint32_t lds_addr(const void * p) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
+}
+template <class V>
+__device__ __forceinline__ V lds_read_asm(const void * p) {
+    V r;
+    if constexpr (sizeof(V) == 16) asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+    else if constexpr (sizeof(V) == 8) asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+    else asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+    return r;
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <class V>
+__device__ __forceinline__ void lds_take(V & v) { asm volatile("" : "+v"(v)); }
 
 // Y[m][n] over the workgroup tile (n0, m0). K advances one stage (KC) per iteration; NST - 1 stages
 // are in flight as direct HBM->LDS copies (buffer_load_dwordx4 ... lds: each lane moves 16 B, a wave
@@ -266,13 +294,14 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // stages per half) and the K-stage its addresses start at
     const int64_t nst = split > 1 ? K / KC / split : (K + KC - 1) / KC;
     const int64_t kst0 = (int64_t) sp * nst;
-    const int64_t rowbytes = K * ESZ;
+    const int64_t rowbytes = K * ESZ;                                  // activation row
+    const int64_t rowbytesA = WF == W_Q4K ? K / 2 : rowbytes;          // weight row (q4_K: 4-bit codes)
 
     // buffer resources rebased at the tile's first weight row and first token, so that every copy's
     // offset stays below 4 GiB
-    const brsrc rA = make_brsrc((const unsigned char *) a.A + n0 * rowbytes, (a.N - n0) * rowbytes);
+    const brsrc rA = make_brsrc((const unsigned char *) a.A + n0 * rowbytesA, (a.N - n0) * rowbytesA);
     const brsrc rB = make_brsrc((const unsigned char *) a.B + m0 * rowbytes, (M - m0) * rowbytes);
-    [[maybe_unused]] brsrc rAd, rBd, rAmin, rBs;
+    [[maybe_unused]] brsrc rAd, rBd, rAmin, rBs, rAsc;
     [[maybe_unused]] const int64_t nsb = K >> 8;
     if constexpr (WF == W_Q32) {
         rAd = make_brsrc(a.Ad + n0 * KB, (a.N - n0) * KB * 2);
@@ -281,6 +310,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     if constexpr (WF == W_Q4K) {
         rAd = make_brsrc((const uint32_t *) a.Ad + n0, (nsb * a.N - n0) * 4);
         rAmin = make_brsrc(a.Amin + n0 * nsb * 16, (a.N - n0) * nsb * 32);
+        rAsc = make_brsrc(a.Asc + n0 * nsb * 8, (a.N - n0) * nsb * 8);
         rBd = make_brsrc((const float *) a.Bd + m0 * nsb, (M - m0) * nsb * 4);
         rBs = make_brsrc(a.Bsum + m0 * (K >> 4), (M - m0) * (K >> 4) * 2);
     }
@@ -300,8 +330,15 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         const uint32_t cb = 16 * ((k0 * ESZ + 128 > rowbytes) ? (c & 3) : c);
         const int L = NW * i + wave;
         const int r = 8 * L + (lane >> 3);
-        if (i < BN / (8 * NW)) dma_to_lds<16>(rA, (uint32_t) r * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
-        else dma_to_lds<16>(rB, tok_row(r - BN) * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
+        if (i < T::AROWS / (8 * NW)) {
+            if constexpr (WF == W_Q4K) {   // LDS row r: weight rows 2r (chunks 0-3) and 2r + 1 (chunks 4-7), 64 B each
+                const int cw = lds_slot(r, lane & 7);
+                dma_to_lds<16>(rA, (uint32_t) (2 * r + (cw >> 2)) * (uint32_t) rowbytesA + 16 * (cw & 3), (uint32_t) (k0 / 2), base + 1024 * L);
+            } else
+                dma_to_lds<16>(rA, (uint32_t) r * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
+        } else {
+            dma_to_lds<16>(rB, tok_row(r - T::AROWS) * (uint32_t) rowbytes + cb, soff, base + 1024 * L);
+        }
     };
     // q8_0 / q4_0 stages issue their PARTS copies one per compute step of the stage NST - 1 earlier
     // (spread, so that no wave stalls behind a burst of copies). Stages past the end copy the last
@@ -311,28 +348,31 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         const int64_t sa = st < nst ? st : nst - 1;
         issue_tile(st, sa, p);
     };
-    // q4_K super-block data of super-block st / 4, copied with stage st when st % 4 == 0
+    // q4_K super-block data of this workgroup's super-block st / 2 (data of K super-block (st + kst0) / 2),
+    // copied with stage st when st is even, into buffer (st / 2) % 3; nothing past the last stage
     auto issue_xsb = [&](int64_t st) {
         if constexpr (WF == W_Q4K) {
-            if ((st & 3) == 0) {
-                // buffer by this workgroup's super-block count, data of K super-block sb (a split
-                // starts at a super-block boundary)
-                const uint32_t sb = (uint32_t) ((st + kst0) >> 2);
-                unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 2) & 1) * T::XSB;
-                constexpr int N1 = BN / 64, N2 = BN / 32, N3 = T::BM / 64, N4 = T::BM / 32;
-                for (int L = wave; L < N1 + N2 + N3 + N4; L += NW) {
+            if ((st & 1) == 0 && st < nst) {
+                const uint32_t sb = (uint32_t) ((st + kst0) >> 1);
+                unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 1) % 3) * T::XSB;
+                constexpr int N1 = BN / 64, N5 = BN / 32, N2 = BN / 32, N3 = T::BM / 64, N4 = T::BM / 32;
+                for (int L = wave; L < N1 + N5 + N2 + N3 + N4; L += NW) {
                     if (L < N1) {
                         dma_to_lds<4>(rAd, (uint32_t) (sb * a.N + 64 * L + lane) * 4, 0, xb + T::X_DW + 256 * L);
-                    } else if (L < N1 + N2) {
-                        const int L2 = L - N1;
+                    } else if (L < N1 + N5) {   // sub-block scales: two lanes per row, one dword each
+                        const int L5 = L - N1;
+                        const uint32_t n = 32 * L5 + (lane >> 1);
+                        dma_to_lds<4>(rAsc, (n * (uint32_t) nsb + sb) * 8 + 4 * (lane & 1), 0, xb + T::X_SC + 256 * L5);
+                    } else if (L < N1 + N5 + N2) {
+                        const int L2 = L - N1 - N5;
                         const uint32_t n = 32 * L2 + (lane >> 1);
                         dma_to_lds<16>(rAmin, ((n * (uint32_t) nsb + sb) * 16 + 8 * (lane & 1)) * 2, 0, xb + T::X_MIN + 1024 * L2);
-                    } else if (L < N1 + N2 + N3) {
-                        const int L3 = L - N1 - N2;
+                    } else if (L < N1 + N5 + N2 + N3) {
+                        const int L3 = L - N1 - N5 - N2;
                         const uint32_t m = tok_row(64 * L3 + lane);
                         dma_to_lds<4>(rBd, (m * (uint32_t) nsb + sb) * 4, 0, xb + T::X_DA + 256 * L3);
                     } else {
-                        const int L4 = L - N1 - N2 - N3;
+                        const int L4 = L - N1 - N5 - N2 - N3;
                         const uint32_t m = tok_row(32 * L4 + (lane >> 1));
                         dma_to_lds<16>(rBs, (m * (uint32_t) (K >> 4) + sb * 16 + 8 * (lane & 1)) * 2, 0, xb + T::X_BS + 1024 * L4);
                     }
@@ -348,14 +388,14 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     };
 
     f16v acc[TI][TJ];
-    [[maybe_unused]] f16v ssb[TI][TJ], accm[TI][TJ];   // q4_K: super-block sums, mins accumulator
+    [[maybe_unused]] f16v accm[TI][TJ];   // q4_K: mins accumulator
     const f16v zero = {};
 #pragma unroll
     for (int i = 0; i < TI; i++)
 #pragma unroll
         for (int j = 0; j < TJ; j++) {
             acc[i][j] = zero;
-            if constexpr (WF == W_Q4K) { ssb[i][j] = zero; accm[i][j] = zero; }
+            if constexpr (WF == W_Q4K) accm[i][j] = zero;
         }
 
     // ---- q8_0 / q4_0 ----
@@ -542,57 +582,208 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
       }
     };
 
-    // q4_K super-block epilogue after stage st (st % 4 == 3)
-    [[maybe_unused]] auto q4k_epilogue = [&](int64_t st) {
-        // super-block epilogue (ggml's x86 vec_dot_q4_K_q8_K): acc += (dw*da) S and, in a second
-        // accumulator, accm += (dmin*da) sum_j m_j bsum_j; the result is acc - accm
-        const unsigned char * xb = smem + NST * T::STAGE + (int) ((st >> 2) & 1) * T::XSB;
-        h8 bs[TJ];
-        float da[TJ];
+    // ---- q4_K ----
+    // Weights stay 4-bit in HBM and LDS. A stage is 128 K-columns: 64 B of codes per weight row (two rows
+    // share an LDS row) and 128 int8 q8_K codes per token; a super-block (256 K) is two stages. Steps
+    // u = (sub-block jl of the stage, tile), tiles i-major, U = 4 TI TJ. Per sub-block the lane's 16
+    // codes are unpacked from 8 bytes (and / shift) and multiplied, four bytes per v_pk_mul_lo_u16, by the
+    // row's 6-bit scale split as sc = 8 sh + sl (sh, sl <= 7, so every byte product is <= 105 and no
+    // carry crosses a byte): two int8 MFMAs then accumulate H += (sh q) . a and L += (sl q) . a over the
+    // whole super-block in int32, the first sub-block starting from zero. At the end of the
+    // super-block isum = 8 H + L is ggml's sum_j sc_j S_j exactly, and the epilogue (ggml's x86
+    // vec_dot_q4_K_q8_K) does acc += (dw*da) isum, accm += (dmin*da) sum_j m_j bsum_j with the mins sum
+    // from one f16 MFMA (exact); the result is acc - accm.
+    // The pipeline is the q8_0 one: operand reads two steps ahead, copies spread over the steps of the
+    // stage NST - 1 earlier, stage st+1 published two steps before the end of stage st. The super-block
+    // data (not the same copy count on every wave) is left out of the barrier counts, which only makes
+    // the waits longer; it is issued before the tile copies of the super-block's first stage, so it has
+    // landed when that stage is published.
+    [[maybe_unused]] auto q4k_main = [&]() {
+      if constexpr (WF == W_Q4K) {
+        constexpr int TT = TI * TJ, U = 4 * TT;
+        static_assert(NST >= 3 && NST <= 4, "three to four stages: one in flight beyond the next, and the super-block buffers' reuse");
+        constexpr int P1 = T::PARTS;
+        constexpr int NBAR = (NST - 3) * P1 + (U - 1) * P1 / U;
+        typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+        typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+        // operand registers by sub-block: with two or more MFMA tiles per wave, the reads two steps ahead
+        // reach at most the next sub-block, so two sets suffice
+        constexpr int NR = TT >= 2 ? 2 : 4, NP = TI == 1 ? 2 : 1;
+        u4v AR[2][TI];            // raw 4-bit codes of sub-blocks jl, jl + 1 (jl even; 8 bytes each per lane)
+        i4v B[NR][TJ];            // int8 activation codes of sub-block jl
+        i4v AH[NP][TI], AL[NP][TI];   // sh * q and sl * q as int8
+        u2v SCR[TI];              // the lane's weight row's eight sub-block scales (bytes)
+        i16v HI[TI][TJ], LO[TI][TJ];
+        auto xsb_of = [&](int64_t st) -> const unsigned char * { return smem + NST * T::STAGE + (int) ((st >> 1) % 3) * T::XSB; };
+        // the row's sub-block scales of the super-block of stage st (read at the end of the stage
+        // before; waited for at the start of stage st)
+        auto ld_sc = [&](int64_t st) {
+            const unsigned char * xb = xsb_of(st);
 #pragma unroll
-        for (int j = 0; j < TJ; j++) {
-            const int rm = 32 * (wm * TJ + j) + l32;
-            bs[j] = *(const h8 *) (xb + T::X_BS + rm * 32 + 16 * g);
-            da[j] = *(const float *) (xb + T::X_DA + 4 * rm);
-        }
+            for (int i = 0; i < TI; i++) SCR[i] = lds_read_asm<u2v>(xb + T::X_SC + 8 * (32 * (wn * TI + i) + l32));
+        };
+        auto take_sc = [&]() {
+            lds_wait();
 #pragma unroll
-        for (int i = 0; i < TI; i++) {
-            const int rn = 32 * (wn * TI + i);
-            const h8 am = *(const h8 *) (xb + T::X_MIN + (rn + l32) * 32 + 16 * g);
-            float dw[16], dm[16];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint4 v = *(const uint4 *) (xb + T::X_DW + 4 * (rn + 8 * q + 4 * g));
-                const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) { dw[4 * q + e] = h2f((uint16_t) (vv[e] & 0xffffu)); dm[4 * q + e] = h2f((uint16_t) (vv[e] >> 16)); }
+            for (int i = 0; i < TI; i++) lds_take(SCR[i]);
+        };
+        auto ld_step = [&](const unsigned char * base, int u) {
+            const int jl = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
+            if (j == 0 && (jl & 1) == 0) {
+                // a stage row's 64 B: [g0: jl 0, 1] [g1: jl 0, 1] [g0: jl 2, 3] [g1: jl 2, 3], 8 B each
+                const int n = 32 * (wn * TI + i) + l32, r = n >> 1;
+                // the 16 lanes of one ds_read_b128 pass (8 LDS rows, both halves of the 64 banks, chunks
+                // c ^ ((r >> 1) & 7) with c in {c0, c0 + 4}) hit 16 different 4-bank groups
+                AR[(jl >> 1) & 1][i] = *(const u4v *) (base + r * 128 + (lds_slot(r, ((n & 1) << 2) + 2 * (jl >> 1) + g) << 4));
             }
+            if (i == 0) B[jl % NR][j] = lds_chunk<i4v>(base, T::AROWS + 32 * (wm * TJ + j) + l32, 2 * jl + g);
+        };
+        auto pk_mul = [](uint32_t c, uint32_t f) -> int {
+            const us2 v = __builtin_bit_cast(us2, c) * (us2) {(unsigned short) f, (unsigned short) f};
+            return __builtin_bit_cast(int, v);
+        };
+        auto mma = [&](int u, auto half_c) {
+            constexpr int HALF = decltype(half_c)::value;
+            const int jl = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
+            const int pb = jl % NP, rb = jl % NR;
+            if (j == 0) {
+                const uint32_t w = SCR[i][HALF];
+                const uint32_t sh = (w >> (8 * jl + 3)) & 7u, sl = (w >> (8 * jl)) & 7u;
+                const u4v ar = AR[(jl >> 1) & 1][i];
+                const uint32_t p0 = (jl & 1) ? ar.z : ar.x, p1 = (jl & 1) ? ar.w : ar.y;
+                const uint32_t c[4] = {p0 & 0x0F0F0F0Fu, (p0 >> 4) & 0x0F0F0F0Fu, p1 & 0x0F0F0F0Fu, (p1 >> 4) & 0x0F0F0F0Fu};
+#pragma unroll
+                for (int k = 0; k < 4; k++) { AH[pb][i][k] = pk_mul(c[k], sh); AL[pb][i][k] = pk_mul(c[k], sl); }
+            }
+            if (HALF == 0 && jl == 0) {
+                HI[i][j] = MFMA_I8(AH[pb][i], B[rb][j], i16v{});
+                LO[i][j] = MFMA_I8(AL[pb][i], B[rb][j], i16v{});
+            } else {
+                HI[i][j] = MFMA_I8(AH[pb][i], B[rb][j], HI[i][j]);
+                LO[i][j] = MFMA_I8(AL[pb][i], B[rb][j], LO[i][j]);
+            }
+        };
+        auto sb_epilogue = [&](int64_t st) {
+            const unsigned char * xb = xsb_of(st);
+            u4v bsr[TJ];
+            uint32_t dar[TJ];
 #pragma unroll
             for (int j = 0; j < TJ; j++) {
-                const f16v ms = MFMA16(am, bs[j], zero);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float d1 = __fmul_rn(dw[r], da[j]), d2 = __fmul_rn(dm[r], da[j]);
-                    acc[i][j][r] = fmaf(d1, ssb[i][j][r], acc[i][j][r]);
-                    accm[i][j][r] = fmaf(d2, ms[r], accm[i][j][r]);
-                }
-                ssb[i][j] = zero;
+                const int rm = 32 * (wm * TJ + j) + l32;
+                bsr[j] = lds_read_asm<u4v>(xb + T::X_BS + rm * 32 + 16 * g);
+                dar[j] = lds_read_asm<uint32_t>(xb + T::X_DA + 4 * rm);
             }
+#pragma unroll
+            for (int i = 0; i < TI; i++) {
+                const int rn = 32 * (wn * TI + i);
+                u4v amr = lds_read_asm<u4v>(xb + T::X_MIN + (rn + l32) * 32 + 16 * g);
+                u4v dwr[4];   // rows 8q + 4g + e of the MFMA tile: (d, dmin) of four consecutive rows
+#pragma unroll
+                for (int q = 0; q < 4; q++) dwr[q] = lds_read_asm<u4v>(xb + T::X_DW + 4 * (rn + 8 * q + 4 * g));
+                lds_wait();
+                lds_take(amr);
+#pragma unroll
+                for (int q = 0; q < 4; q++) lds_take(dwr[q]);
+                if (i == 0) {
+#pragma unroll
+                    for (int j = 0; j < TJ; j++) { lds_take(bsr[j]); lds_take(dar[j]); }
+                }
+                const h8 am = __builtin_bit_cast(h8, amr);
+                f16v ms[TJ];
+#pragma unroll
+                for (int j = 0; j < TJ; j++) ms[j] = MFMA16(am, __builtin_bit_cast(h8, bsr[j]), zero);
+                float da[TJ];
+#pragma unroll
+                for (int j = 0; j < TJ; j++) da[j] = __uint_as_float(dar[j]);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const u4v v = dwr[q];
+                    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float dw = h2f((uint16_t) (vv[e] & 0xffffu)), dm = h2f((uint16_t) (vv[e] >> 16));
+                        const int r = 4 * q + e;
+#pragma unroll
+                        for (int j = 0; j < TJ; j++) {
+                            const int isum = (HI[i][j][r] << 3) + LO[i][j][r];
+                            const float d1 = __fmul_rn(dw, da[j]), d2 = __fmul_rn(dm, da[j]);
+                            acc[i][j][r] = fmaf(d1, (float) isum, acc[i][j][r]);
+                            accm[i][j][r] = fmaf(d2, ms[j][r], accm[i][j][r]);
+                        }
+                    }
+                }
+            }
+        };
+        issue_xsb(0);
+#pragma unroll
+        for (int p = 0; p < P1; p++) issue_part(0, p);
+        stage_barrier<0>();
+        ld_sc(0);
+        ld_step(smem, 0);
+        ld_step(smem, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        auto body = [&](int64_t st, auto cross_c, auto first_c, auto half_c) {
+            constexpr bool CROSS = decltype(cross_c)::value, FIRST = decltype(first_c)::value;
+            constexpr int HALF = decltype(half_c)::value;
+            constexpr int Q = FIRST ? (NST - 1) * P1 : P1;
+            constexpr int NB = FIRST ? (U - 1) * Q / U - P1 : NBAR;
+            static_assert(NB >= 0 && NB < 64, "barrier count");
+            const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
+            const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
+            if constexpr (FIRST) {
+                // super-block data of the stages 1..NST-1 this body copies, before their tile copies
+#pragma unroll
+                for (int s2 = 2; s2 < NST; s2 += 2) issue_xsb(s2);
+            }
+            if constexpr (HALF == 0) take_sc();
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if constexpr (!FIRST) {
+                    if (u == 0) issue_xsb(st + NST - 1);
+                }
+#pragma unroll
+                for (int k = u * Q / U; k < (u + 1) * Q / U; k++) {
+                    if constexpr (FIRST) issue_part(1 + k / P1, k % P1);
+                    else issue_part(st + NST - 1, k);
+                }
+                mma(u, half_c);
+                if (u + 2 < U) ld_step(base, u + 2);
+                if constexpr (CROSS) {
+                    if (u == U - 2) {
+                        stage_barrier<NB>();
+                        ld_step(nbase, 0);
+                    }
+                    if (u == U - 1) {
+                        if constexpr (HALF == 1) ld_sc(st + 1);   // after this stage's last use of SCR
+                        ld_step(nbase, 1);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (HALF == 1) sb_epilogue(st);
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        using H0 = std::integral_constant<int, 0>;
+        using H1 = std::integral_constant<int, 1>;
+        // nst is even (K % 256 == 0; a split has whole super-blocks per half)
+        body(0, T_{}, T_{}, H0{});
+        for (int64_t st = 1; st + 2 < nst; st += 2) {
+            body(st, T_{}, F_{}, H1{});
+            body(st + 1, T_{}, F_{}, H0{});
         }
+        body(nst - 1, F_{}, F_{}, H1{});
+        // the copies issued during the last stages must land before the workgroup's LDS is released
+        __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+      }
     };
 
-    // ---- f16 and q4_K ----
+    // ---- f16 ----
     // A stage holds 64 K-columns (two 32-deep halves); steps u = (half, tile), tiles i-major, two f16
     // MFMAs (32x32x16) per step, U = 2 TI TJ per stage. The same pipeline as q8_0 / q4_0: operand
     // chunks two steps ahead, copies spread over the steps of the stage NST - 1 earlier (stage 0's
     // alone before the first barrier), stage st+1 published two steps before the end of stage st.
-    // q4_K accumulates the super-block sums in ssb and runs its epilogue after every fourth stage.
-    // Its super-block data (one copy set per 4 stages, not the same count on every wave) is left out
-    // of the barrier counts, which only makes the waits longer; it is issued with the first copies of
-    // stage 4 sb, so it has landed when that stage is published. Its double buffer for sb + 1 is
-    // refilled from stage 4 sb + 5 - NST >= 4 sb + 1 (NST <= 4), whose copies follow the barrier
-    // that every wave reaches only after the epilogue of sb - 1.
-    constexpr bool PIPE16 = WF == W_F16 || (WF == W_Q4K && NST >= 3 && NST <= 4);
+    constexpr bool PIPE16 = WF == W_F16;
     [[maybe_unused]] auto f16_main = [&]() {
       if constexpr (PIPE16) {
         constexpr int TT = TI * TJ, U = 2 * TT;
@@ -615,11 +806,9 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         };
         auto mma = [&](int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            f16v & d = WF == W_Q4K ? ssb[i][j] : acc[i][j];
-            d = MFMA16(A0[blk][i], B0[blk][j], d);
-            d = MFMA16(A1[blk][i], B1[blk][j], d);
+            acc[i][j] = MFMA16(A0[blk][i], B0[blk][j], acc[i][j]);
+            acc[i][j] = MFMA16(A1[blk][i], B1[blk][j], acc[i][j]);
         };
-        issue_xsb(0);
 #pragma unroll
         for (int p = 0; p < P1; p++) issue_part(0, p);
         stage_barrier<0>();
@@ -635,9 +824,6 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                if constexpr (WF == W_Q4K && !FIRST) {
-                    if (u == 0) issue_xsb(st + NST - 1);   // copies only when (st + NST - 1) % 4 == 0
-                }
 #pragma unroll
                 for (int k = u * Q / U; k < (u + 1) * Q / U; k++) {
                     if constexpr (FIRST) issue_part(1 + k / P1, k % P1);
@@ -656,9 +842,6 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (WF == W_Q4K) {
-                if ((st & 3) == 3) q4k_epilogue(st);
-            }
         };
         if (nst > 0) body(0, std::true_type{}, std::true_type{});
         for (int64_t st = 1; st + 1 < nst; st++) body(st, std::true_type{}, std::false_type{});
@@ -673,9 +856,12 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const int64_t nfull = WF == W_Q32 ? (split > 1 ? nst : K / KC) : nst;
     if constexpr (WF == W_Q32) {
         q32_main(nfull);
+    } else if constexpr (WF == W_Q4K) {
+        q4k_main();
     } else if constexpr (PIPE16) {
         f16_main();
     } else {
+    // f16 weights whose tile leaves room for fewer than three stages: one barrier per stage
     for (int s = 0; s < NST - 1; s++)
         if (s < nst) issue(s);
 
@@ -689,38 +875,28 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     };
     for (int64_t st = 0; st < nfull; st++) {
         const unsigned char * base = stage_begin(st);
-        {
 #pragma unroll
-            for (int blk = 0; blk < 2; blk++) {
-                h8 a0[TI], a1[TI], b0[TJ], b1[TJ];
+        for (int blk = 0; blk < 2; blk++) {
+            h8 a0[TI], a1[TI], b0[TJ], b1[TJ];
 #pragma unroll
-                for (int i = 0; i < TI; i++) {
-                    const int r = 32 * (wn * TI + i) + l32;
-                    a0[i] = lds_chunk<h8>(base, r, 4 * blk + g);
-                    a1[i] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
-                }
+            for (int i = 0; i < TI; i++) {
+                const int r = 32 * (wn * TI + i) + l32;
+                a0[i] = lds_chunk<h8>(base, r, 4 * blk + g);
+                a1[i] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
+            }
+#pragma unroll
+            for (int j = 0; j < TJ; j++) {
+                const int r = BN + 32 * (wm * TJ + j) + l32;
+                b0[j] = lds_chunk<h8>(base, r, 4 * blk + g);
+                b1[j] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
+            }
+#pragma unroll
+            for (int i = 0; i < TI; i++)
 #pragma unroll
                 for (int j = 0; j < TJ; j++) {
-                    const int r = BN + 32 * (wm * TJ + j) + l32;
-                    b0[j] = lds_chunk<h8>(base, r, 4 * blk + g);
-                    b1[j] = lds_chunk<h8>(base, r, 4 * blk + 2 + g);
+                    acc[i][j] = MFMA16(a0[i], b0[j], acc[i][j]);
+                    acc[i][j] = MFMA16(a1[i], b1[j], acc[i][j]);
                 }
-#pragma unroll
-                for (int i = 0; i < TI; i++)
-#pragma unroll
-                    for (int j = 0; j < TJ; j++) {
-                        if constexpr (WF == W_F16) {
-                            acc[i][j] = MFMA16(a0[i], b0[j], acc[i][j]);
-                            acc[i][j] = MFMA16(a1[i], b1[j], acc[i][j]);
-                        } else {   // W_Q4K: integer sums over the 256-deep super-block
-                            ssb[i][j] = MFMA16(a0[i], b0[j], ssb[i][j]);
-                            ssb[i][j] = MFMA16(a1[i], b1[j], ssb[i][j]);
-                        }
-                    }
-            }
-        }
-        if constexpr (WF == W_Q4K) {
-            if ((st & 3) == 3) q4k_epilogue(st);
         }
     }
     }
@@ -849,11 +1025,13 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
 #pragma unroll
                 for (int i = 0; i < TI; i++) {
                     const int64_t nb = n0 + 32 * (wn * TI + i);
-                    _Float16 * o = (_Float16 *) a.ep.oh + m * a.N + nb + 4 * g;
+                    int8_t * o = (int8_t *) a.ep.oh + m * a.N + nb + 4 * g;
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const h4 hv = {(_Float16) v[i][4 * q], (_Float16) v[i][4 * q + 1], (_Float16) v[i][4 * q + 2], (_Float16) v[i][4 * q + 3]};
-                        *(h4 *) (o + 8 * q) = hv;
+                        uint32_t w = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) w |= ((uint32_t) (int) v[i][4 * q + e] & 0xffu) << (8 * e);
+                        *(uint32_t *) (o + 8 * q) = w;   // int8 codes
                     }
                     if (g == 0) {
                         _Float16 * ob = (_Float16 *) a.ep.ob + m * (a.N / 16) + nb / 16;
@@ -1036,24 +1214,29 @@ int cu_count() {
     return n;
 }
 
+// q4_K runs the tiles whose weight rows pair up into whole 1 KB copies (BN a multiple of 128) and whose
+// four accumulator sets per MFMA tile fit 256 VGPRs with two waves per SIMD (two MFMA tiles per wave)
+bool q4k_tile(int c) { return c == 2 || c == 3 || c == 5 || c == 6; }
+
 // The tile with the least estimated time: whole waves of workgroups over the CUs (one workgroup per
-// CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N; q4_K
-// skips the 256x128 tile (its three accumulator sets do not fit 256 VGPRs with two waves per SIMD).
+// CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N.
 int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
     const int f = g_force_tile.load();
     const int nt = (int) (sizeof(k_tiles) / sizeof(k_tiles[0]));
     const auto bn_of = [](int c) { return 32 * k_tiles[c].wn * k_tiles[c].ti; };
-    if (f >= 0 && f < nt && N % bn_of(f) == 0 && (need_bn == 0 || (bn_of(f) == need_bn && !(wf == W_Q4K && f == 0)))) return f;
+    if (f >= 0 && f < nt && N % bn_of(f) == 0 && (need_bn == 0 || bn_of(f) == need_bn) && (wf != W_Q4K || q4k_tile(f))) return f;
     const int cus = cu_count();
     double best = 1e300;
     int b = need_bn ? -1 : 5;
     for (int c = 0; c < nt; c++) {
         const int64_t bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
         if (N % bn || (need_bn && bn != need_bn)) continue;
-        if (wf == W_Q4K && c == 0) continue;
+        if (wf == W_Q4K && !q4k_tile(c)) continue;
         const int64_t t = (N / bn) * ((M + bm - 1) / bm) * split;
         const double waves = (double) ((t + cus - 1) / cus);
-        const double cost = waves * (double) (bn * bm) / k_tile_eff[c];
+        // q4_K unpacks a wave's weight operand once for its TJ token tiles
+        const double eff = wf == W_Q4K && k_tiles[c].tj == 1 && k_tiles[c].ti > 1 ? 0.8 * k_tile_eff[c] : k_tile_eff[c];
+        const double cost = waves * (double) (bn * bm) / eff;
         if (cost < best) { best = cost; b = c; }
     }
     return b;
@@ -1064,8 +1247,15 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
     const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm * (a.split > 1 ? a.split : 1));
     if constexpr (EPI == EPI_GELU_Q8_K) {   // 256-wide tiles only (pick_tile keeps to them)
         if (c == 6) k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a);
-        if constexpr (WF != W_Q4K)   // q4_K never takes the 256x128 tile
+        if constexpr (WF != W_Q4K)   // q4_K runs the 256x64 tile only
             if (c == 0) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a);
+    } else if constexpr (WF == W_Q4K) {
+        switch (c) {
+            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(a); break;
+            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(a); break;
+            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(a); break;
+            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a); break;
+        }
     } else {
         switch (c) {
             case 0: k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a); break;
@@ -1149,6 +1339,7 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
     a.A = (const _Float16 *) W.w;
     a.Ad = (const uint16_t *) W.wd;
     a.Amin = (const _Float16 *) W.wmin;
+    if (W.fmt == W_Q4K) a.Asc = (const uint8_t *) W.w + W.n_out * (W.n_in / 2);   // scales follow the codes
     a.B = (const _Float16 *) X.q;
     a.Bd = X.d;
     a.Bsum = (const _Float16 *) X.bsum;

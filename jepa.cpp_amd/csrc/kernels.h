@@ -2,8 +2,8 @@
 //
 // Data layouts in HBM (row-major unless stated):
 //   residual stream  x      f32 [rows][D]
-//   GEMM operands    W      int8 [N][K] codes (q8_0 q, q4_0 q-8); f16 [N][K] codes (q4_K sc*q) or f16 weights
-//                    X      int8 [M][K] q8_0 activation codes; f16 [M][K] q8_K codes or f16-rounded values
+//   GEMM operands    W      int8 [N][K] codes (q8_0 q, q4_0 q-8); 4-bit [N][K/2] q4_K codes; f16 weights
+//                    X      int8 [M][K] q8_0 / q8_K activation codes; f16 [M][K] f16-rounded values
 //   scales           q8_0   f16 [rows][K/32];  q8_K  f32 d [rows][K/256] + f16 bsums [rows][K/16]
 //   attention        Q, K   f16 [item*H][R_pad][hd];  V^T f16 [item*H][hd][R_pad] with the tokens of
 //                    every 16-token group stored in the order the PV MFMA reads them
@@ -13,7 +13,7 @@
 
 struct act_view {            // a GEMM activation operand / a quantizer output
     int       fmt = 0;       // afmt
-    void *    q = nullptr;   // int8 [M][K] (A_Q8_0), f16 [M][K] (A_F16 / A_Q8_K) or f32 [M][K] (A_F32)
+    void *    q = nullptr;   // int8 [M][K] (A_Q8_0 / A_Q8_K), f16 [M][K] (A_F16) or f32 [M][K] (A_F32)
     void *    d = nullptr;   // A_Q8_0: f16 [M][K/32]; A_Q8_K: f32 [M][K/256]
     void *    bsum = nullptr;// A_Q8_K: f16 [M][K/16]
     int64_t   ld = 0;        // K

@@ -339,7 +339,7 @@ struct loader {
             L.w = dalloc(t->nbytes + pad_bytes);
             if (!L.w || hipMemcpyAsync(L.w, staging, t->nbytes + pad_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
         } else {
-            L.w = dalloc((size_t) n_in * n_out * (L.fmt == W_Q32 ? 1 : 2));
+            L.w = dalloc(L.fmt == W_Q32 ? (size_t) n_in * n_out : (size_t) n_out * (n_in / 2) + (size_t) n_out * (n_in / 256) * 8);
             if (!L.w) return false;
             if (L.fmt == W_Q32) {
                 L.wd = dalloc((size_t) n_out * (n_in / 32) * 2);

@@ -1,5 +1,5 @@
 // misc.hip - bandwidth-bound kernels: LayerNorm + activation quantization, patchify, prefix rows,
-// load-time weight expansion, and small test hooks.
+// load-time weight repacking, and small test hooks.
 #include "kernels.h"
 #include "model.h"
 
@@ -215,10 +215,10 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
             for (int e = 0; e < 8; e++) bs += q[e];
             bs += dpp_f32<DPP_XOR1>(bs);   // the other 8 values of the 16-group
             if (live) {
-                h8 hv;
+                uint32_t qb[2] = {0u, 0u};
 #pragma unroll
-                for (int e = 0; e < 8; e++) hv[e] = (_Float16) q[e];
-                *(h8 *) ((_Float16 *) out.q + row * D + 8 * o) = hv;
+                for (int e = 0; e < 8; e++) qb[e >> 2] |= ((uint32_t) (int) q[e] & 0xffu) << (8 * (e & 3));
+                *(uint2 *) ((int8_t *) out.q + row * D + 8 * o) = make_uint2(qb[0], qb[1]);   // int8 codes
                 if ((o & 31) == 0) ((float *) out.d)[row * (D / 256) + o / 32] = d;
                 if ((o & 1) == 0) ((_Float16 *) out.bsum)[row * (D / 16) + o / 2] = (_Float16) bs;
             }
@@ -341,8 +341,16 @@ __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t * q, int & d,
     else { d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4); m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4); }
 }
 
-__global__ void k_repack_q4_K(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, _Float16 * w, uint32_t * wd,
-                              _Float16 * wmin) {
+// q4_K for the int8 GEMM, still 4 bits per weight: w [n_out][n_in/2] codes, then wsc [n_out][n_in/256][8]
+// sub-block scales (6-bit, as bytes), wd (d | dmin << 16) [n_in/256][n_out], wmin [n_out][n_in/256][16]
+// f16 mins (m_{k/2}, the operand of the mins MFMA). Codes: each 16-value half g of a 32-value sub-block
+// is 8 bytes, two dwords whose byte b holds values b (low nibble) and b + 4 (high nibble) of its first
+// and of its second eight values, so that (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F) are four
+// consecutive codes each, in the byte order of the activation codes. The four sub-blocks of each 128
+// values (64 B) lie as [g0: sb 0, 1] [g1: sb 0, 1] [g0: sb 2, 3] [g1: sb 2, 3], so that one 16-byte read
+// gives a lane two sub-blocks' halves.
+__global__ void k_repack_q4_K(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, uint8_t * w, uint8_t * wsc,
+                              uint32_t * wd, _Float16 * wmin) {
     const int64_t nsb = n_in / 256;
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= n_out * nsb) return;
@@ -352,17 +360,24 @@ __global__ void k_repack_q4_K(const uint8_t * __restrict__ raw, int64_t n_out, i
     wd[sb * n_out + n] = (uint32_t) blk[0] | ((uint32_t) blk[1] << 8) | ((uint32_t) blk[2] << 16) | ((uint32_t) blk[3] << 24);
     const uint8_t * sc = blk + 4;
     const uint8_t * qs = blk + 16;
-    _Float16 * dst = w + n * n_in + sb * 256;
+    uint8_t * dst = w + n * (n_in / 2) + sb * 128;
     for (int j = 0; j < 8; j++) {
         int s, m;
         q4k_scale_min(j, sc, s, m);
+        wsc[id * 8 + j] = (uint8_t) s;
         wmin[id * 16 + 2 * j] = (_Float16) (float) m;
         wmin[id * 16 + 2 * j + 1] = (_Float16) (float) m;
         const uint8_t * qq = qs + 32 * (j / 2);
-        for (int l = 0; l < 32; l++) {
-            const int q = (j & 1) ? (qq[l] >> 4) : (qq[l] & 0xF);
-            dst[32 * j + l] = (_Float16) (float) (s * q);
-        }
+        uint8_t q[32];
+        for (int l = 0; l < 32; l++) q[l] = (j & 1) ? (qq[l] >> 4) : (qq[l] & 0xF);
+        const int jl = j & 3;   // sub-block within its 128 values
+        uint8_t * d128 = dst + 64 * (j >> 2);
+        for (int h = 0; h < 2; h++)
+            for (int dw = 0; dw < 2; dw++)
+                for (int b = 0; b < 4; b++) {
+                    const int v = 16 * h + 8 * dw + b;
+                    d128[16 * (2 * (jl >> 1) + h) + 8 * (jl & 1) + 4 * dw + b] = (uint8_t) (q[v] | (q[v + 4] << 4));
+                }
     }
 }
 
@@ -398,7 +413,7 @@ __global__ void k_dequant(int gtype, const uint8_t * __restrict__ raw, int64_t n
     }
 }
 
-// activation operand (f16 codes + scales) -> ggml block bytes (q8_0: 34 B, q8_K: 292 B)
+// activation operand (int8 codes + scales) -> ggml block bytes (q8_0: 34 B, q8_K: 292 B)
 __global__ void k_pack_act(act_view a, int64_t M, int64_t K, uint8_t * out) {
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (a.fmt == A_Q8_0) {
@@ -417,7 +432,7 @@ __global__ void k_pack_act(act_view a, int64_t M, int64_t K, uint8_t * out) {
         const float d = ((const float *) a.d)[m * nb + bi];
         const uint32_t db = __builtin_bit_cast(uint32_t, d);
         for (int k = 0; k < 4; k++) o[k] = (uint8_t) (db >> (8 * k));
-        for (int j = 0; j < 256; j++) o[4 + j] = (uint8_t) (int8_t) (float) ((const _Float16 *) a.q)[m * K + bi * 256 + j];
+        for (int j = 0; j < 256; j++) o[4 + j] = (uint8_t) ((const int8_t *) a.q)[m * K + bi * 256 + j];
         for (int j = 0; j < 16; j++) {
             const int16_t s = (int16_t) (float) ((const _Float16 *) a.bsum)[m * (K / 16) + bi * 16 + j];
             o[260 + 2 * j] = (uint8_t) (s & 0xFF); o[261 + 2 * j] = (uint8_t) ((uint16_t) s >> 8);
@@ -509,8 +524,9 @@ void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, voi
     switch (gtype) {
         case T_Q8_0: k_repack_q8_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd); break;
         case T_Q4_0: k_repack_q4_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd); break;
-        case T_Q4_K: k_repack_q4_K<<<nblk(n_out * (n_in / 256), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (_Float16 *) w,
-                                                                                  (uint32_t *) wd, (_Float16 *) wmin); break;
+        case T_Q4_K: k_repack_q4_K<<<nblk(n_out * (n_in / 256), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (uint8_t *) w,
+                                                                                  (uint8_t *) w + n_out * (n_in / 2), (uint32_t *) wd,
+                                                                                  (_Float16 *) wmin); break;
         default: break;
     }
 }

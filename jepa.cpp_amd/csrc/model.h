@@ -84,9 +84,10 @@ struct hparams {
     std::vector<std::string> labels;
 };
 
-// Weight formats on the device. Quantized matrices are expanded once at load into the operand
+// Weight formats on the device. Quantized matrices are repacked once at load into the operand
 // layout of the GEMM kernel plus their scales: q8_0 / q4_0 as int8 codes (q; q - 8) for the int8
-// MFMA; q4_K as exact f16 values sc_j * q (the 6-bit sub-block scale folded in) for the f16 MFMA.
+// MFMA; q4_K stays 4-bit (codes regrouped for an in-register unpack, scales and mins split out) and
+// is unpacked in the GEMM for the int8 MFMA.
 enum wfmt { W_F32 = 0, W_F16 = 1, W_Q32 = 2 /* q8_0, q4_0: f16 scale per 32 */, W_Q4K = 3 };
 // Activation formats consumed by the GEMM (what the producer of a linear's input writes).
 enum afmt { A_F32 = 0, A_F16 = 1, A_Q8_0 = 2, A_Q8_K = 3 };
@@ -96,7 +97,8 @@ struct dev_linear {
     int      fmt = W_F32;
     int64_t  n_out = 0, n_in = 0;
     int64_t  n_valid = 0;         // outputs in the file (n_out is rounded up to 128 for the head's linears)
-    void *   w = nullptr;         // [n_out][n_in]: f32 (W_F32), int8 (W_Q32) or f16 (W_F16, W_Q4K)
+    void *   w = nullptr;         // [n_out][n_in]: f32 (W_F32), int8 (W_Q32), f16 (W_F16); W_Q4K: 4-bit codes
+                                  // [n_out][n_in/2] followed by the 6-bit sub-block scales [n_out][n_in/256][8]
     void *   wd = nullptr;        // W_Q32: f16 d [n_out][n_in/32]; W_Q4K: u32 (f16 d | f16 dmin << 16) [n_in/256][n_out]
     void *   wmin = nullptr;      // W_Q4K: f16 mins [n_out][n_in/256][16] (m_{k/2}, k = 0..15)
     float *  bias = nullptr;      // [n_out] or null
@@ -136,7 +138,7 @@ struct jepa_model {
     hparams hp;
     std::vector<std::pair<std::string, std::string>> raw_kv;
     int device = 0;                 // HIP device ordinal the weights live on
-    size_t n_bytes_weights = 0;     // device bytes of the expanded weights
+    size_t n_bytes_weights = 0;     // device bytes of the repacked weights
     size_t n_bytes_file = 0;        // tensor bytes in the file
     // encoder
     dev_linear patch, patch_img;

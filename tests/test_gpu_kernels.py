@@ -299,8 +299,10 @@ TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128
 @pytest.mark.parametrize("gtype", [gguf.GGML_Q8_0, gguf.GGML_Q4_0, gguf.GGML_Q4_K, gguf.GGML_F16])
 def test_matmul_every_tile(jlib, oracle, gtype, tile):
     """Every workgroup tile shape of the MFMA GEMM, forced, on a ragged token count (M = 389: partial
-    last tile, rows past M clamped) and K = 768 (12 stages, so the pipeline's prologue, steady state
-    and tail all run; three q4_K super-blocks). Block-quantized types bit-exact, f16 within f32 rounding."""
+    last tile, rows past M clamped) and K = 768 (6 or 12 stages, so the pipeline's prologue, steady
+    state and tail all run; three q4_K super-blocks). q4_K runs tiles 2, 3, 5 and 6 only (its weight
+    rows pair up in whole copies and four accumulator sets fit); forcing another tile leaves it on the
+    automatic choice. Block-quantized types bit-exact, f16 within f32 rounding."""
     bn = TILES[tile][0]
     n_out, n_in, M = bn * (3 if bn == 128 else 2) if bn != 64 else 256, 768, 389
     rng = np.random.default_rng(tile * 100 + gtype)
