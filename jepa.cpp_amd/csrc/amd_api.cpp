@@ -294,11 +294,14 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
                                   void * out) {
     if (!qkv || !out || n_items <= 0 || n_tok <= 0 || n_head <= 0 || n_prefix < 0 || tokens_per_slot < 0 ||
         n_tok > 0x40000000) return -1;
-    if (hd != 64 && hd != 32) { jepa_log("jepa: jepa_amd_attention: head width %d (64 or 32)\n", hd); return -1; }
-    if (out_type != T_F32 && out_type != T_Q8_0) { jepa_log("jepa: jepa_amd_attention: output type %d\n", out_type); return -1; }
+    if (!attention_supports(hd)) { jepa_log("jepa: jepa_amd_attention: head width %d (a multiple of 16 up to 128)\n", hd); return -1; }
+    if (out_type != T_F32 && !(out_type == T_Q8_0 && (hd == 64 || hd == 32))) {
+        jepa_log("jepa: jepa_amd_attention: output type %d for head width %d\n", out_type, hd);
+        return -1;
+    }
     dev_scope d(device);
     if (!d.ok) return -1;
-    const int hds = 64;   // stored head width
+    const int hds = attention_stored_width(hd);   // stored head width
     const int64_t R_pad = (n_tok + 127) / 128 * 128;
     const size_t bytes = (size_t) n_items * n_head * R_pad * hds * 2;
     void * q = d.alloc(bytes), * k = d.alloc(bytes), * vt = d.alloc(bytes);

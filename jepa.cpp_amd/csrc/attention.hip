@@ -1,4 +1,5 @@
-// attention.hip - flash attention forward for head_dim 64 on gfx950 (f16 MFMA, f32 softmax).
+// attention.hip - flash attention forward on gfx950 (f16 MFMA, f32 softmax): head width 64 (and 32
+// stored 64 wide) in the LDS-staged kernel below, other multiples of 16 up to 128 in k_attn_any.
 //
 // Computes softmax(Q K^T * scale) V per (item, head): the ggml_flash_attn_ext of reference
 // src/jepa.cpp:416-442 (no mask, K/V in f16 as the reference's ggml_cast does, f32 softmax and f32
@@ -273,16 +274,127 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     }
 }
 
+// Head widths other than 32 and 64 (80 for I-JEPA ViT-H/14): heads stored HDS = 32 * NDT wide with
+// zero padding past hd (Q, K [head][R_pad][HDS], V^T [head][HDS][R_pad] in the PV order of the 16-token
+// groups, as the QKV epilogue writes them). One workgroup = 4 waves = 128 queries of one head, each wave
+// 32 queries over every key; K and V^T operands are read straight from global memory (L2), which suits
+// the short sequences these models run (256 tokens at 224^2). The arithmetic per 32-key block is the
+// fast kernel's: S^T = K . Q^T over NKK = ceil(hd / 16) dim steps (the padded dims are zero), the lazy
+// online softmax in the exp2 form, O^T += V^T . P^T over NDT 32-dim row blocks. f32 output only: q8_0
+// blocks of 32 dims would span heads.
+template <int NKK, int NDT>
+__global__ __launch_bounds__(256) void k_attn_any(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
+                                                  const _Float16 * __restrict__ Vt, float * __restrict__ O, int n_head,
+                                                  int hd, int64_t R, int64_t R_pad, float c, int np, int tpf) {
+    constexpr int HDS = 32 * NDT;
+    static_assert(NKK * 16 <= HDS, "dim steps inside the stored width");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, g = lane >> 5;
+    const int64_t head = blockIdx.y;
+    const int64_t item = head / n_head;
+    const int h = (int) (head - item * n_head);
+    const int64_t q0 = (int64_t) blockIdx.x * 128 + 32 * wave;
+    if (q0 >= R) return;                                  // whole wave past the last query
+    const _Float16 * Qh = Q + head * R_pad * HDS;
+    const _Float16 * Kh = Kp + head * R_pad * HDS;
+    const _Float16 * Vh = Vt + head * HDS * R_pad;
+
+    h8 qv[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; kk++) qv[kk] = *(const h8 *) (Qh + (q0 + l32) * HDS + 16 * kk + 8 * g);
+
+    const f16v zero = {0};
+    f16v acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) acc[dt] = zero;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int2 kr = key_range((int) q0 + l32, (int) R, np, tpf);
+    const int qw = (int) q0;
+    const int lo_min = key_range(qw, (int) R, np, tpf).x;
+    const int hi_max = qw < np ? (int) R : key_range(min(qw + 31, (int) R - 1), (int) R, np, tpf).y;
+    for (int kb0 = (lo_min / 32) * 32; kb0 < hi_max; kb0 += 32) {
+        f16v S = zero;
+#pragma unroll
+        for (int kk = 0; kk < NKK; kk++) S = MFMA16(*(const h8 *) (Kh + (int64_t) (kb0 + l32) * HDS + 16 * kk + 8 * g), qv[kk], S);
+        const int key0 = kb0 + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int key = key0 + 8 * (r >> 2) + (r & 3);
+            if (key < kr.x || key >= kr.y) S[r] = -INFINITY;
+        }
+        float mloc = S[0];
+#pragma unroll
+        for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, S[r]);
+        mloc = halves_max(mloc);
+        if (mloc > m_run && (m_run == -INFINITY || (mloc - m_run) * c > LAZY)) {
+            const float alpha = fast_exp2((m_run - mloc) * c);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[dt][r] *= alpha;
+            m_run = mloc;
+        }
+        const float mc = m_run == -INFINITY ? 0.0f : m_run * c;
+        float p[16], lsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) { p[r] = fast_exp2(fmaf(S[r], c, -mc)); lsum += p[r]; }
+        lsum = halves_sum(lsum);
+        l_run += lsum;
+#pragma unroll
+        for (int kk2 = 0; kk2 < 2; kk2++) {
+            h8 pb;
+#pragma unroll
+            for (int e = 0; e < 8; e++) pb[e] = (_Float16) p[8 * kk2 + e];
+            // V^T row d, keys kb0 + 16 kk2 + 8 g .. + 8 in the order of the S lanes (see the header)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                acc[dt] = MFMA16(*(const h8 *) (Vh + (int64_t) (32 * dt + l32) * R_pad + kb0 + 16 * kk2 + 8 * g), pb, acc[dt]);
+        }
+    }
+    const int64_t q = q0 + l32;
+    if (q >= R) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    float * orow = O + (item * R + q) * ((int64_t) n_head * hd) + (int64_t) h * hd;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const int d = 32 * dt + 8 * qq + 4 * g;
+            if (d < hd)   // hd is a multiple of 16: a group of four is inside or outside as a whole
+                *(float4 *) (orow + d) = make_float4(acc[dt][4 * qq] * inv, acc[dt][4 * qq + 1] * inv, acc[dt][4 * qq + 2] * inv,
+                                                     acc[dt][4 * qq + 3] * inv);
+        }
+}
+
 }  // namespace
+
+int attention_stored_width(int hd) { return hd <= 64 ? 64 : (hd + 31) / 32 * 32; }
+
+bool attention_supports(int hd) { return hd == 32 || hd == 64 || (hd > 0 && hd <= 128 && hd % 16 == 0); }
 
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items,
                       int n_head, int hd, int64_t R, int64_t R_pad, float scale, int n_prefix, int64_t tokens_per_slot,
                       hipStream_t s) {
-    // hd: 64, or 32 (stored 64 wide; checked by the callers)
+    // hd: 64, or 32 (stored 64 wide), or a multiple of 16 up to 128 stored attention_stored_width(hd)
+    // wide (f32 output; checked by the callers)
     const float c = scale * 1.4426950408889634f;   // exp(x*scale) = exp2(x*scale*log2(e))
     const int tpf = (int) tokens_per_slot;
     dim3 grid((unsigned) ((R + QB - 1) / QB), (unsigned) (n_items * n_head));
     const _Float16 * Q = (const _Float16 *) q, * K = (const _Float16 *) k, * V = (const _Float16 *) vt;
+    if (hd != 32 && hd != 64) {
+        float * o = (float *) out.q;
+        switch ((hd + 15) / 16) {
+            case 1: k_attn_any<1, 2><<<grid, 256, 0, s>>>(Q, K, V, o, n_head, hd, R, R_pad, c, n_prefix, tpf); break;
+            case 3: k_attn_any<3, 2><<<grid, 256, 0, s>>>(Q, K, V, o, n_head, hd, R, R_pad, c, n_prefix, tpf); break;
+            case 5: k_attn_any<5, 3><<<grid, 256, 0, s>>>(Q, K, V, o, n_head, hd, R, R_pad, c, n_prefix, tpf); break;
+            case 6: k_attn_any<6, 3><<<grid, 256, 0, s>>>(Q, K, V, o, n_head, hd, R, R_pad, c, n_prefix, tpf); break;
+            case 7: k_attn_any<7, 4><<<grid, 256, 0, s>>>(Q, K, V, o, n_head, hd, R, R_pad, c, n_prefix, tpf); break;
+            case 8: k_attn_any<8, 4><<<grid, 256, 0, s>>>(Q, K, V, o, n_head, hd, R, R_pad, c, n_prefix, tpf); break;
+            default: break;
+        }
+        return;
+    }
     if (out.fmt == A_Q8_0) {
         if (hd == 32) k_attn_hd64<A_Q8_0, 32><<<grid, 512, 0, s>>>(Q, K, V, out.q, out.d, n_head, R, R_pad, c, n_prefix, tpf);
         else k_attn_hd64<A_Q8_0, 64><<<grid, 512, 0, s>>>(Q, K, V, out.q, out.d, n_head, R, R_pad, c, n_prefix, tpf);

@@ -122,7 +122,7 @@ bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, i
 blk_shape enc_blk_shape(const jepa_model * m) {
     const enc_hparams & e = m->hp.enc;
     blk_shape b;
-    b.D = e.embed_dim; b.H = e.n_head; b.hd = e.head_dim(); b.hds = std::max(b.hd, 64); b.eps = e.ln_eps;
+    b.D = e.embed_dim; b.H = e.n_head; b.hd = e.head_dim(); b.hds = attention_stored_width(b.hd); b.eps = e.ln_eps;
     return b;
 }
 
@@ -172,7 +172,7 @@ void enqueue_block(const blk_shape & b, const dev_layer & L, fwd_workspace & w, 
         kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
     }
     w.actA.fmt = L.out.act();
-    if (w.actA.fmt == A_Q8_0) {
+    if (w.actA.fmt == A_Q8_0 && (hd == 64 || hd == 32)) {
         // the attention epilogue writes the out-projection's q8_0 input directly
         kt.run("attention", [&] {
             launch_attention(w.Q, w.Kt, w.Vt, w.actA, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
@@ -314,8 +314,9 @@ bool check_supported(const jepa_model * m) {
         jepa_log("jepa: jepa_encode: family '%s' is not implemented on this path\n", m->hp.family_str.c_str());
         return false;
     }
-    if (e.head_dim() != 64) {
-        jepa_log("jepa: jepa_encode: head_dim %d is not supported by the attention kernel (64 only)\n", e.head_dim());
+    if (e.n_head * e.head_dim() != e.embed_dim || !attention_supports(e.head_dim())) {
+        jepa_log("jepa: jepa_encode: head_dim %d (embed_dim %d / %d heads) is not supported by the attention kernels "
+                 "(a multiple of 16 up to 128)\n", e.head_dim(), e.embed_dim, e.n_head);
         return false;
     }
     if (e.embed_dim % 256 != 0 && e.embed_dim % 128 != 0) {

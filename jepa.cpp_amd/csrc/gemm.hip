@@ -1085,6 +1085,17 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                     if (g == 0) ((uint16_t *) a.ep.od)[m * (a.N / 32) + nb / 32] = f2hbits(d);
                 }
             } else if constexpr (EPI == EPI_QKV) {
+                if (a.ep.hd & 31) {
+                    // head widths that are not a multiple of 32 (80 = I-JEPA ViT-H): a tile's 32 features
+                    // can span two heads, so head and offset are found per group of four features
+                    if (m >= M) continue;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float t[4] = {acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                        epi4<EPI_QKV>(a, m, nb + 8 * q + 4 * g, t);
+                    }
+                    continue;
+                }
                 // the tile's 32 features lie in one head of one of Q, K, V (D and hd are multiples of 32):
                 // head and offset are wave-uniform, the token is one 32-bit division per lane
                 const gemm_epi & ep = a.ep;

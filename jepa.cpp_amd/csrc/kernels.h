@@ -78,6 +78,10 @@ void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w
 // key. tokens_per_slot = 0: full attention.
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items, int n_head,
                       int hd, int64_t R, int64_t R_pad, float scale, int n_prefix, int64_t tokens_per_slot, hipStream_t s);
+// Head widths the attention runs: 32, 64, and other multiples of 16 up to 128 (f32 output only); the
+// width Q, K and V^T are stored with (64 for hd <= 64, else hd rounded up to 32; the rest zero).
+bool attention_supports(int hd);
+int attention_stored_width(int hd);
 
 // Single-query attention of the attentive-pool head: y = softmax(q . K^T * scale) V + q0 per head
 // (hd 64), q / q0 / y [n_head * hd], K / V f32 rows [N][ld]. `part` holds pool_attention_part_floats

@@ -22,7 +22,7 @@ from .gguf import (FTYPE, GGML_F16, GGML_F32, GGML_Q4_0, GGML_Q4_K, GGML_Q8_0, G
 @dataclass(frozen=True)
 class EncoderConfig:
     name: str
-    family: str            # hfvit | vjepa2 | vjepa2_1 | levjepa
+    family: str            # hfvit | ijepa | vjepa2 | vjepa2_1 | levjepa
     embed_dim: int
     n_layer: int
     n_head: int
@@ -85,6 +85,12 @@ CONFIGS = {
                                       pred_dim=384, pred_layers=12, pred_ffn=1536),
     "vitg16_q8_0": EncoderConfig("vjepa2-vitg16-256-synthetic", "vjepa2", 1408, 40, 22, 6144, patch=16, tubelet=2,
                                  img_size=256, n_frames=64, ftype="q8_0", rope_layout="tiled"),
+    # I-JEPA ViT-H/14 224x224 (facebook/ijepa_vith14_1k's shape: 16 x 16 = 256 patch tokens, no CLS, learned /
+    # sincos position table, D 1280, 16 heads of 80, MLP 5120, 32 layers, f32 patch embedding of 588 inputs)
+    "vith14_ijepa_f16": EncoderConfig("ijepa-vith14-224-synthetic", "ijepa", 1280, 32, 16, 5120, patch=14, img_size=224,
+                                      ftype="f16"),
+    "vith14_ijepa_q8_0": EncoderConfig("ijepa-vith14-224-synthetic", "ijepa", 1280, 32, 16, 5120, patch=14,
+                                       img_size=224, ftype="q8_0"),
 }
 
 
@@ -99,6 +105,8 @@ def tiny(family: str, ftype: str, **kw) -> EncoderConfig:
         base = EncoderConfig("tiny-vjepa2_1", "vjepa2_1", 128, 2, 2, 512, patch=16, tubelet=2, img_size=64,
                              n_frames=4, ftype=ftype, rope_layout="interleaved", rope_interpolate=True,
                              rope_ref_grid=16, modality_embed=True, image_patch_embed=True)
+    elif family == "ijepa":   # heads of 80, patch 14 (588 patch inputs)
+        base = EncoderConfig("tiny-ijepa", "ijepa", 640, 2, 8, 2560, patch=14, img_size=112, ftype=ftype)
     elif family == "levjepa":
         base = EncoderConfig("tiny-levjepa", "levjepa", 128, 2, 2, 512, patch=16, tubelet=1, img_size=64, n_frames=4,
                              cls_token=True, ftype=ftype, rope_layout="tiled", attn_mode="block_causal")

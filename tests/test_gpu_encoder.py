@@ -51,14 +51,21 @@ TINY = [("hfvit", "f16", 2, 1, 64), ("hfvit", "q8_0", 1, 2, 64), ("vjepa2", "q8_
         ("vjepa2", "q4_0", 2, 4, 64), ("vjepa2", "f16", 1, 4, 64), ("vjepa2_1", "q8_0", 2, 1, 64), ("vjepa2_1", "q8_0", 1, 4, 64),
         # LeVJEPA: CLS + block-causal mask; 65 rows (one query block), and 8 x 64 + 1 = 513 rows (five query
         # blocks whose temporal slots straddle key tiles), two clips in one call
-        ("levjepa", "q8_0", 1, 4, 64), ("levjepa", "f16", 2, 8, 128), ("levjepa", "q4_k", 1, 4, 64)]
+        ("levjepa", "q8_0", 1, 4, 64), ("levjepa", "f16", 2, 8, 128), ("levjepa", "q4_k", 1, 4, 64),
+        # I-JEPA shape: heads of 80 (the generic-width attention kernel, per-group QKV epilogue, attention
+        # output quantized separately), patch 14 (588 f32 patch inputs); q4_k falls back to q4_0 on the
+        # 640-wide rows, as the reference quantizer does
+        ("ijepa", "f16", 2, 1, 112), ("ijepa", "q8_0", 1, 1, 112), ("ijepa", "q4_k", 1, 1, 112)]
 
 
 @pytest.mark.parametrize("family,ftype,n_batch,n_frames,size", TINY)
 def test_tiny_encoder_parity(jlib, oracle, models_dir, family, ftype, n_batch, n_frames, size):
-    cfg = forge.tiny(family, ftype, ln_random=True, layer_scale=(ftype == "q4_0"),
-                     ffn_dim=1024 if ftype == "q4_k" else 512, embed_dim=256 if ftype == "q4_k" else 128,
-                     n_head=4 if ftype == "q4_k" else 2)
+    if family == "ijepa":
+        cfg = forge.tiny(family, ftype, ln_random=True)
+    else:
+        cfg = forge.tiny(family, ftype, ln_random=True, layer_scale=(ftype == "q4_0"),
+                         ffn_dim=1024 if ftype == "q4_k" else 512, embed_dim=256 if ftype == "q4_k" else 128,
+                         n_head=4 if ftype == "q4_k" else 2)
     got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, n_batch, n_frames, size)
     check_parity(got, want, gtr, wtr, label=f"{family}/{ftype}")
 
@@ -93,6 +100,18 @@ def test_vits16_f16_full(jlib, oracle, models_dir):
     got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, forge.CONFIGS["vits16_f16"], 1, 1, 224)
     assert got.shape == (197, 384)
     check_parity(got, want, gtr, wtr, label="vits16_f16")
+
+
+def test_vith14_ijepa_f16_full(jlib, oracle, models_dir):
+    """I-JEPA ViT-H/14 224x224 (256 tokens, 32 layers, D 1280, 16 heads of 80, patch 14), the shape the
+    reference benchmarks (docs/benchmarks.md:60-65), end to end in f16; mean-pooled as the reference's
+    jepa-embed does for this family. (q8_0: test_gpu_parity.py, per layer and end to end.)"""
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, forge.CONFIGS["vith14_ijepa_f16"], 1, 1, 224)
+    assert got.shape == (256, 1280)
+    check_parity(got, want, gtr, wtr, label="vith14_ijepa_f16")
+    pooled = m.pool_mean(got)
+    c = cos_rows(pooled[None], want.astype(np.float64).mean(0)[None])[0]
+    assert c >= 0.9999, c
 
 
 def test_vitg16_64f_q8_0_first_blocks(jlib, oracle, models_dir):

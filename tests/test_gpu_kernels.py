@@ -422,6 +422,36 @@ def test_attention_hd32(jlib, oracle, n_items, n_tok, H, rope):
     np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))
 
 
+# other head widths (multiples of 16 up to 128, stored rounded up to 32 with zero padding): 80 is I-JEPA
+# ViT-H/14's (16 heads of 80, 256 tokens, RoPE from the reference's hd-80 table layout); 48 and 128 bound
+# the range. Against the double softmax; the q8_0 output is refused (its 32-dim blocks would span heads).
+@pytest.mark.parametrize("n_items,n_tok,H,hd,rope", [(1, 256, 16, 80, False), (2, 197, 3, 80, True), (1, 130, 2, 48, False),
+                                                     (1, 300, 2, 128, True), (1, 33, 1, 80, False)])
+def test_attention_other_widths(jlib, oracle, n_items, n_tok, H, hd, rope):
+    rng = np.random.default_rng(n_tok + 7 * H + hd)
+    D = H * hd
+    qkv = (rng.standard_normal((n_items * n_tok, 3 * D)) * 1.5).astype(np.float32)
+    rc = rs = None
+    if rope:
+        c, s = oracle.rope_tables((1, 1, n_tok), hd, variant=0)
+        rc, rs = dev(c), dev(s)
+    out = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
+    dq = dev(qkv)
+    L = jlib.lib()
+    r = L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, hd, rc.data_ptr() if rope else None,
+                             rs.data_ptr() if rope else None, 0, 0, 0, out.data_ptr())
+    assert r == 0, jlib.error_text()
+    got = host(out).astype(np.float64)
+    ref = _attention_ref(qkv, n_items, n_tok, H, (c.astype(np.float64), s.astype(np.float64)) if rope else None, hd=hd)
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    cos = (got * ref).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(ref, axis=1))
+    assert rel <= 1e-2, rel
+    assert cos.min() >= 0.9999, cos.min()
+    oq = torch.zeros((n_items * n_tok, D // 32 * 34 + 34), dtype=torch.uint8, device="cuda")
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, hd, None, None, 0, 0, gguf.GGML_Q8_0, oq.data_ptr()) == -1
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 72, None, None, 0, 0, 0, out.data_ptr()) == -1
+
+
 # block-causal (LeVJEPA) shapes (n_items, gt, gh, gw, n_prefix, H): the reference's mask KAT shape (65
 # rows), 513 rows (five query blocks; slots of 64 rows against tiles of 64 keys shifted by the CLS),
 # slots of 35 rows with no prefix, and the 16 x 224^2 clip (3137 rows, slots of 196)

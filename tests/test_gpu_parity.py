@@ -1,11 +1,12 @@
 """Full-size encoders on the GPU (through the C ABI) against the CPU oracle, on the benchmark
 configurations: V-JEPA 2 ViT-L/16 16f q8_0 and q4_K, V-JEPA 2.1 ViT-B/16 384^2 at batch 8, LeVJEPA
-ViT-L/16 16f 224^2 (block-causal, 3137 rows); plus the pooled outputs of C1 (CLS) and C3 (mean).
+ViT-L/16 16f 224^2 (block-causal, 3137 rows), I-JEPA ViT-H/14 224^2 q8_0 (32 layers, heads of 80); plus the
+pooled outputs of C1 (CLS) and C3 (mean).
 
 Three views of the same forward:
 
 1. End to end, against the oracle with the reference's CPU arithmetic: token cosine >= 0.9999 (the
-   fixed bar). Quantized activations amplify last-bit differences over 12-24 layers (an int8 / q8_K
+   fixed bar). Quantized activations amplify last-bit differences over 12-32 layers (an int8 / q8_K
    code flips when its input crosses a rounding boundary), so two equally valid summation orders of
    the oracle itself already differ by about 1e-4 in cosine on these models; where that puts the bar
    out of reach the case is marked as a known failure with the measured numbers, not relaxed.
@@ -29,6 +30,7 @@ FULL = {
     "vitl16_q4_k": (1, 16, 256, 2048),
     "vitb16_2_1_q8_0": (8, 1, 384, 576),
     "levjepa_vitl16_q8_0": (1, 16, 224, 3137),
+    "vith14_ijepa_q8_0": (1, 1, 224, 256),
 }
 
 # End-to-end cosine below the fixed bar, with the oracle's own order-to-order distance that shows why
@@ -38,6 +40,8 @@ KNOWN_E2E = {
                    "reaches only cosine 0.99983, below 0.9999",
     "levjepa_vitl16_q8_0": "3137 rows x 24 layers of q8_0 activations: the oracle against itself in reversed "
                            "summation order reaches cosine 0.99990, at the bar",
+    "vith14_ijepa_q8_0": "32 layers of q8_0 activations: the oracle against itself in reversed summation order "
+                         "reaches only cosine 0.99988, below 0.9999",
 }
 
 _cache = {}
