@@ -993,7 +993,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
 #pragma unroll
                 for (int r = 15; r >= 0; r--)
                     if (fabsf(v[i][r]) == am)
-                        key = 2u * (uint32_t) (64 * wn + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3)) + (__float_as_uint(v[i][r]) >> 31);
+                        key = 2u * (uint32_t) (32 * (wn * TI + i) + 8 * (r >> 2) + 4 * g + (r & 3)) + (__float_as_uint(v[i][r]) >> 31);
             key = halves_min_u32(key);
             const int slot = ((j * WM + wm) * 32 + l32) * WN;
             if (g == 0) { xmax[slot + wn] = am; xkey[slot + wn] = key; }
@@ -1204,10 +1204,12 @@ __global__ void k_qkv_split(kargs a, const float * __restrict__ qkv) {
 
 struct tile_cfg { int wn, wm, ti, tj; };
 // eight-wave workgroup tiles (BN x BM): 256x128, 192x128, 128x128 (two wave shapes), 64x128, 128x64,
-// 256x64
-constexpr tile_cfg k_tiles[] = {{4, 2, 2, 2}, {2, 4, 3, 1}, {2, 4, 2, 1}, {4, 2, 1, 2}, {2, 4, 1, 1}, {4, 2, 1, 1}, {4, 2, 2, 1}};
+// 256x64 (two wave shapes; the second, one weight tile and two token tiles per wave, only for the
+// 256-feature q8_K epilogue)
+constexpr tile_cfg k_tiles[] = {{4, 2, 2, 2}, {2, 4, 3, 1}, {2, 4, 2, 1}, {4, 2, 1, 2}, {2, 4, 1, 1}, {4, 2, 1, 1}, {4, 2, 2, 1},
+                                {8, 1, 1, 2}};
 // relative efficiency of one workgroup tile (larger tiles re-read less from L2 and LDS)
-constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66, 0.8};
+constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66, 0.8, 0.8};
 
 std::atomic<int> g_force_tile{-1};
 std::atomic<int> g_force_split{-1};
@@ -1227,7 +1229,7 @@ int cu_count() {
 
 // q4_K runs the tiles whose weight rows pair up into whole 1 KB copies (BN a multiple of 128) and whose
 // four accumulator sets per MFMA tile fit 256 VGPRs with two waves per SIMD (two MFMA tiles per wave)
-bool q4k_tile(int c) { return c == 2 || c == 3 || c == 5 || c == 6; }
+bool q4k_tile(int c) { return c == 2 || c == 3 || c == 5 || c == 6 || c == 7; }
 
 // The tile with the least estimated time: whole waves of workgroups over the CUs (one workgroup per
 // CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N.
@@ -1235,13 +1237,14 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
     const int f = g_force_tile.load();
     const int nt = (int) (sizeof(k_tiles) / sizeof(k_tiles[0]));
     const auto bn_of = [](int c) { return 32 * k_tiles[c].wn * k_tiles[c].ti; };
-    if (f >= 0 && f < nt && N % bn_of(f) == 0 && (need_bn == 0 || bn_of(f) == need_bn) && (wf != W_Q4K || q4k_tile(f))) return f;
+    if (f >= 0 && f < nt && N % bn_of(f) == 0 && (need_bn == 0 || bn_of(f) == need_bn) && (wf != W_Q4K || q4k_tile(f)) &&
+        (f != 7 || need_bn == 256)) return f;
     const int cus = cu_count();
     double best = 1e300;
     int b = need_bn ? -1 : 5;
     for (int c = 0; c < nt; c++) {
         const int64_t bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
-        if (N % bn || (need_bn && bn != need_bn)) continue;
+        if (N % bn || (need_bn && bn != need_bn) || (c == 7 && need_bn != 256)) continue;
         if (wf == W_Q4K && !q4k_tile(c)) continue;
         const int64_t t = (N / bn) * ((M + bm - 1) / bm) * split;
         const double waves = (double) ((t + cus - 1) / cus);
@@ -1258,6 +1261,7 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
     const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm * (a.split > 1 ? a.split : 1));
     if constexpr (EPI == EPI_GELU_Q8_K) {   // 256-wide tiles only (pick_tile keeps to them)
         if (c == 6) k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a);
+        if (c == 7) k_gemm_mfma<WF, EPI, 8, 1, 1, 2><<<grid, 512, 0, s>>>(a);
         if constexpr (WF != W_Q4K)   // q4_K runs the 256x64 tile only
             if (c == 0) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a);
     } else if constexpr (WF == W_Q4K) {

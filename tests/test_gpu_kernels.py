@@ -180,14 +180,16 @@ def _q8k_blocks(raw, n_rows, n_cols):
     return d, q, bs
 
 
-@pytest.mark.parametrize("gtype,out_type", [(gguf.GGML_Q4_K, gguf.GGML_Q8_K), (gguf.GGML_Q8_0, gguf.GGML_Q8_K),
-                                            (gguf.GGML_F16, gguf.GGML_Q8_K), (gguf.GGML_Q8_0, gguf.GGML_Q8_0),
-                                            (gguf.GGML_Q4_0, gguf.GGML_F32)])
-def test_matmul_gelu_epilogue(jlib, oracle, gtype, out_type):
+@pytest.mark.parametrize("gtype,out_type,tile", [(gguf.GGML_Q4_K, gguf.GGML_Q8_K, -1), (gguf.GGML_Q4_K, gguf.GGML_Q8_K, 6),
+                                                 (gguf.GGML_Q8_0, gguf.GGML_Q8_K, -1), (gguf.GGML_Q8_0, gguf.GGML_Q8_K, 7),
+                                                 (gguf.GGML_F16, gguf.GGML_Q8_K, -1), (gguf.GGML_Q8_0, gguf.GGML_Q8_0, -1),
+                                                 (gguf.GGML_Q4_0, gguf.GGML_F32, -1)])
+def test_matmul_gelu_epilogue(jlib, oracle, gtype, out_type, tile):
     """fc1 with its fused epilogue: gelu_erf(X W^T + b) quantized for fc2 in the GEMM (q8_K: one
-    256-block per workgroup row, cross-wave max in LDS). Against the oracle's exact GEMM, libm GELU and
-    ggml quantizer: the GPU's erff and libm's may round differently, so a code can differ where a value
-    sits at a rounding tie; rows 256..511 of W and b are zero (all-zero blocks, d = 0). M = 389 is
+    256-block per workgroup row of waves, cross-wave max in LDS; both 256-wide tiles, 4 waves of 64
+    features (tile 6) and 8 waves of 32 (tile 7, q4_K's default)). Against the oracle's exact GEMM, libm
+    GELU and ggml quantizer: the GPU's erff and libm's may round differently, so a code can differ where
+    a value sits at a rounding tie; rows 256..511 of W and b are zero (all-zero blocks, d = 0). M = 389 is
     ragged. The q8_K output must also hold its own invariants: bsums = sums of the codes, and the block
     maximum coded as -127 at its first position."""
     n_out, n_in, M = 768, 512 if gtype != gguf.GGML_Q4_K else 768, 389
@@ -206,8 +208,13 @@ def test_matmul_gelu_epilogue(jlib, oracle, gtype, out_type):
     else:
         out = torch.zeros(oracle.quantize_act(out_type, ref[:1]).size * M, dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
-    rc = jlib.lib().jepa_amd_matmul_gelu(0, gtype, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, out_type, out.data_ptr(),
-                                         1, None)
+    L = jlib.lib()
+    assert L.jepa_amd_gemm_tile(tile) == 0
+    try:
+        rc = L.jepa_amd_matmul_gelu(0, gtype, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, out_type, out.data_ptr(), 1,
+                                    None)
+    finally:
+        L.jepa_amd_gemm_tile(-1)
     assert rc == 0, jlib.error_text()
     got = host(out)
     if out_type == gguf.GGML_F32:
@@ -292,7 +299,7 @@ def test_matmul_split_k(jlib, oracle, gtype, shape, M):
 
 
 # workgroup tiles of the MFMA GEMM (weight rows x tokens), by index
-TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64), 6: (256, 64)}
+TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64), 6: (256, 64), 7: (256, 64)}
 
 
 @pytest.mark.parametrize("tile", sorted(TILES))
