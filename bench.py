@@ -87,8 +87,8 @@ def time_forward(path, x_host, steps, warmup, kernel_pass=True):
             ctx.encode_device(xin.data_ptr(), x_host.shape, out.data_ptr(), out.numel())
         torch.cuda.synchronize()
         stats = {}
-        classes = ["patchify", "patch_embed", "layernorm", "gemm_q8", "gemm_q4k", "gemm_f16", "attention", "quantize"]
-        classes += [f"{g}.{r}" for g in ("gemm_q8", "gemm_q4k", "gemm_f16") for r in ("qkv", "out", "up", "down")]
+        classes = ["patchify", "patch_embed", "layernorm", "gemm_q8", "gemm_q4_0", "gemm_q4k", "gemm_f16", "attention", "quantize"]
+        classes += [f"{g}.{r}" for g in ("gemm_q8", "gemm_q4_0", "gemm_q4k", "gemm_f16") for r in ("qkv", "out", "up", "down")]
         for cls in classes:
             n, ms = ctx.kernel_stats(cls)
             if n:

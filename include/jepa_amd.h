@@ -151,7 +151,8 @@ int jepa_amd_copy(int device, const float * src_dev, float * dst_dev, int64_t n,
 /* Force the MFMA GEMM onto workgroup tile `index` for later launches whose n_out it divides; -1
  * restores the automatic choice. Process-wide (tests and tuning). Tiles (weight rows x tokens):
  * 0: 256x128, 1: 192x128, 2: 128x128, 3: 128x128 (other wave shape), 4: 64x128, 5: 128x64, 6: 256x64,
- * 7: 256x64 (other wave shape; only for the q8_K GELU epilogue). q4_K weights run tiles 2, 3, 5, 6 and 7;
+ * 7: 256x64 (other wave shape; only for the q8_K GELU epilogue), 8: 384x64 (4-bit q4_0 only). q4_K
+ * weights run tiles 2, 3, 5, 6 and 7, 4-bit q4_0 (rows a multiple of 128) tiles 0, 2, 3, 5, 6, 7 and 8;
  * a tile a launch cannot take leaves that launch on the automatic choice.
  * Returns 0, or -1 for an index past the table. */
 int jepa_amd_gemm_tile(int index);

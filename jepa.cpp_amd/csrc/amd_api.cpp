@@ -170,13 +170,8 @@ namespace {
 bool make_linear(dev_scope & d, const char * who, int wtype, const void * w, int64_t n_out, int64_t n_in, const float * bias,
                  dev_linear & L) {
     L.gtype = wtype; L.n_out = n_out; L.n_in = n_in; L.bias = (float *) bias;
-    switch (wtype) {
-        case T_F32: L.fmt = W_F32; break;
-        case T_F16: L.fmt = W_F16; break;
-        case T_Q8_0: case T_Q4_0: L.fmt = W_Q32; break;
-        case T_Q4_K: L.fmt = W_Q4K; break;
-        default: jepa_log("jepa: %s: weight type %d not supported\n", who, wtype); return false;
-    }
+    L.fmt = weight_format(wtype, n_in);
+    if (L.fmt < 0) { jepa_log("jepa: %s: weight type %d not supported\n", who, wtype); return false; }
     if (L.fmt != W_F32 && (n_out % 128 || n_in % 64 || (L.fmt == W_Q4K && n_in % 256) || n_in > 2048 * 8)) {
         jepa_log("jepa: %s: [%lld x %lld] not supported by the MFMA GEMM (n_out %% 128, n_in %% 64)\n", who, (long long) n_out,
                  (long long) n_in);
@@ -186,8 +181,8 @@ bool make_linear(dev_scope & d, const char * who, int wtype, const void * w, int
         L.w = (void *) w;
         return true;
     }
-    L.w = d.alloc(L.fmt == W_Q32 ? (size_t) n_out * n_in : (size_t) n_out * (n_in / 2) + (size_t) n_out * (n_in / 256) * 8);
-    if (L.fmt == W_Q32) L.wd = d.alloc((size_t) n_out * (n_in / 32) * 2);
+    L.w = d.alloc(weight_code_bytes(L.fmt, n_out, n_in));
+    if (L.fmt == W_Q32 || L.fmt == W_Q40) L.wd = d.alloc((size_t) n_out * (n_in / 32) * 2);
     else {
         L.wd = d.alloc((size_t) n_out * (n_in / 256) * 4);
         L.wmin = d.alloc((size_t) n_out * (n_in / 256) * 32);
@@ -280,8 +275,8 @@ extern "C" int jepa_amd_matmul_gelu(int device, int wtype, const void * w, int64
 extern "C" int jepa_amd_gemm_split(int split) { return gemm_force_split(split); }
 
 extern "C" int jepa_amd_gemm_split_of(int wtype, int64_t n_out, int64_t n_in) {
-    const int wf = wtype == T_Q8_0 || wtype == T_Q4_0 ? W_Q32 : wtype == T_Q4_K ? W_Q4K : wtype == T_F16 ? W_F16 : W_F32;
-    return gemm_split_for(wf, n_out, n_in);
+    const int wf = weight_format(wtype, n_in);
+    return wf < 0 ? 1 : gemm_split_for(wf, n_out, n_in);
 }
 
 extern "C" int jepa_amd_gemm_tile(int index) {

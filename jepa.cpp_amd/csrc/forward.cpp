@@ -127,7 +127,7 @@ blk_shape enc_blk_shape(const jepa_model * m) {
 }
 
 const char * gemm_class(const dev_linear & W) {
-    switch (W.fmt) { case W_F16: return "gemm_f16"; case W_Q32: return "gemm_q8"; case W_Q4K: return "gemm_q4k"; default: return "gemm_f32"; }
+    switch (W.fmt) { case W_F16: return "gemm_f16"; case W_Q32: return "gemm_q8"; case W_Q40: return "gemm_q4_0"; case W_Q4K: return "gemm_q4k"; default: return "gemm_f32"; }
 }
 
 void enqueue_gemm_gelu(const dev_linear & W, const act_view & x, int64_t rows, act_view & out, fwd_workspace & w, hipStream_t s,

@@ -6,9 +6,11 @@
 //   q4_K weights x q8_K activations:         sum_sb (dw*da) * sum_j sc_j S_j  -  (dmin*da) * sum_j m_j bsum_j
 //   f16 weights x f16-rounded activations:   f32 accumulation of exact f16 products
 //
-// q8_0 / q4_0 (int8 codes in HBM and LDS), per 32-deep block b and 32x32 output tile:
+// q8_0 (int8 codes in HBM and LDS) and q4_0 (4-bit codes in HBM and LDS, each unpacked in registers to
+// the int8 16 (q - 8)), per 32-deep block b and 32x32 output tile:
 //   v_mfma_i32_32x32x32_i8   S  = A_b . B_b (with at most two MFMA tiles per wave started from the bits
-//                               of 1.5 * 2^23, so that the int32 result read as a float is 12582912 + S)
+//                               of 1.5 * 2^23, so that the int32 result read as a float is 12582912 + S;
+//                               q4_0: 1.5 * 2^19 + 16 S, read as the float 786432 + S)
 //   v_mfma_f32_32x32x8_f16   c  = dw_b (x) da_b (an outer product of the two f16 scale vectors; one
 //                               non-zero K slot, so every c = dw * da is exact)
 //   32 VALU                  acc = fma(float(S), c, acc): one rounding per block
@@ -46,7 +48,7 @@ namespace {
 
 struct kargs {
     const _Float16 * A;      // [N][K] weight codes (or f16 / f32 weights)
-    const uint16_t * Ad;     // W_Q32: f16 d [N][K/32]; W_Q4K: u32 (d | dmin << 16) [K/256][N]
+    const uint16_t * Ad;     // W_Q32, W_Q40: f16 d [N][K/32]; W_Q4K: u32 (d | dmin << 16) [K/256][N]
     const _Float16 * Amin;   // W_Q4K: [N][K/256][16] sub-block mins, each twice
     const uint8_t * Asc;     // W_Q4K: [N][K/256][8] 6-bit sub-block scales
     const _Float16 * B;      // [M][K] activation codes (or f16 / f32 activations)
@@ -56,7 +58,7 @@ struct kargs {
     int64_t M, N, K;
     int tn, tm;              // workgroup tiles along N and M
     int xa, xb;              // tiles per XCD block along N and M (0: plain order)
-    int split;               // K halves computed by separate workgroups (1 or 2; q8_0 / q4_0 only)
+    int split;               // K halves computed by separate workgroups (1 or 2; q8_0 / q4_0 / q4_K)
     float * part;            // split: raw accumulators of every workgroup [split][tiles][BN*BM]
     int * cnt;               // split: arrivals per tile (0 between launches)
     gemm_epi ep;
@@ -200,7 +202,7 @@ struct tiling {
     static constexpr int BN = 32 * WN * TI, BM = 32 * WM * TJ;
     // LDS rows of 128 B per stage: the weight rows (q4_K: two rows of 64 B of 4-bit codes share one),
     // then the activation rows
-    static constexpr int AROWS = WF == W_Q4K ? BN / 2 : BN;
+    static constexpr int AROWS = WF == W_Q4K || WF == W_Q40 ? BN / 2 : BN;
     static constexpr int ROWS = AROWS + BM;
     static constexpr int ESZ = WF == W_F16 ? 2 : 1;          // bytes per activation code
     static constexpr int KC = 128 / ESZ;                      // K-columns per stage
@@ -219,7 +221,7 @@ struct tiling {
     static constexpr int LDS = NST * STAGE + NXSB * XSB;
     static constexpr int LOADS = ROWS / 8 / NW;    // 1 KB tile loads per wave per stage
     static constexpr int PARTS = LOADS;            // copies per wave per stage (q4_K adds its own)
-    static constexpr int SLD = WF == W_Q32 ? TI + TJ : 0;   // q8_0 / q4_0 scale loads per wave per stage
+    static constexpr int SLD = WF == W_Q32 || WF == W_Q40 ? TI + TJ : 0;   // q8_0 / q4_0 scale loads per wave per stage
     static_assert(NST >= 2, "LDS too small for two stages");
     static_assert(AROWS % (8 * NW) == 0 && BN % 64 == 0 && BM % 64 == 0 && ROWS % (8 * NW) == 0, "load split");
     static_assert((NST - 2) * PARTS < 64, "vmcnt range");
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // has to fetch (xa BN + xb BM rows per K-column) are fewest.
     // split-K (residual and plain epilogues only; elsewhere it folds away): workgroups
     // [s * tiles, (s + 1) * tiles) compute K half s of every tile
-    constexpr bool SPLITTABLE = (WF == W_Q32 || WF == W_Q4K) && (EPI == EPI_RESID || EPI == EPI_F32);
+    constexpr bool SPLITTABLE = (WF == W_Q32 || WF == W_Q40 || WF == W_Q4K) && (EPI == EPI_RESID || EPI == EPI_F32);
     const int split = SPLITTABLE ? a.split : 1;
     const int ntile = a.tn * a.tm;
     const int sp = split > 1 ? (int) blockIdx.x / ntile : 0;
@@ -295,7 +297,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const int64_t nst = split > 1 ? K / KC / split : (K + KC - 1) / KC;
     const int64_t kst0 = (int64_t) sp * nst;
     const int64_t rowbytes = K * ESZ;                                  // activation row
-    const int64_t rowbytesA = WF == W_Q4K ? K / 2 : rowbytes;          // weight row (q4_K: 4-bit codes)
+    const int64_t rowbytesA = WF == W_Q4K || WF == W_Q40 ? K / 2 : rowbytes;   // weight row (4-bit codes)
 
     // buffer resources rebased at the tile's first weight row and first token, so that every copy's
     // offset stays below 4 GiB
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     const brsrc rB = make_brsrc((const unsigned char *) a.B + m0 * rowbytes, (M - m0) * rowbytes);
     [[maybe_unused]] brsrc rAd, rBd, rAmin, rBs, rAsc;
     [[maybe_unused]] const int64_t nsb = K >> 8;
-    if constexpr (WF == W_Q32) {
+    if constexpr (WF == W_Q32 || WF == W_Q40) {
         rAd = make_brsrc(a.Ad + n0 * KB, (a.N - n0) * KB * 2);
         rBd = make_brsrc((const uint16_t *) a.Bd + m0 * KB, (M - m0) * KB * 2);
     }
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         const int L = NW * i + wave;
         const int r = 8 * L + (lane >> 3);
         if (i < T::AROWS / (8 * NW)) {
-            if constexpr (WF == W_Q4K) {   // LDS row r: weight rows 2r (chunks 0-3) and 2r + 1 (chunks 4-7), 64 B each
+            if constexpr (WF == W_Q4K || WF == W_Q40) {   // LDS row r: weight rows 2r (chunks 0-3) and 2r + 1 (chunks 4-7), 64 B each
                 const int cw = lds_slot(r, lane & 7);
                 dma_to_lds<16>(rA, (uint32_t) (2 * r + (cw >> 2)) * (uint32_t) rowbytesA + 16 * (cw & 3), (uint32_t) (k0 / 2), base + 1024 * L);
             } else
@@ -449,7 +451,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         }
     };
     [[maybe_unused]] auto q32_main = [&](int64_t nfull) {
-      if constexpr (WF == W_Q32) {
+      if constexpr (WF == W_Q32 || WF == W_Q40) {
         constexpr int TT = TI * TJ, U = 4 * TT;
         static_assert(NST >= 3, "the in-stage barrier needs a stage in flight beyond the next one");
         // copies of this wave still allowed in flight at the barrier that publishes stage st+1 (held
@@ -465,7 +467,11 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         // NST-3 bodies' copies in between, this body's scale loads and its copies up to step U-2
         // (exactly that for st = 1; later bodies add older scale loads, which only tightens the wait).
         constexpr int NBAR = (NST - 3) * P1 + T::SLD + (U - 1) * P1 / U;
-        i4v A[4][TI], B[4][TJ];
+        // q4_0 (W_Q40): 4-bit codes in HBM and LDS, read as one 16-byte chunk per two blocks (the q4_K
+        // layout) and unpacked at the step's first MFMA into A[0]
+        constexpr bool P4 = WF == W_Q40;
+        i4v A[P4 ? 1 : 4][TI], B[4][TJ];
+        [[maybe_unused]] u4v AR[2][TI];
         h4 SA[TI], SB[4][TJ];
         u2v RS0A[TI], RS0B[TJ], RS1A[TI], RS1B[TJ];   // raw scales: stage st+2 (being loaded), st+1
         i16v S[2];
@@ -475,21 +481,47 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         // (|S| <= 32 * 128 * 128 here), so one f32 subtraction gives float(S) exactly (measured ~7 %
         // faster than v_cvt_f32_i32). Larger wave tiles cannot spare the 16 VGPRs the constant takes
         // as an MFMA operand and convert with v_cvt_f32_i32.
-        constexpr bool MAGIC = TI * TJ <= 2;
+        // q4_0 codes are 16 (q - 8) (the signed nibble in the high half of a byte), so the MFMA sums
+        // 16 S; it starts from the bits of 1.5 * 2^19, where a float's unit in the last place is 1/16:
+        // read as a float, M + 16 S is exactly 786432 + S (|S| <= 32 * 8 * 127). Without the constant
+        // the accumulators take float(16 S) (exact: |16 S| < 2^24) and hold 16 times the sums, scaled
+        // back once after the last stage: a power-of-two factor commutes with every rounding of the
+        // fma chain (values far from the f32 subnormal range), so the result is the same bits.
+        constexpr bool MAGIC = TI * TJ <= (P4 ? 3 : 2);   // (4-bit operands leave room for three)
         i16v magic;
 #pragma unroll
-        for (int r = 0; r < 16; r++) magic[r] = MAGIC ? 0x4B400000 : 0;
+        for (int r = 0; r < 16; r++) magic[r] = MAGIC ? (P4 ? 0x49400000 : 0x4B400000) : 0;
         float neg_magic;   // in a VGPR: a VALU op with an SGPR operand issues at half rate here
-        asm("v_mov_b32 %0, 0xcb400000" : "=v"(neg_magic));
+        if constexpr (P4) asm("v_mov_b32 %0, 0xc9400000" : "=v"(neg_magic));
+        else asm("v_mov_b32 %0, 0xcb400000" : "=v"(neg_magic));
         auto ld_step = [&](const unsigned char * base, int u) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            if (j == 0) A[blk][i] = lds_chunk<i4v>(base, 32 * (wn * TI + i) + l32, 2 * blk + g);
-            if (i == 0) B[blk][j] = lds_chunk<i4v>(base, BN + 32 * (wm * TJ + j) + l32, 2 * blk + g);
+            if constexpr (P4) {
+                if (j == 0 && (blk & 1) == 0) {
+                    const int n = 32 * (wn * TI + i) + l32, r = n >> 1;
+                    AR[blk >> 1][i] = *(const u4v *) (base + r * 128 + (lds_slot(r, ((n & 1) << 2) + 2 * (blk >> 1) + g) << 4));
+                }
+            } else {
+                if (j == 0) A[blk][i] = lds_chunk<i4v>(base, 32 * (wn * TI + i) + l32, 2 * blk + g);
+            }
+            if (i == 0) B[blk][j] = lds_chunk<i4v>(base, T::AROWS + 32 * (wm * TJ + j) + l32, 2 * blk + g);
         };
         auto mma = [&](int u, const h4 (&sa)[TI], const h4 (&sb)[4][TJ]) {
             const int blk = u / TT, t = u % TT, i = t / TJ, j = t % TJ;
-            if constexpr (MAGIC) S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], magic);
-            else S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], i16v{});
+            if constexpr (P4) {
+                if (j == 0) {
+                    // byte b of each code dword holds codes b (low nibble) and b + 4 (high nibble)
+                    const u4v ar = AR[blk >> 1][i];
+                    const uint32_t p0 = (blk & 1) ? ar.z : ar.x, p1 = (blk & 1) ? ar.w : ar.y;
+                    A[0][i] = i4v{(int) ((p0 << 4) & 0xF0F0F0F0u), (int) (p0 & 0xF0F0F0F0u), (int) ((p1 << 4) & 0xF0F0F0F0u),
+                                  (int) (p1 & 0xF0F0F0F0u)};
+                }
+                if constexpr (MAGIC) S[u & 1] = MFMA_I8(A[0][i], B[blk][j], magic);
+                else S[u & 1] = MFMA_I8(A[0][i], B[blk][j], i16v{});
+            } else {
+                if constexpr (MAGIC) S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], magic);
+                else S[u & 1] = MFMA_I8(A[blk][i], B[blk][j], i16v{});
+            }
             C[u & 1] = MFMA8(sa[i], sb[blk][j], zero);
         };
         auto valu = [&](int u) {
@@ -579,6 +611,14 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         }
         // the copies issued during the last stages must land before the workgroup's LDS is released
         __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+        if constexpr (P4 && !MAGIC) {
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < TJ; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = __fmul_rn(acc[i][j][r], 0.0625f);
+        }
       }
     };
 
@@ -853,8 +893,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
 
     // q8_0 / q4_0 with K % 128 == 64 end in a half stage, peeled off the loop so that the loop body
     // has one path (the accumulators then stay in place across iterations)
-    const int64_t nfull = WF == W_Q32 ? (split > 1 ? nst : K / KC) : nst;
-    if constexpr (WF == W_Q32) {
+    const int64_t nfull = WF == W_Q32 || WF == W_Q40 ? (split > 1 ? nst : K / KC) : nst;
+    if constexpr (WF == W_Q32 || WF == W_Q40) {
         q32_main(nfull);
     } else if constexpr (WF == W_Q4K) {
         q4k_main();
@@ -1207,9 +1247,9 @@ struct tile_cfg { int wn, wm, ti, tj; };
 // 256x64 (two wave shapes; the second, one weight tile and two token tiles per wave, only for the
 // 256-feature q8_K epilogue)
 constexpr tile_cfg k_tiles[] = {{4, 2, 2, 2}, {2, 4, 3, 1}, {2, 4, 2, 1}, {4, 2, 1, 2}, {2, 4, 1, 1}, {4, 2, 1, 1}, {4, 2, 2, 1},
-                                {8, 1, 1, 2}};
+                                {8, 1, 1, 2}, {4, 2, 3, 1}};
 // relative efficiency of one workgroup tile (larger tiles re-read less from L2 and LDS)
-constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66, 0.8, 0.8};
+constexpr double k_tile_eff[] = {1.0, 0.95, 0.85, 0.85, 0.65, 0.66, 0.8, 0.8, 0.9};
 
 std::atomic<int> g_force_tile{-1};
 std::atomic<int> g_force_split{-1};
@@ -1227,9 +1267,15 @@ int cu_count() {
     return n;
 }
 
-// q4_K runs the tiles whose weight rows pair up into whole 1 KB copies (BN a multiple of 128) and whose
-// four accumulator sets per MFMA tile fit 256 VGPRs with two waves per SIMD (two MFMA tiles per wave)
-bool q4k_tile(int c) { return c == 2 || c == 3 || c == 5 || c == 6 || c == 7; }
+// 4-bit weights (q4_K, packed q4_0) run the tiles whose weight rows pair up into whole 1 KB copies (BN
+// a multiple of 128); q4_K, whose four accumulator sets per MFMA tile must fit 256 VGPRs with two waves
+// per SIMD, at most two MFMA tiles per wave. The 384x64 tile (for N = 3072: 256 tiles at M = 2048, the
+// role the 192x128 tile has for int8 weights) fits three LDS stages only with 4-bit weights.
+bool tile_ok(int wf, int c) {
+    if (wf == W_Q4K) return c == 2 || c == 3 || c == 5 || c == 6 || c == 7;
+    if (wf == W_Q40) return c != 1 && c != 4;
+    return c != 8;
+}
 
 // The tile with the least estimated time: whole waves of workgroups over the CUs (one workgroup per
 // CU) times the work of one tile, discounted by the tile's efficiency. Only tiles dividing N.
@@ -1237,7 +1283,7 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
     const int f = g_force_tile.load();
     const int nt = (int) (sizeof(k_tiles) / sizeof(k_tiles[0]));
     const auto bn_of = [](int c) { return 32 * k_tiles[c].wn * k_tiles[c].ti; };
-    if (f >= 0 && f < nt && N % bn_of(f) == 0 && (need_bn == 0 || bn_of(f) == need_bn) && (wf != W_Q4K || q4k_tile(f)) &&
+    if (f >= 0 && f < nt && N % bn_of(f) == 0 && (need_bn == 0 || bn_of(f) == need_bn) && tile_ok(wf, f) &&
         (f != 7 || need_bn == 256)) return f;
     const int cus = cu_count();
     double best = 1e300;
@@ -1245,7 +1291,7 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
     for (int c = 0; c < nt; c++) {
         const int64_t bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
         if (N % bn || (need_bn && bn != need_bn) || (c == 7 && need_bn != 256)) continue;
-        if (wf == W_Q4K && !q4k_tile(c)) continue;
+        if (!tile_ok(wf, c)) continue;
         const int64_t t = (N / bn) * ((M + bm - 1) / bm) * split;
         const double waves = (double) ((t + cus - 1) / cus);
         // q4_K unpacks a wave's weight operand once for its TJ token tiles
@@ -1264,8 +1310,10 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
         if (c == 7) k_gemm_mfma<WF, EPI, 8, 1, 1, 2><<<grid, 512, 0, s>>>(a);
         if constexpr (WF != W_Q4K)   // q4_K runs the 256x64 tile only
             if (c == 0) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a);
-    } else if constexpr (WF == W_Q4K) {
+    } else if constexpr (WF == W_Q4K || WF == W_Q40) {
         switch (c) {
+            case 0: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a); break;
+            case 8: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 3, 1><<<grid, 512, 0, s>>>(a); break;
             case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(a); break;
             case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(a); break;
             case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(a); break;
@@ -1336,7 +1384,7 @@ int gemm_split_for(int wf, int64_t N, int64_t K) {
     // each of whole 128-column stages. The partial-sum exchange costs a few microseconds, which pays
     // off from K = 2048 (fc2: 43.6 -> 37.4 us) but not at K = 1024 (out-proj: 18 -> 21 us).
     // q4_K: each half starts at a super-block (256 columns) and spans whole 4-stage super-blocks
-    if (!(wf == W_Q32 && K % 256 == 0) && !(wf == W_Q4K && K % 512 == 0)) return 1;
+    if (!((wf == W_Q32 || wf == W_Q40) && K % 256 == 0) && !(wf == W_Q4K && K % 512 == 0)) return 1;
     const int f = g_force_split.load();
     if (f >= 1) return f >= 2 ? 2 : 1;
     return N <= SPLIT_MAX_N && K >= 2048 ? 2 : 1;
@@ -1377,6 +1425,7 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
     switch (W.fmt) {
         case W_F16: dispatch_mfma<W_F16>(a, s, nullptr); break;
         case W_Q32: dispatch_mfma<W_Q32>(a, s, sw); break;
+        case W_Q40: dispatch_mfma<W_Q40>(a, s, sw); break;
         case W_Q4K: dispatch_mfma<W_Q4K>(a, s, sw); break;
     }
 }

@@ -106,7 +106,7 @@ void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, voi
                    void * wmin, hipStream_t s);
 
 // test hooks
-// force the MFMA GEMM onto workgroup tile `index` (0..5) for every later launch whose N it divides;
+// force the MFMA GEMM onto workgroup tile `index` (0..8) for every later launch whose N it divides;
 // -1 restores the automatic choice. Returns -1 for an index past the table.
 int gemm_force_tile(int index);
 // force the split-K choice: 1 off, 2 on where the shape allows it, -1 automatic

@@ -315,15 +315,11 @@ struct loader {
         if (pad_out) n_out = (n_out + 127) / 128 * 128;
         const size_t pad_bytes = (size_t) (n_out - n_file) * (t->nbytes / (size_t) n_file);
         L.gtype = t->type; L.n_in = n_in; L.n_out = n_out; L.n_valid = n_file;
-        switch (t->type) {
-            case T_F32: L.fmt = W_F32; break;
-            case T_F16: L.fmt = W_F16; break;
-            case T_Q8_0: case T_Q4_0: L.fmt = W_Q32; break;
-            case T_Q4_K: L.fmt = W_Q4K; break;
-            default:
-                jepa_log("jepa: tensor %s has dtype %s, which this engine has no GEMM kernel for "
-                         "(f32, f16, q8_0, q4_0 and q4_K are supported)\n", wname.c_str(), ggml_traits(t->type).name);
-                return false;
+        L.fmt = weight_format(t->type, n_in);
+        if (L.fmt < 0) {
+            jepa_log("jepa: tensor %s has dtype %s, which this engine has no GEMM kernel for "
+                     "(f32, f16, q8_0, q4_0 and q4_K are supported)\n", wname.c_str(), ggml_traits(t->type).name);
+            return false;
         }
         if (L.fmt != W_F32 && (n_out % 128 != 0 || n_in % 64 != 0)) {
             jepa_log("jepa: tensor %s is [%" PRId64 " x %" PRId64 "]: the MFMA GEMM needs rows that are a multiple of 64 and a "
@@ -339,9 +335,9 @@ struct loader {
             L.w = dalloc(t->nbytes + pad_bytes);
             if (!L.w || hipMemcpyAsync(L.w, staging, t->nbytes + pad_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
         } else {
-            L.w = dalloc(L.fmt == W_Q32 ? (size_t) n_in * n_out : (size_t) n_out * (n_in / 2) + (size_t) n_out * (n_in / 256) * 8);
+            L.w = dalloc(weight_code_bytes(L.fmt, n_out, n_in));
             if (!L.w) return false;
-            if (L.fmt == W_Q32) {
+            if (L.fmt == W_Q32 || L.fmt == W_Q40) {
                 L.wd = dalloc((size_t) n_out * (n_in / 32) * 2);
                 if (!L.wd) return false;
             } else {

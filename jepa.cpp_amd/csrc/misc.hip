@@ -310,7 +310,8 @@ __global__ void k_cls_rows(float * x, const float * cls, const float * pos, int6
 // ------------------------------------------------------------------------------------------------
 // weight expansion at load (ggml blocks -> GEMM operand arrays)
 // ------------------------------------------------------------------------------------------------
-// q8_0 / q4_0 weights -> int8 codes [n_out][n_in] (q, or q - 8) + f16 d [n_out][n_in/32]
+// q8_0 weights, and q4_0 rows not a multiple of 128 -> int8 codes [n_out][n_in] (q, or q - 8) + f16 d
+// [n_out][n_in/32]
 __global__ void k_repack_q8_0(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, int8_t * w, uint16_t * wd) {
     const int64_t nb = n_in / 32;
     const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -334,6 +335,37 @@ __global__ void k_repack_q4_0(const uint8_t * __restrict__ raw, int64_t n_out, i
         dst[j]      = (int8_t) ((blk[2 + j] & 0xF) - 8);
         dst[j + 16] = (int8_t) ((blk[2 + j] >> 4) - 8);
     }
+}
+
+// q4_0 rows that are a multiple of 128 stay 4-bit: codes [n_out][n_in/2] + f16 d [n_out][n_in/32]. Each
+// code is q - 8 as a 4-bit two's complement (q ^ 8), so that a nibble moved to the high half of a byte
+// is the int8 16 (q - 8). A block of 32 is two halves g of 16 values, each 8 bytes: two dwords whose
+// byte b holds values b (low nibble) and b + 4 (high nibble) of its first and of its second eight
+// values, so that (w << 4) & 0xF0F0F0F0 and w & 0xF0F0F0F0 are four consecutive codes each. The four
+// blocks of each 128 values (64 B) lie as [g0: blocks 0, 1] [g1: blocks 0, 1] [g0: blocks 2, 3] [g1:
+// blocks 2, 3], one 16-byte read per lane and two blocks. ggml's q4_0 block (the reference's ggml
+// quantizer) is d, then 16 bytes whose low nibbles are values 0..15 and high nibbles values 16..31.
+__global__ void k_repack_q4_0_packed(const uint8_t * __restrict__ raw, int64_t n_out, int64_t n_in, uint32_t * w, uint16_t * wd) {
+    const int64_t nb = n_in / 32;
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= n_out * nb) return;
+    const uint8_t * blk = raw + id * 18;
+    wd[id] = (uint16_t) (blk[0] | (blk[1] << 8));
+    const int64_t n = id / nb, bi = id % nb;
+    uint8_t v[32];
+    for (int j = 0; j < 16; j++) {
+        v[j] = (blk[2 + j] & 0xF) ^ 8;
+        v[j + 16] = (blk[2 + j] >> 4) ^ 8;
+    }
+    // block bi of the row: 128-value group bi / 4, pair (bi % 4) / 2, 8-byte slot bi % 2 of each chunk
+    uint32_t * row = w + n * (n_in / 8);
+    const int64_t base = (bi / 4) * 16 + ((bi % 4) >> 1) * 8 + (bi & 1) * 2;   // dwords
+    for (int g = 0; g < 2; g++)
+        for (int dw = 0; dw < 2; dw++) {
+            uint32_t x = 0;
+            for (int b = 0; b < 4; b++) x |= (uint32_t) (v[16 * g + 8 * dw + b] | (v[16 * g + 8 * dw + 4 + b] << 4)) << (8 * b);
+            row[base + 4 * g + dw] = x;
+        }
 }
 
 __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t * q, int & d, int & m) {
@@ -523,7 +555,13 @@ void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, voi
                    hipStream_t s) {
     switch (gtype) {
         case T_Q8_0: k_repack_q8_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd); break;
-        case T_Q4_0: k_repack_q4_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd); break;
+        case T_Q4_0:
+            if (weight_format(T_Q4_0, n_in) == W_Q40)
+                k_repack_q4_0_packed<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (uint32_t *) w,
+                                                                                   (uint16_t *) wd);
+            else
+                k_repack_q4_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd);
+            break;
         case T_Q4_K: k_repack_q4_K<<<nblk(n_out * (n_in / 256), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (uint8_t *) w,
                                                                                   (uint8_t *) w + n_out * (n_in / 2), (uint32_t *) wd,
                                                                                   (_Float16 *) wmin); break;

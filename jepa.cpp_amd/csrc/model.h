@@ -85,10 +85,35 @@ struct hparams {
 };
 
 // Weight formats on the device. Quantized matrices are repacked once at load into the operand
-// layout of the GEMM kernel plus their scales: q8_0 / q4_0 as int8 codes (q; q - 8) for the int8
-// MFMA; q4_K stays 4-bit (codes regrouped for an in-register unpack, scales and mins split out) and
-// is unpacked in the GEMM for the int8 MFMA.
-enum wfmt { W_F32 = 0, W_F16 = 1, W_Q32 = 2 /* q8_0, q4_0: f16 scale per 32 */, W_Q4K = 3 };
+// layout of the GEMM kernel plus their scales: q8_0 as int8 codes for the int8 MFMA; q4_0 and q4_K
+// stay 4-bit (codes regrouped for an in-register unpack; q4_K's scales and mins split out) and are
+// unpacked in the GEMM for the int8 MFMA. q4_0 rows whose length is not a multiple of 128 (one
+// 64-column LDS stage of 4-bit codes would be 32 bytes) are expanded to int8 codes q - 8 instead.
+enum wfmt {
+    W_F32 = 0, W_F16 = 1,
+    W_Q32 = 2,   // int8 codes, f16 scale per 32 (q8_0; q4_0 rows not a multiple of 128)
+    W_Q4K = 3,   // q4_K, 4-bit
+    W_Q40 = 4,   // q4_0, 4-bit codes, f16 scale per 32
+};
+
+// device format of a ggml weight type for rows of n_in values; -1: no GEMM for the type
+inline int weight_format(int gtype, int64_t n_in) {
+    switch (gtype) {
+        case T_F32: return W_F32;
+        case T_F16: return W_F16;
+        case T_Q8_0: return W_Q32;
+        case T_Q4_0: return n_in % 128 == 0 ? W_Q40 : W_Q32;
+        case T_Q4_K: return W_Q4K;
+        default: return -1;
+    }
+}
+
+// bytes of the code array dev_linear::w of a quantized format (q4_K: codes, then its sub-block scales)
+inline size_t weight_code_bytes(int fmt, int64_t n_out, int64_t n_in) {
+    if (fmt == W_Q32) return (size_t) n_out * n_in;
+    if (fmt == W_Q40) return (size_t) n_out * (n_in / 2);
+    return (size_t) n_out * (n_in / 2) + (size_t) n_out * (n_in / 256) * 8;
+}
 // Activation formats consumed by the GEMM (what the producer of a linear's input writes).
 enum afmt { A_F32 = 0, A_F16 = 1, A_Q8_0 = 2, A_Q8_K = 3 };
 
@@ -97,13 +122,14 @@ struct dev_linear {
     int      fmt = W_F32;
     int64_t  n_out = 0, n_in = 0;
     int64_t  n_valid = 0;         // outputs in the file (n_out is rounded up to 128 for the head's linears)
-    void *   w = nullptr;         // [n_out][n_in]: f32 (W_F32), int8 (W_Q32), f16 (W_F16); W_Q4K: 4-bit codes
-                                  // [n_out][n_in/2] followed by the 6-bit sub-block scales [n_out][n_in/256][8]
-    void *   wd = nullptr;        // W_Q32: f16 d [n_out][n_in/32]; W_Q4K: u32 (f16 d | f16 dmin << 16) [n_in/256][n_out]
+    void *   w = nullptr;         // [n_out][n_in]: f32 (W_F32), int8 (W_Q32), f16 (W_F16); W_Q40: 4-bit codes
+                                  // [n_out][n_in/2]; W_Q4K: 4-bit codes [n_out][n_in/2] followed by the 6-bit
+                                  // sub-block scales [n_out][n_in/256][8]
+    void *   wd = nullptr;        // W_Q32, W_Q40: f16 d [n_out][n_in/32]; W_Q4K: u32 (f16 d | f16 dmin << 16) [n_in/256][n_out]
     void *   wmin = nullptr;      // W_Q4K: f16 mins [n_out][n_in/256][16] (m_{k/2}, k = 0..15)
     float *  bias = nullptr;      // [n_out] or null
     afmt act() const {
-        switch (fmt) { case W_F32: return A_F32; case W_F16: return A_F16; case W_Q32: return A_Q8_0; default: return A_Q8_K; }
+        switch (fmt) { case W_F32: return A_F32; case W_F16: return A_F16; case W_Q32: case W_Q40: return A_Q8_0; default: return A_Q8_K; }
     }
 };
 

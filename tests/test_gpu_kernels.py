@@ -299,7 +299,8 @@ def test_matmul_split_k(jlib, oracle, gtype, shape, M):
 
 
 # workgroup tiles of the MFMA GEMM (weight rows x tokens), by index
-TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64), 6: (256, 64), 7: (256, 64)}
+TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64), 6: (256, 64), 7: (256, 64),
+         8: (384, 64)}
 
 
 @pytest.mark.parametrize("tile", sorted(TILES))
@@ -307,9 +308,11 @@ TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128
 def test_matmul_every_tile(jlib, oracle, gtype, tile):
     """Every workgroup tile shape of the MFMA GEMM, forced, on a ragged token count (M = 389: partial
     last tile, rows past M clamped) and K = 768 (6 or 12 stages, so the pipeline's prologue, steady
-    state and tail all run; three q4_K super-blocks). q4_K runs tiles 2, 3, 5 and 6 only (its weight
-    rows pair up in whole copies and four accumulator sets fit); forcing another tile leaves it on the
-    automatic choice. Block-quantized types bit-exact, f16 within f32 rounding."""
+    state and tail all run; three q4_K super-blocks). The 4-bit layouts need tiles whose weight rows
+    pair up in whole copies: q4_0 runs every tile but 1 and 4 (and alone tile 8, whose three LDS
+    stages fit only with 4-bit weights), q4_K tiles 2, 3, 5 and 6 (four accumulator sets must fit);
+    forcing another tile leaves a launch on the automatic choice.
+    Block-quantized types bit-exact, f16 within f32 rounding."""
     bn = TILES[tile][0]
     n_out, n_in, M = bn * (3 if bn == 128 else 2) if bn != 64 else 256, 768, 389
     rng = np.random.default_rng(tile * 100 + gtype)
@@ -337,6 +340,40 @@ def test_matmul_every_tile(jlib, oracle, gtype, tile):
         assert diff.size == 0, f"{len(diff)} outputs differ, first {diff[:4].tolist()}, max abs {np.abs(got - want).max():.3e}"
     else:
         assert np.abs(got - want).max() <= 2e-5 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("n_in,tile", [(704, -1), (704, 1), (768, 0), (768, 5), (768, 8), (1152, -1)])
+def test_matmul_q4_0_layouts(jlib, oracle, n_in, tile):
+    """q4_0 rows that are a multiple of 128 stay 4-bit on the device (codes 16 (q - 8) unpacked in
+    registers, the 1.5 * 2^19 float offset on the integer sums); other multiples of 64 are expanded to
+    int8 codes at load. Both bit-exact with the oracle, on a ragged M, with weights that use the whole
+    4-bit range (codes 0 and 15 in every block) and a block of all-equal values."""
+    n_out, M = 768, 389
+    rng = np.random.default_rng(n_in + tile)
+    w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    w[:, 0::32] = 0.08; w[:, 1::32] = -0.08             # both extremes of every block
+    w[7, 64:96] = 0.01                                  # one constant block
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    x[3] = 0.0
+    bias = (rng.standard_normal(n_out) * 0.02).astype(np.float32)
+    raw = gguf.quantize(gguf.GGML_Q4_0, w)
+    codes = raw.reshape(n_out, n_in // 32, 18)[:, :, 2:]
+    q = np.concatenate([(codes & 0xF).ravel(), (codes >> 4).ravel()])
+    assert q.min() == 0 and q.max() == 15
+    want = _mul_mat_as_gpu(jlib, oracle, gguf.GGML_Q4_0, raw, n_out, n_in, x, bias)
+    dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
+    y = torch.zeros((M, n_out), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    L = jlib.lib()
+    assert L.jepa_amd_gemm_tile(tile) == 0
+    try:
+        rc = L.jepa_amd_matmul(0, gguf.GGML_Q4_0, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, y.data_ptr(), 2, None)
+    finally:
+        L.jepa_amd_gemm_tile(-1)
+    assert rc == 0, jlib.error_text()
+    got = host(y)
+    diff = np.argwhere(got.view(np.uint32) != want.view(np.uint32))
+    assert diff.size == 0, f"{len(diff)} outputs differ, first {diff[:4].tolist()}, max abs {np.abs(got - want).max():.3e}"
 
 
 def test_gemm_tile_hook_rejects_unknown(jlib):
