@@ -5,12 +5,14 @@
 // src/jepa.cpp:416-442 (no mask, K/V in f16 as the reference's ggml_cast does, f32 softmax and f32
 // accumulation). Q arrives with 3-D RoPE already applied by the QKV GEMM epilogue.
 //
-// Work split: one workgroup = 8 waves = 128 queries of one head. Waves 0-3 own 32 queries each and
-// sweep the first half of the key tiles, waves 4-7 the same queries over the second half (two waves
-// per SIMD: one wave's exp2 / VALU phase overlaps the other's MFMAs); the two halves are merged
-// through LDS at the end. Keys come in tiles of 64: the K tile (64 keys x 64 dims) and the V^T tile
-// (64 dims x 64 keys), 128 B per row, are copied HBM->LDS directly (buffer_load_dwordx4 ... lds) into
-// a swizzled layout (lds_slot), NST - 1 tiles ahead of the one being used.
+// Work split: one workgroup = 128 queries of one head, in QG query groups of QT 32-query MFMA tiles
+// (QG x QT = 4) times KS = 4 key splits, one wave each: QT = 1 is 16 waves (four per SIMD, 128
+// VGPRs each: enough waves to hide the MFMA / exp / LDS latencies of the softmax chain), QT = 2 is 8
+// waves whose every K and V^T read from LDS feeds two MFMAs; QT = 1 measured faster (30.3 against
+// 32.9 us at 2048 tokens x 16 heads). The splits are merged through LDS at the end. Keys come in
+// tiles of 64: the K tile (64 keys x 64 dims) and the V^T tile (64 dims x 64 keys), 128 B per row, are
+// copied HBM->LDS directly (buffer_load_dwordx4 ... lds) into a swizzled layout (lds_slot),
+// double-buffered per split: tile s + 1 is copied while tile s is used.
 // MFMA roles are chosen so that softmax statistics need no cross-lane reduction beyond one
 // xor-32 exchange:
 //   S^T[key][q] = K . Q^T     A = K tile rows (keys), B = Q^T (held in registers for the sweep)
@@ -33,11 +35,12 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int HD = 64, QB = 128, KT = 64, NST = 4;
+constexpr int HD = 64, QB = 128, KT = 64, KS = 4;
 constexpr int TILE = KT * 128;                  // one K or V^T tile: 64 rows of 128 B
 constexpr int STAGE = 2 * TILE;                 // K + V^T
-constexpr int HALF = NST * STAGE;               // LDS of one key half
+constexpr int SPLIT = 2 * STAGE;                // LDS of one key split: two stages
 constexpr float LAZY = 8.0f;                    // keep the running max while growth <= 2^8
+constexpr int ATTN_QT = 1;                      // query tiles per wave (see the work split above)
 
 // 2^x by the hardware v_exp_f32 alone: exp2f adds a denormal-range fix-up (compare, select, add,
 // ldexp) around it, which softmax weights do not need (a weight below 2^-126 next to a running
@@ -75,17 +78,21 @@ __device__ __forceinline__ int2 key_range(int q, int R, int np, int tpf) {
 // HDO: the heads' real width, 64, or 32 for heads stored 64 wide with a zero upper half (their
 // second Q.K^T dim pair and second P.V row block are skipped: both are zero).
 // np / tpf select the block-causal mask (tpf = 0: none); key tiles that no query of the workgroup
-// sees are not visited, 32-key blocks that no query of a wave sees are skipped by that wave.
-template <int OUT, int HDO>
-__global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
-                                                      const _Float16 * __restrict__ Vt, void * __restrict__ O,
-                                                      void * __restrict__ Od, int n_head, int64_t R, int64_t R_pad,
-                                                      float c, int np, int tpf) {
-    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * HALF];
+// sees are not visited. MASKED = false (no block-causal mask, R a multiple of 64: every key of every
+// visited tile is visible to every query) drops the per-key mask code from the loop.
+template <int OUT, int HDO, bool MASKED, int QT>
+__global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
+                                                                   const _Float16 * __restrict__ Vt, void * __restrict__ O,
+                                                                   void * __restrict__ Od, int n_head, int64_t R, int64_t R_pad,
+                                                                   float c, int np, int tpf) {
+    constexpr int NKK = HDO / 16, NDT = HDO / 32;       // Q.K^T dim steps, P.V row blocks
+    constexpr int QG = 4 / QT;                          // query groups: QG x QT x 32 = 128 queries
+    constexpr int QW = 32 * QT;                         // queries per wave
+    constexpr int CPW = 16 / QG;                        // 1 KB copies per wave per tile
+    __shared__ __attribute__((aligned(16))) unsigned char smem[KS * SPLIT];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, g = lane >> 5;
-    const int qg = wave & 3, kh = wave >> 2;            // query group, key half
-    const int hw = wave & 3;                            // wave index inside its half (loads)
+    const int qg = wave % QG, ks = wave / QG;           // query group, key split
     // XCD-aware order: workgroups go to the 8 XCDs round-robin by linear id, so linear id L runs on
     // XCD L % 8. Renumber so that each XCD's share is a contiguous range of (head, query block): the
     // query blocks of one head then share one XCD's L2 for that head's K / V^T instead of all eight
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     const int64_t head = rl / gx;
     const int64_t item = head / n_head;
     const int h = (int) (head - item * n_head);
-    const int64_t q0 = (int64_t) qblk * QB + qg * 32;
+    const int64_t q0 = (int64_t) qblk * QB + qg * QW;   // this wave's queries: q0 .. q0 + QW - 1
 
     const _Float16 * Qh = Q + head * R_pad * HD;
     // buffer resources over this head's K rows and V^T rows (offsets below 4 GiB per head)
@@ -104,172 +111,271 @@ __global__ __launch_bounds__(512, 1) void k_attn_hd64(const _Float16 * __restric
     const brsrc rV = make_brsrc(Vt + head * HD * R_pad, R_pad * HD * 2);
 
     // key tiles of this workgroup: the union of its queries' key ranges (the first query has the
-    // lowest bound, the last the highest; a prefix row among them reads everything)
+    // lowest bound, the last the highest; a prefix row among them reads everything), dealt to the
+    // KS splits in contiguous runs (the first ntile % KS splits take one more)
     const int qa = (int) qblk * QB, qz = min((int) R, qa + QB) - 1;
     const int klo_wg = key_range(qa, (int) R, np, tpf).x;
     const int khi_wg = qa < np ? (int) R : key_range(qz, (int) R, np, tpf).y;
     const int tfirst = klo_wg / KT;
     const int ntile = (khi_wg + KT - 1) / KT - tfirst;
-    const int nt = (ntile + 1) / 2;                     // tiles per half (the second may have one less)
-    const int t0 = tfirst + kh * nt;                    // first tile of this half
-    const int my_nt = kh == 0 ? nt : ntile - nt;
-    unsigned char * hbase = smem + kh * HALF;
+    const int nbase = ntile / KS, nrem = ntile % KS;
+    const int nt = nbase + (nrem > 0);                  // loop trips (the longest split)
+    const int my_nt = nbase + (ks < nrem);
+    const int t0 = tfirst + ks * nbase + min(ks, nrem); // first tile of this split
+    unsigned char * sbase = smem + ks * SPLIT;
 
-    // stage s of this half: tile t0 + s. Each of the half's 4 waves copies 4 of the 16 row-groups.
+    // tile s of this split into stage s % 2, copied by the split's QG waves: 16 row-groups of 8 rows
+    // (K rows, then V^T rows), row-group L = QG i + qg for this wave
     auto issue = [&](int s) {
         if (s >= my_nt) return;
-        unsigned char * base = hbase + (s % NST) * STAGE;
+        unsigned char * base = sbase + (s & 1) * STAGE;
         const int64_t key0 = (int64_t) (t0 + s) * KT;
-        // lane fills slot lane % 8 of row r; all rows this wave copies are 8 hw + lane / 8 modulo 32
-        const int cch = lds_slot(8 * hw + (lane >> 3), lane & 7);
+        // lane fills slot lane % 8 of row r; all rows this wave copies agree modulo 16 (QG is even)
+        const int cch = lds_slot(8 * (qg & 1) + (lane >> 3), lane & 7);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int L = 4 * i + hw;                   // 0..7: K rows 8L..8L+7; 8..15: V^T rows
+        for (int i = 0; i < CPW; i++) {
+            const int L = QG * i + qg;                  // 0..7: K rows 8L..8L+7; 8..15: V^T rows
             const uint32_t r = 8 * (L & 7) + (lane >> 3);
-            if (i < 2) dma_to_lds<16>(rK, r * (HD * 2) + 16 * cch, (uint32_t) key0 * (HD * 2), base + 1024 * (L & 7));
+            if (L < 8) dma_to_lds<16>(rK, r * (HD * 2) + 16 * cch, (uint32_t) key0 * (HD * 2), base + 1024 * (L & 7));
             else dma_to_lds<16>(rV, r * (uint32_t) R_pad * 2 + 16 * cch, (uint32_t) key0 * 2, base + TILE + 1024 * (L & 7));
         }
     };
+    issue(0);
 
-    h8 qv[4];
+    // Q^T operands of the query tiles (rows past R are zero in the padded layout)
+    h8 qv[QT][NKK];
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) qv[kk] = *(const h8 *) (Qh + (q0 + l32) * HD + 16 * kk + 8 * g);
+    for (int qt = 0; qt < QT; qt++)
+#pragma unroll
+        for (int kk = 0; kk < NKK; kk++) qv[qt][kk] = *(const h8 *) (Qh + (q0 + 32 * qt + l32) * HD + 16 * kk + 8 * g);
 
     const f16v zero = {0};
-    f16v acc0 = zero, acc1 = zero;
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    // this lane's key range, and the wave's bounds on it: a 32-key block below lo_max or reaching
-    // past hi_min needs the per-key mask, one below lo_min or past hi_max is invisible to all lanes
-    const int2 kr = key_range((int) q0 + l32, (int) R, np, tpf);
+    f16v acc[QT][NDT];
+    float m_run[QT], l_run[QT];
+    int2 kr[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) acc[qt][dt] = zero;
+        m_run[qt] = -INFINITY; l_run[qt] = 0.0f;
+        kr[qt] = key_range((int) q0 + 32 * qt + l32, (int) R, np, tpf);   // this lane's key range per tile
+    }
+    // the wave's bounds on its queries' ranges: a 32-key block below lo_max or reaching past hi_min
+    // needs the per-key mask (blocks no query of the wave sees are masked whole)
     const int qw = (int) q0, qp = max(qw, np);
-    const int lo_min = key_range(qw, (int) R, np, tpf).x, lo_max = key_range(qw + 31, (int) R, np, tpf).x;
-    const int hi_min = qp <= qw + 31 ? key_range(qp, (int) R, np, tpf).y : (int) R;
-    const int hi_max = qw < np ? (int) R : key_range(qw + 31, (int) R, np, tpf).y;
+    const int lo_max = key_range(qw + QW - 1, (int) R, np, tpf).x;
+    const int hi_min = qp <= qw + QW - 1 ? key_range(qp, (int) R, np, tpf).y : (int) R;
 
-    for (int s = 0; s < NST - 1; s++) issue(s);
-    for (int s = 0; s < nt; s++) {
-        // tile s has landed once only the copies of the NST - 2 younger tiles are outstanding; the
-        // half with fewer tiles issues fewer, so its waits are conservative
-        if (s + NST - 2 < my_nt) tile_barrier<(NST - 2) * 4>();
-        else tile_barrier<0>();
-        issue(s + NST - 1);
-        if (s >= my_nt) continue;                       // (second half, odd tile count) barrier only
-        const unsigned char * sK = hbase + (s % NST) * STAGE;
-        const unsigned char * sV = sK + TILE;
-        const int64_t kt = (int64_t) (t0 + s) * KT;
+    // One 32-key block kb of a tile and one query tile qt form a unit with four phases: A (S = K.Q^T,
+    // NKK chained MFMAs), M (mask, row maximum, the rare lazy rescale), E (exp2, row sum, f16 weights:
+    // VALU only) and P (O^T += V^T.P^T, MFMAs). The units of a tile, kb-major, are software-pipelined
+    // so that each unit's E runs while the next unit's A MFMAs execute and its P MFMAs while the next
+    // unit's M runs: a wave keeps the matrix core and the VALU busy together.
+    auto qk = [&](int qt, const h8 (&kc)[NKK]) {
+        f16v S = zero;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            const int kb0 = (int) kt + 32 * kb;
-            if (kb0 + 32 <= lo_min || kb0 >= hi_max) continue;     // no query of this wave sees them
-            f16v S = zero;
+        for (int kk = 0; kk < NKK; kk++) S = MFMA16(kc[kk], qv[qt][kk], S);
+        return S;
+    };
+    // M: keys past R or outside a lane's range (block-causal) to -inf, then the lazy maximum
+    auto mx = [&](int qt, f16v & S, int kb0) {
+        if (MASKED && (kb0 < lo_max || kb0 + 32 > hi_min)) {
+            const int key0 = kb0 + 4 * g;
 #pragma unroll
-            for (int kk = 0; kk < HDO / 16; kk++) S = MFMA16(lds_chunk(sK, 32 * kb + l32, 2 * kk + g), qv[kk], S);
-            if (kb0 < lo_max || kb0 + 32 > hi_min) {                 // keys past R or outside a lane's range
-                const int key0 = kb0 + 4 * g;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = key0 + 8 * (r >> 2) + (r & 3);
-                    if (key < kr.x || key >= kr.y) S[r] = -INFINITY;
-                }
-            }
-            float mloc = S[0];
-#pragma unroll
-            for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, S[r]);
-            mloc = halves_max(mloc);
-            if (mloc > m_run && (m_run == -INFINITY || (mloc - m_run) * c > LAZY)) {
-                // move the reference maximum; rescale what was accumulated against the old one
-                const float alpha = fast_exp2((m_run - mloc) * c);
-                l_run *= alpha;
-#pragma unroll
-                for (int r = 0; r < 16; r++) { acc0[r] *= alpha; acc1[r] *= alpha; }
-                m_run = mloc;
-            }
-            const float mc = m_run == -INFINITY ? 0.0f : m_run * c;   // no key seen yet: S is -inf too
-            float p[16], lsum = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) { p[r] = fast_exp2(fmaf(S[r], c, -mc)); lsum += p[r]; }
-            lsum = halves_sum(lsum);
-            l_run += lsum;
-#pragma unroll
-            for (int kk2 = 0; kk2 < 2; kk2++) {
-                h8 pb;
-#pragma unroll
-                for (int e = 0; e < 8; e++) pb[e] = (_Float16) p[8 * kk2 + e];
-                const int ch = 4 * kb + 2 * kk2 + g;
-                acc0 = MFMA16(lds_chunk(sV, l32, ch), pb, acc0);
-                if constexpr (HDO == 64) acc1 = MFMA16(lds_chunk(sV, 32 + l32, ch), pb, acc1);
+            for (int r = 0; r < 16; r++) {
+                const int key = key0 + 8 * (r >> 2) + (r & 3);
+                if (key < kr[qt].x || key >= kr[qt].y) S[r] = -INFINITY;
             }
         }
-    }
-
-    // merge the two key halves: the second half's waves publish (m, l, acc) through LDS
-    __syncthreads();
-    float * xs = (float *) smem + (size_t) (qg * 64 + lane) * 34;
-    if (kh == 1) {
-        xs[0] = m_run; xs[1] = l_run;
+        float mloc = fmaxf(fmaxf(fmaxf(S[0], S[1]), fmaxf(S[2], S[3])), fmaxf(fmaxf(S[4], S[5]), fmaxf(S[6], S[7])));
+        mloc = fmaxf(mloc, fmaxf(fmaxf(fmaxf(S[8], S[9]), fmaxf(S[10], S[11])), fmaxf(fmaxf(S[12], S[13]), fmaxf(S[14], S[15]))));
+        mloc = halves_max(mloc);
+        const bool move = mloc > m_run[qt] && (m_run[qt] == -INFINITY || (mloc - m_run[qt]) * c > LAZY);
+        if (__builtin_amdgcn_ballot_w64(move) != 0) {   // rare after the first blocks: a uniform branch
+            // move the reference maximum; rescale what was accumulated against the old one (the empty
+            // volatile asm keeps the compiler from executing this block speculatively on every block)
+            asm volatile("");
+            const float alpha = move ? fast_exp2((m_run[qt] - mloc) * c) : 1.0f;
+            l_run[qt] *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; r++) { xs[2 + r] = acc0[r]; xs[18 + r] = acc1[r]; }
-    }
-    __syncthreads();
-    if (kh == 1) return;
-    {
-        const float m1 = xs[0], l1 = xs[1];
-        const float m = fmaxf(m_run, m1);
-        const float a0 = m_run == -INFINITY ? 0.0f : fast_exp2((m_run - m) * c);
-        const float a1 = m1 == -INFINITY ? 0.0f : fast_exp2((m1 - m) * c);
-        l_run = fmaf(l_run, a0, l1 * a1);
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[qt][dt][r] *= alpha;
+            m_run[qt] = move ? mloc : m_run[qt];
+        }
+    };
+    // E: weights 2^(s c - m c) as the f16 B operand of the P.V MFMA, their f32 sum into l
+    auto ex = [&](int qt, const f16v & S, h8 (&pb)[2]) {
+        const float mc = m_run[qt] == -INFINITY ? 0.0f : m_run[qt] * c;   // no key seen yet: S is -inf too
+        float p[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            acc0[r] = fmaf(acc0[r], a0, xs[2 + r] * a1);
-            acc1[r] = fmaf(acc1[r], a0, xs[18 + r] * a1);
+            p[r] = fast_exp2(fmaf(S[r], c, -mc));
+            pb[r >> 3][r & 7] = (_Float16) p[r];
+        }
+        const float s0 = (p[0] + p[1]) + (p[2] + p[3]), s1 = (p[4] + p[5]) + (p[6] + p[7]);
+        const float s2 = (p[8] + p[9]) + (p[10] + p[11]), s3 = (p[12] + p[13]) + (p[14] + p[15]);
+        l_run[qt] += halves_sum((s0 + s1) + (s2 + s3));
+    };
+    auto pv = [&](int qt, const h8 (&pb)[2], const h8 (&vc)[2][NDT]) {
+#pragma unroll
+        for (int kk2 = 0; kk2 < 2; kk2++)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) acc[qt][dt] = MFMA16(vc[kk2][dt], pb[kk2], acc[qt][dt]);
+    };
+    // one MFMA, then n VALU instructions, four times: the interleave of an A phase with E's VALU work
+    auto interleave = [] {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
+        }
+    };
+    constexpr int U = 2 * QT;                           // units per tile
+
+    for (int s = 0; s < nt; s++) {
+        // tile s has landed (this wave's copies: vmcnt(0); the other waves': the barrier), and every
+        // wave is past tile s - 1, whose stage tile s + 1 now refills
+        tile_barrier<0>();
+        issue(s + 1);
+        if (s >= my_nt) continue;                       // (a split with one tile less) barrier only
+        const unsigned char * sK = sbase + (s & 1) * STAGE;
+        const unsigned char * sV = sK + TILE;
+        const int kt = (t0 + s) * KT;
+        h8 kc[NKK], vc[2][2][NDT], pb[2];
+        f16v S[U];
+        auto load_k = [&](int kb) {
+#pragma unroll
+            for (int kk = 0; kk < NKK; kk++) kc[kk] = lds_chunk(sK, 32 * kb + l32, 2 * kk + g);
+        };
+        auto load_v = [&](int kb) {
+#pragma unroll
+            for (int kk2 = 0; kk2 < 2; kk2++)
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) vc[kb][kk2][dt] = lds_chunk(sV, 32 * dt + l32, 4 * kb + 2 * kk2 + g);
+        };
+        load_k(0);
+        load_v(0);
+        S[0] = qk(0, kc);                               // A(0)
+        mx(0, S[0], kt);                                // M(0)
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int qt = u % QT, kb = u / QT;
+            if (u + 1 < U) {
+                const int qn = (u + 1) % QT, kn = (u + 1) / QT;
+                if (kn != kb) load_k(kn);
+                S[u + 1] = qk(qn, kc);                  // A(u+1) with E(u)
+                ex(qt, S[u], pb);
+                interleave();
+                if (kn != kb) load_v(kn);
+                pv(qt, pb, vc[kb]);                     // P(u) with M(u+1)
+                mx(qn, S[u + 1], kt + 32 * kn);
+            } else {
+                ex(qt, S[u], pb);                       // E, P of the tile's last unit
+                pv(qt, pb, vc[kb]);
+            }
         }
     }
 
-    const int64_t q = q0 + l32;
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    float o0[16], o1[16];
+    // merge the key splits: splits 1..KS-1 publish (m, l, acc) through LDS (value-major, one float
+    // per lane per bank), split 0 combines them in split order
+    constexpr int NV = QT * (2 + 16 * NDT);             // floats per lane: per query tile m, l, acc
+    __syncthreads();                                    // every wave is past its last stage read
+    if (ks > 0) {
+        float * xs = (float *) smem + (size_t) ((ks - 1) * QG + qg) * NV * 64 + lane;
 #pragma unroll
-    for (int r = 0; r < 16; r++) { o0[r] = acc0[r] * inv; o1[r] = acc1[r] * inv; }
+        for (int qt = 0; qt < QT; qt++) {
+            float * x = xs + (size_t) qt * (NV / QT) * 64;
+            x[0] = m_run[qt]; x[64] = l_run[qt];
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) x[(2 + 16 * dt + r) * 64] = acc[qt][dt][r];
+        }
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+        float mi[KS], ai[KS];
+        mi[0] = m_run[qt];
+        float m = m_run[qt];
+#pragma unroll
+        for (int k = 1; k < KS; k++) {
+            mi[k] = ((const float *) smem)[(size_t) ((k - 1) * QG + qg) * NV * 64 + (size_t) qt * (NV / QT) * 64 + lane];
+            m = fmaxf(m, mi[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < KS; k++) ai[k] = mi[k] == -INFINITY ? 0.0f : fast_exp2((mi[k] - m) * c);
+        float l = l_run[qt] * ai[0];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[qt][dt][r] *= ai[0];
+#pragma unroll
+        for (int k = 1; k < KS; k++) {
+            const float * x = (const float *) smem + (size_t) ((k - 1) * QG + qg) * NV * 64 + (size_t) qt * (NV / QT) * 64 + lane;
+            l = fmaf(x[64], ai[k], l);
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[qt][dt][r] = fmaf(x[(2 + 16 * dt + r) * 64], ai[k], acc[qt][dt][r]);
+        }
+        l_run[qt] = l;
+    }
+
     const int64_t DD = (int64_t) n_head * HDO;
-    if constexpr (OUT == A_Q8_0) {
-        // dims 0-31 (acc0) and 32-63 (acc1) are one q8_0 block each, split over lanes l32 and l32+32
-        float am0 = 0.0f, am1 = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; r++) { am0 = fmaxf(am0, fabsf(o0[r])); am1 = fmaxf(am1, fabsf(o1[r])); }
-        am0 = halves_max(am0);
-        am1 = halves_max(am1);
-        if (q >= R) return;
-        const float id0 = am0 != 0.0f ? 127.0f / am0 : 0.0f, id1 = am1 != 0.0f ? 127.0f / am1 : 0.0f;
-        int8_t * crow = (int8_t *) O + (item * R + q) * DD + h * HDO;
+    for (int qt = 0; qt < QT; qt++) {
+        const int64_t q = q0 + 32 * qt + l32;
+        const float inv = l_run[qt] > 0.0f ? 1.0f / l_run[qt] : 0.0f;
+        float o[NDT][16];
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            uint32_t w0 = 0, w1 = 0;
+        for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int c0 = (int) fminf(fmaxf(rintf(o0[4 * qq + e] * id0), -128.0f), 127.0f);
-                const int c1 = (int) fminf(fmaxf(rintf(o1[4 * qq + e] * id1), -128.0f), 127.0f);
-                w0 |= ((uint32_t) c0 & 0xffu) << (8 * e);
-                w1 |= ((uint32_t) c1 & 0xffu) << (8 * e);
+            for (int r = 0; r < 16; r++) o[dt][r] = acc[qt][dt][r] * inv;
+        if constexpr (OUT == A_Q8_0) {
+            // each 32-dim row block is one q8_0 block, split over lanes l32 and l32 + 32
+            float am[NDT];
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                am[dt] = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; r++) am[dt] = fmaxf(am[dt], fabsf(o[dt][r]));
+                am[dt] = halves_max(am[dt]);
             }
-            const int d = 8 * qq + 4 * g;
-            *(uint32_t *) (crow + d) = w0;
-            if constexpr (HDO == 64) *(uint32_t *) (crow + 32 + d) = w1;
-        }
-        if (g == 0) {
-            uint16_t * drow = (uint16_t *) Od + (item * R + q) * (DD / 32) + h * (HDO / 32);
-            drow[0] = f2hbits(am0 / 127.0f);
-            if constexpr (HDO == 64) drow[1] = f2hbits(am1 / 127.0f);
-        }
-    } else {
-        if (q >= R) return;
-        float * orow = (float *) O + (item * R + q) * DD + h * HDO;
+            if (q < R) {
+                int8_t * crow = (int8_t *) O + (item * R + q) * DD + h * HDO;
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            const int d = 8 * qq + 4 * g;
-            *(float4 *) (orow + d) = make_float4(o0[4 * qq], o0[4 * qq + 1], o0[4 * qq + 2], o0[4 * qq + 3]);
-            if constexpr (HDO == 64)
-                *(float4 *) (orow + 32 + d) = make_float4(o1[4 * qq], o1[4 * qq + 1], o1[4 * qq + 2], o1[4 * qq + 3]);
+                for (int dt = 0; dt < NDT; dt++) {
+                    const float id = am[dt] != 0.0f ? 127.0f / am[dt] : 0.0f;
+#pragma unroll
+                    for (int qq = 0; qq < 4; qq++) {
+                        uint32_t w = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int cq = (int) fminf(fmaxf(rintf(o[dt][4 * qq + e] * id), -128.0f), 127.0f);
+                            w |= ((uint32_t) cq & 0xffu) << (8 * e);
+                        }
+                        *(uint32_t *) (crow + 32 * dt + 8 * qq + 4 * g) = w;
+                    }
+                }
+                if (g == 0) {
+                    uint16_t * drow = (uint16_t *) Od + (item * R + q) * (DD / 32) + h * (HDO / 32);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; dt++) drow[dt] = f2hbits(am[dt] / 127.0f);
+                }
+            }
+        } else {
+            if (q < R) {
+                float * orow = (float *) O + (item * R + q) * DD + h * HDO;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                    for (int qq = 0; qq < 4; qq++)
+                        *(float4 *) (orow + 32 * dt + 8 * qq + 4 * g) =
+                            make_float4(o[dt][4 * qq], o[dt][4 * qq + 1], o[dt][4 * qq + 2], o[dt][4 * qq + 3]);
+            }
         }
     }
 }
@@ -395,11 +501,15 @@ void launch_attention(const void * q, const void * k, const void * vt, const act
         }
         return;
     }
+    const bool masked = tpf > 0 || R % KT != 0;
+    constexpr int QT = ATTN_QT;
+    static_assert(QT == 1 || QT == 2, "one or two query tiles per wave");
+    auto go = [&](auto kern, void * od) { kern<<<grid, 64 * KS * 4 / QT, 0, s>>>(Q, K, V, out.q, od, n_head, R, R_pad, c, n_prefix, tpf); };
     if (out.fmt == A_Q8_0) {
-        if (hd == 32) k_attn_hd64<A_Q8_0, 32><<<grid, 512, 0, s>>>(Q, K, V, out.q, out.d, n_head, R, R_pad, c, n_prefix, tpf);
-        else k_attn_hd64<A_Q8_0, 64><<<grid, 512, 0, s>>>(Q, K, V, out.q, out.d, n_head, R, R_pad, c, n_prefix, tpf);
+        if (hd == 32) masked ? go(k_attn_hd64<A_Q8_0, 32, true, QT>, out.d) : go(k_attn_hd64<A_Q8_0, 32, false, QT>, out.d);
+        else masked ? go(k_attn_hd64<A_Q8_0, 64, true, QT>, out.d) : go(k_attn_hd64<A_Q8_0, 64, false, QT>, out.d);
     } else {
-        if (hd == 32) k_attn_hd64<A_F32, 32><<<grid, 512, 0, s>>>(Q, K, V, out.q, nullptr, n_head, R, R_pad, c, n_prefix, tpf);
-        else k_attn_hd64<A_F32, 64><<<grid, 512, 0, s>>>(Q, K, V, out.q, nullptr, n_head, R, R_pad, c, n_prefix, tpf);
+        if (hd == 32) masked ? go(k_attn_hd64<A_F32, 32, true, QT>, nullptr) : go(k_attn_hd64<A_F32, 32, false, QT>, nullptr);
+        else masked ? go(k_attn_hd64<A_F32, 64, true, QT>, nullptr) : go(k_attn_hd64<A_F32, 64, false, QT>, nullptr);
     }
 }

@@ -407,8 +407,8 @@ def _attention_ref(qkv, n_items, n_tok, H, rope=None, mask=None, hd=64):
     return out
 
 
-# token counts cover: even / odd numbers of 64-key tiles (the two key halves of a workgroup get equal or
-# unequal shares), one tile (the second half is empty), a last tile with a single valid key, padding
+# token counts cover: 64-key tile counts that the four key splits of a workgroup share equally or not,
+# one tile (three splits empty), a last tile with a single valid key, padding
 ATTN_CASES = [(1, 2048, 4, True), (2, 197, 6, False), (1, 576, 2, True), (3, 17, 2, False), (1, 129, 1, False),
               (1, 64, 1, False), (2, 65, 2, True)]
 
