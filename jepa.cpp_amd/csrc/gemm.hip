@@ -102,6 +102,21 @@ __device__ __forceinline__ float gelu_erf(float x) {
     return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
 }
 
+// The residual epilogue with the row's current values x already loaded: x + (t + bias) * ls
+__device__ __forceinline__ void resid4(const kargs & a, int64_t m, int64_t n, float t[4], float4 x) {
+    const gemm_epi & ep = a.ep;
+    if (a.bias) {
+        const float4 b = *(const float4 *) (a.bias + n);
+        t[0] = __fadd_rn(t[0], b.x); t[1] = __fadd_rn(t[1], b.y); t[2] = __fadd_rn(t[2], b.z); t[3] = __fadd_rn(t[3], b.w);
+    }
+    if (ep.ls) {
+        const float4 v = *(const float4 *) (ep.ls + n);
+        t[0] = __fmul_rn(t[0], v.x); t[1] = __fmul_rn(t[1], v.y); t[2] = __fmul_rn(t[2], v.z); t[3] = __fmul_rn(t[3], v.w);
+    }
+    x.x = __fadd_rn(x.x, t[0]); x.y = __fadd_rn(x.y, t[1]); x.z = __fadd_rn(x.z, t[2]); x.w = __fadd_rn(x.w, t[3]);
+    *(float4 *) (ep.y + m * ep.ldy + n) = x;
+}
+
 __device__ __forceinline__ int perm16(int64_t tok) {
     // position of token `tok` inside its 16-token group of V^T (see attention.hip)
     const int key = (int) (tok & 15);
@@ -450,6 +465,24 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             }
         }
     };
+    // Residual epilogue (int8 and 4-bit weights): the rows it adds to are loaded during the last K
+    // stage, so that their latency hides under that stage's MFMAs instead of following them (rows
+    // past M read row M - 1; their results are dropped). Not for 4-tile waves: no registers left.
+    constexpr bool RPF = EPI == EPI_RESID && (WF == W_Q32 || WF == W_Q40 || WF == W_Q4K) && TI * TJ < 4;
+    [[maybe_unused]] float4 xres[RPF ? TI : 1][RPF ? TJ : 1][4];
+    [[maybe_unused]] auto prefetch_resid = [&]() {
+        if constexpr (RPF) {
+#pragma unroll
+            for (int j = 0; j < TJ; j++) {
+                const int64_t m = m0 + 32 * (wm * TJ + j) + l32, mm = m < M ? m : M - 1;
+#pragma unroll
+                for (int i = 0; i < TI; i++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        xres[i][j][q] = *(const float4 *) (a.ep.y + mm * a.ep.ldy + n0 + 32 * (wn * TI + i) + 8 * q + 4 * g);
+            }
+        }
+    };
     [[maybe_unused]] auto q32_main = [&](int64_t nfull) {
       if constexpr (WF == W_Q32 || WF == W_Q40) {
         constexpr int TT = TI * TJ, U = 4 * TT;
@@ -594,6 +627,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         // unused buffer, read and discarded)
         if (nfull > 0) body(0, std::true_type{}, std::true_type{});
         for (int64_t st = 1; st + 1 < nfull; st++) body(st, std::true_type{}, std::false_type{});
+        prefetch_resid();
         if (nfull > 1) body(nfull - 1, std::false_type{}, std::false_type{});
         // final half stage (K % 128 == 64): blocks 0 and 1 of stage nfull, after all copies landed
         if (nfull < nst) {
@@ -812,6 +846,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             body(st, T_{}, F_{}, H1{});
             body(st + 1, T_{}, F_{}, H0{});
         }
+        prefetch_resid();
         body(nst - 1, F_{}, F_{}, H1{});
         // the copies issued during the last stages must land before the workgroup's LDS is released
         __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
@@ -1185,7 +1220,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 for (int q = 0; q < 4; q++) {
                     const int64_t n = nb + 8 * q + 4 * g;
                     float t[4] = {acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                    epi4<EPI>(a, m, n, t);
+                    if constexpr (RPF) resid4(a, m, n, t, xres[i][j][q]);
+                    else epi4<EPI>(a, m, n, t);
                 }
             }
         }
