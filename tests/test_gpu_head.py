@@ -35,9 +35,12 @@ def _tiny(ftype, **kw):
                       ffn_dim=1024 if big else 512, n_head=4 if big else 2, **kw)
 
 
-@pytest.mark.parametrize("ftype,n_tok", [("q8_0", 40), ("q8_0", 300), ("q4_0", 513), ("f16", 257), ("q4_k", 300), ("f32", 64)])
+@pytest.mark.parametrize("ftype,n_tok", [("q8_0", 40), ("q8_0", 300), ("q4_0", 513), ("f16", 257), ("q4_k", 300), ("f32", 64),
+                                         ("q8_0", 2500)])
 def test_tiny_head_parity(jlib, oracle, models_dir, ftype, n_tok):
-    """Head alone on the same rows: 1 to 3 key chunks of the pool attention, every weight format."""
+    """Head alone on the same rows, every weight format: the pool attention's 64-key chunks from 1 to 40
+    (the merge pass takes eight chunks per wave at a time, then the rest one by one: 2500 rows give 40
+    chunks, the last one of 4 keys, so a wave runs both loops)."""
     cfg = _tiny(ftype)
     path = forge.cached_model(cfg, models_dir)
     m = jlib.Model(path)
