@@ -237,6 +237,10 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
         // tile s has landed (this wave's copies: vmcnt(0); the other waves': the barrier), and every
         // wave is past tile s - 1, whose stage tile s + 1 now refills
         tile_barrier<0>();
+        // a wave raises its issue priority for the first half of the tile and drops it after: the
+        // waves of a SIMD otherwise share it by age, and the oldest would idle at the next barrier
+        // while the youngest finishes (measured 30.0 -> 29.5 us at 2048 tokens x 16 heads)
+        __builtin_amdgcn_s_setprio(1);
         issue(s + 1);
         if (s >= my_nt) continue;                       // (a split with one tile less) barrier only
         const unsigned char * sK = sbase + (s & 1) * STAGE;
@@ -269,6 +273,7 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
                 interleave();
                 if (kn != kb) load_v(kn);
                 pv(qt, pb, vc[kb]);                     // P(u) with M(u+1)
+                if (u == U / 2 - 1) __builtin_amdgcn_s_setprio(0);
                 mx(qn, S[u + 1], kt + 32 * kn);
             } else {
                 ex(qt, S[u], pb);                       // E, P of the tile's last unit
@@ -280,6 +285,7 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
     // merge the key splits: splits 1..KS-1 publish (m, l, acc) through LDS (value-major, one float
     // per lane per bank), split 0 combines them in split order
     constexpr int NV = QT * (2 + 16 * NDT);             // floats per lane: per query tile m, l, acc
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();                                    // every wave is past its last stage read
     if (ks > 0) {
         float * xs = (float *) smem + (size_t) ((ks - 1) * QG + qg) * NV * 64 + lane;
