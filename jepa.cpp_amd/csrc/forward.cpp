@@ -228,7 +228,7 @@ bool ensure_workspace(jepa_context * ctx, int n_items, int n_chans, int n_frames
     } else {
         w->tubelet = 1;
         w->Np = (int64_t) (height / P) * (width / P);
-        w->prefix = e.cls_token ? 1 : 0;
+        w->prefix = (e.cls_token ? 1 : 0) + e.n_registers;
         w->K = (int64_t) e.in_chans * P * P;
     }
     const int64_t D = e.embed_dim, F = e.ffn_dim, H = e.n_head, hd = e.head_dim();
@@ -289,10 +289,13 @@ void enqueue_forward(jepa_context * ctx, const float * in, float * out, float * 
         if (w.video && e.modality_embed) ep.addvec = w.image_path ? m->mod_img : m->mod_video;
         if (!w.video && m->pos_embed) ep.addrows = m->pos_embed;
         kt.run("patch_embed", [&] { launch_gemm(pe, pa, n_items * w.Np, ep, s, &w.split); });
-        // CLS row in front: image families add its position row; the video family with one (levjepa)
-        // gives it no position (reference src/jepa.cpp:865-880)
-        if (e.cls_token)
-            kt.run("cls", [&] { launch_cls_rows(w.x, m->cls_token, w.video ? nullptr : m->pos_embed, n_items, R, D, s); });
+        // CLS and register rows in front: image families add their position rows; the video families
+        // give them no position (reference src/jepa.cpp:598-608, 865-880)
+        if (w.prefix > 0)
+            kt.run("cls", [&] {
+                launch_prefix_rows(w.x, e.cls_token ? m->cls_token : nullptr, m->reg_tokens, e.n_registers,
+                                   w.video ? nullptr : m->pos_embed, n_items, R, D, s);
+            });
     }
     if (trace) launch_copy_f32(w.x, trace, rows * D, s);
     // block-causal attention (levjepa): temporal slots of gh*gw patch rows after the prefix rows
@@ -357,7 +360,7 @@ int64_t encode_device(jepa_context * ctx, const float * in_dev, int n_batch, int
     if (!video && m->pos_embed && m->pos_rows != R) {
         jepa_log("jepa: token grid %dx%d (+%d prefix) = %lld tokens does not match enc.pos_embed (%lld rows); "
                  "position-table interpolation is not implemented yet - feed a %dx%d input\n",
-                 height / e.patch_size, width / e.patch_size, e.cls_token ? 1 : 0, (long long) R, (long long) m->pos_rows, e.img_size,
+                 height / e.patch_size, width / e.patch_size, (e.cls_token ? 1 : 0) + e.n_registers, (long long) R, (long long) m->pos_rows, e.img_size,
                  e.img_size);
         return -1;
     }

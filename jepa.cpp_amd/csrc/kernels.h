@@ -96,6 +96,10 @@ void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_ite
 
 // prefix (CLS) rows: x[it*R + 0][n] = cls[n] (+ pos[n])
 void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D, hipStream_t s);
+// rows 0 .. (cls ? 1 : 0) + n_reg - 1 of every item of R rows: CLS, then the register rows [n_reg][D],
+// each plus its row of pos when pos is not null
+void launch_prefix_rows(float * x, const float * cls, const float * reg, int n_reg, const float * pos, int64_t n_items, int64_t R,
+                        int64_t D, hipStream_t s);
 
 // f32 values -> ggml blocks of dst_type (q8_0, q4_0, q4_K) or f16, bit-exact with ggml's reference
 // quantizers; n a multiple of the block size. Returns false for another type or a ragged n.

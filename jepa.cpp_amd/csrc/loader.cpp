@@ -458,9 +458,14 @@ extern "C" jepa_model * jepa_model_load_ex(const char * path, const jepa_model_p
             else { m->pos_rows = t->ne[1]; ok = L.vec("enc.pos_embed", -1, &m->pos_embed); }
         }
         if (ok && e.cls_token && !m->cls_token) { jepa_log("jepa: cls_token=true but enc.cls_token missing\n"); ok = false; }
-        if (ok && e.n_registers > 0) {
-            jepa_log("jepa: jepa.enc.n_registers = %d: register tokens are not implemented on this path\n", e.n_registers);
-            ok = false;
+        if (ok && e.n_registers > 0) {   // enc.reg_tokens [n_registers rows of D], f32 (src/jepa-gguf.cpp:959-979)
+            const gguf::tensor_info * t = f.tensor("enc.reg_tokens");
+            if (!t || t->ne[0] != D || t->ne[1] != e.n_registers || t->ne[2] != 1 || t->ne[3] != 1) {
+                jepa_log("jepa: jepa.enc.n_registers is %d but enc.reg_tokens is %s\n", e.n_registers, t ? "a different shape" : "missing");
+                ok = false;
+            } else {
+                ok = L.vec("enc.reg_tokens", D * e.n_registers, &m->reg_tokens, true);
+            }
         }
         if (ok && !e.qkv_fused) { jepa_log("jepa: separate attn_q/k/v weights are not implemented on this path (qkv_fused = false)\n"); ok = false; }
         m->layers.resize((size_t) e.n_layer);

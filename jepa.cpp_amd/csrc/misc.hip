@@ -307,6 +307,20 @@ __global__ void k_cls_rows(float * x, const float * cls, const float * pos, int6
     x[it * R * D + n] = v;
 }
 
+// Prefix rows of every item, in front of its patch rows: the CLS row (when cls), then n_reg register
+// rows, each plus its position row when pos is given (reference src/jepa.cpp:598-608: the registers
+// and then the CLS row are concatenated in front, the position table is added to every row)
+__global__ void k_prefix_rows(float * x, const float * cls, const float * reg, int n_reg, const float * pos, int64_t n_items,
+                              int64_t R, int64_t D) {
+    const int nc = cls ? 1 : 0, np = nc + n_reg;
+    const int64_t id = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= n_items * np * D) return;
+    const int64_t it = id / (np * D), p = (id / D) % np, n = id % D;
+    float v = p < nc ? cls[n] : reg[(p - nc) * D + n];
+    if (pos) v = __fadd_rn(v, pos[p * D + n]);
+    x[(it * R + p) * D + n] = v;
+}
+
 // ------------------------------------------------------------------------------------------------
 // weight expansion at load (ggml blocks -> GEMM operand arrays)
 // ------------------------------------------------------------------------------------------------
@@ -545,6 +559,12 @@ void launch_patchify(const float * in, void * rows, bool half_out, int64_t n_ite
         if (half_out) k_patchify_rows<true><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, v);
         else k_patchify_rows<false><<<nblk(total, 256), 256, 0, s>>>(in, rows, n_items, C, T, H, W, P, tub, v);
     }
+}
+
+void launch_prefix_rows(float * x, const float * cls, const float * reg, int n_reg, const float * pos, int64_t n_items, int64_t R,
+                        int64_t D, hipStream_t s) {
+    const int np = (cls ? 1 : 0) + n_reg;
+    if (np > 0) k_prefix_rows<<<nblk(n_items * np * D, 256), 256, 0, s>>>(x, cls, reg, n_reg, pos, n_items, R, D);
 }
 
 void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_items, int64_t R, int64_t D, hipStream_t s) {

@@ -170,6 +170,7 @@ struct jepa_model {
     dev_linear patch, patch_img;
     float * pos_embed = nullptr; int64_t pos_rows = 0;
     float * cls_token = nullptr;
+    float * reg_tokens = nullptr;   // [n_registers][D]
     float * mod_img = nullptr, * mod_video = nullptr;
     float * norm_w = nullptr, * norm_b = nullptr;
     std::vector<dev_layer> layers;

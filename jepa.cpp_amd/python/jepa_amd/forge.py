@@ -32,6 +32,7 @@ class EncoderConfig:
     img_size: int = 224
     n_frames: int = 1
     cls_token: bool = False
+    n_registers: int = 0    # register tokens after the CLS row (enc.reg_tokens)
     ftype: str = "q8_0"     # f16 | q8_0 | q4_0 | q4_k
     rope_layout: str = ""   # tiled | interleaved ('' for non-rope families)
     rope_interpolate: bool = False
@@ -178,7 +179,7 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
         if cfg.rope_ref_grid:
             w.add("jepa.enc.rope_ref_grid", cfg.rope_ref_grid)
     w.add("jepa.enc.cls_token", cfg.cls_token)
-    w.add("jepa.enc.n_registers", 0)
+    w.add("jepa.enc.n_registers", cfg.n_registers)
     w.add("jepa.enc.qkv_fused", True)
     w.add("jepa.enc.modality_embed", cfg.modality_embed)
     w.add("jepa.enc.image_patch_embed", cfg.image_patch_embed)
@@ -249,8 +250,10 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
         vec("enc.mod_embed_video", D)
     if cfg.cls_token:
         vec("enc.cls_token", D)
+    if cfg.n_registers:
+        w.add_tensor("enc.reg_tokens", GGML_F32, (D, cfg.n_registers), normal(cfg.n_registers, D))
     if not video:
-        n_tok = (cfg.img_size // cfg.patch) ** 2 + (1 if cfg.cls_token else 0)
+        n_tok = (cfg.img_size // cfg.patch) ** 2 + (1 if cfg.cls_token else 0) + cfg.n_registers
         w.add_tensor("enc.pos_embed", GGML_F32, (D, n_tok), normal(n_tok, D))
     def block(p, D=D, F=F):
         ln(p + "ln1", D)

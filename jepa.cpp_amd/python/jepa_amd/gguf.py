@@ -22,8 +22,9 @@ import numpy as np
 # ggml_type ids stored in tensor infos
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q8_K = 0, 1, 2, 8, 12, 15
 TYPE_NAMES = {GGML_F32: "f32", GGML_F16: "f16", GGML_Q4_0: "q4_0", GGML_Q8_0: "q8_0", GGML_Q4_K: "q4_K"}
+GGML_BF16 = 30
 BLOCK = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q4_0: (32, 18), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144),
-         GGML_Q8_K: (256, 292)}
+         GGML_Q8_K: (256, 292), GGML_BF16: (1, 2)}
 # general.file_type values (GGML_FTYPE_*), reference src/jepa-gguf.cpp:62-93
 FTYPE = {"f32": 0, "f16": 1, "q4_0": 2, "q8_0": 7, "q4_k": 12}
 

@@ -1060,7 +1060,7 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
     const int file_type = (int) gg_int(&f, "general.file_type", 0);
     const int hd = H > 0 ? D / H : 0;
     const int n_layers = n_layers_limit > 0 && n_layers_limit < L ? n_layers_limit : L;
-    if ((!video && !image) || D <= 0 || H <= 0 || n_chans != C || n_reg != 0) {
+    if ((!video && !image) || D <= 0 || H <= 0 || n_chans != C || n_reg < 0) {
         fprintf(stderr, "oracle: family '%s' / shape not covered by the oracle\n", fam);
         gg_close(&f); return -1;
     }
@@ -1080,7 +1080,9 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
     if (height % P || width % P || T % tub) { fprintf(stderr, "oracle: shape not encodable\n"); gg_close(&f); return -1; }
     const int GT = T / tub, GH = height / P, GW = width / P;
     const int64_t Np = (int64_t) GT * GH * GW;
-    const int np = cls ? 1 : 0;                 /* CLS row in front (hfvit; levjepa: the video family with one) */
+    /* prefix rows in front of the patch rows: the CLS row (hfvit; levjepa: the video family with one),
+     * then the register rows (src/jepa.cpp:598-608 and 868-881 concatenate the registers, then CLS) */
+    const int np = (cls ? 1 : 0) + n_reg;
     const int64_t R = Np + np;
     const int block_causal = !strcmp(gg_str(&f, "jepa.enc.attn_mode", "full"), "block_causal");
     if (block_causal && !video) { fprintf(stderr, "oracle: block_causal needs a video family\n"); gg_close(&f); return -1; }
@@ -1134,6 +1136,12 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
             const float * ct = gg_vec(&f, "enc.cls_token");
             if (!ct) goto done;
             memcpy(x, ct, sizeof(float) * D);
+        }
+        if (n_reg > 0) {   /* enc.reg_tokens [n_reg][D] after the CLS row (src/jepa.cpp:598-601, 868-874) */
+            const gg_tensor * rt = gg_tensor_find(&f, "enc.reg_tokens");
+            const float * rv = gg_vec(&f, "enc.reg_tokens");
+            if (!rt || !rv || rt->ne[0] != D || rt->ne[1] != n_reg) { fprintf(stderr, "oracle: enc.reg_tokens missing or mis-shaped\n"); goto done; }
+            memcpy(x + (int64_t) (cls ? 1 : 0) * D, rv, sizeof(float) * n_reg * D);
         }
         if (image) {
             const float * pos = gg_vec(&f, "enc.pos_embed");

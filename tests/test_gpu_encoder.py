@@ -70,6 +70,22 @@ def test_tiny_encoder_parity(jlib, oracle, models_dir, family, ftype, n_batch, n
     check_parity(got, want, gtr, wtr, label=f"{family}/{ftype}")
 
 
+@pytest.mark.parametrize("family,ftype,n_reg,n_batch,n_frames", [("hfvit", "f16", 4, 2, 1), ("hfvit", "q8_0", 1, 1, 2),
+                                                                  ("vjepa2", "q8_0", 2, 1, 4), ("levjepa", "q8_0", 3, 1, 4)])
+def test_tiny_register_tokens(jlib, oracle, models_dir, family, ftype, n_reg, n_batch, n_frames):
+    """Register tokens (reference src/jepa.cpp:598-601, 868-874): rows [CLS, registers, patches]; the
+    image families add their position rows to them, the video families give them identity RoPE rows
+    and, block-causal, the prefix rows' full view. Mean pooling skips all prefix rows."""
+    cfg = forge.tiny(family, ftype, ln_random=True, n_registers=n_reg)
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, n_batch, n_frames, 64)
+    check_parity(got, want, gtr, wtr, label=f"{family}/{ftype} + {n_reg} registers")
+    npre = (1 if cfg.cls_token else 0) + n_reg
+    assert jlib.lib().jepa_model_n_prefix_tokens(m.ptr) == npre
+    rows = got.shape[0] // (n_batch * (1 if family != "hfvit" else n_frames))
+    pooled = m.pool_mean(got[:rows])
+    np.testing.assert_allclose(pooled, got[npre:rows].astype(np.float64).mean(0), rtol=0, atol=1e-6 * np.abs(got).max())
+
+
 def test_batch_equals_single(jlib, models_dir):
     """Items of one call equal separate calls bit for bit (reference tests/test-batch.cpp:12-21)."""
     for family, nb, nf in (("hfvit", 3, 1), ("vjepa2", 2, 4)):

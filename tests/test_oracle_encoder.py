@@ -168,6 +168,8 @@ def forward64(path, x):
         h = rows @ T("enc.patch_embed.weight").T + T("enc.patch_embed.bias")
         if has("enc.mod_embed_video"):
             h = h + T("enc.mod_embed_video")
+        if kv.get("jepa.enc.n_registers", 0):        # registers, then the CLS row, go in front
+            h = np.concatenate([T("enc.reg_tokens").reshape(-1, D), h])
         if kv.get("jepa.enc.cls_token"):
             h = np.concatenate([T("enc.cls_token")[None], h])
         if has("enc.pos_embed"):
@@ -178,8 +180,8 @@ def forward64(path, x):
             rope = _rope_tables64(grid, hd, 0 if kv["jepa.enc.rope_freq_layout"] == "tiled" else 1,
                                   bool(kv.get("jepa.enc.rope_interpolate")), (ref, ref), float(kv["jepa.enc.rope_theta"]))
         n = h.shape[0]
-        npre = n - rows.shape[0]                  # CLS rows in front of the patch rows
-        if rope is not None and npre:             # the CLS is not rotated (identity rows)
+        npre = n - rows.shape[0]                  # CLS and register rows in front of the patch rows
+        if rope is not None and npre:             # the prefix is not rotated (identity rows)
             rope = (np.vstack([np.ones((npre, hd)), rope[0]]), np.vstack([np.zeros((npre, hd)), rope[1]]))
         mask = np.zeros((n, n))
         if kv.get("jepa.enc.attn_mode") == "block_causal":
@@ -198,7 +200,8 @@ def forward64(path, x):
 
 
 @pytest.mark.parametrize("family,kw", [("hfvit", {}), ("hfvit", {"layer_scale": True}), ("vjepa2", {}),
-                                       ("vjepa2_1", {}), ("levjepa", {})])
+                                       ("vjepa2_1", {}), ("levjepa", {}), ("hfvit", {"n_registers": 4}),
+                                       ("vjepa2", {"n_registers": 2}), ("levjepa", {"n_registers": 3})])
 def test_oracle_encoder_matches_float64_forward(family, kw, tmp_path):
     cfg = forge.tiny(family, "f32", ln_random=True, **kw)
     path = forge.cached_model(cfg, str(tmp_path))
