@@ -297,23 +297,67 @@ struct loader {
         return t ? t->ne[1] : 0;
     }
 
+    // several tensors into device staging back to back, then pad_bytes of zeros
+    bool to_staging_n(const std::vector<const gguf::tensor_info *> & ts, size_t pad_bytes) {
+        if (ts.size() == 1) return to_staging(*ts[0], pad_bytes);
+        size_t total = pad_bytes;
+        for (const auto * t : ts) total += t->nbytes;
+        if (staging_size < total) {
+            if (staging) hipFree(staging);
+            staging = nullptr;
+            staging_size = 0;
+            if (hipMalloc(&staging, total) != hipSuccess) { jepa_log("jepa: hipMalloc(staging) failed\n"); return false; }
+            staging_size = total;
+        }
+        size_t off = 0;
+        for (const auto * t : ts) {   // host buffer reused per tensor: each copy completes before the next read
+            if (!read(*t) || hipMemcpyAsync((char *) staging + off, host.data(), t->nbytes, hipMemcpyHostToDevice, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess) return false;
+            off += t->nbytes;
+        }
+        return pad_bytes == 0 || (hipMemsetAsync((char *) staging + off, 0, pad_bytes, s) == hipSuccess && hipStreamSynchronize(s) == hipSuccess);
+    }
+
     // pad_out: the device matrix gets n_out rounded up to 128 rows (zero weights and bias), for the
     // linears whose output count the file chooses freely (the classifier); L.n_valid keeps n_out
     bool linear(const std::string & wname, const std::string & bname, int64_t n_in, int64_t n_out, dev_linear & L, bool required,
                 bool pad_out = false) {
-        const gguf::tensor_info * t = f.tensor(wname);
-        if (!t) {
-            if (required) { jepa_log("jepa: required tensor '%s' missing from %s\n", wname.c_str(), m->path.c_str()); return false; }
-            return true;
+        return linear_n({wname}, {bname}, n_in, n_out, L, required, pad_out);
+    }
+
+    // One device linear from the weight tensors wnames stacked along the outputs (each [n_in, n_out /
+    // parts], the same dtype; quantized blocks never cross a row, so the stacked rows are the fused
+    // matrix's) with their biases likewise: the separate attn_q / attn_k / attn_v of an unfused block,
+    // whose three linears the reference runs one by one (src/jepa.cpp:408-414)
+    bool linear_n(const std::vector<std::string> & wnames, const std::vector<std::string> & bnames, int64_t n_in, int64_t n_out,
+                  dev_linear & L, bool required, bool pad_out = false) {
+        const std::string & wname = wnames[0];
+        const int64_t n_part = n_out / (int64_t) wnames.size();
+        std::vector<const gguf::tensor_info *> ts;
+        for (const auto & name : wnames) {
+            const gguf::tensor_info * t = f.tensor(name);
+            if (!t) {
+                if (required || !ts.empty()) { jepa_log("jepa: required tensor '%s' missing from %s\n", name.c_str(), m->path.c_str()); return false; }
+                return true;
+            }
+            if (t->ne[0] != n_in || t->ne[1] != n_part || t->ne[2] != 1 || t->ne[3] != 1) {
+                jepa_log("jepa: tensor %s has shape [%" PRId64 ", %" PRId64 "], expected [%" PRId64 ", %" PRId64 "]\n",
+                         name.c_str(), t->ne[0], t->ne[1], n_in, n_part);
+                return false;
+            }
+            if (!ts.empty() && t->type != ts[0]->type) {
+                jepa_log("jepa: tensor %s is %s but %s is %s: the parts of one linear have to share a dtype\n", name.c_str(),
+                         ggml_traits(t->type).name, wname.c_str(), ggml_traits(ts[0]->type).name);
+                return false;
+            }
+            ts.push_back(t);
         }
-        if (t->ne[0] != n_in || t->ne[1] != n_out || t->ne[2] != 1 || t->ne[3] != 1) {
-            jepa_log("jepa: tensor %s has shape [%" PRId64 ", %" PRId64 "], expected [%" PRId64 ", %" PRId64 "]\n",
-                     wname.c_str(), t->ne[0], t->ne[1], n_in, n_out);
-            return false;
-        }
+        const gguf::tensor_info * t = ts[0];
+        size_t nbytes = 0;
+        for (const auto * p : ts) nbytes += p->nbytes;
         const int64_t n_file = n_out;
         if (pad_out) n_out = (n_out + 127) / 128 * 128;
-        const size_t pad_bytes = (size_t) (n_out - n_file) * (t->nbytes / (size_t) n_file);
+        const size_t pad_bytes = (size_t) (n_out - n_file) * (nbytes / (size_t) n_file);
         L.gtype = t->type; L.n_in = n_in; L.n_out = n_out; L.n_valid = n_file;
         L.fmt = weight_format(t->type, n_in);
         if (L.fmt < 0) {
@@ -330,10 +374,10 @@ struct loader {
             jepa_log("jepa: tensor %s: %" PRId64 " outputs is not a multiple of 4\n", wname.c_str(), n_out);
             return false;
         }
-        if (!to_staging(*t, pad_bytes)) return false;
+        if (!to_staging_n(ts, pad_bytes)) return false;
         if (L.fmt == W_F32 || L.fmt == W_F16) {
-            L.w = dalloc(t->nbytes + pad_bytes);
-            if (!L.w || hipMemcpyAsync(L.w, staging, t->nbytes + pad_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
+            L.w = dalloc(nbytes + pad_bytes);
+            if (!L.w || hipMemcpyAsync(L.w, staging, nbytes + pad_bytes, hipMemcpyDeviceToDevice, s) != hipSuccess) return false;
         } else {
             L.w = dalloc(weight_code_bytes(L.fmt, n_out, n_in));
             if (!L.w) return false;
@@ -348,22 +392,46 @@ struct loader {
             launch_repack(t->type, staging, n_out, n_in, L.w, L.wd, L.wmin, s);
         }
         if (hipStreamSynchronize(s) != hipSuccess) { jepa_log("jepa: weight upload of %s failed\n", wname.c_str()); return false; }
-        return vec(bname, n_file, &L.bias, false, n_out);
+        if (bnames.size() == 1) return vec(bnames[0], n_file, &L.bias, false, n_out);
+        // stacked biases: all present or none
+        int present = 0;
+        for (const auto & b : bnames) present += f.tensor(b) ? 1 : 0;
+        if (present == 0) return true;
+        std::vector<float> all;
+        for (const auto & b : bnames) {
+            const gguf::tensor_info * bt = f.tensor(b);
+            if (!bt || bt->type != T_F32 || bt->ne[0] * bt->ne[1] * bt->ne[2] * bt->ne[3] != n_part) {
+                jepa_log("jepa: bias %s has to be f32 with %" PRId64 " values, like the other parts'\n", b.c_str(), n_part);
+                return false;
+            }
+            if (!read(*bt)) return false;
+            const float * v = (const float *) host.data();
+            all.insert(all.end(), v, v + n_part);
+        }
+        all.resize((size_t) n_out, 0.0f);
+        L.bias = (float *) dalloc(all.size() * 4);
+        return L.bias && hipMemcpy(L.bias, all.data(), all.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
     }
 
     // one pre-LN block "<p>ln1.weight" ... (src/jepa-gguf.cpp:236-252 names) of FFN width F (0: the
     // ffn_up tensor's row count)
     bool block(const std::string & p, int64_t D, int64_t F, dev_layer & Ly, int64_t inner = 0) {
         if (inner <= 0) inner = D;   // attention width n_head * head_dim
+        // the attention input projection: attn_qkv, or attn_q / attn_k / attn_v (the reference uses
+        // attn_qkv when the file has it, src/jepa.cpp:399-414)
+        const bool fused = f.tensor(p + "attn_qkv.weight") != nullptr;
+        const bool split = f.tensor(p + "attn_q.weight") && f.tensor(p + "attn_k.weight") && f.tensor(p + "attn_v.weight");
         if (!f.tensor(p + "ln1.weight") || !f.tensor(p + "ln2.weight") || !f.tensor(p + "attn_out.weight") || !f.tensor(p + "ffn_up.weight") ||
-            !f.tensor(p + "ffn_down.weight") || !f.tensor(p + "attn_qkv.weight")) {
-            jepa_log("jepa: block %s* is incomplete: needs ln1/ln2/attn_out/ffn_up/ffn_down and attn_qkv\n", p.c_str());
+            !f.tensor(p + "ffn_down.weight") || (!fused && !split)) {
+            jepa_log("jepa: block %s* is incomplete: needs ln1/ln2/attn_out/ffn_up/ffn_down and attn_qkv (or attn_q/k/v)\n", p.c_str());
             return false;
         }
         if (F <= 0) F = rows_of(p + "ffn_up.weight");
         return vec(p + "ln1.weight", D, &Ly.ln1_w) && vec(p + "ln1.bias", D, &Ly.ln1_b) && vec(p + "ln2.weight", D, &Ly.ln2_w) &&
                vec(p + "ln2.bias", D, &Ly.ln2_b) && vec(p + "ls1", D, &Ly.ls1) && vec(p + "ls2", D, &Ly.ls2) &&
-               linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * inner, Ly.qkv, true) &&
+               (fused ? linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * inner, Ly.qkv, true)
+                      : linear_n({p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"},
+                                 {p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"}, D, 3 * inner, Ly.qkv, true)) &&
                linear(p + "attn_out.weight", p + "attn_out.bias", inner, D, Ly.out, true) &&
                linear(p + "ffn_up.weight", p + "ffn_up.bias", D, F, Ly.up, true) &&
                linear(p + "ffn_down.weight", p + "ffn_down.bias", F, D, Ly.down, true);
@@ -467,7 +535,6 @@ extern "C" jepa_model * jepa_model_load_ex(const char * path, const jepa_model_p
                 ok = L.vec("enc.reg_tokens", D * e.n_registers, &m->reg_tokens, true);
             }
         }
-        if (ok && !e.qkv_fused) { jepa_log("jepa: separate attn_q/k/v weights are not implemented on this path (qkv_fused = false)\n"); ok = false; }
         m->layers.resize((size_t) e.n_layer);
         for (int i = 0; i < e.n_layer && ok; i++) ok = L.block("enc.blk." + std::to_string(i) + ".", D, e.ffn_dim, m->layers[(size_t) i]);
         if (ok && e.modality_embed && video && !m->mod_video) {

@@ -33,6 +33,7 @@ class EncoderConfig:
     n_frames: int = 1
     cls_token: bool = False
     n_registers: int = 0    # register tokens after the CLS row (enc.reg_tokens)
+    qkv_fused: bool = True  # False: separate attn_q / attn_k / attn_v (the rows of the fused matrix)
     ftype: str = "q8_0"     # f16 | q8_0 | q4_0 | q4_k
     rope_layout: str = ""   # tiled | interleaved ('' for non-rope families)
     rope_interpolate: bool = False
@@ -180,7 +181,7 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
             w.add("jepa.enc.rope_ref_grid", cfg.rope_ref_grid)
     w.add("jepa.enc.cls_token", cfg.cls_token)
     w.add("jepa.enc.n_registers", cfg.n_registers)
-    w.add("jepa.enc.qkv_fused", True)
+    w.add("jepa.enc.qkv_fused", cfg.qkv_fused)
     w.add("jepa.enc.modality_embed", cfg.modality_embed)
     w.add("jepa.enc.image_patch_embed", cfg.image_patch_embed)
     w.add("jepa.enc.layer_scale", cfg.layer_scale)
@@ -257,8 +258,19 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
         w.add_tensor("enc.pos_embed", GGML_F32, (D, n_tok), normal(n_tok, D))
     def block(p, D=D, F=F):
         ln(p + "ln1", D)
-        mat(p + "attn_qkv.weight", 3 * D, D, _block_type(cfg, D))
-        vec(p + "attn_qkv.bias", 3 * D)
+        if cfg.qkv_fused:
+            mat(p + "attn_qkv.weight", 3 * D, D, _block_type(cfg, D))
+            vec(p + "attn_qkv.bias", 3 * D)
+        else:   # the same random draws as the fused matrix, written as its three row blocks
+            gt = _block_type(cfg, D)
+            x = normal(3 * D, D, std=cfg.w_std)
+            for j, nm in enumerate("qkv"):
+                part = np.ascontiguousarray(x[j * D:(j + 1) * D])
+                w.add_tensor(p + f"attn_{nm}.weight", gt, (D, D),
+                             dev_q4k(part) if gt == GGML_Q4_K and dev_q4k is not None else quantize(gt, part))
+            b = normal(3 * D, std=0.02)
+            for j, nm in enumerate("qkv"):
+                w.add_tensor(p + f"attn_{nm}.bias", GGML_F32, (D,), np.ascontiguousarray(b[j * D:(j + 1) * D]))
         mat(p + "attn_out.weight", D, D, _block_type(cfg, D))
         vec(p + "attn_out.bias", D)
         ln(p + "ln2", D)

@@ -1003,11 +1003,17 @@ static int block_fwd(const gg_file * f, const char * pre, float * x, int64_t R, 
     float * o = (float *) malloc(sizeof(float) * R * D);
     float * ff = (float *) malloc(sizeof(float) * R * F);
     or_layer_norm(x, R, D, gg_vec(f, TN(n1, "ln1.weight")), gg_vec(f, TN(n2, "ln1.bias")), eps, h);
-    if (linear(f, TN(n1, "attn_qkv.weight"), TN(n2, "attn_qkv.bias"), h, R, D, 3 * D, qkv, n_threads)) goto out;
-    for (int64_t r = 0; r < R; r++) {
-        memcpy(q + r * D, qkv + r * 3 * D, sizeof(float) * D);
-        memcpy(kk + r * D, qkv + r * 3 * D + D, sizeof(float) * D);
-        memcpy(vv + r * D, qkv + r * 3 * D + 2 * D, sizeof(float) * D);
+    if (gg_tensor_find(f, TN(n1, "attn_qkv.weight"))) {
+        if (linear(f, TN(n1, "attn_qkv.weight"), TN(n2, "attn_qkv.bias"), h, R, D, 3 * D, qkv, n_threads)) goto out;
+        for (int64_t r = 0; r < R; r++) {
+            memcpy(q + r * D, qkv + r * 3 * D, sizeof(float) * D);
+            memcpy(kk + r * D, qkv + r * 3 * D + D, sizeof(float) * D);
+            memcpy(vv + r * D, qkv + r * 3 * D + 2 * D, sizeof(float) * D);
+        }
+    } else {   /* separate q, k, v linears (src/jepa.cpp:408-414) */
+        if (linear(f, TN(n1, "attn_q.weight"), TN(n2, "attn_q.bias"), h, R, D, D, q, n_threads) ||
+            linear(f, TN(n1, "attn_k.weight"), TN(n2, "attn_k.bias"), h, R, D, D, kk, n_threads) ||
+            linear(f, TN(n1, "attn_v.weight"), TN(n2, "attn_v.bias"), h, R, D, D, vv, n_threads)) goto out;
     }
     if (rope_c) {   /* q and k rotated before the 1/sqrt(d) scale (src/jepa.cpp:880-882) */
         or_rope_apply(q, R, H, hd, rope_c, rope_s);

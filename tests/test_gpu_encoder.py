@@ -86,6 +86,21 @@ def test_tiny_register_tokens(jlib, oracle, models_dir, family, ftype, n_reg, n_
     np.testing.assert_allclose(pooled, got[npre:rows].astype(np.float64).mean(0), rtol=0, atol=1e-6 * np.abs(got).max())
 
 
+@pytest.mark.parametrize("family,ftype", [("vjepa2", "q8_0"), ("vjepa2", "q4_k"), ("hfvit", "f16"), ("levjepa", "q4_0")])
+def test_tiny_separate_qkv(jlib, oracle, models_dir, family, ftype):
+    """Blocks with separate attn_q / attn_k / attn_v (jepa.enc.qkv_fused = false; reference
+    src/jepa.cpp:408-414) against the oracle, and bit-identical to the same weights stored fused: the
+    loader stacks the three matrices into the fused projection."""
+    kw = dict(ffn_dim=1024, embed_dim=256, n_head=4) if ftype == "q4_k" else {}
+    fused = forge.tiny(family, ftype, ln_random=True, **kw)
+    split = forge.tiny(family, ftype, ln_random=True, qkv_fused=False, **kw)
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, split, 1, 1 if family == "hfvit" else 4, 64)
+    check_parity(got, want, gtr, wtr, label=f"{family}/{ftype} separate q/k/v")
+    m2 = jlib.Model(forge.cached_model(fused, models_dir))
+    same = jlib.Context(m2).encode(x)
+    np.testing.assert_array_equal(got.view(np.uint32), same.view(np.uint32))
+
+
 def test_batch_equals_single(jlib, models_dir):
     """Items of one call equal separate calls bit for bit (reference tests/test-batch.cpp:12-21)."""
     for family, nb, nf in (("hfvit", 3, 1), ("vjepa2", 2, 4)):

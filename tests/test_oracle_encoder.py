@@ -54,7 +54,10 @@ def _block64(T, has, p, h, D, H, rope, mask, kv_f16):
     """One pre-LN block (reference src/jepa.cpp:444-471) in float64."""
     n, hd = h.shape[0], D // H
     a = _ln(h, T(p + "ln1.weight"), T(p + "ln1.bias"), 1e-6)
-    qkv = a @ T(p + "attn_qkv.weight").T + T(p + "attn_qkv.bias")
+    if has(p + "attn_qkv.weight"):
+        qkv = a @ T(p + "attn_qkv.weight").T + T(p + "attn_qkv.bias")
+    else:   # separate q, k, v linears (reference src/jepa.cpp:408-414)
+        qkv = np.concatenate([a @ T(p + f"attn_{j}.weight").T + T(p + f"attn_{j}.bias") for j in "qkv"], axis=1)
     q, k, v = (qkv[:, j * D:(j + 1) * D].reshape(n, H, hd) for j in range(3))
     if rope is not None:
         q, k = _rot(q, rope[0][:, None], rope[1][:, None]), _rot(k, rope[0][:, None], rope[1][:, None])
@@ -201,7 +204,8 @@ def forward64(path, x):
 
 @pytest.mark.parametrize("family,kw", [("hfvit", {}), ("hfvit", {"layer_scale": True}), ("vjepa2", {}),
                                        ("vjepa2_1", {}), ("levjepa", {}), ("hfvit", {"n_registers": 4}),
-                                       ("vjepa2", {"n_registers": 2}), ("levjepa", {"n_registers": 3})])
+                                       ("vjepa2", {"n_registers": 2}), ("levjepa", {"n_registers": 3}),
+                                       ("hfvit", {"qkv_fused": False}), ("vjepa2", {"qkv_fused": False})])
 def test_oracle_encoder_matches_float64_forward(family, kw, tmp_path):
     cfg = forge.tiny(family, "f32", ln_random=True, **kw)
     path = forge.cached_model(cfg, str(tmp_path))
