@@ -223,6 +223,15 @@ static float make_qkx2_quants(int n, int nmax, const float * x, const float * we
     return scale;
 }
 
+/* One make_qkx2_quants fit of n <= 256 values, exported so the tests can check the fit itself (the
+ * q4_K block only keeps its 6-bit requantization). Returns -1 for n out of range. */
+float or_make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L, float * the_min,
+                          float rmin, float rdelta, int nstep) {
+    uint8_t Laux[256];
+    if (n <= 0 || n > 256) return -1.0f;
+    return make_qkx2_quants(n, nmax, x, weights, L, the_min, Laux, rmin, rdelta, nstep);
+}
+
 /* ggml quantize_row_q4_K_ref (same source as above): per 32-value sub-block, weights
  * av_x + |x| with av_x = sqrt(mean x^2), make_qkx2_quants(32, 15, rmin -1, rdelta 0.1, 20 steps);
  * the 8 scales and mins quantized to 6 bits against their maxima (d = max_scale/63, dmin =

@@ -43,6 +43,8 @@ size_t or_row_size(int type, int64_t n);
 void or_quantize_q8_0_ref(const float * x, void * blocks, int64_t n);
 void or_quantize_q4_0_ref(const float * x, void * blocks, int64_t n);
 void or_quantize_q4_K(const float * x, void * blocks, int64_t n);
+float or_make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L, float * the_min,
+                          float rmin, float rdelta, int nstep);
 /* activation quantizers as the x86 CPU backend runs them inside mul_mat */
 void or_quantize_q8_0_act(const float * x, void * blocks, int64_t n);
 void or_quantize_q8_K_act(const float * x, void * blocks, int64_t n);

@@ -68,6 +68,8 @@ def lib() -> C.CDLL:
         for fn in ("or_fp32_to_fp16_row", "or_fp16_to_fp32_row"):
             getattr(L, fn).argtypes = [vp, vp, i64]
             getattr(L, fn).restype = None
+        L.or_make_qkx2_quants.argtypes = [C.c_int, C.c_int, vp, vp, vp, vp, C.c_float, C.c_float, C.c_int]
+        L.or_make_qkx2_quants.restype = C.c_float
         L.or_set_reverse_block_order.argtypes = [C.c_int]
         L.or_set_reverse_block_order.restype = None
         L.or_set_k_split.argtypes = [C.c_int]
@@ -115,6 +117,18 @@ def quantize(fn: str, x: np.ndarray, block_type: int) -> np.ndarray:
 def quantize_weight(t: int, x: np.ndarray) -> np.ndarray:
     fn = {OR_Q8_0: "or_quantize_q8_0_ref", OR_Q4_0: "or_quantize_q4_0_ref", OR_Q4_K: "or_quantize_q4_K"}[t]
     return quantize(fn, x, t)
+
+
+def make_qkx2_quants(x: np.ndarray, w: np.ndarray, nmax: int = 15, rmin: float = -1.0, rdelta: float = 0.1,
+                     nstep: int = 20):
+    """One asymmetric fit of the values x with weights w: (scale, min, levels) with x ~ scale * L + min."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    L = np.zeros(x.size, np.uint8)
+    the_min = C.c_float(0)
+    s = lib().or_make_qkx2_quants(x.size, nmax, x.ctypes.data, w.ctypes.data, L.ctypes.data, C.addressof(the_min),
+                                  rmin, rdelta, nstep)
+    return float(s), -the_min.value, L
 
 
 def quantize_act(t: int, x: np.ndarray) -> np.ndarray:

@@ -107,6 +107,144 @@ def test_q4_K_dequantize_matches_numpy_and_bounds():
     assert np.all(np.abs(y.reshape(-1, 32) - xs).max(1) <= step * 0.75 + 2e-3)
 
 
+def _q4k_subblocks(rng, count):
+    """Sub-blocks of 32 values of the shapes the fit treats differently: centred, all positive (the
+    min clamps to 0), uniform, heavy-tailed, and one outlier over a tiny spread."""
+    out = []
+    for i in range(count):
+        k = i % 5
+        if k == 0:
+            x = rng.standard_normal(32)
+        elif k == 1:
+            x = rng.standard_normal(32) + 3.0
+        elif k == 2:
+            x = rng.uniform(-1, 1, 32)
+        elif k == 3:
+            x = rng.standard_t(2, 32)
+        else:
+            x = rng.standard_normal(32) * 0.01
+            x[rng.integers(32)] = 0.5
+        out.append(x.astype(np.float32))
+    return out
+
+
+def _q4k_weights(x):
+    # the weights quantize_row_q4_K_ref gives a sub-block: sqrt(mean x^2) + |x|
+    return (np.float32(np.sqrt(np.float32((x * x).sum()) / np.float32(32))) + np.abs(x)).astype(np.float32)
+
+
+def _wls(L, x, w):
+    """Weighted least-squares scale and min of x ~ s * L + m by numpy's lstsq, the min clamped to <= 0
+    (then the scale alone is refitted)."""
+    sw = np.sqrt(w)
+    (s, m), *_ = np.linalg.lstsq(np.stack([L, np.ones_like(L)], 1) * sw[:, None], x * sw, rcond=None)
+    if m > 0:
+        m, s = 0.0, float((w * L * x).sum() / (w * L * L).sum())
+    return float(s), float(m)
+
+
+def test_q4_K_subblock_fit_replays_the_candidate_search():
+    """make_qkx2_quants (ggml-quants.c of ggml 36da5713, which the reference pins and does not ship) is
+    pinned without retyping its sums: a float64 replay of its search, each candidate's scale and min
+    solved by numpy's weighted lstsq, must pick the same levels. Candidate i has levels
+    clamp(rint(iscale (x - min)), 0, 15) with iscale = (-1 + 0.1 i + 15) / (max - min) over the current
+    min, which an accepted candidate replaces (a search over a fixed min picks other levels on many
+    sub-blocks). Every result is also a weighted least-squares fit of its own levels, or the min/max
+    start, and never worse than that start."""
+    rng = np.random.default_rng(7)
+    n = same = 0
+    for x in _q4k_subblocks(rng, 1500):
+        w = _q4k_weights(x)
+        s, m, L = O.make_qkx2_quants(x, w)
+        x64, w64, L64 = x.astype(np.float64), w.astype(np.float64), L.astype(np.float64)
+        err = lambda s_, m_, L_: float((w64 * (s_ * L_ + m_ - x64) ** 2).sum())
+        mn, mx = np.float32(min(float(x.min()), 0.0)), np.float32(x.max())
+        isc = np.float32(15) / (mx - mn)
+        L0 = np.clip(np.rint(isc * (x - mn)), 0, 15).astype(np.float64)
+        s0, m0 = float(np.float32(1) / isc), float(mn)
+        rs, rm, rL, best = s0, m0, L0, err(s0, m0, L0)
+        for i in range(21):
+            isc = (np.float32(-1) + np.float32(0.1) * np.float32(i) + np.float32(15)) / (mx - np.float32(rm))
+            Li = np.clip(np.rint(isc * (x - np.float32(rm))), 0, 15).astype(np.float64)
+            if Li.min() == Li.max():
+                continue
+            cs, cm = _wls(Li, x64, w64)
+            e = err(cs, cm, Li)
+            if e < best:
+                rs, rm, rL, best = cs, cm, Li, e
+        n += 1
+        e = err(s, m, L64)
+        assert e <= err(s0, m0, L0) * (1 + 1e-6)
+        if np.array_equal(L64, L0) and abs(s - s0) <= 1e-6 * s0:
+            pass                                           # kept the min/max start
+        else:
+            fs, fm = _wls(L64, x64, w64)
+            assert abs(s - fs) <= 2e-4 * abs(fs) and abs(m - fm) <= 2e-4 * abs(fs), (s, m, fs, fm)
+        if np.array_equal(L64, rL):
+            same += 1
+            assert abs(s - rs) <= 2e-4 * abs(rs) and abs(m - rm) <= 2e-4 * abs(rs)
+        else:
+            # a near-tie decided the other way in float32 sums: then no worse than the replay's pick
+            assert e <= best * (1 + 1e-4), (e, best)
+    assert same >= 0.99 * n, (same, n)
+
+
+def test_q4_K_block_scales_and_final_levels():
+    """quantize_row_q4_K_ref after the fits: d = f16(max scale / 63), dmin = f16(max min / 63), six-bit
+    sub-block scales and mins rint(63 * s_j / max), and every value re-fitted to the nearest level of
+    its quantized sub-block scale and min, clamped to [0, 15]."""
+    rng = np.random.default_rng(11)
+    subs = _q4k_subblocks(rng, 8 * 40)
+    x = np.concatenate(subs).reshape(40, 256)
+    raw = O.quantize_weight(O.OR_Q4_K, x).reshape(-1, 144)
+    d = raw[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dmin = raw[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    sc, mq = gguf.q4k_scales_mins(raw[:, 4:16])
+    y = O.dequantize(O.OR_Q4_K, raw, 256).reshape(40, 8, 32)
+    for b in range(40):
+        fits = [O.make_qkx2_quants(v, _q4k_weights(v)) for v in x[b].reshape(8, 32)]
+        scales = np.array([f[0] for f in fits], np.float32)
+        mins = np.array([-f[1] for f in fits], np.float32)
+        ms, mm = scales.max(), mins.max()
+        assert d[b] == np.float16(ms / np.float32(63)).astype(np.float32)
+        assert dmin[b] == np.float16(mm / np.float32(63)).astype(np.float32)
+        np.testing.assert_array_equal(sc[b], np.minimum(np.rint(np.float32(63) / ms * scales), 63))
+        np.testing.assert_array_equal(mq[b], np.minimum(np.rint(np.float32(63) / mm * mins), 63))
+        for j in range(8):
+            dj, mj = np.float32(d[b] * sc[b, j]), np.float32(dmin[b] * mq[b, j])
+            if dj == 0:
+                continue
+            xs = x[b, 32 * j:32 * j + 32].astype(np.float64)
+            levels = dj * np.arange(16, dtype=np.float64) - mj
+            nearest = levels[np.abs(xs[:, None] - levels[None, :]).argmin(1)]
+            np.testing.assert_allclose(y[b, j], nearest, rtol=0, atol=1e-5 * float(dj))
+
+
+def test_q4_K_recovers_values_on_its_own_grid():
+    """Values that lie exactly on a q4_K grid (f16 d and dmin, six-bit scales and mins with 63 among
+    them, every sub-block using levels 0 and 15) come back exactly: the fit, the requantization of the
+    scales and the final levels all reproduce the grid."""
+    rng = np.random.default_rng(12)
+    for _ in range(20):
+        d = np.float32(np.float16(rng.uniform(1e-3, 2e-2)))
+        dmin = np.float32(np.float16(rng.uniform(1e-3, 2e-2)))
+        sc = rng.integers(1, 64, 8)
+        sc[rng.integers(8)] = 63
+        m = rng.integers(0, 64, 8)
+        m[rng.integers(8)] = 63
+        q = rng.integers(0, 16, (8, 32))
+        q[:, 0], q[:, 1] = 0, 15
+        a = (d * sc.astype(np.float32)).astype(np.float32)
+        b = (dmin * m.astype(np.float32)).astype(np.float32)
+        x = ((a[:, None] * q.astype(np.float32)).astype(np.float32) - b[:, None]).reshape(1, 256)
+        raw = O.quantize_weight(O.OR_Q4_K, x)
+        y = O.dequantize(O.OR_Q4_K, raw, 256)
+        np.testing.assert_allclose(y, x, rtol=0, atol=1e-6 * float(np.abs(x).max()))
+        got_sc, got_m = gguf.q4k_scales_mins(raw.reshape(-1, 144)[:, 4:16])
+        np.testing.assert_array_equal(got_sc[0], sc)
+        np.testing.assert_array_equal(got_m[0], m)
+
+
 # ------------------------------------------------------------------------------ activation quantizers
 def test_q8_0_activation_rounds_half_to_even():
     """The x86 CPU path rounds x*127/amax half-to-even (quantize_row_q8_0, AVX2); roundf (half away
