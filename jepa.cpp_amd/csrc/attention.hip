@@ -151,13 +151,16 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
 
     const f16v zero = {0};
     f16v acc[QT][NDT];
-    float m_run[QT], l_run[QT];
+    // running maximum in the exp2 domain: mcs = max(s) * c (-inf before the first visible key) and
+    // nm = -mcs (0 before the first key), the addend of every score's fma; a block moves it when its
+    // largest exponent exceeds thr (-inf before the first visible key, LAZY after)
+    float mcs[QT], nm[QT], thr[QT], l_run[QT];
     int2 kr[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; qt++) {
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) acc[qt][dt] = zero;
-        m_run[qt] = -INFINITY; l_run[qt] = 0.0f;
+        mcs[qt] = -INFINITY; nm[qt] = 0.0f; thr[qt] = -INFINITY; l_run[qt] = 0.0f;
         kr[qt] = key_range((int) q0 + 32 * qt + l32, (int) R, np, tpf);   // this lane's key range per tile
     }
     // the wave's bounds on its queries' ranges: a 32-key block below lo_max or reaching past hi_min
@@ -177,7 +180,10 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
         for (int kk = 0; kk < NKK; kk++) S = MFMA16(kc[kk], qv[qt][kk], S);
         return S;
     };
-    // M: keys past R or outside a lane's range (block-causal) to -inf, then the lazy maximum
+    // M: keys past R or outside a lane's range (block-causal) to -inf, the exponents t = s c - mcs
+    // (in place of the scores), then the lazy maximum. The maximum is taken over the fma results, which
+    // the compiler knows to be canonical floats: over the raw MFMA results it would first canonicalize
+    // every value (an extra v_max_f32 each, for IEEE NaN semantics).
     auto mx = [&](int qt, f16v & S, int kb0) {
         if (MASKED && (kb0 < lo_max || kb0 + 32 > hi_min)) {
             const int key0 = kb0 + 4 * g;
@@ -187,30 +193,39 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
                 if (key < kr[qt].x || key >= kr[qt].y) S[r] = -INFINITY;
             }
         }
-        float mloc = fmaxf(fmaxf(fmaxf(S[0], S[1]), fmaxf(S[2], S[3])), fmaxf(fmaxf(S[4], S[5]), fmaxf(S[6], S[7])));
-        mloc = fmaxf(mloc, fmaxf(fmaxf(fmaxf(S[8], S[9]), fmaxf(S[10], S[11])), fmaxf(fmaxf(S[12], S[13]), fmaxf(S[14], S[15]))));
-        mloc = halves_max(mloc);
-        const bool move = mloc > m_run[qt] && (m_run[qt] == -INFINITY || (mloc - m_run[qt]) * c > LAZY);
+#pragma unroll
+        for (int r = 0; r < 16; r++) S[r] = fmaf(S[r], c, nm[qt]);
+        float tl = fmaxf(fmaxf(fmaxf(S[0], S[1]), fmaxf(S[2], S[3])), fmaxf(fmaxf(S[4], S[5]), fmaxf(S[6], S[7])));
+        tl = fmaxf(tl, fmaxf(fmaxf(fmaxf(S[8], S[9]), fmaxf(S[10], S[11])), fmaxf(fmaxf(S[12], S[13]), fmaxf(S[14], S[15]))));
+        tl = halves_max_nonan(tl);
+        // the first visible key sets the maximum; later, it moves when a block's exceeds it by 2^LAZY
+        const bool move = tl > thr[qt];
         if (__builtin_amdgcn_ballot_w64(move) != 0) {   // rare after the first blocks: a uniform branch
-            // move the reference maximum; rescale what was accumulated against the old one (the empty
-            // volatile asm keeps the compiler from executing this block speculatively on every block)
+            // move the reference maximum by tl; rescale what was accumulated against the old one and
+            // shift this block's exponents (the empty volatile asm keeps the compiler from executing
+            // this block speculatively on every block)
             asm volatile("");
-            const float alpha = move ? fast_exp2((m_run[qt] - mloc) * c) : 1.0f;
+            const bool first = mcs[qt] == -INFINITY;
+            const float sh = move ? tl : 0.0f;
+            const float alpha = first ? 0.0f : fast_exp2(-sh);   // nothing accumulated yet: 0, not 2^-sh
             l_run[qt] *= alpha;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[qt][dt][r] *= alpha;
-            m_run[qt] = move ? mloc : m_run[qt];
+#pragma unroll
+            for (int r = 0; r < 16; r++) S[r] = __fsub_rn(S[r], sh);
+            mcs[qt] = move ? (first ? tl : mcs[qt] + tl) : mcs[qt];
+            nm[qt] = mcs[qt] == -INFINITY ? 0.0f : -mcs[qt];
+            thr[qt] = mcs[qt] == -INFINITY ? -INFINITY : LAZY;
         }
     };
-    // E: weights 2^(s c - m c) as the f16 B operand of the P.V MFMA, their f32 sum into l
+    // E: weights 2^t as the f16 B operand of the P.V MFMA, their f32 sum into l
     auto ex = [&](int qt, const f16v & S, h8 (&pb)[2]) {
-        const float mc = m_run[qt] == -INFINITY ? 0.0f : m_run[qt] * c;   // no key seen yet: S is -inf too
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            p[r] = fast_exp2(fmaf(S[r], c, -mc));
+            p[r] = fast_exp2(S[r]);
             pb[r >> 3][r & 7] = (_Float16) p[r];
         }
         const float s0 = (p[0] + p[1]) + (p[2] + p[3]), s1 = (p[4] + p[5]) + (p[6] + p[7]);
@@ -292,7 +307,7 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
 #pragma unroll
         for (int qt = 0; qt < QT; qt++) {
             float * x = xs + (size_t) qt * (NV / QT) * 64;
-            x[0] = m_run[qt]; x[64] = l_run[qt];
+            x[0] = mcs[qt]; x[64] = l_run[qt];
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
@@ -304,15 +319,15 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
 #pragma unroll
     for (int qt = 0; qt < QT; qt++) {
         float mi[KS], ai[KS];
-        mi[0] = m_run[qt];
-        float m = m_run[qt];
+        mi[0] = mcs[qt];
+        float m = mcs[qt];
 #pragma unroll
         for (int k = 1; k < KS; k++) {
             mi[k] = ((const float *) smem)[(size_t) ((k - 1) * QG + qg) * NV * 64 + (size_t) qt * (NV / QT) * 64 + lane];
             m = fmaxf(m, mi[k]);
         }
 #pragma unroll
-        for (int k = 0; k < KS; k++) ai[k] = mi[k] == -INFINITY ? 0.0f : fast_exp2((mi[k] - m) * c);
+        for (int k = 0; k < KS; k++) ai[k] = mi[k] == -INFINITY ? 0.0f : fast_exp2(mi[k] - m);
         float l = l_run[qt] * ai[0];
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
