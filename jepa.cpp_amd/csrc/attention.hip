@@ -21,14 +21,18 @@
 // The B operand of the PV MFMA takes the 8 keys (4g..4g+3, 8+4g..8+4g+3 of each 16) that the S
 // accumulator layout leaves in lane group g; V^T is stored with the same key order inside every
 // 16-token group (written that way by the QKV epilogue), so both operands agree without shuffles.
-// The running maximum is only moved when a tile's maximum exceeds it by more than 2^8 (in the
-// exp2 domain), so the accumulators are rescaled a few times per sweep instead of every tile.
+// Scores become exponents t = s c - M in one fma (c = scale log2 e, M the running maximum already
+// scaled by c), the weights are 2^t; M is only moved when a block's largest t exceeds 8 (weights up to
+// 2^8), so the accumulators are rescaled a few times per sweep instead of every block. The row sums
+// add the f16 weights that the P.V MFMA uses (v_dot2_f32_f16 against (1, 1)).
 #include "kernels.h"
 #include "model.h"
 #include "lds_dma.h"
 #include "lanes.h"
+#include "quant_dev.h"
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
@@ -195,9 +199,11 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
         }
 #pragma unroll
         for (int r = 0; r < 16; r++) S[r] = fmaf(S[r], c, nm[qt]);
-        float tl = fmaxf(fmaxf(fmaxf(S[0], S[1]), fmaxf(S[2], S[3])), fmaxf(fmaxf(S[4], S[5]), fmaxf(S[6], S[7])));
-        tl = fmaxf(tl, fmaxf(fmaxf(fmaxf(S[8], S[9]), fmaxf(S[10], S[11])), fmaxf(fmaxf(S[12], S[13]), fmaxf(S[14], S[15]))));
-        tl = halves_max_nonan(tl);
+        // a chain of three-input maxima (v_max3_f32): 8 ops for 16 values
+        float tl = fmaxf(fmaxf(S[0], S[1]), S[2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) tl = fmaxf(fmaxf(tl, S[r]), S[r + 1]);
+        tl = halves_max_nonan(fmaxf(tl, S[15]));
         // the first visible key sets the maximum; later, it moves when a block's exceeds it by 2^LAZY
         const bool move = tl > thr[qt];
         if (__builtin_amdgcn_ballot_w64(move) != 0) {   // rare after the first blocks: a uniform branch
@@ -220,17 +226,20 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
             thr[qt] = mcs[qt] == -INFINITY ? -INFINITY : LAZY;
         }
     };
-    // E: weights 2^t as the f16 B operand of the P.V MFMA, their f32 sum into l
+    // E: weights 2^t as the f16 B operand of the P.V MFMA, and the f32 sum of those f16 weights into
+    // l (v_dot2_f32_f16 against (1, 1): eight ops instead of fifteen adds, and the normalizer is the
+    // sum of the weights the P.V products actually used)
+    const h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
     auto ex = [&](int qt, const f16v & S, h8 (&pb)[2]) {
-        float p[16];
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            p[r] = fast_exp2(S[r]);
-            pb[r >> 3][r & 7] = (_Float16) p[r];
+        for (int r = 0; r < 16; r++) pb[r >> 3][r & 7] = (_Float16) fast_exp2(S[r]);
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            s0 = __builtin_amdgcn_fdot2(h2{pb[0][2 * k], pb[0][2 * k + 1]}, one2, s0, false);
+            s1 = __builtin_amdgcn_fdot2(h2{pb[1][2 * k], pb[1][2 * k + 1]}, one2, s1, false);
         }
-        const float s0 = (p[0] + p[1]) + (p[2] + p[3]), s1 = (p[4] + p[5]) + (p[6] + p[7]);
-        const float s2 = (p[8] + p[9]) + (p[10] + p[11]), s3 = (p[12] + p[13]) + (p[14] + p[15]);
-        l_run[qt] += halves_sum((s0 + s1) + (s2 + s3));
+        l_run[qt] += halves_sum(s0 + s1);
     };
     auto pv = [&](int qt, const h8 (&pb)[2], const h8 (&vc)[2][NDT]) {
 #pragma unroll
@@ -375,8 +384,7 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
                         uint32_t w = 0;
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
-                            const int cq = (int) fminf(fmaxf(rintf(o[dt][4 * qq + e] * id), -128.0f), 127.0f);
-                            w |= ((uint32_t) cq & 0xffu) << (8 * e);
+                            w |= q8_byte(o[dt][4 * qq + e], id) << (8 * e);
                         }
                         *(uint32_t *) (crow + 32 * dt + 8 * qq + 4 * g) = w;
                     }
@@ -434,11 +442,13 @@ __global__ __launch_bounds__(256) void k_attn_any(const _Float16 * __restrict__ 
     f16v acc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; dt++) acc[dt] = zero;
-    float m_run = -INFINITY, l_run = 0.0f;
+    // the running maximum in the exp2 domain, as in k_attn_hd64: mcs, its negation nm, threshold thr
+    float mcs = -INFINITY, nm = 0.0f, thr = -INFINITY, l_run = 0.0f;
     const int2 kr = key_range((int) q0 + l32, (int) R, np, tpf);
     const int qw = (int) q0;
     const int lo_min = key_range(qw, (int) R, np, tpf).x;
     const int hi_max = qw < np ? (int) R : key_range(min(qw + 31, (int) R - 1), (int) R, np, tpf).y;
+    const h2 one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
     for (int kb0 = (lo_min / 32) * 32; kb0 < hi_max; kb0 += 32) {
         f16v S = zero;
 #pragma unroll
@@ -449,35 +459,40 @@ __global__ __launch_bounds__(256) void k_attn_any(const _Float16 * __restrict__ 
             const int key = key0 + 8 * (r >> 2) + (r & 3);
             if (key < kr.x || key >= kr.y) S[r] = -INFINITY;
         }
-        float mloc = S[0];
 #pragma unroll
-        for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, S[r]);
-        mloc = halves_max(mloc);
-        if (mloc > m_run && (m_run == -INFINITY || (mloc - m_run) * c > LAZY)) {
-            const float alpha = fast_exp2((m_run - mloc) * c);
+        for (int r = 0; r < 16; r++) S[r] = fmaf(S[r], c, nm);
+        float tl = fmaxf(fmaxf(S[0], S[1]), S[2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) tl = fmaxf(fmaxf(tl, S[r]), S[r + 1]);
+        tl = halves_max_nonan(fmaxf(tl, S[15]));
+        if (tl > thr) {
+            const bool first = mcs == -INFINITY;
+            const float alpha = first ? 0.0f : fast_exp2(-tl);
             l_run *= alpha;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[dt][r] *= alpha;
-            m_run = mloc;
-        }
-        const float mc = m_run == -INFINITY ? 0.0f : m_run * c;
-        float p[16], lsum = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; r++) { p[r] = fast_exp2(fmaf(S[r], c, -mc)); lsum += p[r]; }
-        lsum = halves_sum(lsum);
-        l_run += lsum;
+            for (int r = 0; r < 16; r++) S[r] = __fsub_rn(S[r], tl);
+            mcs = first ? tl : mcs + tl;
+            nm = -mcs;
+            thr = LAZY;
+        }
+        float lsum = 0.0f;
 #pragma unroll
         for (int kk2 = 0; kk2 < 2; kk2++) {
             h8 pb;
 #pragma unroll
-            for (int e = 0; e < 8; e++) pb[e] = (_Float16) p[8 * kk2 + e];
+            for (int e = 0; e < 8; e++) pb[e] = (_Float16) fast_exp2(S[8 * kk2 + e]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) lsum = __builtin_amdgcn_fdot2(h2{pb[2 * e], pb[2 * e + 1]}, one2, lsum, false);
             // V^T row d, keys kb0 + 16 kk2 + 8 g .. + 8 in the order of the S lanes (see the header)
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
                 acc[dt] = MFMA16(*(const h8 *) (Vh + (int64_t) (32 * dt + l32) * R_pad + kb0 + 16 * kk2 + 8 * g), pb, acc[dt]);
         }
+        l_run += halves_sum(lsum);
     }
     const int64_t q = q0 + l32;
     if (q >= R) return;

@@ -27,6 +27,7 @@
 #include "model.h"
 #include "lds_dma.h"
 #include "lanes.h"
+#include "quant_dev.h"
 
 #include <hip/hip_fp16.h>
 
@@ -67,39 +68,27 @@ struct kargs {
 __device__ __forceinline__ float h2f(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2hbits(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
 
-// erf(z) for z >= 0 without a divergent branch: both pieces are evaluated and one is selected.
-//   z <  0.875: z * P(z^2), P of degree 5
-//   z >= 0.875: 1 - 2^Q(min(z, 4)), Q of degree 6 ~ log2(erfc(z)); erfc(4) = 1.5e-8 gives exactly 1.0f
-// Coefficients from fit_gelu_erf.py (least squares toward equal ripple); the float32 evaluation stays
-// within 1.5 * 2^-24 of erf, about the accuracy of a library erff, at some 24 VALU ops per value
-// instead of the ~35 (plus branch masks) of erff's two-branch form.
-__device__ __forceinline__ float erf_nonneg(float z) {
-    const float s = __fmul_rn(z, z);
-    float p = -6.065624184e-04f;
-    p = fmaf(p, s, 5.004569888e-03f);
-    p = fmaf(p, s, -2.677160688e-02f);
-    p = fmaf(p, s, 1.128184572e-01f);
-    p = fmaf(p, s, -3.761247694e-01f);
-    p = fmaf(p, s, 1.128379107e+00f);
-    const float small = __fmul_rn(z, p);
-    const float zc = fminf(z, 4.0f);
-    float q = 3.032335662e-04f;
-    q = fmaf(q, zc, -4.579299595e-03f);
-    q = fmaf(q, zc, 3.277245909e-02f);
-    q = fmaf(q, zc, -1.513156891e-01f);
-    q = fmaf(q, zc, -9.177885652e-01f);
-    q = fmaf(q, zc, -1.627714038e+00f);
-    q = fmaf(q, zc, -9.482709720e-05f);
-    const float large = __fsub_rn(1.0f, __builtin_amdgcn_exp2f(q));
-    return z < 0.875f ? small : large;
-}
-
+// GELU(x) = 0.5 x (1 + erf(x / sqrt 2)) = x Phi(x) (ggml_vec_gelu_erf_f32, reference
+// docs/ggml-notes.md:291-292), Phi the standard normal CDF, from its tail h(t) = Phi(-t), t = |x|:
+//   Phi(x) = 1 - h(t) for x >= 0, h(t) for x < 0,   h(t) = 2^Q(min(t, 5.5)), Q of degree 8 with Q(0) = -1
+// One polynomial and one hardware exp2 per value, no branch: 14 VALU ops where erf's two-piece form
+// (both pieces evaluated, one selected) took 25. Coefficients from fit_gelu.py (fitted with weight h,
+// so the absolute error of Phi is minimised; Q(0) = -1 gives Phi(0) = 1/2 exactly): the float32
+// evaluation stays within 1.5 units of 2^-24 of Phi (2.5 with exp2 two units off), about the accuracy
+// of the libm erff form. At t = 5.5, h = 1.9e-8 < 2^-25, so 1 - h is 1.0f and GELU(x) = x beyond.
 __device__ __forceinline__ float gelu_erf(float x) {
-    // 0.5*x*(1 + erf(x/sqrt(2))) - ggml_vec_gelu_erf_f32 (reference docs/ggml-notes.md:291-292);
-    // erf is odd and |x| * c rounds like x * c, so erf(x c) = sign(x) erf_nonneg(|x| c)
-    const float SQRT_2_INV = 0.70710678118654752440084436210484f;
-    const float e = copysignf(erf_nonneg(__fmul_rn(fabsf(x), SQRT_2_INV)), x);
-    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
+    const float t = fminf(fabsf(x), 5.5f);
+    float q = -2.248140163e-06f;
+    q = fmaf(q, t, 3.268636283e-05f);
+    q = fmaf(q, t, -1.560558158e-04f);
+    q = fmaf(q, t, -2.054840443e-04f);
+    q = fmaf(q, t, 7.147170603e-03f);
+    q = fmaf(q, t, -5.254988000e-02f);
+    q = fmaf(q, t, -4.591920078e-01f);
+    q = fmaf(q, t, -1.151106834e+00f);
+    q = fmaf(q, t, -1.0f);
+    const float h = __builtin_amdgcn_exp2f(q);
+    return __fmul_rn(x, x >= 0.0f ? __fsub_rn(1.0f, h) : h);
 }
 
 // The residual epilogue with the row's current values x already loaded: x + (t + bias) * ls
@@ -1152,8 +1141,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                         uint32_t o = 0;
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
-                            const int qi = (int) fminf(fmaxf(rintf(v[4 * q + e] * id), -128.0f), 127.0f);
-                            o |= ((uint32_t) qi & 0xffu) << (8 * e);
+                            o |= q8_byte(v[4 * q + e], id) << (8 * e);
                         }
                         *(uint32_t *) ((int8_t *) a.ep.oq + m * a.N + n) = o;   // int8 codes
                     }

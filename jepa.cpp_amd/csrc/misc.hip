@@ -2,6 +2,7 @@
 // load-time weight repacking, and small test hooks.
 #include "kernels.h"
 #include "model.h"
+#include "quant_dev.h"
 
 #include <hip/hip_fp16.h>
 
@@ -180,8 +181,7 @@ __global__ __launch_bounds__(256) void k_rownorm(const float * __restrict__ x, i
                 uint32_t qb[2] = {0u, 0u};
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    const int qi = (int) fminf(fmaxf(rintf(v[i][e] * id), -128.0f), 127.0f);
-                    qb[e >> 2] |= ((uint32_t) qi & 0xffu) << (8 * (e & 3));
+                    qb[e >> 2] |= q8_byte(v[i][e], id) << (8 * (e & 3));
                 }
                 *(uint2 *) ((int8_t *) out.q + row * D + 8 * o) = make_uint2(qb[0], qb[1]);
                 if ((o & 3) == 0) ((uint16_t *) out.d)[row * (D / 32) + o / 4] = f2hbits(d);

@@ -668,36 +668,28 @@ void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, 
 
 static int g_round;   /* rounding switches, see or_set_rounding below */
 
-/* the GPU epilogue's erf for z >= 0 (OR_ROUND_GELU): z*P(z^2) below 0.875, 1 - 2^Q(min(z, 4)) above,
- * both evaluated and one selected, with the same coefficients and float operations */
-static float gpu_erf_nonneg(float z) {
-    const float s = z * z;
-    float p = -6.065624184e-04f;
-    p = fmaf(p, s, 5.004569888e-03f);
-    p = fmaf(p, s, -2.677160688e-02f);
-    p = fmaf(p, s, 1.128184572e-01f);
-    p = fmaf(p, s, -3.761247694e-01f);
-    p = fmaf(p, s, 1.128379107e+00f);
-    const float small = z * p;
-    const float zc = fminf(z, 4.0f);
-    float q = 3.032335662e-04f;
-    q = fmaf(q, zc, -4.579299595e-03f);
-    q = fmaf(q, zc, 3.277245909e-02f);
-    q = fmaf(q, zc, -1.513156891e-01f);
-    q = fmaf(q, zc, -9.177885652e-01f);
-    q = fmaf(q, zc, -1.627714038e+00f);
-    q = fmaf(q, zc, -9.482709720e-05f);
-    const float large = 1.0f - exp2f(q);
-    return z < 0.875f ? small : large;
+/* the GPU epilogue's GELU (OR_ROUND_GELU): x Phi(x) with the normal tail h(t) = Phi(-t), t = |x|, as
+ * 2^Q(min(t, 5.5)), Q of degree 8 in Horner fmas, Phi = 1 - h for x >= 0 and h below, with the same
+ * coefficients and float operations (exp2f in place of the hardware exp2) */
+static float gpu_gelu(float x) {
+    const float t = fminf(fabsf(x), 5.5f);
+    float q = -2.248140163e-06f;
+    q = fmaf(q, t, 3.268636283e-05f);
+    q = fmaf(q, t, -1.560558158e-04f);
+    q = fmaf(q, t, -2.054840443e-04f);
+    q = fmaf(q, t, 7.147170603e-03f);
+    q = fmaf(q, t, -5.254988000e-02f);
+    q = fmaf(q, t, -4.591920078e-01f);
+    q = fmaf(q, t, -1.151106834e+00f);
+    q = fmaf(q, t, -1.0f);
+    const float h = exp2f(q);
+    return x * (x >= 0.0f ? 1.0f - h : h);
 }
 
 /* ggml_vec_gelu_erf_f32 (docs/ggml-notes.md:291-292): 0.5*x*(1+erf(x/sqrt(2))) with libm erff */
 float or_gelu_erf(float x) {
     const float SQRT_2_INV = 0.70710678118654752440084436210484f;
-    if (g_round & 8) {
-        const float e = copysignf(gpu_erf_nonneg(fabsf(x) * SQRT_2_INV), x);
-        return (0.5f * x) * (1.0f + e);
-    }
+    if (g_round & 8) return gpu_gelu(x);
     return 0.5f * x * (1.0f + erff(x * SQRT_2_INV));
 }
 
@@ -785,11 +777,12 @@ void or_block_causal_mask(int gt, int gh, int gw, int n_prefix, float * out) {
  * adds can be measured on its own:
  *   OR_ROUND_Q16  (1): with f16 K/V, q is rounded to f16 before Q.K^T (the f16 matrix-core attention,
  *                      and ggml's own per-row CPU path and CUDA kernels)
- *   OR_ROUND_P16  (2): with f16 K/V, the softmax weights are rounded to f16 before P.V (the sum of the
- *                      weights stays f32, as in the GPU kernel)
+ *   OR_ROUND_P16  (2): with f16 K/V, the softmax weights are rounded to f16 before P.V, and the f32
+ *                      normalizer sums those rounded weights (as the GPU kernel's dot2 row sums do)
  *   OR_ROUND_EXP2 (4): weights as 2^(s*c - m*c) with c = scale*log2(e) in float, s the raw dot and m
  *                      the largest raw dot (the GPU kernel's exp2 form), instead of e^(s*scale - max)
- *   OR_ROUND_GELU (8): erf from the GPU epilogue's branch-free polynomial pair instead of libm erff */
+ *   OR_ROUND_GELU (8): GELU as the GPU epilogue computes it (one polynomial for log2 of the normal tail
+ *                      and one exp2) instead of libm erff */
 static int g_round = 0;
 void or_set_rounding(int bits) { g_round = bits; }
 int or_get_rounding(void) { return g_round; }
@@ -837,8 +830,8 @@ void or_attention(const float * q, const float * k, const float * v, int64_t n_q
                 const float mc = mx * c2;
                 for (int64_t j = 0; j < n_kv; j++) {
                     const float p = exp2_form ? exp2f(fmaf(sc[j], c2, -mc)) : expf(sc[j] - mx);
-                    sum += p;
                     const float pv = ((g_round & 2) && kv_f16) ? or_fp16_to_fp32(or_fp32_to_fp16(p)) : p;
+                    sum += pv;
                     const float * vj = vh + j * hd;
                     for (int d = 0; d < hd; d++) acc[d] = fmaf(pv, vj[d], acc[d]);
                 }

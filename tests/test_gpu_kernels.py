@@ -236,11 +236,11 @@ def test_matmul_gelu_epilogue(jlib, oracle, gtype, out_type, tile):
 
 
 def test_gelu_epilogue_every_f16_input(jlib, oracle):
-    """The fused GELU (branch-free erf: z P(z^2) below 0.875, 1 - 2^Q(z) above) on every finite f16
-    value in [-12, 12], through an f16 identity GEMM (exact: one product of 1.0 per output), against
-    the oracle's libm form 0.5 x (1 + erff(x / sqrt 2)). Both erf evaluations are within ~1.5 units of
-    2^-24 of erf, so outputs agree to 0.5 |x| 3.6e-7 plus an output rounding; subnormal and zero
-    inputs, the branch point z = 0.875 and the saturation of erf to 1 are all in the set."""
+    """The fused GELU (x Phi(x), the normal tail Phi(-|x|) as 2^Q(min(|x|, 5.5)) with one polynomial and
+    one hardware exp2) on every finite f16 value in [-12, 12], through an f16 identity GEMM (exact: one
+    product of 1.0 per output), against the oracle's libm form 0.5 x (1 + erff(x / sqrt 2)). Both are
+    within a few units of 2^-24 of Phi, so outputs agree to 0.5 |x| 3.6e-7 plus an output rounding;
+    subnormal and zero inputs, the clamp at 5.5 and the saturation of Phi to 1 are all in the set."""
     h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
     h = h[h <= 12.0]
     x = np.concatenate([h, -h[1:]])

@@ -385,6 +385,30 @@ def test_gelu_erf_against_math_erf():
         assert abs(got - ref) <= 4e-7 * max(1.0, abs(ref)), (v, got, ref)
 
 
+def test_gpu_gelu_form_against_float64():
+    """The oracle's restatement of the GPU epilogue's GELU (x Phi(x), the normal tail h = Phi(-|x|) as
+    2^Q(min(|x|, 5.5)) with one degree-8 polynomial) against the exact x Phi(x): Phi within 3 units of
+    2^-24 over every f16 value in [-12, 12] and a dense sample, GELU(x) = x exactly from 5.5 on, and
+    GELU(0) = 0. A coefficient slip, a dropped Horner step or a swapped branch moves Phi far past this."""
+    from scipy.special import erfc
+    h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    h = h[h <= 12.0]
+    x = np.concatenate([h, -h[1:], np.linspace(-8, 8, 400001, dtype=np.float32)]).astype(np.float32)
+    prev = O.get_rounding()
+    try:
+        O.set_rounding(O.ROUND_GELU)
+        got = O.gelu_erf_array(x).astype(np.float64)
+    finally:
+        O.set_rounding(prev)
+    xd = x.astype(np.float64)
+    phi = 0.5 * erfc(-xd / np.sqrt(2.0))
+    exact = xd * phi
+    err = np.abs(got - exact)
+    # |x| * (3 units of 2^-24 in Phi) plus the final product's rounding
+    assert np.all(err <= np.abs(xd) * 3 * 2.0 ** -24 + np.abs(exact) * 2.0 ** -24), float((err / np.maximum(np.abs(xd), 1e-30)).max())
+    assert np.all(got[x >= 5.5] == x[x >= 5.5]) and np.all(got[x == 0] == 0)
+
+
 def test_attention_against_float64():
     rng = np.random.default_rng(10)
     n, H, hd = 77, 3, 64
