@@ -411,10 +411,10 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // Scale operands, read once per stage: the weight row's four f16 block scales, as they lie in LDS,
     // fill K-slots 0-3 (both lane groups); the token's scale of block blk alone fills K-slot blk of lane
     // group 0 (group 1 is zero), so the product picks dw_blk * da_blk.
-    // The 32 VALU ops per step (magic-offset subtraction + fma) and the two MFMAs bound this path:
-    // with two or more waves per SIMD the MFMA results and the VALU results share the register-file
-    // write bandwidth (about 32 dwords per cycle per SIMD, measured), so they mostly serialize.
-    // Everything else is meant to hide behind them:
+    // The 32 VALU ops per step (magic-offset subtraction or conversion, then the fma) bound this path:
+    // at four cycles each they take four times the int8 MFMA's 32 cycles, and the matrix unit runs
+    // alongside them (VALU work during 60-70 % of its busy cycles, by counters). Everything else is
+    // meant to hide behind them:
     //  - software pipeline: operand chunks are read two steps ahead, the MFMAs of step u+1 are issued
     //    before the VALU work of step u, across stage boundaries;
     //  - the barrier that publishes stage st+1 sits two steps before the end of stage st, after the
