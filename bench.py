@@ -100,6 +100,22 @@ def time_forward(path, x_host, steps, warmup, kernel_pass=True):
     return res
 
 
+def forward_roofline(cfg, items, frames, rows, ms_per_step):
+    """Whole-forward roofline of one step: the time the forward would take at the dense peaks with every
+    contraction on its unit and nothing else (linear GEMMs on int8 for block-quantized weights or f16,
+    attention and patch embedding on f16), against the measured step. Block-causal attention (LeVJEPA)
+    counts its visible keys only (53.1 % of the 3137 x 3137 clip)."""
+    d, f, nl = cfg.embed_dim, cfg.ffn_dim, cfg.n_layer
+    gemm = 2.0 * rows * (4 * d * d + 2 * d * f) * nl * items
+    attn = 4.0 * rows * rows * d * nl * items * (0.531 if cfg.attn_mode == "block_causal" else 1.0)
+    pdim = 3 * cfg.patch * cfg.patch * (cfg.tubelet if frames > 1 else 1)   # one frame: the image patch embedding
+    patch = 2.0 * rows * pdim * d * items
+    gpeak = PEAK_F16_TFLOPS if cfg.ftype == "f16" else PEAK_INT8_TOPS
+    t_min = gemm / (gpeak * 1e12) + (attn + patch) / (PEAK_F16_TFLOPS * 1e12)
+    return {"t_min_ms": round(t_min * 1e3, 4), "frac": round(t_min * 1e3 / ms_per_step, 4),
+            "gemm_op": gemm, "attn_flop": attn, "gemm_peak": gpeak}
+
+
 def time_extra(name, steps):
     """Device time of one call of a row next to the encoder, median over `steps` calls after one warm call."""
     import ctypes as C
@@ -221,7 +237,7 @@ def main():
         sys.exit(2)
     import numpy as np
     import torch
-    from jepa_amd import inputs
+    from jepa_amd import forge, inputs
 
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
@@ -257,6 +273,7 @@ def main():
                                        "frac": round(ATTN_FLOP / (att["per_step_ms"] * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
                                        "avg_launch_ms": round(att["avg_ms"], 5)}
     extra["kernel_ms_per_clip"] = {c: round(v["per_step_ms"], 4) for c, v in k.items()}
+    extra["forward_roofline"] = forward_roofline(forge.CONFIGS["vitl16_q8_0"], 1, 16, N_TOK, ms_per_step)
     if not args.no_q4k:
         p4 = make_model("vitl16_q4_k")
         log("bench: timing q4_K")
@@ -269,6 +286,7 @@ def main():
             ach = GEMM_OPS / (g4["per_step_ms"] * 1e-3) / 1e12
             q4["gemm_roofline"] = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                                    "frac": round(ach / PEAK_INT8_TOPS, 4)}
+        q4["forward_roofline"] = forward_roofline(forge.CONFIGS["vitl16_q4_k"], 1, 16, N_TOK, q4["ms_per_step"])
         extra["q4_k"] = q4
     # the other encoder configurations: (batch, frames, size) of one step and what one item is
     shapes = {"vits16_f16": (1, 1, 224, "images"), "vitb16_2_1_q8_0": (8, 1, 384, "images"),
@@ -284,10 +302,12 @@ def main():
         log(f"bench: timing {name}")
         st = max(3, min(args.steps, 20))
         rc = time_forward(pc, xc, st, max(2, min(args.warmup, 3)), kernel_pass=False)
+        mps = rc["elapsed_s"] / st * 1e3
         extra.setdefault("configs", {})[name] = {
             "value": round(b * st / rc["elapsed_s"], 3), "unit": f"{unit}/s", "items_per_step": b,
-            "tokens_per_item": rc["rows"], "ms_per_step": round(rc["elapsed_s"] / st * 1e3, 4),
-            "p50_ms": round(float(np.median(rc["device_ms"])), 4), "steps": st}
+            "tokens_per_item": rc["rows"], "ms_per_step": round(mps, 4),
+            "p50_ms": round(float(np.median(rc["device_ms"])), 4), "steps": st,
+            "forward_roofline": forward_roofline(forge.CONFIGS[name], b, t, rc["rows"], mps)}
     for name in [e for e in args.extras.split(",") if e]:
         res = time_extra(name, max(5, min(args.steps, 20)))
         if res is not None:
