@@ -437,6 +437,40 @@ def test_attention(jlib, oracle, n_items, n_tok, H, rope):
     assert cos.min() >= 0.9999, cos.min()
 
 
+@pytest.mark.parametrize("hd,n_tok,order", [(64, 2048, "rising"), (64, 1000, "falling"), (80, 300, "rising"), (64, 333, "spikes")])
+def test_attention_running_maximum_moves(jlib, oracle, hd, n_tok, order):
+    """Scores spread over a wide range in key order, so the running maximum (kept in the exp2 domain and
+    moved only when a block exceeds it by 2^8) moves many times per sweep: key norms rising along the
+    sequence (a move in most blocks), falling (set by the first block, never moved), or a few isolated
+    keys far above the rest (moves in single blocks, some key splits never see one). Both kernels (head
+    width 64 and the generic width 80) against the float64 softmax."""
+    rng = np.random.default_rng(n_tok + hd)
+    H = 2
+    D = H * hd
+    qkv = rng.standard_normal((n_tok, 3 * D)).astype(np.float32)
+    j = np.arange(n_tok, dtype=np.float32)[:, None]
+    if order == "rising":
+        gain = 0.05 + 6.0 * j / n_tok
+    elif order == "falling":
+        gain = 6.05 - 6.0 * j / n_tok
+    else:
+        gain = np.full_like(j, 0.3)
+        gain[rng.choice(n_tok, 5, replace=False)] = 8.0
+    qkv[:, D:2 * D] *= gain                                   # the keys
+    qkv[:, :D] *= 2.0                                        # the queries
+    out = torch.zeros((n_tok, D), dtype=torch.float32, device="cuda")
+    dq = dev(qkv)
+    r = jlib.lib().jepa_amd_attention(0, dq.data_ptr(), 1, n_tok, H, hd, None, None, 0, 0, 0, out.data_ptr())
+    assert r == 0, jlib.error_text()
+    got = host(out).astype(np.float64)
+    ref = _attention_ref(qkv, 1, n_tok, H, hd=hd)
+    assert np.isfinite(got).all()
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    cos = (got * ref).sum(1) / (np.linalg.norm(got, axis=1) * np.linalg.norm(ref, axis=1))
+    assert rel <= 1e-2, rel
+    assert cos.min() >= 0.9999, cos.min()
+
+
 # head width 32 (the masked predictor's 12 x 32 heads): stored 64 wide with a zero upper half
 @pytest.mark.parametrize("n_items,n_tok,H,rope", [(1, 300, 12, True), (2, 65, 3, False), (1, 2048, 2, True)])
 def test_attention_hd32(jlib, oracle, n_items, n_tok, H, rope):
