@@ -1017,6 +1017,57 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
         }
     }
 
+    // The bias values of the wave's features and, in the QKV epilogue, the RoPE table rows of the
+    // workgroup's tokens are fetched for all tiles before the first output store: a load issued after
+    // a store cannot be moved ahead of it, so loads made inside the tile loops each waited one memory
+    // round trip. The RoPE rows (head widths 32 and 64) are copied HBM->LDS into the stage buffers,
+    // which the main loop no longer needs, by buffer copies of whole rows (the rows of consecutive
+    // tokens are contiguous), and read per lane from LDS; gathering them per lane from the tables (a
+    // 16-byte piece of 32 different rows per load) cost ~4 us of the ViT-L QKV GEMM's 31. 16-byte
+    // chunk c of row r sits in slot c ^ (r mod chunks per row), so the 32 tokens of one LDS read fall
+    // on different banks. Rows past M copy row M - 1 (their results are dropped).
+    [[maybe_unused]] const unsigned char * lrc = nullptr;
+    [[maybe_unused]] const unsigned char * lrs = nullptr;
+    if constexpr (EPI == EPI_QKV) {
+        const int hd = a.ep.hd;
+        if (a.ep.rope_c && (hd == 32 || hd == 64) && n0 < 2 * (int64_t) a.ep.D && 2 * T::BM * hd * 4 <= T::LDS) {
+            __builtin_amdgcn_s_waitcnt(0);      // no HBM->LDS copy of this wave still in flight
+            __syncthreads();                    // every wave is past its last read of the stage buffers
+            unsigned char * wc = smem;
+            unsigned char * ws = smem + T::BM * hd * 4;
+            const int cpr = hd / 4;                             // 16-byte chunks per row
+            const int rpi = 64 / cpr;                           // rows per 1 KB copy
+            const int64_t rows_tab = (int64_t) a.ep.R;          // table rows
+            const brsrc tc = make_brsrc(a.ep.rope_c, rows_tab * hd * 4);
+            const brsrc tsn = make_brsrc(a.ep.rope_s, rows_tab * hd * 4);
+            const int r_l = lane / cpr, slot = lane - r_l * cpr;
+            for (int k = wave; k < T::BM / rpi; k += NW) {      // 1 KB copies, dealt to the waves
+                const int r = k * rpi + r_l;
+                const int64_t m = m0 + r, mm = m < M ? m : M - 1;
+                const uint32_t off = (uint32_t) ((mm % rows_tab) * hd * 4 + ((slot ^ (r & (cpr - 1))) << 4));
+                dma_to_lds<16>(tc, off, 0, wc + k * 1024);
+                dma_to_lds<16>(tsn, off, 0, ws + k * 1024);
+            }
+            lrc = wc; lrs = ws;
+        }
+    }
+    constexpr bool BPRE = EPI == EPI_GELU_Q8_0 || EPI == EPI_GELU_Q8_K || EPI == EPI_QKV;
+    [[maybe_unused]] float4 bpre[BPRE ? TI : 1][4];
+    if constexpr (BPRE) {
+#pragma unroll
+        for (int i = 0; i < TI; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                bpre[i][q] = a.bias ? *(const float4 *) (a.bias + n0 + 32 * (wn * TI + i) + 8 * q + 4 * g)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    if constexpr (EPI == EPI_QKV) {
+        if (lrc) {
+            __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0): this wave's row copies (and bias loads) have landed
+            __syncthreads();
+        }
+    }
+
     if constexpr (EPI == EPI_GELU_Q8_K) {
         // q8_K activation of the next linear (quantize_row_q8_K_ref): per token and 256 features,
         // max = the first value of largest |x|, iscale = -127/max, q = min(127, rne(iscale*x)),
@@ -1041,8 +1092,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             for (int i = 0; i < TI; i++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const int64_t n = n0 + 32 * (wn * TI + i) + 8 * q + 4 * g;
-                    const float4 b = a.bias ? *(const float4 *) (a.bias + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    const float4 b = bpre[i][q];
                     const float bb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
@@ -1121,8 +1171,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 float v[16];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const int64_t n = nb + 8 * q + 4 * g;
-                    const float4 b = a.bias ? *(const float4 *) (a.bias + n) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    const float4 b = bpre[i][q];
                     v[4 * q + 0] = gelu_erf(__fadd_rn(acc[i][j][4 * q + 0], b.x));
                     v[4 * q + 1] = gelu_erf(__fadd_rn(acc[i][j][4 * q + 1], b.y));
                     v[4 * q + 2] = gelu_erf(__fadd_rn(acc[i][j][4 * q + 2], b.z));
@@ -1173,20 +1222,35 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 float t[16];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float4 b = a.bias ? *(const float4 *) (a.bias + nb + 8 * q + 4 * g) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    const float4 b = bpre[i][q];
                     const float bb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
                     for (int e = 0; e < 4; e++) t[4 * q + e] = a.bias ? __fadd_rn(acc[i][j][4 * q + e], bb[e]) : acc[i][j][4 * q + e];
                 }
                 if (which < 2) {
                     _Float16 * dst = (_Float16 *) (which == 0 ? ep.q : ep.k) + (head * ep.R_pad + tok) * hds + dbase;
+                    float4 c4[4], s4[4];
+                    if (ep.rope_c) {
+                        const int lr = 32 * (wm * TJ + j) + l32;      // the token's row of the workgroup
+                        const int cpr = hd / 4;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            if (lrc) {
+                                const int off = lr * hd * 4 + ((((dbase + 8 * q) >> 2) ^ (lr & (cpr - 1))) << 4);
+                                c4[q] = *(const float4 *) (lrc + off);
+                                s4[q] = *(const float4 *) (lrs + off);
+                            } else {
+                                c4[q] = *(const float4 *) (ep.rope_c + (int64_t) tok * hd + dbase + 8 * q);
+                                s4[q] = *(const float4 *) (ep.rope_s + (int64_t) tok * hd + dbase + 8 * q);
+                            }
+                        }
+                    }
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         float o[4] = {t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]};
                         if (ep.rope_c) {
                             // out = x*C + swap(x)*S' (reference src/rope3d.cpp:136-164): two products, one add
-                            const float4 c = *(const float4 *) (ep.rope_c + (int64_t) tok * hd + dbase + 8 * q);
-                            const float4 sn = *(const float4 *) (ep.rope_s + (int64_t) tok * hd + dbase + 8 * q);
+                            const float4 c = c4[q], sn = s4[q];
                             o[0] = __fadd_rn(__fmul_rn(t[4 * q + 0], c.x), __fmul_rn(t[4 * q + 1], sn.x));
                             o[1] = __fadd_rn(__fmul_rn(t[4 * q + 1], c.y), __fmul_rn(t[4 * q + 0], sn.y));
                             o[2] = __fadd_rn(__fmul_rn(t[4 * q + 2], c.z), __fmul_rn(t[4 * q + 3], sn.z));
