@@ -1467,15 +1467,17 @@ void dispatch_mfma(kargs a, hipStream_t s, const gemm_split_ws * sw) {
 }  // namespace
 
 int gemm_split_for(int wf, int64_t N, int64_t K) {
-    // q8_0 / q4_0 GEMMs with N <= 1024 cannot fill 256 CUs with tiles big enough to run well
-    // (2048 tokens x 1024 outputs is 64 tiles of 256x128); two workgroups per tile, one per K half,
-    // each of whole 128-column stages. The partial-sum exchange costs a few microseconds, which pays
-    // off from K = 2048 (fc2: 43.6 -> 37.4 us) but not at K = 1024 (out-proj: 18 -> 21 us).
-    // q4_K: each half starts at a super-block (256 columns) and spans whole 4-stage super-blocks
+    // GEMMs with N <= 1024 cannot fill 256 CUs with tiles big enough to run well (2048 tokens x 1024
+    // outputs is 64 tiles of 256x128); split-K gives each 128x128 tile two workgroups, one per K half
+    // (each of whole 128-column stages; q4_K: each half starts at a super-block and spans whole
+    // 4-stage super-blocks), at the cost of a partial-sum exchange (~2 us: the stores, the arrival
+    // atomic, the partner's loads). By default it runs for q4_K from K = 2048 (ViT-L fc2: 41 -> 35 us);
+    // the q8_0 / q4_0 fc2 runs as fast on the unsplit 128x64 tile (~39 us either way, with 20 MB less
+    // HBM traffic), and neither pays at K = 1024 (out-proj: 12.8 -> 16.8 us). The hook forces either.
     if (!((wf == W_Q32 || wf == W_Q40) && K % 256 == 0) && !(wf == W_Q4K && K % 512 == 0)) return 1;
     const int f = g_force_split.load();
     if (f >= 1) return f >= 2 ? 2 : 1;
-    return N <= SPLIT_MAX_N && K >= 2048 ? 2 : 1;
+    return wf == W_Q4K && N <= SPLIT_MAX_N && K >= 2048 ? 2 : 1;
 }
 
 void gemm_split_ws_size(int64_t max_rows, int64_t * part_floats, int64_t * cnt_n) {
