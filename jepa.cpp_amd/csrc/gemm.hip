@@ -1382,8 +1382,11 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
         if (!tile_ok(wf, c)) continue;
         const int64_t t = (N / bn) * ((M + bm - 1) / bm) * split;
         const double waves = (double) ((t + cus - 1) / cus);
-        // q4_K unpacks a wave's weight operand once for its TJ token tiles
-        const double eff = wf == W_Q4K && k_tiles[c].tj == 1 && k_tiles[c].ti > 1 ? 0.8 * k_tile_eff[c] : k_tile_eff[c];
+        // q4_K unpacks a wave's weight operand once for its TJ token tiles: tiles with two token tiles
+        // per wave gain (ViT-L qkv, N 3072: 128x128 33.3 us against 36.7 us for three rounds of
+        // 128x64), tiles with several weight tiles and one token tile lose
+        double eff = k_tile_eff[c];
+        if (wf == W_Q4K) eff *= k_tiles[c].tj >= 2 ? 1.1 : k_tiles[c].ti > 1 ? 0.8 : 1.0;
         const double cost = waves * (double) (bn * bm) / eff;
         if (cost < best) { best = cost; b = c; }
     }
