@@ -92,18 +92,28 @@ __device__ __forceinline__ float gelu_erf(float x) {
 }
 
 // The residual epilogue with the row's current values x already loaded: x + (t + bias) * ls
-__device__ __forceinline__ void resid4(const kargs & a, int64_t m, int64_t n, float t[4], float4 x) {
+// (bias b and layer scale v already loaded: zero / unused when absent)
+__device__ __forceinline__ void resid4(const kargs & a, int64_t m, int64_t n, float t[4], float4 x, float4 b, float4 v) {
     const gemm_epi & ep = a.ep;
     if (a.bias) {
-        const float4 b = *(const float4 *) (a.bias + n);
         t[0] = __fadd_rn(t[0], b.x); t[1] = __fadd_rn(t[1], b.y); t[2] = __fadd_rn(t[2], b.z); t[3] = __fadd_rn(t[3], b.w);
     }
     if (ep.ls) {
-        const float4 v = *(const float4 *) (ep.ls + n);
         t[0] = __fmul_rn(t[0], v.x); t[1] = __fmul_rn(t[1], v.y); t[2] = __fmul_rn(t[2], v.z); t[3] = __fmul_rn(t[3], v.w);
     }
     x.x = __fadd_rn(x.x, t[0]); x.y = __fadd_rn(x.y, t[1]); x.z = __fadd_rn(x.z, t[2]); x.w = __fadd_rn(x.w, t[3]);
     *(float4 *) (ep.y + m * ep.ldy + n) = x;
+}
+
+// The f32-output epilogue with its operands already loaded: bias b, modality vector v, position row r
+__device__ __forceinline__ void f32out4(const kargs & a, int64_t m, int64_t n, float t[4], float4 b, float4 v, float4 r) {
+    const gemm_epi & ep = a.ep;
+    if (a.bias) { t[0] = __fadd_rn(t[0], b.x); t[1] = __fadd_rn(t[1], b.y); t[2] = __fadd_rn(t[2], b.z); t[3] = __fadd_rn(t[3], b.w); }
+    if (ep.addvec) { t[0] = __fadd_rn(t[0], v.x); t[1] = __fadd_rn(t[1], v.y); t[2] = __fadd_rn(t[2], v.z); t[3] = __fadd_rn(t[3], v.w); }
+    if (ep.addrows) { t[0] = __fadd_rn(t[0], r.x); t[1] = __fadd_rn(t[1], r.y); t[2] = __fadd_rn(t[2], r.z); t[3] = __fadd_rn(t[3], r.w); }
+    const int64_t item = m / ep.rin, rr = m - item * ep.rin;
+    const int64_t row = item * ep.rout + ep.pre + rr;
+    *(float4 *) (ep.y + row * ep.ldy + n) = make_float4(t[0], t[1], t[2], t[3]);
 }
 
 __device__ __forceinline__ int perm16(int64_t tok) {
@@ -1051,7 +1061,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
             lrc = wc; lrs = ws;
         }
     }
-    constexpr bool BPRE = EPI == EPI_GELU_Q8_0 || EPI == EPI_GELU_Q8_K || EPI == EPI_QKV;
+    constexpr bool BPRE = true;
     [[maybe_unused]] float4 bpre[BPRE ? TI : 1][4];
     if constexpr (BPRE) {
 #pragma unroll
@@ -1268,12 +1278,43 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 }
             } else {
                 if (m >= M) continue;
+                // every load of the tile's four groups (residual rows, layer scale, modality vector,
+                // position rows) before its first store
+                const gemm_epi & ep = a.ep;
+                const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                float4 o1[4], o2[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int64_t n = nb + 8 * q + 4 * g;
+                    o1[q] = z4; o2[q] = z4;
+                    if constexpr (EPI == EPI_RESID) {
+                        if constexpr (!RPF) o1[q] = *(const float4 *) (ep.y + m * ep.ldy + n);
+                        if (ep.ls) o2[q] = *(const float4 *) (ep.ls + n);
+                    } else if constexpr (EPI == EPI_F32) {
+                        if (ep.addvec) o1[q] = *(const float4 *) (ep.addvec + n);
+                        if (ep.addrows) {
+                            const int64_t item = m / ep.rin, rr = m - item * ep.rin;
+                            o2[q] = *(const float4 *) (ep.addrows + (ep.pre + rr) * ep.ldy + n);
+                        }
+                    }
+                }
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const int64_t n = nb + 8 * q + 4 * g;
                     float t[4] = {acc[i][j][4 * q + 0], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                    if constexpr (RPF) resid4(a, m, n, t, xres[i][j][q]);
-                    else epi4<EPI>(a, m, n, t);
+                    if constexpr (EPI == EPI_RESID) {
+                        if constexpr (RPF) resid4(a, m, n, t, xres[i][j][q], bpre[i][q], o2[q]);
+                        else resid4(a, m, n, t, o1[q], bpre[i][q], o2[q]);
+                    } else if constexpr (EPI == EPI_F32) {
+                        f32out4(a, m, n, t, bpre[i][q], o1[q], o2[q]);
+                    } else {
+                        // GELU to f32 / f16: the bias is the only operand
+                        const float4 b = bpre[i][q];
+                        if (a.bias) { t[0] = __fadd_rn(t[0], b.x); t[1] = __fadd_rn(t[1], b.y); t[2] = __fadd_rn(t[2], b.z); t[3] = __fadd_rn(t[3], b.w); }
+                        kargs nb_a = a;
+                        nb_a.bias = nullptr;
+                        epi4<EPI>(nb_a, m, n, t);
+                    }
                 }
             }
         }
