@@ -13,7 +13,8 @@ Also reported on the same JSON line:
                 from the committed rocprofv3 counter summary when present.
   q4_k          the same workload with q4_K weights.
   configs       the other benchmark configurations measured by default: LeJEPA ViT-S/16 224^2 f16 (1 image,
-                CLS + learned positions) and V-JEPA 2.1 ViT-B/16 384^2 q8_0 (8 images per call, image path).
+                CLS + learned positions), V-JEPA 2.1 ViT-B/16 384^2 q8_0 (8 images per call, image path) and
+                V-JEPA 2 ViT-g/16 64 frames 256^2 q8_0 (8192 tokens, 40 layers, 1 clip).
   cpu_baseline  the CPU oracle (a C restatement of ggml's CPU semantics, not ggml) on this host's cores:
                 the whole 24-block clip, 1 warmup + 3 measured runs, mean (the reference's CPU protocol,
                 docs/benchmarks.md:41-53), with the host CPU model and core counts from lscpu.
@@ -221,9 +222,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-q4k", action="store_true", help="skip the q4_K line")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--configs", default="vits16_f16,vitb16_2_1_q8_0",
-                    help="also time these encoder configurations (comma list; default: vits16_f16, vitb16_2_1_q8_0; also "
-                         "vitg16_q8_0, levjepa_vitl16_q8_0, vitl16_q8_0 = the headline model with 4 clips per call; '' for none)")
+    ap.add_argument("--configs", default="vits16_f16,vitb16_2_1_q8_0,vitg16_q8_0",
+                    help="also time these encoder configurations (comma list; default: vits16_f16, vitb16_2_1_q8_0, "
+                         "vitg16_q8_0; also levjepa_vitl16_q8_0, vitl16_q8_0 = the headline model with 4 clips per call; "
+                         "'' for none)")
     ap.add_argument("--extras", default="",
                     help="also time the rows next to the encoder (comma list: head = ViT-L SSv2 attentive-pool head on "
                          "2048 tokens; predictor = ViT-L masked predictor, 1024 context + 1024 target rows; quantizer = "

@@ -81,7 +81,8 @@ int jepa_amd_matmul_gelu(int device, int wtype, const void * w_dev, int64_t n_ou
  * rows read every key, a patch row reads the patch keys of its own and earlier temporal slots of
  * tokens_per_slot rows, and no prefix key; 0 is full attention. out_type 0 (f32): out_dev f32
  * [n_items*n_tok][n_head*hd]; 8 (q8_0): out_dev ggml q8_0 blocks of those rows, as the attention
- * kernel's fused epilogue quantizes them for the out-projection. */
+ * kernel's fused epilogue quantizes them for the out-projection; 1 (f16, head widths 32 and 64):
+ * out_dev f16 rows, the f32 values rounded to nearest, the input of an f16 out-projection. */
 int jepa_amd_attention(int device, const float * qkv_dev, int64_t n_items, int64_t n_tok, int n_head, int hd,
                        const float * rope_c_dev, const float * rope_s_dev, int n_prefix, int64_t tokens_per_slot,
                        int out_type, void * out_dev);
@@ -101,9 +102,12 @@ int jepa_amd_preprocess_frames_device(int device, const jepa_preprocess_params *
  * device array of 32 MiB that every GPU the library runs on holds until the process ends; a call
  * whose scratch would exceed it (about n_frames * h * crop * 3 bytes plus the tables) is refused
  * with -1 and a message. Work is queued on `stream` (a hipStream_t of `device`; NULL: the null
- * stream) and the call returns after it finished, with the same output, bit for bit, as
- * jepa_amd_preprocess_frames_device. Calls on one GPU share that array: calls that overlap on one
- * GPU (from several threads or streams) race and must be serialised by the caller. */
+ * stream) and the call returns without waiting for it; the output is, bit for bit, that of
+ * jepa_amd_preprocess_frames_device. Nothing is copied from host memory: the tables reach the
+ * device as kernel arguments, so the call can be captured into a HIP graph (make one call on the
+ * device before capturing, which looks up the array's address) and the graph replayed on new frames
+ * of the same geometry. Calls on one GPU share the array: calls whose work overlaps on one GPU (on
+ * different streams, or graph replays beside eager calls) race, and the caller orders them. */
 int jepa_amd_preprocess_frames_device_noalloc(int device, const jepa_preprocess_params * p, const uint8_t * frames_dev, int n_frames,
                                               int h, int w, float * out_dev, int64_t out_cap, int * out_h, int * out_w, void * stream);
 

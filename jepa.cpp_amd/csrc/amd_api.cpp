@@ -290,7 +290,7 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
     if (!qkv || !out || n_items <= 0 || n_tok <= 0 || n_head <= 0 || n_prefix < 0 || tokens_per_slot < 0 ||
         n_tok > 0x40000000) return -1;
     if (!attention_supports(hd)) { jepa_log("jepa: jepa_amd_attention: head width %d (a multiple of 16 up to 128)\n", hd); return -1; }
-    if (out_type != T_F32 && !(out_type == T_Q8_0 && (hd == 64 || hd == 32))) {
+    if (out_type != T_F32 && !((out_type == T_Q8_0 || out_type == T_F16) && (hd == 64 || hd == 32))) {
         jepa_log("jepa: jepa_amd_attention: output type %d for head width %d\n", out_type, hd);
         return -1;
     }
@@ -313,6 +313,8 @@ extern "C" int jepa_amd_attention(int device, const float * qkv, int64_t n_items
     const int64_t rows = n_items * n_tok, D = (int64_t) n_head * hd;
     if (out_type == T_F32) {
         o.fmt = A_F32; o.q = out; o.ld = D;
+    } else if (out_type == T_F16) {
+        o.fmt = A_F16; o.q = out; o.ld = D;
     } else {
         o.fmt = A_Q8_0; o.ld = D;
         o.q = d.alloc((size_t) rows * D);

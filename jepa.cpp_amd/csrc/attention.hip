@@ -77,7 +77,7 @@ __device__ __forceinline__ int2 key_range(int q, int R, int np, int tpf) {
     return make_int2(np, min(R, np + ((q - np) / tpf + 1) * tpf));
 }
 
-// OUT: A_F32 writes O f32 [item*R][H*HDO]; A_Q8_0 writes the q8_0 activation of the next linear
+// OUT: A_F32 writes O f32 [item*R][H*HDO], A_F16 the same rounded to f16; A_Q8_0 writes the q8_0 activation of the next linear
 // (int8 codes [item*R][H*HDO] + f16 d per 32), the same values the separate quantizer would produce.
 // HDO: the heads' real width, 64, or 32 for heads stored 64 wide with a zero upper half (their
 // second Q.K^T dim pair and second P.V row block are skipped: both are zero).
@@ -395,6 +395,19 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
                     for (int dt = 0; dt < NDT; dt++) drow[dt] = f2hbits(am[dt] / 127.0f);
                 }
             }
+        } else if constexpr (OUT == A_F16) {
+            // the f16 input of an f16 out-projection: the f32 values rounded to nearest, as the
+            // separate conversion would
+            if (q < R) {
+                _Float16 * orow = (_Float16 *) O + (item * R + q) * DD + h * HDO;
+                typedef _Float16 h4o __attribute__((ext_vector_type(4)));
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                    for (int qq = 0; qq < 4; qq++)
+                        *(h4o *) (orow + 32 * dt + 8 * qq + 4 * g) = h4o{(_Float16) o[dt][4 * qq], (_Float16) o[dt][4 * qq + 1],
+                                                                          (_Float16) o[dt][4 * qq + 2], (_Float16) o[dt][4 * qq + 3]};
+            }
         } else {
             if (q < R) {
                 float * orow = (float *) O + (item * R + q) * DD + h * HDO;
@@ -544,6 +557,9 @@ void launch_attention(const void * q, const void * k, const void * vt, const act
     if (out.fmt == A_Q8_0) {
         if (hd == 32) masked ? go(k_attn_hd64<A_Q8_0, 32, true, QT>, out.d) : go(k_attn_hd64<A_Q8_0, 32, false, QT>, out.d);
         else masked ? go(k_attn_hd64<A_Q8_0, 64, true, QT>, out.d) : go(k_attn_hd64<A_Q8_0, 64, false, QT>, out.d);
+    } else if (out.fmt == A_F16) {
+        if (hd == 32) masked ? go(k_attn_hd64<A_F16, 32, true, QT>, nullptr) : go(k_attn_hd64<A_F16, 32, false, QT>, nullptr);
+        else masked ? go(k_attn_hd64<A_F16, 64, true, QT>, nullptr) : go(k_attn_hd64<A_F16, 64, false, QT>, nullptr);
     } else {
         if (hd == 32) masked ? go(k_attn_hd64<A_F32, 32, true, QT>, nullptr) : go(k_attn_hd64<A_F32, 32, false, QT>, nullptr);
         else masked ? go(k_attn_hd64<A_F32, 64, true, QT>, nullptr) : go(k_attn_hd64<A_F32, 64, false, QT>, nullptr);

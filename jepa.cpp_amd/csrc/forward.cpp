@@ -172,8 +172,8 @@ void enqueue_block(const blk_shape & b, const dev_layer & L, fwd_workspace & w, 
         kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
     }
     w.actA.fmt = L.out.act();
-    if (w.actA.fmt == A_Q8_0 && (hd == 64 || hd == 32)) {
-        // the attention epilogue writes the out-projection's q8_0 input directly
+    if ((w.actA.fmt == A_Q8_0 || w.actA.fmt == A_F16) && (hd == 64 || hd == 32)) {
+        // the attention epilogue writes the out-projection's q8_0 or f16 input directly
         kt.run("attention", [&] {
             launch_attention(w.Q, w.Kt, w.Vt, w.actA, n_items, H, hd, R, w.R_pad, 1.0f / sqrtf((float) hd), n_prefix, slot_rows, s);
         });

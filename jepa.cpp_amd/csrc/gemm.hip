@@ -1321,42 +1321,91 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     }
 }
 
-// f32 weights x f32 activations (hfvit patch embedding and f32 files): VALU FMA, 64x64 tiles,
-// each thread 4 tokens x 4 consecutive features, K staged 16 at a time through LDS.
+// f32 weights x f32 activations (hfvit patch embedding and f32 files): VALU FMA on tiles of 16 tokens x
+// 32 features, so that even a one-image patch embedding (196 x 384 outputs) runs on 156 workgroups.
+// A workgroup stages up to F32_KC columns of its 16 activation rows and 32 weight rows in LDS at once,
+// transposed (k-major), then each of its four waves sums one quarter of those columns: a lane holds 2
+// tokens x 4 consecutive features, one 8-byte and one 16-byte LDS read per 8 FMAs. The four partial
+// sums meet in LDS and are added in wave order; a K longer than F32_KC runs several such chunks, each
+// chunk's total added to the running sum.
+constexpr int F32_KC = 768;
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_f32(kargs a) {
-    __shared__ float sW[16][64 + 4];
-    __shared__ float sX[16][64 + 4];
-    const int tid = threadIdx.x;
-    const int tn = tid & 15, tm = tid >> 4;
-    const int64_t n0 = (int64_t) blockIdx.x * 64, m0 = (int64_t) blockIdx.y * 64;
+    __shared__ __attribute__((aligned(16))) float sX[F32_KC][16];
+    __shared__ __attribute__((aligned(16))) float sW[F32_KC][32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t n0 = (int64_t) blockIdx.x * 32, m0 = (int64_t) blockIdx.y * 16;
     const float * W = (const float *) a.A;
     const float * X = (const float *) a.B;
-    float acc[4][4] = {{0}};
-    for (int64_t k0 = 0; k0 < a.K; k0 += 16) {
-        for (int c = tid; c < 64 * 16; c += 256) {
-            const int r = c >> 4, kk = c & 15;
-            const int64_t n = n0 + r, m = m0 + r, k = k0 + kk;
-            sW[kk][r] = (n < a.N && k < a.K) ? W[n * a.K + k] : 0.0f;
-            sX[kk][r] = (m < a.M && k < a.K) ? X[m * a.K + k] : 0.0f;
+    const int tg = lane >> 3, fg = lane & 7;            // tokens 2 tg, 2 tg + 1; features 4 fg .. 4 fg + 3
+    const bool al = (a.K & 3) == 0 && (((uintptr_t) X | (uintptr_t) W) & 15) == 0;   // rows 16-byte aligned
+    float tot[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+    float * red = &sW[0][0];                            // [3][64][8] partials of waves 1..3 (reuses sW)
+    for (int64_t k0 = 0; k0 < a.K; k0 += F32_KC) {
+        const int kc = (int) (a.K - k0 < F32_KC ? a.K - k0 : F32_KC);
+        __syncthreads();                                // the previous chunk's reads (and reduction) are done
+        // rows of 4 consecutive k (float4 loads along k); rows past M / N and columns past K read as 0
+        for (int c = tid; c < 16 * (F32_KC / 4); c += 256) {
+            const int r = c / (F32_KC / 4), kk = 4 * (c % (F32_KC / 4));
+            if (kk >= kc) continue;
+            const int64_t m = m0 + r;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (m < a.M) {
+                const float * src = X + m * a.K + k0 + kk;
+                if (kk + 4 <= kc && al) v = *(const float4 *) src;
+                else { v.x = src[0]; if (kk + 1 < kc) v.y = src[1]; if (kk + 2 < kc) v.z = src[2]; if (kk + 3 < kc) v.w = src[3]; }
+            }
+            sX[kk][r] = v.x; sX[kk + 1][r] = v.y; sX[kk + 2][r] = v.z; sX[kk + 3][r] = v.w;
+        }
+        for (int c = tid; c < 32 * (F32_KC / 4); c += 256) {
+            const int r = c / (F32_KC / 4), kk = 4 * (c % (F32_KC / 4));
+            if (kk >= kc) continue;
+            const int64_t n = n0 + r;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (n < a.N) {
+                const float * src = W + n * a.K + k0 + kk;
+                if (kk + 4 <= kc && al) v = *(const float4 *) src;
+                else { v.x = src[0]; if (kk + 1 < kc) v.y = src[1]; if (kk + 2 < kc) v.z = src[2]; if (kk + 3 < kc) v.w = src[3]; }
+            }
+            sW[kk][r] = v.x; sW[kk + 1][r] = v.y; sW[kk + 2][r] = v.z; sW[kk + 3][r] = v.w;
         }
         __syncthreads();
+        const int q = (kc + 3) / 4;                     // columns per wave (the last wave may get fewer)
+        const int kb = wave * q, ke = kb + q < kc ? kb + q : kc;
+        float acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+        for (int k = kb; k < ke; k++) {
+            const float2 x = *(const float2 *) &sX[k][2 * tg];
+            const float4 w = *(const float4 *) &sW[k][4 * fg];
+            acc[0][0] = fmaf(x.x, w.x, acc[0][0]); acc[0][1] = fmaf(x.x, w.y, acc[0][1]);
+            acc[0][2] = fmaf(x.x, w.z, acc[0][2]); acc[0][3] = fmaf(x.x, w.w, acc[0][3]);
+            acc[1][0] = fmaf(x.y, w.x, acc[1][0]); acc[1][1] = fmaf(x.y, w.y, acc[1][1]);
+            acc[1][2] = fmaf(x.y, w.z, acc[1][2]); acc[1][3] = fmaf(x.y, w.w, acc[1][3]);
+        }
+        __syncthreads();                                // every wave is past its reads of sW
+        if (wave > 0) {
 #pragma unroll
-        for (int kk = 0; kk < 16; kk++) {
-            float w[4], x[4];
+            for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) { w[e] = sW[kk][4 * tn + e]; x[e] = sX[kk][4 * tm + e]; }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc[i][e] = fmaf(x[i], w[e], acc[i][e]);
+                for (int e = 0; e < 4; e++) red[((wave - 1) * 64 + lane) * 8 + 4 * i + e] = acc[i][e];
         }
         __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float v = acc[i][e];
+                    for (int w = 0; w < 3; w++) v = __fadd_rn(v, red[(w * 64 + lane) * 8 + 4 * i + e]);
+                    tot[i][e] = k0 == 0 ? v : __fadd_rn(tot[i][e], v);
+                }
+        }
     }
+    if (wave == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int64_t m = m0 + 4 * tm + i, n = n0 + 4 * tn;
-        if (m < a.M && n < a.N) epi4<EPI>(a, m, n, acc[i]);
+        for (int i = 0; i < 2; i++) {
+            const int64_t m = m0 + 2 * tg + i, n = n0 + 4 * fg;
+            if (m < a.M && n < a.N) epi4<EPI>(a, m, n, tot[i]);
+        }
     }
 }
 
@@ -1546,7 +1595,7 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
     if (M <= 0) return;
     if (a.ep.kind == EPI_F32 && a.ep.rin <= 0) { a.ep.rin = M; a.ep.rout = M; a.ep.pre = 0; }   // identity row map
     if (W.fmt == W_F32) {
-        dim3 grid((unsigned) ((a.N + 63) / 64), (unsigned) ((M + 63) / 64));
+        dim3 grid((unsigned) ((a.N + 31) / 32), (unsigned) ((M + 15) / 16));
         switch (ep.kind) {
             case EPI_F32:      k_gemm_f32<EPI_F32><<<grid, 256, 0, s>>>(a); break;
             case EPI_RESID:    k_gemm_f32<EPI_RESID><<<grid, 256, 0, s>>>(a); break;

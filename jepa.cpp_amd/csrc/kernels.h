@@ -105,9 +105,10 @@ void launch_prefix_rows(float * x, const float * cls, const float * reg, int n_r
 // quantizers; n a multiple of the block size. Returns false for another type or a ragged n.
 bool launch_quantize_rows(int dst_type, const float * x, int64_t n, void * y, hipStream_t s);
 
-// weight expansion at load: raw ggml blocks (device) -> dev_linear operand arrays
+// weight expansion at load: raw ggml blocks (device) -> dev_linear operand arrays (int8: q4_0 rows
+// go to the int8 layout of q8_0 whatever their length, for a linear whose parts mix the two)
 void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd,
-                   void * wmin, hipStream_t s);
+                   void * wmin, hipStream_t s, bool int8 = false);
 
 // test hooks
 // force the MFMA GEMM onto workgroup tile `index` (0..8) for every later launch whose N it divides;

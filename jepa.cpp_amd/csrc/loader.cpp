@@ -345,12 +345,21 @@ struct loader {
                          name.c_str(), t->ne[0], t->ne[1], n_in, n_part);
                 return false;
             }
-            if (!ts.empty() && t->type != ts[0]->type) {
-                jepa_log("jepa: tensor %s is %s but %s is %s: the parts of one linear have to share a dtype\n", name.c_str(),
-                         ggml_traits(t->type).name, wname.c_str(), ggml_traits(ts[0]->type).name);
-                return false;
-            }
             ts.push_back(t);
+        }
+        // Parts of different dtypes: the reference runs each part as its own linear. q8_0 and q4_0 parts
+        // mix exactly: both take q8_0 activations and q4_0's codes q - 8 are int8 codes under the same
+        // f16 scale, so every part expands to the int8 layout and one GEMM gives each part's own dot
+        // products. Any other mix (its parts would need different activation formats) is refused.
+        bool mixed = false;
+        for (const auto * p : ts) mixed |= p->type != ts[0]->type;
+        if (mixed) {
+            for (const auto * p : ts)
+                if (p->type != T_Q8_0 && p->type != T_Q4_0) {
+                    jepa_log("jepa: the parts of %s are of different dtypes (%s, ...): only q8_0 and q4_0 parts can be "
+                             "mixed in one linear here\n", wname.c_str(), ggml_traits(p->type).name);
+                    return false;
+                }
         }
         const gguf::tensor_info * t = ts[0];
         size_t nbytes = 0;
@@ -358,8 +367,8 @@ struct loader {
         const int64_t n_file = n_out;
         if (pad_out) n_out = (n_out + 127) / 128 * 128;
         const size_t pad_bytes = (size_t) (n_out - n_file) * (nbytes / (size_t) n_file);
-        L.gtype = t->type; L.n_in = n_in; L.n_out = n_out; L.n_valid = n_file;
-        L.fmt = weight_format(t->type, n_in);
+        L.gtype = mixed ? (int) T_Q8_0 : t->type; L.n_in = n_in; L.n_out = n_out; L.n_valid = n_file;
+        L.fmt = mixed ? (int) W_Q32 : weight_format(t->type, n_in);
         if (L.fmt < 0) {
             jepa_log("jepa: tensor %s has dtype %s, which this engine has no GEMM kernel for "
                      "(f32, f16, q8_0, q4_0 and q4_K are supported)\n", wname.c_str(), ggml_traits(t->type).name);
@@ -389,19 +398,33 @@ struct loader {
                 L.wmin = dalloc((size_t) n_out * (n_in / 256) * 16 * 2);
                 if (!L.wd || !L.wmin) return false;
             }
-            launch_repack(t->type, staging, n_out, n_in, L.w, L.wd, L.wmin, s);
+            if (!mixed) {
+                launch_repack(t->type, staging, n_out, n_in, L.w, L.wd, L.wmin, s);
+            } else {
+                size_t off = 0;
+                for (size_t p = 0; p < ts.size(); p++) {
+                    launch_repack(ts[p]->type, (const char *) staging + off, n_part, n_in, (int8_t *) L.w + (size_t) p * n_part * n_in,
+                                  (uint16_t *) L.wd + (size_t) p * n_part * (n_in / 32), nullptr, s, true);
+                    off += ts[p]->nbytes;
+                }
+            }
         }
         if (hipStreamSynchronize(s) != hipSuccess) { jepa_log("jepa: weight upload of %s failed\n", wname.c_str()); return false; }
         if (bnames.size() == 1) return vec(bnames[0], n_file, &L.bias, false, n_out);
-        // stacked biases: all present or none
+        // stacked biases, each optional on its own (the reference adds each part's bias when present,
+        // src/jepa.cpp:408-414, src/jepa-gguf.cpp:712-714): an absent part adds zeros
         int present = 0;
         for (const auto & b : bnames) present += f.tensor(b) ? 1 : 0;
         if (present == 0) return true;
         std::vector<float> all;
         for (const auto & b : bnames) {
             const gguf::tensor_info * bt = f.tensor(b);
-            if (!bt || bt->type != T_F32 || bt->ne[0] * bt->ne[1] * bt->ne[2] * bt->ne[3] != n_part) {
-                jepa_log("jepa: bias %s has to be f32 with %" PRId64 " values, like the other parts'\n", b.c_str(), n_part);
+            if (!bt) {
+                all.insert(all.end(), (size_t) n_part, 0.0f);
+                continue;
+            }
+            if (bt->type != T_F32 || bt->ne[0] * bt->ne[1] * bt->ne[2] * bt->ne[3] != n_part) {
+                jepa_log("jepa: bias %s has to be f32 with %" PRId64 " values\n", b.c_str(), n_part);
                 return false;
             }
             if (!read(*bt)) return false;

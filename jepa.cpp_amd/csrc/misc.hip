@@ -572,11 +572,11 @@ void launch_cls_rows(float * x, const float * cls, const float * pos, int64_t n_
 }
 
 void launch_repack(int gtype, const void * raw, int64_t n_out, int64_t n_in, void * w, void * wd, void * wmin,
-                   hipStream_t s) {
+                   hipStream_t s, bool int8) {
     switch (gtype) {
         case T_Q8_0: k_repack_q8_0<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (int8_t *) w, (uint16_t *) wd); break;
         case T_Q4_0:
-            if (weight_format(T_Q4_0, n_in) == W_Q40)
+            if (!int8 && weight_format(T_Q4_0, n_in) == W_Q40)
                 k_repack_q4_0_packed<<<nblk(n_out * (n_in / 32), 256), 256, 0, s>>>((const uint8_t *) raw, n_out, n_in, (uint32_t *) w,
                                                                                    (uint16_t *) wd);
             else

@@ -115,6 +115,24 @@ size_t preprocess_scratch_bytes(const jepa_preprocess_params * p, const pre_plan
            align256((size_t) n_frames * h * g.crop * 3);
 }
 
+namespace {
+
+// Table bytes travel to the device as kernel arguments, PUT_CHUNK bytes per launch: a launch copies
+// its arguments when it is enqueued (and a captured launch keeps them in its graph node), so no host
+// buffer has to outlive the call, no pinned staging is needed and nothing waits on the stream.
+constexpr int PUT_CHUNK = 3072;
+struct put_args {
+    unsigned char * dst;
+    uint32_t n;
+    unsigned char b[PUT_CHUNK];
+};
+
+__global__ void k_put_bytes(put_args a) {
+    for (uint32_t i = threadIdx.x; i < a.n; i += blockDim.x) a.dst[i] = a.b[i];
+}
+
+}  // namespace
+
 bool launch_preprocess(const jepa_preprocess_params * p, const pre_plan & g, const uint8_t * frames, int n_frames, int h, int w,
                        float * out, void * scratch, hipStream_t s) {
     const resample_axis hx = resample_axis_for(w, g.rw, p->resample), vx = resample_axis_for(h, g.rh, p->resample);
@@ -139,7 +157,13 @@ bool launch_preprocess(const jepa_preprocess_params * p, const pre_plan & g, con
     };
     const dev_axis dh = upload(hx, g.rw == w), dv = upload(vx, g.rh == h);
     uint8_t * mid = (uint8_t *) dev + off;
-    if (hipMemcpyAsync(scratch, blob.data(), off, hipMemcpyHostToDevice, s) != hipSuccess) return false;
+    for (size_t o = 0; o < off; o += PUT_CHUNK) {
+        put_args pa;
+        pa.dst = dev + o;
+        pa.n = (uint32_t) std::min<size_t>(PUT_CHUNK, off - o);
+        memcpy(pa.b, blob.data() + o, pa.n);
+        k_put_bytes<<<1, 256, 0, s>>>(pa);
+    }
     norm_params np;
     for (int c = 0; c < 3; c++) { np.mean[c] = g.mean[c]; np.stdv[c] = g.stdv[c]; }
     np.inv = g.inv;
@@ -147,8 +171,7 @@ bool launch_preprocess(const jepa_preprocess_params * p, const pre_plan & g, con
     const int64_t n1 = (int64_t) n_frames * h * g.crop, n2 = (int64_t) n_frames * g.crop * g.crop;
     k_resize_rows<<<(unsigned) ((n1 + 255) / 256), 256, 0, s>>>(frames, mid, n_frames, h, w, g.crop, g.ox, g.rw, dh);
     k_resize_cols_norm<<<(unsigned) ((n2 + 255) / 256), 256, 0, s>>>(mid, out, n_frames, h, g.crop, g.oy, g.ox, g.rh, g.rw, dv, np);
-    // the blob must outlive the copy: wait for it here (pageable source)
-    return hipStreamSynchronize(s) == hipSuccess;
+    return hipGetLastError() == hipSuccess;
 }
 
 // ---------------------------------------------------------------------------------------------------

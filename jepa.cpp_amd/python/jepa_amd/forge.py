@@ -34,6 +34,8 @@ class EncoderConfig:
     cls_token: bool = False
     n_registers: int = 0    # register tokens after the CLS row (enc.reg_tokens)
     qkv_fused: bool = True  # False: separate attn_q / attn_k / attn_v (the rows of the fused matrix)
+    qkv_parts: str = ""     # split q / k / v: per part "<dtype>" or "<dtype>+b" (with its bias), comma list; "": all
+                            # parts of the file type with biases
     ftype: str = "q8_0"     # f16 | q8_0 | q4_0 | q4_k
     rope_layout: str = ""   # tiled | interleaved ('' for non-rope families)
     rope_interpolate: bool = False
@@ -263,14 +265,18 @@ def write_model(cfg: EncoderConfig, path: str) -> str:
             vec(p + "attn_qkv.bias", 3 * D)
         else:   # the same random draws as the fused matrix, written as its three row blocks
             gt = _block_type(cfg, D)
+            parts = cfg.qkv_parts.split(",") if cfg.qkv_parts else [""] * 3
+            types = [_QTYPE[q.split("+")[0]] if q else gt for q in parts]
             x = normal(3 * D, D, std=cfg.w_std)
             for j, nm in enumerate("qkv"):
                 part = np.ascontiguousarray(x[j * D:(j + 1) * D])
-                w.add_tensor(p + f"attn_{nm}.weight", gt, (D, D),
-                             dev_q4k(part) if gt == GGML_Q4_K and dev_q4k is not None else quantize(gt, part))
+                pt = types[j]
+                w.add_tensor(p + f"attn_{nm}.weight", pt, (D, D),
+                             dev_q4k(part) if pt == GGML_Q4_K and dev_q4k is not None else quantize(pt, part))
             b = normal(3 * D, std=0.02)
             for j, nm in enumerate("qkv"):
-                w.add_tensor(p + f"attn_{nm}.bias", GGML_F32, (D,), np.ascontiguousarray(b[j * D:(j + 1) * D]))
+                if not parts[j] or parts[j].endswith("+b"):
+                    w.add_tensor(p + f"attn_{nm}.bias", GGML_F32, (D,), np.ascontiguousarray(b[j * D:(j + 1) * D]))
         mat(p + "attn_out.weight", D, D, _block_type(cfg, D))
         vec(p + "attn_out.bias", D)
         ln(p + "ln2", D)

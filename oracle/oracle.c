@@ -402,7 +402,113 @@ static float dot_f32_8acc(const float * a, const float * b, int64_t n) {
     return s;
 }
 
+/* ggml's x86 summation order (g_ggml_lanes = 1), ggml 36da5713, the submodule the reference pins
+ * (docs/benchmarks.md:36) and builds with GGML_LLAMAFILE=ON (:37):
+ *  - q8_0 and q4_0 weights x q8_0 activations run through llamafile's tinyBLAS_Q0_AVX tiles
+ *    (ggml-cpu/llamafile/sgemm.cpp) or, for shapes it declines, ggml_vec_dot_q8_0_q8_0 /
+ *    ggml_vec_dot_q4_0_q8_0 (ggml-cpu/arch/x86/quants.c, AVX2 path). Both keep one __m256 of eight
+ *    float lanes per output: the byte products of a 32-block are summed four consecutive bytes per
+ *    int32 lane (_mm256_dpbusd_epi32, or maddubs + madd), converted to float, and each lane takes
+ *    fma(dw * da, lane, acc) block by block; the eight lanes are then added by hsum_float_8. The
+ *    reference measured the two paths bit-identical (docs/ggml-notes.md:246-251).
+ *  - q4_K weights x q8_K activations run ggml_vec_dot_q4_K_q8_K (AVX2 path; llamafile has no
+ *    k-quant tiles): per super-block, eight int32 lanes sum sc_j * (four consecutive products) over
+ *    the eight sub-blocks (maddubs, then madd with the broadcast scale), and acc += (y.d * x.d) * lane
+ *    per lane; the mins go to four float lanes, lane k = m_2k bsum_2k + m_2k+1 bsum_2k+1 (madd of the
+ *    mins with the pairwise-added bsums), acc_m += (-y.d * x.dmin) * lane. The result is
+ *    hsum_float_8(acc) plus the two-step horizontal sum of acc_m.
+ * hsum_float_8(v) = ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)): the high 128 bits added to
+ * the low, then movehl, then movehdup. */
+static int g_ggml_lanes = 0;
+void or_set_ggml_lanes(int on) { g_ggml_lanes = on; }
+int or_get_ggml_lanes(void) { return g_ggml_lanes; }
+
+static float hsum_lanes8(const float v[8]) { return ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7])); }
+static float hsum_lanes4(const float v[4]) { return (v[0] + v[2]) + (v[1] + v[3]); }
+
+/* one output in ggml's x86 lane order: q = weight codes (int8, q4 values unsigned for q4_K), a =
+ * activation codes, nb blocks (32) or super-blocks (256) */
+static float dot_ggml_lanes(int wtype, const int8_t * q, const int8_t * a, int64_t nb, const float * dwr, const float * dmr,
+                            const float * dar, const int32_t * scr, const int32_t * mr, const int32_t * bsr) {
+    if (wtype == OR_Q4_K) {
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, accm[4] = {0, 0, 0, 0};
+        for (int64_t b = 0; b < nb; b++) {
+            int32_t sumi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int j = 0; j < 8; j++) {
+                const int8_t * qj = q + b * QK_K + 32 * j;
+                const int8_t * aj = a + b * QK_K + 32 * j;
+                for (int l = 0; l < 8; l++) {
+                    int32_t p = 0;
+                    for (int e = 4 * l; e < 4 * l + 4; e++) p += (int32_t) (uint8_t) qj[e] * (int32_t) aj[e];
+                    sumi[l] += scr[b * 8 + j] * p;
+                }
+            }
+            const float d = dar[b] * dwr[b];
+            const float dmin = -dar[b] * dmr[b];
+            for (int l = 0; l < 8; l++) acc[l] = fmaf(d, (float) sumi[l], acc[l]);
+            for (int k = 0; k < 4; k++) {
+                const int32_t prod = mr[b * 8 + 2 * k] * bsr[b * 8 + 2 * k] + mr[b * 8 + 2 * k + 1] * bsr[b * 8 + 2 * k + 1];
+                accm[k] = fmaf(dmin, (float) prod, accm[k]);
+            }
+        }
+        return hsum_lanes8(acc) + hsum_lanes4(accm);
+    }
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t b = 0; b < nb; b++) {
+        const float d = dwr[b] * dar[b];
+        for (int l = 0; l < 8; l++) {
+            int32_t si = 0;
+            for (int e = 4 * l; e < 4 * l + 4; e++) si += (int32_t) q[b * 32 + e] * (int32_t) a[b * 32 + e];
+            acc[l] = fmaf(d, (float) si, acc[l]);
+        }
+    }
+    return hsum_lanes8(acc);
+}
+
+/* or_vec_dot in the lane order: the row's codes and scales expanded, then dot_ggml_lanes */
+static float vec_dot_lanes(int wtype, int64_t n, const void * wrow, const void * arow) {
+    const int kq = wtype == OR_Q4_K ? QK_K : 32;
+    const int64_t nb = n / kq;
+    int8_t * q = (int8_t *) malloc((size_t) n), * a = (int8_t *) malloc((size_t) n);
+    float * dw = (float *) malloc(sizeof(float) * nb * 3);
+    int32_t * ib = (int32_t *) malloc(sizeof(int32_t) * nb * 24);
+    if (!q || !a || !dw || !ib) { free(q); free(a); free(dw); free(ib); return NAN; }
+    float * dm = dw + nb, * da = dw + 2 * nb;
+    int32_t * sc = ib, * mn = ib + nb * 8, * bs = ib + nb * 16;
+    for (int64_t b = 0; b < nb; b++) {
+        if (wtype == OR_Q4_K) {
+            const blk_q4_K * X = (const blk_q4_K *) wrow + b; const blk_q8_K * Y = (const blk_q8_K *) arow + b;
+            dw[b] = or_fp16_to_fp32(X->d); dm[b] = or_fp16_to_fp32(X->dmin); da[b] = Y->d;
+            for (int j = 0; j < 8; j++) {
+                uint8_t s6, m6;
+                q4k_scale_min(j, X->scales, &s6, &m6);
+                sc[b * 8 + j] = s6; mn[b * 8 + j] = m6;
+                bs[b * 8 + j] = (int32_t) Y->bsums[2 * j] + (int32_t) Y->bsums[2 * j + 1];
+                for (int l = 0; l < 32; l++) q[b * QK_K + 32 * j + l] = (int8_t) ((j & 1) ? (X->qs[32 * (j / 2) + l] >> 4) : (X->qs[32 * (j / 2) + l] & 0xF));
+            }
+            memcpy(a + b * QK_K, Y->qs, QK_K);
+        } else {
+            const blk_q8_0 * Y = (const blk_q8_0 *) arow + b;
+            da[b] = or_fp16_to_fp32(Y->d);
+            memcpy(a + b * 32, Y->qs, 32);
+            if (wtype == OR_Q8_0) {
+                const blk_q8_0 * X = (const blk_q8_0 *) wrow + b;
+                dw[b] = or_fp16_to_fp32(X->d);
+                memcpy(q + b * 32, X->qs, 32);
+            } else {
+                const blk_q4_0 * X = (const blk_q4_0 *) wrow + b;
+                dw[b] = or_fp16_to_fp32(X->d);
+                for (int j = 0; j < 16; j++) { q[b * 32 + j] = (int8_t) ((X->qs[j] & 0xF) - 8); q[b * 32 + j + 16] = (int8_t) ((X->qs[j] >> 4) - 8); }
+            }
+        }
+    }
+    const float r = dot_ggml_lanes(wtype, q, a, nb, dw, dm, da, sc, mn, bs);
+    free(q); free(a); free(dw); free(ib);
+    return r;
+}
+
 float or_vec_dot(int wtype, int64_t n, const void * wrow, const void * arow) {
+    if (g_ggml_lanes && (wtype == OR_Q8_0 || wtype == OR_Q4_0 || wtype == OR_Q4_K)) return vec_dot_lanes(wtype, n, wrow, arow);
     switch (wtype) {
         case OR_F32: return dot_f32_8acc((const float *) wrow, (const float *) arow, n);
         case OR_F16: {
@@ -584,7 +690,10 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
             const int8_t * a = qa + m * n_in;
             const int8_t * q = qw + o * n_in;
             float s = 0.0f, sm = 0.0f;
-            if (wtype == OR_Q4_K && g_k_split > 1 && nb % g_k_split == 0) {
+            if (g_ggml_lanes) {
+                s = dot_ggml_lanes(wtype, q, a, nb, dw + o * nb, dmw + o * nb, da + m * nb, scw + o * nb * 8, mw + o * nb * 8,
+                                   bsa + m * nb * 8);
+            } else if (wtype == OR_Q4_K && g_k_split > 1 && nb % g_k_split == 0) {
                 /* each K range gives its own main and mins chains and their difference; the range
                    results are added in order */
                 const int64_t per = nb / g_k_split;
@@ -1050,6 +1159,10 @@ out:
 static const float * g_teacher = NULL;
 static int64_t g_teacher_n = 0;
 void or_set_teacher(const float * trace, int64_t n_floats) { g_teacher = trace; g_teacher_n = trace ? n_floats : 0; }
+/* With a teacher, blocks before g_first_block are not run: their trace entries are the teacher's own
+ * (entry l + 1 = teacher entry l + 1), so a deep model's last blocks can be checked alone. */
+static int g_first_block = 0;
+void or_set_first_block(int l0) { g_first_block = l0 < 0 ? 0 : l0; }
 
 int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_chans, int n_frames,
                        int height, int width, float * out, int64_t out_cap, float * trace, int64_t trace_cap,
@@ -1171,6 +1284,11 @@ int64_t or_encode_file(const char * path, const float * in, int n_batch, int n_c
                 const int64_t off = (((int64_t) it * (n_layers + 1)) + l) * R * D;
                 if (off + R * D > g_teacher_n) { fprintf(stderr, "oracle: teacher trace too small\n"); goto done; }
                 memcpy(x, g_teacher + off, sizeof(float) * R * D);
+                if (l < g_first_block) {
+                    if (off + 2 * R * D > g_teacher_n) { fprintf(stderr, "oracle: teacher trace too small\n"); goto done; }
+                    if (trace) memcpy(trace + (((int64_t) it * (n_layers + 1)) + l + 1) * R * D, g_teacher + off + R * D, sizeof(float) * R * D);
+                    continue;
+                }
             }
             if (block_fwd(&f, pre, x, R, D, H, video ? rope_c : NULL, rope_s, mask, kv_f16, eps, n_threads)) goto done;
             if (trace) memcpy(trace + (((int64_t) it * (n_layers + 1)) + l + 1) * R * D, x, sizeof(float) * R * D);

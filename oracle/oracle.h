@@ -62,6 +62,9 @@ int or_mul_mat(int wtype, const void * w, int64_t n_out, int64_t n_in,
 /* 1: sum the per-block terms of quantized dots from the last K-block to the first (see oracle.c) */
 void or_set_reverse_block_order(int on);
 void or_set_k_split(int s);
+/* 1: quantized dots summed in ggml's x86 lane order (AVX2 vec_dot / llamafile tinyBLAS), 0: one chain */
+void or_set_ggml_lanes(int on);
+int  or_get_ggml_lanes(void);
 /* 1: with f16 K/V, round q and the softmax weights to f16 too (an f16 matrix-core attention) */
 void or_set_attn_f16(int on);
 /* rounding switches (bits: 1 f16 q, 2 f16 softmax weights, 4 exp2 form, 8 GPU erf polynomial) */
@@ -69,6 +72,8 @@ void or_set_rounding(int bits);
 int  or_get_rounding(void);
 /* teacher forcing of the encoder: block l starts from trace entry l (NULL: off) */
 void or_set_teacher(const float * trace, int64_t n_floats);
+/* teacher forcing only: blocks before l0 are skipped (their trace entries are the teacher's) */
+void or_set_first_block(int l0);
 
 void or_layer_norm(const float * x, int64_t n_rows, int64_t d, const float * w, const float * b,
                    float eps, float * y);

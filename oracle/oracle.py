@@ -70,6 +70,12 @@ def lib() -> C.CDLL:
             getattr(L, fn).restype = None
         L.or_make_qkx2_quants.argtypes = [C.c_int, C.c_int, vp, vp, vp, vp, C.c_float, C.c_float, C.c_int]
         L.or_make_qkx2_quants.restype = C.c_float
+        L.or_set_first_block.argtypes = [C.c_int]
+        L.or_set_first_block.restype = None
+        L.or_set_ggml_lanes.argtypes = [C.c_int]
+        L.or_set_ggml_lanes.restype = None
+        L.or_get_ggml_lanes.argtypes = []
+        L.or_get_ggml_lanes.restype = C.c_int
         L.or_set_reverse_block_order.argtypes = [C.c_int]
         L.or_set_reverse_block_order.restype = None
         L.or_set_k_split.argtypes = [C.c_int]
@@ -297,6 +303,17 @@ def gelu_erf_array(x: np.ndarray) -> np.ndarray:
     return y
 
 
+def set_ggml_lanes(on: bool) -> None:
+    """Sum the quantized dots in ggml's x86 lane order (AVX2 vec_dot / llamafile tiles: eight float lanes
+    of four consecutive products, q4_K mins in four lanes, horizontal sums at the end) instead of one
+    chain per output."""
+    lib().or_set_ggml_lanes(1 if on else 0)
+
+
+def get_ggml_lanes() -> bool:
+    return bool(lib().or_get_ggml_lanes())
+
+
 def set_reverse_block_order(on: bool) -> None:
     lib().or_set_reverse_block_order(1 if on else 0)
 
@@ -325,14 +342,17 @@ def get_rounding() -> int:
     return int(lib().or_get_rounding())
 
 
-def encode_teacher(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, teacher: np.ndarray):
+def encode_teacher(path: str, x: np.ndarray, n_items: int, rows: int, dim: int, teacher: np.ndarray, first_block: int = 0):
     """Oracle forward in which block l starts from teacher[:, l] (teacher [n_items][L + 1][rows][dim],
     e.g. the GPU's residual-stream trace): returns the oracle's trace, whose entry l + 1 is the
-    oracle's block l applied to the teacher's entry l (entry 0 is the oracle's own patch embedding)."""
+    oracle's block l applied to the teacher's entry l (entry 0 is the oracle's own patch embedding).
+    Blocks before first_block are not run (their entries are the teacher's own)."""
     t = np.ascontiguousarray(teacher, dtype=np.float32)
     n_layers = t.shape[1] - 1
     lib().or_set_teacher(_p(t), t.size)
+    lib().or_set_first_block(int(first_block))
     try:
         return _encode(path, np.ascontiguousarray(x, dtype=np.float32), rows, dim, n_layers, True, n_items)
     finally:
         lib().or_set_teacher(None, 0)
+        lib().or_set_first_block(0)

@@ -3,10 +3,12 @@
 For each benchmark model the oracle's forward with the reference's CPU arithmetic is compared with the
 oracle's forward after one change at a time: each of the GPU kernels' roundings (oracle.ROUND_*: f16 q
 before Q.K^T, f16 softmax weights before P.V, the exp2 form of the softmax, the GPU's erf polynomial),
-all four together, and the per-block float sums taken in the reverse K order (another valid ggml
-summation order, no GPU rounding at all). The token cosine (mean and min) and the final residual-stream
-rel_max of each against the reference arithmetic show how far each source alone carries a 12-24
-layer quantized encoder.
+all four together, the per-block float sums taken in the reverse K order (another valid summation
+order, no GPU rounding at all), and the quantized dots summed in ggml's own x86 lane order (AVX2
+vec_dot / llamafile tinyBLAS: eight float lanes of four consecutive products per output, the q4_K mins
+in four lanes, horizontal sums at the end; oracle.set_ggml_lanes). The token cosine (mean and min) and
+the final residual-stream rel_max of each against the reference arithmetic show how far each source
+alone carries a 12-24 layer quantized encoder.
 
     python tests/parity_attribution.py [model ...]     (models: vitl16_q8_0 vitl16_q4_k vitb16_2_1_q8_0 levjepa_vitl16_q8_0)
 """
@@ -30,9 +32,11 @@ FULL = {
     "vitb16_2_1_q8_0": (8, 1, 384, 576),
     "levjepa_vitl16_q8_0": (1, 16, 224, 3137),
 }
-CASES = [("f16 q", O.ROUND_Q16, False), ("f16 softmax weights", O.ROUND_P16, False), ("exp2 softmax", O.ROUND_EXP2, False),
-         ("erf polynomial", O.ROUND_GELU, False), ("all four GPU roundings", O.ROUND_GPU, False),
-         ("reversed block order", 0, True)]
+# (label, rounding bits, reversed block order, ggml lane order)
+CASES = [("f16 q", O.ROUND_Q16, False, False), ("f16 softmax weights", O.ROUND_P16, False, False),
+         ("exp2 softmax", O.ROUND_EXP2, False, False), ("erf polynomial", O.ROUND_GELU, False, False),
+         ("all four GPU roundings", O.ROUND_GPU, False, False), ("reversed block order", 0, True, False),
+         ("ggml x86 lane order", 0, False, True)]
 
 
 def cos_rows(a, b):
@@ -54,12 +58,15 @@ def main(names):
         t0 = time.time()
         ref, _ = O.encode(path, x, n_items, rows, cfg.embed_dim)
         print(f"{name}: reference arithmetic in {time.time() - t0:.1f} s", flush=True)
-        for label, bits, rev in CASES:
-            O.set_rounding(bits); O.set_reverse_block_order(rev)
+        only = os.environ.get("ATTRIBUTION_CASES")
+        for label, bits, rev, lanes in CASES:
+            if only and label not in only.split(","):
+                continue
+            O.set_rounding(bits); O.set_reverse_block_order(rev); O.set_ggml_lanes(lanes)
             try:
                 got, _ = O.encode(path, x, n_items, rows, cfg.embed_dim)
             finally:
-                O.set_rounding(0); O.set_reverse_block_order(False)
+                O.set_rounding(0); O.set_reverse_block_order(False); O.set_ggml_lanes(False)
             c = cos_rows(got, ref)
             rel = float(np.abs(got.astype(np.float64) - ref).max() / np.abs(ref).max())
             print(f"| {name} | {label} | {c.mean():.7f} | {c.min():.6f} | {rel:.2e} |", flush=True)

@@ -62,6 +62,10 @@ def _act_rows(rng, n_rows, n_cols):
     x[3, 0:256:2] = 3.0; x[3, 1:256:2] = -3.0             # equal |x| of both signs: first wins (q8_K)
     x[4, 7] = 1000.0                                      # one outlier
     x[5] = np.round(x[5] * 4) / 4                         # exact halves after scaling are likely
+    # a q8_0 block where x * (127 / amax) lands on the ties 1.5 and 3.5 but x * (1 / d) and x / d one
+    # unit below them (the reciprocal form of ggml's x86 quantize_row_q8_0 decides the codes)
+    x[6, 0:32] = 0.25
+    x[6, 0], x[6, 1], x[6, 2], x[6, 3], x[6, 4] = 47.53804397583008, 0.5614729523658752, 1.3101035356521606, -0.5614729523658752, -1.3101035356521606
     return x
 
 
@@ -127,15 +131,16 @@ def _mul_mat_as_gpu(jlib, oracle, gtype, raw, n_out, n_in, x, bias, split=None):
 C2_SHAPES = [(3072, 1024), (1024, 1024), (4096, 1024), (1024, 4096)]
 
 
-@pytest.mark.parametrize("gtype", [gguf.GGML_Q8_0, gguf.GGML_Q4_0, gguf.GGML_Q4_K, gguf.GGML_F16])
+@pytest.mark.parametrize("gtype,M", [(gguf.GGML_Q8_0, 256), (gguf.GGML_Q4_0, 256), (gguf.GGML_Q4_K, 256), (gguf.GGML_F16, 256),
+                                     (gguf.GGML_Q8_0, 2048), (gguf.GGML_Q4_0, 2048), (gguf.GGML_Q4_K, 2048)])
 @pytest.mark.parametrize("shape", C2_SHAPES)
-def test_matmul_vs_oracle(jlib, oracle, gtype, shape):
-    """GEMM microbench shapes (ViT-L qkv / proj / fc1 / fc2). q8_0, q4_0 and q4_K: bit-exact with the
-    oracle's ggml vec_dot restatement (same exact block sums, same fma per block in K order, q4_K's
-    mins in their own accumulator); f16 within f32 summation-order rounding."""
+def test_matmul_vs_oracle(jlib, oracle, gtype, M, shape):
+    """GEMM microbench shapes (ViT-L qkv / proj / fc1 / fc2), at 256 tokens and, for the block-quantized
+    types, at the configured 2048 tokens (the tiles and workgroup counts the encoder runs). q8_0, q4_0
+    and q4_K: bit-exact with the oracle's ggml vec_dot restatement (same exact block sums, same fma per
+    block in K order, q4_K's mins in their own accumulator); f16 within f32 summation-order rounding."""
     n_out, n_in = shape
-    rng = np.random.default_rng(n_out * 7 + n_in + gtype)
-    M = 256
+    rng = np.random.default_rng(n_out * 7 + n_in + gtype + M)
     w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
     x = rng.standard_normal((M, n_in)).astype(np.float32)
     bias = (rng.standard_normal(n_out) * 0.02).astype(np.float32)
@@ -580,6 +585,23 @@ def test_attention_fused_q8_0_equals_separate_quantizer(jlib, oracle, n_items, n
     assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, 64, None, None, 0, 0, gguf.GGML_Q8_0, oq.data_ptr()) == 0
     want = oracle.quantize_act(oracle.OR_Q8_0, host(o32))
     np.testing.assert_array_equal(host(oq), want.reshape(host(oq).shape))
+
+
+@pytest.mark.parametrize("n_items,n_tok,H,hd", [(1, 197, 6, 64), (2, 256, 4, 64), (1, 65, 2, 32)])
+def test_attention_f16_output_equals_rounded_f32(jlib, n_items, n_tok, H, hd):
+    """The attention epilogue's f16 output (the input of an f16 out-projection) is the f32 output
+    rounded to nearest, what the separate conversion would give."""
+    rng = np.random.default_rng(n_tok * 5 + H)
+    D = H * hd
+    qkv = (rng.standard_normal((n_items * n_tok, 3 * D)) * 1.5).astype(np.float32)
+    dq = dev(qkv)
+    o32 = torch.zeros((n_items * n_tok, D), dtype=torch.float32, device="cuda")
+    o16 = torch.zeros((n_items * n_tok, D), dtype=torch.float16, device="cuda")
+    L = jlib.lib()
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, hd, None, None, 0, 0, 0, o32.data_ptr()) == 0
+    assert L.jepa_amd_attention(0, dq.data_ptr(), n_items, n_tok, H, hd, None, None, 0, 0, gguf.GGML_F16, o16.data_ptr()) == 0
+    want = host(o32).astype(np.float16)
+    np.testing.assert_array_equal(host(o16).view(np.uint16), want.view(np.uint16))
 
 
 # ------------------------------------------------------------------------------------------------ ingest

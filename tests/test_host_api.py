@@ -147,3 +147,61 @@ def test_reference_jepa_bench_links_unchanged(L, tmp_path):
     assert r.returncode == 0, r.stderr[-3000:]
     r = subprocess.run([str(exe), "--help"], capture_output=True, text=True, timeout=60)
     assert "usage" in (r.stdout + r.stderr).lower()
+
+
+@pytest.mark.skipif(not os.path.isfile(os.path.join(REFERENCE_TOOLS, "jepa-bench.cpp")) or shutil.which("g++") is None,
+                    reason="the reference tree (tools/jepa-bench.cpp) is not present")
+@pytest.mark.parametrize("shape", [(1, 1, 224, 224, 1234), (2, 3, 16, 24, 0), (1, 2, 32, 32, 987654321)])
+def test_synthetic_input_equals_reference_make_input(L, tmp_path, shape):
+    """jepa_amd.inputs.make_input against the reference's own make_input (tools/jepa-bench.cpp:124-149),
+    compiled from the reference file as it lies (its main renamed by the harness) and linked against
+    libjepa.so for jepa_preprocess_default_params (NULL model: the ImageNet defaults both use): every
+    float bit for bit, including seed 0 (the generator's fixed replacement seed)."""
+    B, T, H, W, seed = shape
+    src = tmp_path / "make_input_harness.cpp"
+    src.write_text(
+        "#define main jepa_bench_main\n"
+        f'#include "{os.path.join(REFERENCE_TOOLS, "jepa-bench.cpp")}"\n'
+        "#undef main\n"
+        "int main(int argc, char ** argv) {\n"
+        "    const std::vector<float> x = make_input(nullptr, atoi(argv[1]), atoi(argv[2]), atoi(argv[3]), atoi(argv[4]),\n"
+        "                                            strtoull(argv[5], nullptr, 10));\n"
+        "    return fwrite(x.data(), sizeof(float), x.size(), stdout) == x.size() ? 0 : 1;\n"
+        "}\n")
+    exe = tmp_path / "make_input_harness"
+    lib_dir = os.path.join(ROOT, "jepa.cpp_amd")
+    cmd = ["g++", "-std=c++17", "-O1", "-w", "-I", os.path.join(ROOT, "include"), "-I", REFERENCE_TOOLS, str(src),
+           "-L", lib_dir, "-ljepa", f"-Wl,-rpath,{lib_dir}", "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    r = subprocess.run([str(exe), str(B), str(T), str(H), str(W), str(seed)], capture_output=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    want = np.frombuffer(r.stdout, dtype=np.float32).reshape(B, 3, T, H, W)
+    from jepa_amd import inputs
+    got = inputs.make_input(B, T, H, W, seed=seed)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+REFERENCE_ROOT = os.path.dirname(REFERENCE_TOOLS)
+
+
+@pytest.mark.skipif(not os.path.isfile(os.path.join(REFERENCE_TOOLS, "jepa-embed.cpp")) or shutil.which("g++") is None,
+                    reason="the reference tree (tools/jepa-embed.cpp) is not present")
+@pytest.mark.parametrize("tool", ["jepa-embed", "jepa-classify"])
+def test_reference_embed_tools_link_unchanged(L, tmp_path, tool):
+    """tools/jepa-embed.cpp and tools/jepa-classify.cpp of the reference, each with tools/video-decode.cpp
+    (the reference's own tool recipe, CMakeLists.txt:90-102: include paths src/ and third_party/ for
+    npy.h and the stb headers), compiled as they lie against include/jepa.h of this repository and
+    linked against libjepa.so with --no-undefined: every entry point they call (preprocessing, image
+    loading, pooling, the head, device queries) resolves to this library, and the program runs its
+    usage text (no model, no GPU)."""
+    exe = tmp_path / tool
+    lib_dir = os.path.join(ROOT, "jepa.cpp_amd")
+    cmd = ["g++", "-std=c++17", "-O1", "-w", "-I", os.path.join(ROOT, "include"), "-I", REFERENCE_TOOLS,
+           "-I", os.path.join(REFERENCE_ROOT, "src"), "-I", os.path.join(REFERENCE_ROOT, "third_party"),
+           os.path.join(REFERENCE_TOOLS, f"{tool}.cpp"), os.path.join(REFERENCE_TOOLS, "video-decode.cpp"),
+           "-L", lib_dir, "-ljepa", f"-Wl,-rpath,{lib_dir}", "-Wl,--no-undefined", "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    r = subprocess.run([str(exe), "--help"], capture_output=True, text=True, timeout=60)
+    assert "usage" in (r.stdout + r.stderr).lower()

@@ -260,6 +260,34 @@ def test_q8_0_activation_rounds_half_to_even():
     np.testing.assert_array_equal(q[1:9], [0, 2, 2, 0, -2, -2, 126, -4])
 
 
+def test_q8_0_activation_reciprocal_form():
+    """ggml's x86 quantize_row_q8_0 (AVX2 path, ggml 36da5713) multiplies by id = 127 / amax, computed
+    once per block in float32; the _ref form takes id = 1 / d with d = amax / 127, and a third reading
+    divides x / d. At amax = 47.538044 the two reciprocals differ in the last bit (2.6715446 against
+    2.6715443), and the x below sit where that decides the code: x * (127 / amax) rounds to exactly
+    1.5 and 3.5 in float32 (ties, half-even: 2 and 4), while x * (1 / d) and x / d land one unit below
+    (codes 1 and 3). The oracle must give the 127 / amax codes."""
+    from fractions import Fraction as Fr
+    f = np.float32
+    amax = f(47.53804397583008)
+    xs = [f(0.5614729523658752), f(1.3101035356521606)]
+    id_a = f(127) / amax
+    d = amax / f(127)
+    id_b = f(1) / d
+    assert id_a != id_b
+    # the products, exactly: float32 rounding of the exact rational products
+    for x, tie in zip(xs, (Fr(3, 2), Fr(7, 2))):
+        assert Fr(float(f(x * id_a))) == tie
+        assert Fr(float(f(x * id_b))) < tie and Fr(float(f(x / d))) < tie
+    x = np.zeros(32, np.float32)
+    x[0] = amax
+    x[1], x[2], x[3], x[4] = xs[0], xs[1], -xs[0], -xs[1]
+    raw = O.quantize_act(O.OR_Q8_0, x)
+    q = raw[2:].view(np.int8)
+    assert raw[:2].copy().view(np.float16)[0] == np.float16(d)
+    np.testing.assert_array_equal(q[:5], [127, 2, 4, -2, -4])
+
+
 def test_q8_0_activation_scale_and_zero_block():
     rng = np.random.default_rng(5)
     x = rng.standard_normal(64).astype(np.float32)
@@ -362,6 +390,136 @@ def test_mul_mat_equals_vec_dot(gtype):
     for m in range(M):
         for o in range(n_out):
             want = np.float32(np.float32(O.vec_dot(gtype, n_in, raw[o], act[m])) + bias[o])
+            assert y[m, o].view(np.uint32) == want.view(np.uint32), (m, o)
+
+
+# ------------------------------------------------------------------------------ ggml's x86 lane order
+@pytest.fixture
+def lanes():
+    O.set_ggml_lanes(True)
+    yield
+    O.set_ggml_lanes(False)
+
+
+def _lane_dot(gtype, w, x, no_mins=False):
+    wr = O.quantize_weight(gtype, w)
+    if no_mins:                       # q4_K: dmin = 0 in every super-block, so the mins term is zero
+        wr.reshape(-1, 144)[:, 2:4] = 0
+    ar = O.quantize_act(O.OR_Q8_K if gtype == O.OR_Q4_K else O.OR_Q8_0, x)
+    return np.float32(O.vec_dot(gtype, w.size, wr, ar))
+
+
+@pytest.mark.parametrize("gtype", [O.OR_Q8_0, O.OR_Q4_0, O.OR_Q4_K])
+def test_ggml_lanes_one_lane_is_the_block_chain(gtype):
+    """With the activations zero outside the four elements 4l..4l+3 of every 32-element group, only
+    lane l of ggml's eight is ever non-zero: its per-block fma chain is the whole dot and the
+    horizontal sum adds zeros, so the lane order equals the one-chain order bit for bit, for every l
+    (q4_K with dmin set to zero in every super-block, so the mins lanes vanish too). This pins which
+    elements share a lane (four consecutive ones) and that a lane takes one fma per block."""
+    rng = np.random.default_rng(30 + gtype)
+    n = 1024
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    nm = gtype == O.OR_Q4_K
+    for l in range(8):
+        x = rng.standard_normal(n).astype(np.float32)
+        keep = np.zeros(32, bool)
+        keep[4 * l:4 * l + 4] = True
+        x[~np.tile(keep, n // 32)] = 0.0
+        O.set_ggml_lanes(False)
+        chain = _lane_dot(gtype, w, x, nm)
+        O.set_ggml_lanes(True)
+        try:
+            lane = _lane_dot(gtype, w, x, nm)
+        finally:
+            O.set_ggml_lanes(False)
+        assert lane.view(np.uint32) == chain.view(np.uint32), (l, lane, chain)
+
+
+def _move_groups(v, perm):
+    """element group g (elements 4g..4g+3 of every 32-element block) moved to group perm[g]"""
+    b = v.reshape(-1, 8, 4)
+    out = np.empty_like(b)
+    out[:, list(perm), :] = b
+    return out.reshape(v.shape)
+
+
+@pytest.mark.parametrize("gtype", [O.OR_Q8_0, O.OR_Q4_0])
+def test_ggml_lanes_horizontal_sum_symmetries(lanes, gtype):
+    """hsum_float_8 = ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)) is unchanged when lanes are
+    exchanged by the symmetries of that tree (0<->4; the pair (0,4)<->(2,6); the halves
+    (0,4,2,6)<->(1,5,3,7)). Moving the element groups of both operands that way moves whole lanes, so
+    the dot must come out bit-identical; the one-chain order sees only exact integer block sums and is
+    unchanged by any move. Exchanging lanes 0 and 1 alone is not a symmetry of the tree and changes
+    the value on these data, which shows the lanes are really summed apart."""
+    rng = np.random.default_rng(40 + gtype)
+    n = 4096
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    x = (rng.standard_normal(n) * np.repeat(rng.uniform(0.1, 10.0, n // 32), 32)).astype(np.float32)
+    base = _lane_dot(gtype, w, x)
+    # (the block quantizers are permutation-equivariant within a block: the scale comes from the
+    # block's largest magnitude, each code from its own value)
+    sym = [(4, 1, 2, 3, 0, 5, 6, 7), (2, 1, 0, 3, 6, 5, 4, 7), (1, 0, 3, 2, 5, 4, 7, 6)]
+    for perm in sym:
+        got = _lane_dot(gtype, _move_groups(w, perm), _move_groups(x, perm))
+        assert got.view(np.uint32) == base.view(np.uint32), (perm, got, base)
+    swap01 = (1, 0, 2, 3, 4, 5, 6, 7)
+    other = _lane_dot(gtype, _move_groups(w, swap01), _move_groups(x, swap01))
+    assert other != base
+
+
+def test_ggml_lanes_q4_K_against_simd_restatement(lanes):
+    """q4_K x q8_K in ggml's AVX2 form, restated with numpy arrays shaped as the registers: per
+    super-block an [8] int32 register of sc_j * (four consecutive products) summed over sub-blocks,
+    acc[8] += (y.d * x.d) * sumi; a [4] register of m_2k q8s_2k + m_2k+1 q8s_2k+1 with q8s the
+    pairwise-added bsums, acc_m[4] += (-y.d * x.dmin) * prod; then hsum_float_8(acc) + the two-step
+    sum of acc_m. Weights of both signs (non-zero mins) and activations of varying block scale."""
+    rng = np.random.default_rng(50)
+    n = 2048
+    f = np.float32
+    for trial in range(4):
+        w = (rng.standard_normal(n) * 0.05 + 0.01 * trial).astype(np.float32)
+        x = (rng.standard_normal(n) * np.repeat(rng.uniform(0.2, 5.0, n // 256), 256)).astype(np.float32)
+        wr = O.quantize_weight(O.OR_Q4_K, w)
+        ar = O.quantize_act(O.OR_Q8_K, x)
+        got = np.float32(O.vec_dot(O.OR_Q4_K, n, wr, ar))
+        acc = np.zeros(8, np.float32)
+        accm = np.zeros(4, np.float32)
+        for sb in range(n // 256):
+            blk = wr[sb * 144:(sb + 1) * 144]
+            a = ar[sb * 292:(sb + 1) * 292]
+            d = f(blk[0:2].copy().view(np.float16)[0]); dmin = f(blk[2:4].copy().view(np.float16)[0])
+            sc, m = gguf.q4k_scales_mins(blk[None, 4:16])
+            qs = blk[16:]
+            q8 = a[4:260].view(np.int8).astype(np.int64).reshape(8, 32)
+            yd = a[:4].copy().view(np.float32)[0]
+            bs = a[260:].copy().view(np.int16).astype(np.int64)
+            q4 = np.stack([(qs[32 * (j // 2):32 * (j // 2) + 32] & 0xF) if j % 2 == 0 else (qs[32 * (j // 2):32 * (j // 2) + 32] >> 4)
+                           for j in range(8)]).astype(np.int64)
+            sumi = ((q4 * q8).reshape(8, 8, 4).sum(2) * sc[0].astype(np.int64)[:, None]).sum(0)     # [8] lanes
+            q8s = bs.reshape(8, 2).sum(1)
+            prod = (m[0].astype(np.int64) * q8s).reshape(4, 2).sum(1)                            # [4] lanes
+            dd, dm = f(yd * d), f(-yd * dmin)
+            acc = np.array([_f32_fma(f(v), dd, c) for v, c in zip(sumi, acc)], np.float32)
+            accm = np.array([_f32_fma(f(v), dm, c) for v, c in zip(prod, accm)], np.float32)
+        h8 = f(f(f(acc[0] + acc[4]) + f(acc[2] + acc[6])) + f(f(acc[1] + acc[5]) + f(acc[3] + acc[7])))
+        h4 = f(f(accm[0] + accm[2]) + f(accm[1] + accm[3]))
+        want = f(h8 + h4)
+        assert got.view(np.uint32) == want.view(np.uint32), (trial, got, want)
+
+
+@pytest.mark.parametrize("gtype", [O.OR_Q8_0, O.OR_Q4_K])
+def test_ggml_lanes_mul_mat_equals_vec_dot(lanes, gtype):
+    """The pre-expanded mul_mat path and vec_dot agree in the lane order too."""
+    rng = np.random.default_rng(60 + gtype)
+    n_out, n_in, M = 6, 512, 4
+    w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    raw = O.quantize_weight(gtype, w)
+    y = O.mul_mat(gtype, raw, n_out, n_in, x, None)
+    for m in range(M):
+        act = O.quantize_act(O.OR_Q8_K if gtype == O.OR_Q4_K else O.OR_Q8_0, x[m])
+        for o in range(n_out):
+            want = np.float32(O.vec_dot(gtype, n_in, raw[o], act))
             assert y[m, o].view(np.uint32) == want.view(np.uint32), (m, o)
 
 
