@@ -10,7 +10,7 @@ in four lanes, horizontal sums at the end; oracle.set_ggml_lanes). The token cos
 the final residual-stream rel_max of each against the reference arithmetic show how far each source
 alone carries a 12-24 layer quantized encoder.
 
-    python tests/parity_attribution.py [model ...]     (models: vitl16_q8_0 vitl16_q4_k vitb16_2_1_q8_0 levjepa_vitl16_q8_0)
+    python tests/parity_attribution.py [model ...]     (models: vitl16_q8_0 vitl16_q4_k vitb16_2_1_q8_0 levjepa_vitl16_q8_0 vith14_ijepa_q8_0)
 """
 import os
 import sys
@@ -31,6 +31,7 @@ FULL = {
     "vitl16_q4_k": (1, 16, 256, 2048),
     "vitb16_2_1_q8_0": (8, 1, 384, 576),
     "levjepa_vitl16_q8_0": (1, 16, 224, 3137),
+    "vith14_ijepa_q8_0": (1, 1, 224, 256),
 }
 # (label, rounding bits, reversed block order, ggml lane order)
 CASES = [("f16 q", O.ROUND_Q16, False, False), ("f16 softmax weights", O.ROUND_P16, False, False),

@@ -33,15 +33,18 @@ FULL = {
     "vith14_ijepa_q8_0": (1, 1, 224, 256),
 }
 
-# End-to-end cosine below the fixed bar, with the oracle's own order-to-order distance that shows why
-# (measured: the oracle against itself with its per-block sums reversed; see the attribution table).
+# End-to-end cosine below the fixed bar: (floor, why). The floor sits just under the measured cosine, so a
+# regression still fails; the reason quotes the oracle against itself in ggml's own x86 summation order
+# (AVX2 vec_dot / llamafile tiles, oracle.set_ggml_lanes) and in reversed block order, measured on the CPU
+# (tests/parity_attribution.py): two valid orders of the reference arithmetic already differ by that much.
 KNOWN_E2E = {
-    "vitl16_q4_k": "q8_K activations over 24 layers: the oracle against itself in reversed summation order "
-                   "reaches only cosine 0.99983, below 0.9999",
-    "levjepa_vitl16_q8_0": "3137 rows x 24 layers of q8_0 activations: the oracle against itself in reversed "
-                           "summation order reaches cosine 0.99990, at the bar",
-    "vith14_ijepa_q8_0": "32 layers of q8_0 activations: the oracle against itself in reversed summation order "
-                         "reaches only cosine 0.99988, below 0.9999",
+    "vitl16_q4_k": (0.9997, "q8_K activations over 24 layers: the oracle in ggml's x86 lane order against the oracle's "
+                            "one-chain order reaches only cosine 0.99983 (reversed block order 0.99983), below 0.9999"),
+    "levjepa_vitl16_q8_0": (0.99985, "3137 rows x 24 layers of q8_0 activations: the oracle in ggml's x86 lane order "
+                                     "against its one-chain order reaches cosine 0.99990 (reversed block order 0.99990), "
+                                     "at the bar"),
+    "vith14_ijepa_q8_0": (0.99980, "32 layers of q8_0 activations: the oracle in ggml's x86 lane order against its "
+                                   "one-chain order reaches cosine 0.99988 (reversed block order 0.99988), below 0.9999"),
 }
 
 _cache = {}
@@ -71,16 +74,24 @@ def _run(jlib, oracle, models_dir, name):
     got, gtr = ctx.encode_trace(x, n_items, rows)
     print(f"{name}: GPU done", flush=True)
     prev = oracle.get_rounding()
+    want_lanes = None
     try:
         oracle.set_rounding(0)
         want, wtr = oracle.encode(path, x, n_items, rows, m.dim, n_layers=m.n_layer, trace=True)
         _, ttr = oracle.encode_teacher(path, x, n_items, rows, m.dim, gtr)
+        if name in KNOWN_E2E:
+            # the same arithmetic with the quantized dots in ggml's own x86 lane order
+            oracle.set_ggml_lanes(True)
+            try:
+                want_lanes, _ = oracle.encode(path, x, n_items, rows, m.dim)
+            finally:
+                oracle.set_ggml_lanes(False)
         oracle.set_rounding(oracle.ROUND_GPU)
         _, mtr = oracle.encode_teacher(path, x, n_items, rows, m.dim, gtr)
     finally:
         oracle.set_rounding(prev)
     print(f"{name}: oracle done", flush=True)
-    r = dict(model=m, got=got, gtr=gtr, want=want, wtr=wtr, ttr=ttr, mtr=mtr, rows=rows, n_items=n_items)
+    r = dict(model=m, got=got, gtr=gtr, want=want, wtr=wtr, ttr=ttr, mtr=mtr, rows=rows, n_items=n_items, want_lanes=want_lanes)
     _cache.clear()          # one full-size model's traces at a time
     _cache[name] = r
     return r
@@ -93,8 +104,18 @@ def test_end_to_end(jlib, oracle, models_dir, name):
     rl = [rel_max(r["gtr"][:, l], r["wtr"][:, l]) for l in range(r["gtr"].shape[1])]
     print(f"{name}: end-to-end token cosine mean {c.mean():.7f} min {c.min():.6f}; residual-stream rel_max "
           f"by layer: first {rl[1]:.2e}, last {rl[-1]:.2e}, max {max(rl):.2e}")
-    if c.mean() < 0.9999 and name in KNOWN_E2E:
-        pytest.xfail(f"cosine {c.mean():.6f}: {KNOWN_E2E[name]}")
+    if r["want_lanes"] is not None:
+        cl = cos_rows(r["got"], r["want_lanes"])
+        co = cos_rows(r["want"], r["want_lanes"])
+        print(f"{name}: against the oracle in ggml's x86 lane order: GPU cosine mean {cl.mean():.7f} min {cl.min():.6f}; "
+              f"oracle one-chain order against it {co.mean():.7f}")
+        if cl.mean() >= 0.9999:
+            return          # within the bar of ggml's own summation order
+    if name in KNOWN_E2E:
+        floor, why = KNOWN_E2E[name]
+        assert c.mean() >= floor, (c.mean(), floor)
+        if c.mean() < 0.9999:
+            pytest.xfail(f"cosine {c.mean():.6f}: {why}")
     assert c.mean() >= 0.9999, (c.mean(), c.min())
 
 
