@@ -174,6 +174,27 @@ def time_extra(name, steps):
     return None
 
 
+def step_ceiling():
+    """ns per 32x32x32 step of one SIMD for the q8_0 GEMM's inner step from registers alone
+    (jepa_amd_gemm_step_probe), and the int8 rate it allows over all SIMDs."""
+    import ctypes as C
+    from jepa_amd import _lib
+    L = _lib.lib()
+    simds = 4 * 256
+    out = {}
+    names = {0: "whole_step", 1: "mfma_half_only", 2: "valu_half_only", 3: "halves_in_separate_waves"}
+    for wps in (2, 4):
+        for mode in (0, 1, 2, 3):
+            ns = C.c_double(0)
+            if L.jepa_amd_gemm_step_probe(0, mode, wps, 20000, C.byref(ns)) != 0 or ns.value <= 0:
+                log(f"bench: step probe mode {mode} failed: {_lib.error_text()}")
+                return None
+            tops = 65536.0 / (ns.value * 1e-9) * simds / 1e12
+            out[f"{names[mode]}_{wps}_waves_per_simd"] = {"ns_per_step": round(ns.value, 2), "tops": round(tops, 1),
+                                                         "frac_of_int8_peak": round(tops / PEAK_INT8_TOPS, 4)}
+    return out
+
+
 def host_cpu():
     """Model name, sockets and physical cores of this host (lscpu), for the CPU baseline's record."""
     import subprocess
@@ -268,6 +289,15 @@ def main():
                 "kernel": "gemm_q8 (q8_0 x q8_0 GEMMs: qkv, out, fc1, fc2)", "avg_launch_ms": round(gq["avg_ms"], 5),
                 "ops_per_launch": ops_per_launch, "peak_note": "int8 dense 5.0 POP/s; block sums on v_mfma_i32_32x32x32_i8, per-32-block f32 scale epilogue on the VALU"}
     extra = {}
+    # the ceiling of the q8_0 GEMM's arithmetic on this chip: its inner step (int8 MFMA block sum, f16
+    # scale-product MFMA, 16 conversions + 16 fmas) timed from registers alone, whole step per wave
+    # (the kernels' form) and split into MFMA-only and VALU-only waves (overlap across waves)
+    ceil = step_ceiling()
+    if ceil and roof:
+        best = ceil["whole_step_2_waves_per_simd"]
+        roof["step_ceiling_tops"] = best["tops"]
+        roof["frac_of_step_ceiling"] = round(roof["achieved"] / best["tops"], 4)
+        extra["gemm_step_ceiling"] = ceil
     att = k.get("attention")
     if att:
         extra["attention_roofline"] = {"bound": "mfma", "achieved": round(ATTN_FLOP / (att["per_step_ms"] * 1e-3) / 1e12, 2),

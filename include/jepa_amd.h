@@ -149,6 +149,14 @@ int jepa_amd_mfma_probe(int device, const float * a, const float * b, float * d)
 int jepa_amd_rope_tables(int head_dim, int grid_t, int grid_h, int grid_w, int variant, int interpolate, int train_h, int train_w,
                          float theta, const int32_t * ids, int64_t n_rows, int signed_sin, float * cos_out, float * sin_out);
 
+/* Throughput ceiling of the q8_0 GEMM's inner step from registers alone (no memory, no barriers), one
+ * workgroup per CU with waves_per_simd (1-4) waves on each SIMD: per 32x32x32 block and MFMA tile one
+ * int8 MFMA (the block sum), one f16 MFMA (the scale products) and 32 VALU ops (16 conversions, 16
+ * fmas). mode 0: the whole step in each wave (the kernels' form); 1: the two MFMAs alone; 2: the VALU
+ * ops alone; 3: even waves the MFMA half, odd waves the VALU half. *ns_per_step: nanoseconds of one SIMD
+ * per whole step (65536 int8 ops). No counterpart in the reference: a measurement hook. */
+int jepa_amd_gemm_step_probe(int device, int mode, int waves_per_simd, int iters, double * ns_per_step);
+
 /* Copy of n float32 values between device buffers (a plain copy kernel, for counter calibration). */
 int jepa_amd_copy(int device, const float * src_dev, float * dst_dev, int64_t n, int reps, double * ms);
 

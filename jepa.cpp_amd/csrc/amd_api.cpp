@@ -350,6 +350,32 @@ extern "C" int jepa_amd_mfma_probe(int device, const float * a, const float * b,
     return hipMemcpy(dd, dc, 32 * 32 * 4, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
 }
 
+extern "C" int jepa_amd_gemm_step_probe(int device, int mode, int waves_per_simd, int iters, double * ns_per_step) {
+    if (mode < 0 || mode > 3 || waves_per_simd < 1 || waves_per_simd > 4 || iters < 1 || iters > 1000000 || !ns_per_step) return -1;
+    dev_scope d(device);
+    if (!d.ok) return -1;
+    int dev = 0, n_cu = 0;
+    hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0) n_cu = 256;
+    float * sink = (float *) d.alloc((size_t) n_cu * 256 * waves_per_simd * 4);
+    if (!sink) return -1;
+    launch_step_probe(mode, waves_per_simd, iters, n_cu, sink, d.s);   // warm
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0); hipEventCreate(&e1);
+    hipEventRecord(e0, d.s);
+    launch_step_probe(mode, waves_per_simd, iters, n_cu, sink, d.s);
+    hipEventRecord(e1, d.s);
+    const int rc = d.finish();
+    float ms = 0;
+    hipEventElapsedTime(&ms, e0, e1);
+    hipEventDestroy(e0); hipEventDestroy(e1);
+    // one workgroup per CU, waves_per_simd waves on each of its 4 SIMDs, 2 * iters (half or whole) steps each;
+    // a whole step is counted once per wave of modes 0-2 and once per pair of waves of mode 3
+    const double steps_per_simd = 2.0 * iters * waves_per_simd / (mode == 3 ? 2.0 : 1.0);
+    *ns_per_step = (double) ms * 1e6 / steps_per_simd;
+    return rc;
+}
+
 extern "C" int jepa_amd_copy(int device, const float * src, float * dst, int64_t n, int reps, double * ms) {
     if (!src || !dst || n <= 0) return -1;
     dev_scope d(device);

@@ -125,3 +125,5 @@ void launch_copy_f32(const float * src, float * dst, int64_t n, hipStream_t s);
 // MFMA layout probe (test hook): D = A * B for 32x32x16 f16 with A [32][16], B [16][32] row-major f32
 // inputs; writes D [32][32] using the register layout the GEMM epilogues assume.
 void launch_mfma_probe(const float * a, const float * b, float * d, hipStream_t s);
+// the q8_0 GEMM step from registers alone (jepa_amd_gemm_step_probe); sink: n_wg * 256 * waves_per_simd floats
+void launch_step_probe(int mode, int waves_per_simd, int iters, int n_wg, float * sink, hipStream_t s);

@@ -416,6 +416,88 @@ void launch_copy_f32(const float * src, float * dst, int64_t n, hipStream_t s) {
     k_copy_f32<<<nblk((n + 3) / 4, 256), 256, 0, s>>>(src, dst, n);
 }
 
+// ------------------------------------------------------------------------------------------------
+// The throughput ceiling of the q8_0 GEMM's inner step, measured from registers alone (no memory, no
+// barriers): per 32x32x32 block and MFMA tile, one v_mfma_i32_32x32x32_i8 (exact block sum S), one
+// v_mfma_f32_32x32x8_f16 (scale products dw * da) and 32 VALU ops (16 conversions of S, 16 fmas into
+// the f32 accumulators). mode 0: the whole step in every wave, the MFMAs of step u+1 issued before the
+// VALU work of step u (the kernels' pipeline); 1: the two MFMAs alone; 2: the 32 VALU ops alone;
+// 3: the step split over waves, even waves running the MFMA half and odd waves the VALU half (the
+// bound if the matrix unit overlapped VALU work of other waves; the waves of a SIMD alternate by their
+// slot on it). Each wave runs 2 * iters half or whole
+// steps; `sink` keeps the results live.
+// ------------------------------------------------------------------------------------------------
+typedef int i4v_ __attribute__((ext_vector_type(4)));
+typedef int i16v_ __attribute__((ext_vector_type(16)));
+template <int MODE>
+__global__ __launch_bounds__(1024) void k_step_probe(float * sink, int iters) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    i4v_ A0 = {lane, lane * 3, lane * 5, lane * 7}, B0 = {lane + 1, lane * 2, lane * 9, lane * 11};
+    i4v_ A1 = A0 + 1, B1 = B0 + 2;
+    h4 sa, sb;
+    for (int i = 0; i < 4; i++) { sa[i] = (_Float16) (0.001f * (lane + i)); sb[i] = (_Float16) (0.002f * (lane - i)); }
+    f16v acc = {}, C[2] = {};
+    i16v_ S[2] = {}, iv = {};
+    for (int r = 0; r < 16; r++) iv[r] = (lane + r) & 63;
+    float y[16];
+    for (int r = 0; r < 16; r++) y[r] = 1.0f + r * 1e-3f;
+    // mode 3 pairs the waves of each SIMD by their slot on it (HW_ID bits 3:0), whatever order the
+    // workgroup's waves were dealt to the SIMDs in
+    (void) wave;
+    const int slot = MODE == 3 ? (int) (__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 4) & 15) : 0;
+    const bool mfma_wave = MODE == 3 ? (slot & 1) == 0 : MODE != 2;
+    const bool valu_wave = MODE == 3 ? (slot & 1) == 1 : MODE != 1;
+    if (MODE == 0) { S[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, i16v_{}, 0, 0, 0); C[0] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sb, f16v{}, 0, 0, 0); }
+    // one loop per role (a role branch inside the loop body serialises the MFMAs)
+    if (MODE == 0) {
+        for (int it = 0; it < iters; it++) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                asm volatile("" : "+v"(A0), "+v"(B0), "+v"(A1), "+v"(B1), "+v"(sa), "+v"(sb));
+                S[u ^ 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(u ? A0 : A1, u ? B0 : B1, i16v_{}, 0, 0, 0);
+                C[u ^ 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sb, f16v{}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[r] = fmaf((float) S[u][r], C[u][r], acc[r]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else if (mfma_wave) {
+        for (int it = 0; it < iters; it++) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                asm volatile("" : "+v"(A0), "+v"(B0), "+v"(A1), "+v"(B1), "+v"(sa), "+v"(sb));
+                S[u ^ 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(u ? A0 : A1, u ? B0 : B1, i16v_{}, 0, 0, 0);
+                C[u ^ 1] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sb, f16v{}, 0, 0, 0);
+                asm volatile("" :: "v"(S[u]), "v"(C[u]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else if (valu_wave) {
+        for (int it = 0; it < iters; it++) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                asm volatile("" : "+v"(iv));
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[r] = fmaf((float) iv[r], y[r], acc[r]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    float t = 0.0f;
+    for (int r = 0; r < 16; r++) t += acc[r] + (float) S[0][r] + C[0][r];
+    sink[(size_t) blockIdx.x * blockDim.x + threadIdx.x] = t;
+}
+
+void launch_step_probe(int mode, int waves_per_simd, int iters, int n_wg, float * sink, hipStream_t s) {
+    const dim3 block((unsigned) (256 * waves_per_simd));
+    switch (mode) {
+        case 0: k_step_probe<0><<<n_wg, block, 0, s>>>(sink, iters); break;
+        case 1: k_step_probe<1><<<n_wg, block, 0, s>>>(sink, iters); break;
+        case 2: k_step_probe<2><<<n_wg, block, 0, s>>>(sink, iters); break;
+        default: k_step_probe<3><<<n_wg, block, 0, s>>>(sink, iters); break;
+    }
+}
+
 void launch_mfma_probe(const float * a, const float * b, float * d, hipStream_t s) {
     k_mfma_probe<<<1, 64, 0, s>>>(a, b, d);
 }

@@ -124,6 +124,7 @@ def lib() -> C.CDLL:
         "jepa_amd_attention": (C.c_int, [C.c_int, vp, i64, i64, C.c_int, C.c_int, vp, vp, C.c_int, i64, C.c_int, vp]),
         "jepa_amd_mfma_probe": (C.c_int, [C.c_int, vp, vp, vp]),
         "jepa_amd_copy": (C.c_int, [C.c_int, vp, vp, i64, C.c_int, C.POINTER(C.c_double)]),
+        "jepa_amd_gemm_step_probe": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]),
         "jepa_amd_gemm_tile": (C.c_int, [C.c_int]),
         "jepa_amd_gemm_split": (C.c_int, [C.c_int]),
         "jepa_amd_gemm_split_of": (C.c_int, [C.c_int, i64, i64]),

@@ -604,6 +604,23 @@ def test_attention_f16_output_equals_rounded_f32(jlib, n_items, n_tok, H, hd):
     np.testing.assert_array_equal(host(o16).view(np.uint16), want.view(np.uint16))
 
 
+def test_gemm_step_probe(jlib):
+    """The register-only step probe (the q8_0 GEMM's ceiling measurement) runs for every mode and
+    occupancy; each half alone is faster than the whole step, and bad arguments are refused."""
+    L = jlib.lib()
+    res = {}
+    for wps in (2, 4):
+        for mode in range(4):
+            ns = C.c_double(0)
+            assert L.jepa_amd_gemm_step_probe(0, mode, wps, 2000, C.byref(ns)) == 0, jlib.error_text()
+            assert 1.0 < ns.value < 10000.0, (mode, wps, ns.value)
+            res[mode, wps] = ns.value
+        assert res[1, wps] < res[0, wps] and res[2, wps] < res[0, wps], res
+    ns = C.c_double(0)
+    assert L.jepa_amd_gemm_step_probe(0, 4, 2, 10, C.byref(ns)) == -1
+    assert L.jepa_amd_gemm_step_probe(0, 0, 5, 10, C.byref(ns)) == -1
+
+
 # ------------------------------------------------------------------------------------------------ ingest
 def _pre_params(jlib, resize_short=224, crop=224, resample=0, mode=0, fused=True):
     p = jlib.PreprocessParams()
