@@ -117,6 +117,32 @@ def forward_roofline(cfg, items, frames, rows, ms_per_step):
             "gemm_op": gemm, "attn_flop": attn, "gemm_peak": gpeak}
 
 
+# the other encoder configurations: (batch, frames, size) of one step and what one item is
+CONFIG_SHAPES = {"vits16_f16": (1, 1, 224, "images"), "vitb16_2_1_q8_0": (8, 1, 384, "images"),
+                 "vitg16_q8_0": (1, 64, 256, "clips"), "levjepa_vitl16_q8_0": (1, 16, 224, "clips"),
+                 "vitl16_q8_0": (4, 16, 256, "clips")}   # the headline model, 4 clips per call (serving throughput)
+
+
+def time_config(name, steps, warmup):
+    """Rate of one of CONFIG_SHAPES: up to 20 device-resident forwards after a few warm ones."""
+    import numpy as np
+    from jepa_amd import forge, inputs
+    if name not in CONFIG_SHAPES:
+        log(f"bench: unknown configuration {name}")
+        return None
+    b, t, sz, unit = CONFIG_SHAPES[name]
+    pc = make_model(name)
+    xc = inputs.make_input(b, t, sz, sz, seed=1234)
+    log(f"bench: timing {name}")
+    st = max(3, min(steps, 20))
+    rc = time_forward(pc, xc, st, max(2, min(warmup, 3)), kernel_pass=False)
+    mps = rc["elapsed_s"] / st * 1e3
+    return {"value": round(b * st / rc["elapsed_s"], 3), "unit": f"{unit}/s", "items_per_step": b,
+            "tokens_per_item": rc["rows"], "ms_per_step": round(mps, 4),
+            "p50_ms": round(float(np.median(rc["device_ms"])), 4), "steps": st,
+            "forward_roofline": forward_roofline(forge.CONFIGS[name], b, t, rc["rows"], mps)}
+
+
 def time_extra(name, steps):
     """Device time of one call of a row next to the encoder, median over `steps` calls after one warm call."""
     import ctypes as C
@@ -251,6 +277,8 @@ def main():
                     help="also time the rows next to the encoder (comma list: head = ViT-L SSv2 attentive-pool head on "
                          "2048 tokens; predictor = ViT-L masked predictor, 1024 context + 1024 target rows; quantizer = "
                          "the q8_0 / q4_K block quantizers over 64 Mi weights)")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="time only the --configs configurations (no headline line; for per-configuration profiles)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run the library's plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -265,6 +293,12 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.configs_only:
+        res = {}
+        for name in [c for c in args.configs.split(",") if c]:
+            res[name] = time_config(name, args.steps, args.warmup)
+        print(json.dumps({"configs": res}), flush=True)
+        return
     x = inputs.make_input(1, 16, 256, 256, seed=1234)          # jepa-bench's seeded pixels
     path = make_model("vitl16_q8_0")
     log("bench: timing q8_0")
@@ -320,26 +354,10 @@ def main():
                                    "frac": round(ach / PEAK_INT8_TOPS, 4)}
         q4["forward_roofline"] = forward_roofline(forge.CONFIGS["vitl16_q4_k"], 1, 16, N_TOK, q4["ms_per_step"])
         extra["q4_k"] = q4
-    # the other encoder configurations: (batch, frames, size) of one step and what one item is
-    shapes = {"vits16_f16": (1, 1, 224, "images"), "vitb16_2_1_q8_0": (8, 1, 384, "images"),
-              "vitg16_q8_0": (1, 64, 256, "clips"), "levjepa_vitl16_q8_0": (1, 16, 224, "clips"),
-              "vitl16_q8_0": (4, 16, 256, "clips")}   # the headline model, 4 clips per call (serving throughput)
     for name in [c for c in args.configs.split(",") if c]:
-        if name not in shapes:
-            log(f"bench: unknown configuration {name}")
-            continue
-        b, t, sz, unit = shapes[name]
-        pc = make_model(name)
-        xc = inputs.make_input(b, t, sz, sz, seed=1234)
-        log(f"bench: timing {name}")
-        st = max(3, min(args.steps, 20))
-        rc = time_forward(pc, xc, st, max(2, min(args.warmup, 3)), kernel_pass=False)
-        mps = rc["elapsed_s"] / st * 1e3
-        extra.setdefault("configs", {})[name] = {
-            "value": round(b * st / rc["elapsed_s"], 3), "unit": f"{unit}/s", "items_per_step": b,
-            "tokens_per_item": rc["rows"], "ms_per_step": round(mps, 4),
-            "p50_ms": round(float(np.median(rc["device_ms"])), 4), "steps": st,
-            "forward_roofline": forward_roofline(forge.CONFIGS[name], b, t, rc["rows"], mps)}
+        r_c = time_config(name, args.steps, args.warmup)
+        if r_c is not None:
+            extra.setdefault("configs", {})[name] = r_c
     for name in [e for e in args.extras.split(",") if e]:
         res = time_extra(name, max(5, min(args.steps, 20)))
         if res is not None:

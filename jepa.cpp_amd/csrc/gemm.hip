@@ -1324,15 +1324,18 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
 // f32 weights x f32 activations (hfvit patch embedding and f32 files): VALU FMA on tiles of 16 tokens x
 // 32 features, so that even a one-image patch embedding (196 x 384 outputs) runs on 156 workgroups.
 // A workgroup stages up to F32_KC columns of its 16 activation rows and 32 weight rows in LDS at once,
-// transposed (k-major), then each of its four waves sums one quarter of those columns: a lane holds 2
-// tokens x 4 consecutive features, one 8-byte and one 16-byte LDS read per 8 FMAs. The four partial
-// sums meet in LDS and are added in wave order; a K longer than F32_KC runs several such chunks, each
-// chunk's total added to the running sum.
-constexpr int F32_KC = 768;
+// row-major as loaded (16-byte stores; rows padded by 4 floats so that the rows one read touches fall
+// on different banks), then each of its sixteen waves (four per SIMD, to hide the LDS and FMA
+// latencies) sums one slice of those columns, four columns at a time: a lane holds 2 tokens x 4
+// consecutive features, six 16-byte LDS reads per 32 FMAs. The partial sums meet in LDS and are added
+// in wave order; a K longer than F32_KC runs several such
+// chunks, each chunk's total added to the running sum.
+constexpr int F32_KC = 768, F32_LD = F32_KC + 4;
+constexpr int F32_NW = 16;                              // waves per workgroup, one K slice each
 template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm_f32(kargs a) {
-    __shared__ __attribute__((aligned(16))) float sX[F32_KC][16];
-    __shared__ __attribute__((aligned(16))) float sW[F32_KC][32];
+__global__ __launch_bounds__(64 * F32_NW) void k_gemm_f32(kargs a) {
+    __shared__ __attribute__((aligned(16))) float sX[16][F32_LD];
+    __shared__ __attribute__((aligned(16))) float sW[32][F32_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t n0 = (int64_t) blockIdx.x * 32, m0 = (int64_t) blockIdx.y * 16;
     const float * W = (const float *) a.A;
@@ -1340,46 +1343,58 @@ __global__ __launch_bounds__(256) void k_gemm_f32(kargs a) {
     const int tg = lane >> 3, fg = lane & 7;            // tokens 2 tg, 2 tg + 1; features 4 fg .. 4 fg + 3
     const bool al = (a.K & 3) == 0 && (((uintptr_t) X | (uintptr_t) W) & 15) == 0;   // rows 16-byte aligned
     float tot[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-    float * red = &sW[0][0];                            // [3][64][8] partials of waves 1..3 (reuses sW)
+    float * red = &sW[0][0];                            // [F32_NW - 1][64][8] partials of waves 1.. (reuses sW)
+    // one 4-column piece of row r of a (rows past `rows`, columns past kc read as 0)
+    auto piece = [&](const float * base, int64_t row, int64_t rows, int64_t k0, int kk, int kc) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (row < rows) {
+            const float * src = base + row * a.K + k0 + kk;
+            if (kk + 4 <= kc && al) v = *(const float4 *) src;
+            else { v.x = src[0]; if (kk + 1 < kc) v.y = src[1]; if (kk + 2 < kc) v.z = src[2]; if (kk + 3 < kc) v.w = src[3]; }
+        }
+        return v;
+    };
     for (int64_t k0 = 0; k0 < a.K; k0 += F32_KC) {
         const int kc = (int) (a.K - k0 < F32_KC ? a.K - k0 : F32_KC);
+        const int kc4 = (kc + 3) & ~3;                  // columns staged: kc rounded up to 4 (zeros past kc)
         __syncthreads();                                // the previous chunk's reads (and reduction) are done
-        // rows of 4 consecutive k (float4 loads along k); rows past M / N and columns past K read as 0
-        for (int c = tid; c < 16 * (F32_KC / 4); c += 256) {
-            const int r = c / (F32_KC / 4), kk = 4 * (c % (F32_KC / 4));
-            if (kk >= kc) continue;
-            const int64_t m = m0 + r;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (m < a.M) {
-                const float * src = X + m * a.K + k0 + kk;
-                if (kk + 4 <= kc && al) v = *(const float4 *) src;
-                else { v.x = src[0]; if (kk + 1 < kc) v.y = src[1]; if (kk + 2 < kc) v.z = src[2]; if (kk + 3 < kc) v.w = src[3]; }
+        // every load is issued before the LDS stores (a store between two loads would hold the second
+        // back: the compiler cannot tell the rows from LDS); 9 pieces per thread, one round trip
+        constexpr int PT = 16 * (F32_KC / 4) / (64 * F32_NW);   // pieces per thread per 16 rows
+        float4 v[3][PT];
+#pragma unroll
+        for (int b = 0; b < 3; b++)                     // rows 0-15 of X, then 0-15 and 16-31 of W
+#pragma unroll
+            for (int i = 0; i < PT; i++) {
+                const int c = tid + 64 * F32_NW * i, r = c / (F32_KC / 4), kk = 4 * (c % (F32_KC / 4));
+                v[b][i] = kk < kc ? (b == 0 ? piece(X, m0 + r, a.M, k0, kk, kc) : piece(W, n0 + 16 * (b - 1) + r, a.N, k0, kk, kc))
+                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
-            sX[kk][r] = v.x; sX[kk + 1][r] = v.y; sX[kk + 2][r] = v.z; sX[kk + 3][r] = v.w;
-        }
-        for (int c = tid; c < 32 * (F32_KC / 4); c += 256) {
-            const int r = c / (F32_KC / 4), kk = 4 * (c % (F32_KC / 4));
-            if (kk >= kc) continue;
-            const int64_t n = n0 + r;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (n < a.N) {
-                const float * src = W + n * a.K + k0 + kk;
-                if (kk + 4 <= kc && al) v = *(const float4 *) src;
-                else { v.x = src[0]; if (kk + 1 < kc) v.y = src[1]; if (kk + 2 < kc) v.z = src[2]; if (kk + 3 < kc) v.w = src[3]; }
+#pragma unroll
+        for (int b = 0; b < 3; b++)
+#pragma unroll
+            for (int i = 0; i < PT; i++) {
+                const int c = tid + 64 * F32_NW * i, r = c / (F32_KC / 4), kk = 4 * (c % (F32_KC / 4));
+                if (kk < kc) *(float4 *) (b == 0 ? &sX[r][kk] : &sW[16 * (b - 1) + r][kk]) = v[b][i];
             }
-            sW[kk][r] = v.x; sW[kk + 1][r] = v.y; sW[kk + 2][r] = v.z; sW[kk + 3][r] = v.w;
-        }
         __syncthreads();
-        const int q = (kc + 3) / 4;                     // columns per wave (the last wave may get fewer)
-        const int kb = wave * q, ke = kb + q < kc ? kb + q : kc;
+        const int q = ((kc4 / 4 + F32_NW - 1) / F32_NW) * 4;   // columns per wave, a multiple of 4
+        const int kb = wave * q, ke = kb + q < kc4 ? kb + q : kc4;
         float acc[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-        for (int k = kb; k < ke; k++) {
-            const float2 x = *(const float2 *) &sX[k][2 * tg];
-            const float4 w = *(const float4 *) &sW[k][4 * fg];
-            acc[0][0] = fmaf(x.x, w.x, acc[0][0]); acc[0][1] = fmaf(x.x, w.y, acc[0][1]);
-            acc[0][2] = fmaf(x.x, w.z, acc[0][2]); acc[0][3] = fmaf(x.x, w.w, acc[0][3]);
-            acc[1][0] = fmaf(x.y, w.x, acc[1][0]); acc[1][1] = fmaf(x.y, w.y, acc[1][1]);
-            acc[1][2] = fmaf(x.y, w.z, acc[1][2]); acc[1][3] = fmaf(x.y, w.w, acc[1][3]);
+        for (int k = kb; k < ke; k += 4) {
+            const float4 x0 = *(const float4 *) &sX[2 * tg][k], x1 = *(const float4 *) &sX[2 * tg + 1][k];
+            float4 w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = *(const float4 *) &sW[4 * fg + e][k];
+            const float xa[2][4] = {{x0.x, x0.y, x0.z, x0.w}, {x1.x, x1.y, x1.z, x1.w}};
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float wv = j == 0 ? w[e].x : j == 1 ? w[e].y : j == 2 ? w[e].z : w[e].w;
+                    acc[0][e] = fmaf(xa[0][j], wv, acc[0][e]);
+                    acc[1][e] = fmaf(xa[1][j], wv, acc[1][e]);
+                }
         }
         __syncthreads();                                // every wave is past its reads of sW
         if (wave > 0) {
@@ -1395,7 +1410,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(kargs a) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float v = acc[i][e];
-                    for (int w = 0; w < 3; w++) v = __fadd_rn(v, red[(w * 64 + lane) * 8 + 4 * i + e]);
+                    for (int w = 0; w < F32_NW - 1; w++) v = __fadd_rn(v, red[(w * 64 + lane) * 8 + 4 * i + e]);
                     tot[i][e] = k0 == 0 ? v : __fadd_rn(tot[i][e], v);
                 }
         }
@@ -1597,10 +1612,10 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
     if (W.fmt == W_F32) {
         dim3 grid((unsigned) ((a.N + 31) / 32), (unsigned) ((M + 15) / 16));
         switch (ep.kind) {
-            case EPI_F32:      k_gemm_f32<EPI_F32><<<grid, 256, 0, s>>>(a); break;
-            case EPI_RESID:    k_gemm_f32<EPI_RESID><<<grid, 256, 0, s>>>(a); break;
-            case EPI_GELU_F32: k_gemm_f32<EPI_GELU_F32><<<grid, 256, 0, s>>>(a); break;
-            case EPI_QKV:      k_gemm_f32<EPI_QKV><<<grid, 256, 0, s>>>(a); break;
+            case EPI_F32:      k_gemm_f32<EPI_F32><<<grid, 64 * F32_NW, 0, s>>>(a); break;
+            case EPI_RESID:    k_gemm_f32<EPI_RESID><<<grid, 64 * F32_NW, 0, s>>>(a); break;
+            case EPI_GELU_F32: k_gemm_f32<EPI_GELU_F32><<<grid, 64 * F32_NW, 0, s>>>(a); break;
+            case EPI_QKV:      k_gemm_f32<EPI_QKV><<<grid, 64 * F32_NW, 0, s>>>(a); break;
             default: jepa_log("jepa: internal error: epilogue %d has no f32 GEMM\n", ep.kind); break;
         }
         return;
