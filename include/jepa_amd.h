@@ -111,11 +111,13 @@ int jepa_amd_preprocess_frames_device(int device, const jepa_preprocess_params *
 int jepa_amd_preprocess_frames_device_noalloc(int device, const jepa_preprocess_params * p, const uint8_t * frames_dev, int n_frames,
                                               int h, int w, float * out_dev, int64_t out_cap, int * out_h, int * out_w, void * stream);
 
-/* Split-K of the q8_0 / q4_0 GEMMs (two workgroups per output tile, one per K half, the second to
- * finish adding the first's partial sums): jepa_amd_gemm_split forces it off (1), on where the shape
- * allows (2) or back to the automatic choice (-1) for later launches; jepa_amd_gemm_split_of returns
- * the halves a GEMM of this weight type and shape runs in with the residual or plain f32 epilogue
- * (the choice depends on n_out and n_in only; the other epilogues do not split). */
+/* Split-K of the GEMMs with the residual or plain f32 epilogue (S workgroups per output tile, one per
+ * K part; the last to finish adds the parts' sums in part order): q8_0 / q4_0 / q4_K run in 1 or 2
+ * halves chosen from n_out and n_in only; f16 weights in 1 to 4 parts when the tiles leave most CUs
+ * idle (few rows) and K >= 1024. jepa_amd_gemm_split forces S for later launches (1 = off; 2 for the
+ * int8 / 4-bit types; 2, 3 or 4 for f16 where K allows, else unsplit) or restores the automatic choice (-1);
+ * jepa_amd_gemm_split_of returns the halves of a q8_0 / q4_0 / q4_K GEMM of this shape (1 for f16,
+ * whose parts depend on the row count; the other epilogues do not split). */
 int jepa_amd_gemm_split(int split);
 int jepa_amd_gemm_split_of(int wtype, int64_t n_out, int64_t n_in);
 

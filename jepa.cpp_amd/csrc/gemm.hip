@@ -288,8 +288,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     // block of xa x xb tiles, chosen on the host so that the weight and activation rows the XCD's L2
     // has to fetch (xa BN + xb BM rows per K-column) are fewest.
     // split-K (residual and plain epilogues only; elsewhere it folds away): workgroups
-    // [s * tiles, (s + 1) * tiles) compute K half s of every tile
-    constexpr bool SPLITTABLE = (WF == W_Q32 || WF == W_Q40 || WF == W_Q4K) && (EPI == EPI_RESID || EPI == EPI_F32);
+    // [s * tiles, (s + 1) * tiles) compute K part s of every tile
+    constexpr bool SPLITTABLE = (EPI == EPI_RESID || EPI == EPI_F32);
     const int split = SPLITTABLE ? a.split : 1;
     const int ntile = a.tn * a.tm;
     const int sp = split > 1 ? (int) blockIdx.x / ntile : 0;
@@ -986,16 +986,20 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
 
     if constexpr (SPLITTABLE) {
         if (split > 1) {
-            // Publish this half's accumulators; of the two workgroups of a tile, the second to arrive
-            // adds the other's (a + b == b + a, so the result does not depend on which one that is)
-            // and runs the epilogue, the first leaves. Nothing waits on another workgroup.
+            // Publish this part's accumulators; of the `split` workgroups of a tile, the last to arrive
+            // adds all parts in split order, p0 + p1 + ... + p(split-1) (its own from registers), and runs
+            // the epilogue; the others leave. The result does not depend on the arrival order, and
+            // nothing waits on another workgroup.
             // The partials bypass the XCD-private L2s (cache policy sc1, what agent-scope atomic loads
             // and stores use), so no L2 write-back or invalidation is needed: once this wave's stores
             // have completed (vmcnt(0)) they are visible to every XCD, and the arrival counter is an
             // agent-coherent atomic.
-            constexpr int TT = TI * TJ, SC1 = 16;
+            constexpr int TT = TI * TJ, SC1 = 16, SMAX = WF == W_F16 ? 4 : 2;   // parts: f16 up to 4, else halves
             const int64_t tile_floats = (int64_t) BN * T::BM;
-            const brsrc rmine = make_brsrc(a.part + ((int64_t) sp * ntile + bid) * tile_floats, tile_floats * 4);
+            const brsrc rall = make_brsrc(a.part, (int64_t) split * ntile * tile_floats * 4);
+            auto part_off = [&](int k, int t, int q) {   // byte offset of this lane's 4 floats of part k
+                return (uint32_t) ((((int64_t) k * ntile + bid) * tile_floats) * 4 + ((t * 4 + q) * T::NT + tid) * 16);
+            };
 #pragma unroll
             for (int t = 0; t < TT; t++)
 #pragma unroll
@@ -1003,24 +1007,56 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                     const f16v & v = acc[t / TJ][t % TJ];
                     const u4v b = {__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]), __float_as_uint(v[4 * q + 2]),
                                    __float_as_uint(v[4 * q + 3])};
-                    __builtin_amdgcn_raw_buffer_store_b128(b, rmine, ((t * 4 + q) * T::NT + tid) * 16, 0, SC1);
+                    __builtin_amdgcn_raw_buffer_store_b128(b, rall, part_off(sp, t, q), 0, SC1);
                 }
             __builtin_amdgcn_s_waitcnt(0x0f70);    // vmcnt(0): this wave's partial has been written
             __syncthreads();
             int * flag = (int *) smem;              // the stage buffers are free (all copies landed)
             if (tid == 0) flag[0] = atomicAdd(a.cnt + bid, 1);
             __syncthreads();
-            if (flag[0] == 0) return;               // first of the pair
+            if (flag[0] != split - 1) return;       // not the last part to arrive
             if (tid == 0) __hip_atomic_store(a.cnt + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next launch
-            const brsrc rother = make_brsrc(a.part + ((int64_t) (1 - sp) * ntile + bid) * tile_floats, tile_floats * 4);
+            // v[4q..4q+3] = p0 + p1 + ... in split order, with part k's values in o[k] (sp's own: v)
+            auto add_parts = [&](f16v & v, int q, const auto & o) {
+                const float4 mine = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+                float4 sum = mine;
+#pragma unroll
+                for (int k = 0; k < SMAX; k++) {
+                    if (k >= split) break;
+                    const float4 x = k == sp ? mine : make_float4(__uint_as_float(o[k].x), __uint_as_float(o[k].y),
+                                                                  __uint_as_float(o[k].z), __uint_as_float(o[k].w));
+                    if (k == 0) sum = x;
+                    else {
+                        sum.x = __fadd_rn(sum.x, x.x); sum.y = __fadd_rn(sum.y, x.y);
+                        sum.z = __fadd_rn(sum.z, x.z); sum.w = __fadd_rn(sum.w, x.w);
+                    }
+                }
+                v[4 * q] = sum.x; v[4 * q + 1] = sum.y; v[4 * q + 2] = sum.z; v[4 * q + 3] = sum.w;
+            };
 #pragma unroll
             for (int t = 0; t < TT; t++) {
+                f16v & v = acc[t / TJ][t % TJ];
+                if constexpr (WF == W_F16) {
+                    // the other parts' values of the whole 32x32 tile in flight at once (one memory
+                    // round trip per tile; the f16 tiles that split, one MFMA tile per wave, have the
+                    // registers)
+                    u4v o[4][SMAX];
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const u4v o = __builtin_amdgcn_raw_buffer_load_b128(rother, ((t * 4 + q) * T::NT + tid) * 16, 0, SC1);
-                    f16v & v = acc[t / TJ][t % TJ];
-                    v[4 * q] = __fadd_rn(v[4 * q], __uint_as_float(o.x)); v[4 * q + 1] = __fadd_rn(v[4 * q + 1], __uint_as_float(o.y));
-                    v[4 * q + 2] = __fadd_rn(v[4 * q + 2], __uint_as_float(o.z)); v[4 * q + 3] = __fadd_rn(v[4 * q + 3], __uint_as_float(o.w));
+                    for (int q = 0; q < 4; q++)
+#pragma unroll
+                        for (int k = 0; k < SMAX; k++)
+                            if (k < split && k != sp) o[q][k] = __builtin_amdgcn_raw_buffer_load_b128(rall, part_off(k, t, q), 0, SC1);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) add_parts(v, q, o[q]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        u4v o[SMAX];
+#pragma unroll
+                        for (int k = 0; k < SMAX; k++)
+                            if (k < split && k != sp) o[k] = __builtin_amdgcn_raw_buffer_load_b128(rall, part_off(k, t, q), 0, SC1);
+                        add_parts(v, q, o);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);   // one tile's loads in flight at a time (registers)
             }
@@ -1528,10 +1564,36 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
     }
 }
 
+// K parts of an f16-weight GEMM whose tiles leave most CUs idle (the residual GEMMs of a ViT-S/16 image:
+// 197 tokens x 384 outputs are 12 tiles of 128x64, and fc2's K = 1536 is 24 stages per tile, copied at
+// the ~80 GB/s one CU's copies sustain). Each of the S parts covers whole 64-column stages. Measured at
+// 197 rows (us, S = 1 / 2 / 3 / 4): K 1536 12.4 / 10.6 / 9.7 / 9.4, K 3072 (N 768) 21.0 / 15.3 / 12.8 /
+// 11.9, K 384 6.3 / 7.6 / 7.7 / -, K 768 (N 768) 8.4 / 8.8 / 8.6 / 8.8: the exchange (partial stores, the
+// arrival atomic, the last part's loads) costs ~2 us, so only K >= 1024 (16 stages) splits, into the
+// largest S of 4, 3, 2 that leaves each part 4 stages and each workgroup its own CU. The summation order
+// then depends on the row count through the tile count (rounding-level differences between batch sizes,
+// as f16 files have in the reference's batched graph); the hook forces S (1 = off).
+int f16_split(int64_t K, int64_t tiles, int64_t tile_floats, const gemm_split_ws & sw) {
+    constexpr int KC16 = 64;
+    if (K % KC16) return 1;
+    const int64_t nst = K / KC16;
+    const int cus = cu_count();
+    const int f = g_force_split.load();
+    if (f == 1 || (f < 1 && (tiles * 2 > cus || nst < 16))) return 1;
+    for (int S : {4, 3, 2}) {
+        if (f >= 2 && S != f) continue;
+        if (nst % S || nst / S < (f >= 2 ? 2 : 4) || tiles * S > cus || tiles * tile_floats * S > sw.part_floats ||
+            tiles > sw.cnt_n) continue;
+        return S;
+    }
+    return 1;
+}
+
 template <int WF>
 void dispatch_mfma(kargs a, hipStream_t s, const gemm_split_ws * sw) {
     // split-K runs with the residual and plain epilogues (the N <= 1024 GEMMs of an encoder block)
-    a.split = sw && sw->part && sw->cnt && (a.ep.kind == EPI_RESID || a.ep.kind == EPI_F32) ? gemm_split_for(WF, a.N, a.K) : 1;
+    const bool can_split = sw && sw->part && sw->cnt && (a.ep.kind == EPI_RESID || a.ep.kind == EPI_F32);
+    a.split = can_split && WF != W_F16 ? gemm_split_for(WF, a.N, a.K) : 1;
     a.part = nullptr; a.cnt = nullptr;
     const int c = pick_tile(WF, a.N, a.M, a.ep.kind == EPI_GELU_Q8_K ? 256 : 0, a.split);
     if (c < 0) {
@@ -1541,6 +1603,7 @@ void dispatch_mfma(kargs a, hipStream_t s, const gemm_split_ws * sw) {
     const int bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
     a.tn = (int) (a.N / bn);
     a.tm = (int) ((a.M + bm - 1) / bm);
+    if (WF == W_F16 && can_split) a.split = f16_split(a.K, (int64_t) a.tn * a.tm, (int64_t) bn * bm, *sw);
     if (a.split > 1) {
         const int64_t tiles = (int64_t) a.tn * a.tm;
         if (tiles * bn * bm * a.split > sw->part_floats || tiles > sw->cnt_n) {
@@ -1589,9 +1652,10 @@ int gemm_split_for(int wf, int64_t N, int64_t K) {
 }
 
 void gemm_split_ws_size(int64_t max_rows, int64_t * part_floats, int64_t * cnt_n) {
-    // tiles x BN x BM <= (rows rounded up to 128) x N for every tile, two halves; tiles <= that / 64^2
+    // tiles x BN x BM <= (rows rounded up to 128) x N for every tile: two halves (int8 / 4-bit weights),
+    // up to four parts for up to 1024 rows (f16 weights); tiles <= that / 64^2
     const int64_t rows = (max_rows + 127) / 128 * 128;
-    *part_floats = 2 * rows * SPLIT_MAX_N;
+    *part_floats = (rows <= 1024 ? 4 : 2) * rows * SPLIT_MAX_N;
     *cnt_n = (rows / 64) * (SPLIT_MAX_N / 64) + 64;
 }
 
@@ -1621,7 +1685,7 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
         return;
     }
     switch (W.fmt) {
-        case W_F16: dispatch_mfma<W_F16>(a, s, nullptr); break;
+        case W_F16: dispatch_mfma<W_F16>(a, s, sw); break;
         case W_Q32: dispatch_mfma<W_Q32>(a, s, sw); break;
         case W_Q40: dispatch_mfma<W_Q40>(a, s, sw); break;
         case W_Q4K: dispatch_mfma<W_Q4K>(a, s, sw); break;
@@ -1629,7 +1693,8 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
 }
 
 int gemm_force_split(int split) {
-    g_force_split.store(split < 1 ? -1 : split > 2 ? 2 : split);
+    // int8 / 4-bit weights: 1 or 2 halves; f16 weights: 1 to 4 parts (f16_split)
+    g_force_split.store(split < 1 ? -1 : split > 4 ? 4 : split);
     return 0;
 }
 

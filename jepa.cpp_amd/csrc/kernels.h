@@ -48,9 +48,10 @@ struct gemm_epi {
 
 struct dev_linear;
 
-// Scratch of the split-K GEMMs (q8_0 / q4_0 weights with N <= 1024: two workgroups per output tile,
-// one per K half): the raw accumulators of both halves and one arrival counter per tile, which must
-// be zero before the first launch (every launch leaves them zero). Sizes from gemm_split_ws_size.
+// Scratch of the split-K GEMMs (int8 / 4-bit weights with N <= 1024: two workgroups per output tile,
+// one per K half; f16 weights over few rows: up to four K parts): the raw accumulators of every part
+// and one arrival counter per tile, which must be zero before the first launch (every launch leaves
+// them zero). Sizes from gemm_split_ws_size.
 struct gemm_split_ws {
     float * part = nullptr;
     int * cnt = nullptr;
@@ -61,8 +62,9 @@ void gemm_split_ws_size(int64_t max_rows, int64_t * part_floats, int64_t * cnt_n
 // Y = X W^T (+ epilogue). M = rows of X. Without split scratch every tile is one workgroup.
 void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm_epi & ep, hipStream_t s,
                  const gemm_split_ws * sw = nullptr);
-// K halves the GEMM of this weight format and shape runs in (1 or 2); depends on N and K only, so
-// that the summation order of an output never depends on the number of rows
+// K halves the int8 / 4-bit GEMM of this weight format and shape runs in (1 or 2); depends on N and K
+// only, so that the summation order of an output never depends on the number of rows (f16 weights:
+// chosen per launch from the tile count, 1 here)
 int gemm_split_for(int wf, int64_t N, int64_t K);
 
 // LayerNorm (ggml_norm + affine) of x [M][D] written in `out` format; w/b may be null (no affine).

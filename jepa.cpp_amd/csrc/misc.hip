@@ -13,7 +13,6 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 namespace {
 
-__device__ __forceinline__ uint16_t f2hbits(float f) { return __builtin_bit_cast(uint16_t, (_Float16) f); }
 __device__ __forceinline__ float h2f(uint16_t b) { return (float) __builtin_bit_cast(_Float16, b); }
 
 // ------------------------------------------------------------------------------------------------

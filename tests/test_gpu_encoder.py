@@ -123,15 +123,22 @@ def test_tiny_separate_qkv_unsupported_mix_refused(jlib, models_dir):
 
 
 def test_batch_equals_single(jlib, models_dir):
-    """Items of one call equal separate calls bit for bit (reference tests/test-batch.cpp:12-21)."""
-    for family, nb, nf in (("hfvit", 3, 1), ("vjepa2", 2, 4)):
-        cfg = forge.tiny(family, "q8_0")
+    """Items of one call equal separate calls bit for bit (reference tests/test-batch.cpp:12-21): q8_0, whose
+    K halves depend on the shape only. f16 weights split K by the tile count, which the batch changes, so
+    there the reference's gate for files other than f32 applies: worst-row cosine >= 1 - 1e-6."""
+    for family, nb, nf, wt in (("hfvit", 3, 1, "q8_0"), ("vjepa2", 2, 4, "q8_0"), ("hfvit", 3, 1, "f16")):
+        cfg = forge.tiny(family, wt)
         m = jlib.Model(forge.cached_model(cfg, models_dir))
         ctx = jlib.Context(m)
         x = inputs.make_input(nb, nf, 64, 64, seed=5)
         both = ctx.encode(x)
         parts = np.concatenate([ctx.encode(x[i:i + 1]) for i in range(nb)])
-        np.testing.assert_array_equal(both.view(np.uint32), parts.view(np.uint32))
+        if wt == "q8_0":
+            np.testing.assert_array_equal(both.view(np.uint32), parts.view(np.uint32))
+        else:
+            a, b = both.astype(np.float64), parts.astype(np.float64)
+            cos = (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+            assert cos.min() >= 1 - 1e-6, cos.min()
 
 
 def test_graph_replay_equals_direct(jlib, models_dir):

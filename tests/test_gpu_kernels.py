@@ -305,6 +305,48 @@ def test_matmul_split_k(jlib, oracle, gtype, shape, M):
     assert np.abs(got[1] - got[2]).max() <= 1e-5 * np.abs(got[1]).max()
 
 
+@pytest.mark.parametrize("shape", [(384, 1536), (384, 384), (1024, 4096)])
+def test_matmul_f16_split_parts(jlib, oracle, shape):
+    """f16 split-K over few rows (S workgroups per tile, one per K part of whole 64-column stages; the last
+    to finish adds the parts in part order and runs the epilogue): every S the shape allows, forced, within
+    f32 summation-order rounding of the oracle; three launches in a row, then a new call, give the same bits
+    (the arrival counters come back to zero and the sum does not depend on the arrival order); 197 rows
+    (one ViT-S/16 image: ragged against the 64-row tiles)."""
+    n_out, n_in = shape
+    M = 197
+    rng = np.random.default_rng(n_out + 3 * n_in)
+    w = (rng.standard_normal((n_out, n_in)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    bias = (rng.standard_normal(n_out) * 0.02).astype(np.float32)
+    raw = gguf.quantize(gguf.GGML_F16, w)
+    want = oracle.mul_mat(gguf.GGML_F16, raw, n_out, n_in, x, bias)
+    dw, dx, db = dev(raw.reshape(-1)), dev(x), dev(bias)
+    L = jlib.lib()
+    scale = np.abs(want).max()
+    ran = []
+    for S in (1, 2, 3, 4):
+        if (n_in // 64) % S or n_in // 64 // S < 2:
+            continue
+        outs = []
+        for reps in (3, 1):
+            y = torch.full((M, n_out), float("nan"), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            assert L.jepa_amd_gemm_split(S) == 0
+            try:
+                rc = L.jepa_amd_matmul(0, gguf.GGML_F16, dw.data_ptr(), n_out, n_in, db.data_ptr(), dx.data_ptr(), M, y.data_ptr(),
+                                       reps, None)
+            finally:
+                L.jepa_amd_gemm_split(-1)
+            assert rc == 0, jlib.error_text()
+            outs.append(host(y))
+        np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+        err = np.abs(outs[0] - want).max()
+        assert err <= 2e-5 * scale, (S, err / scale)
+        ran.append(S)
+    print(f"{shape}: parts {ran} within 2e-5 of the oracle, repeatable")
+    assert len(ran) >= 3
+
+
 # workgroup tiles of the MFMA GEMM (weight rows x tokens), by index
 TILES = {0: (256, 128), 1: (192, 128), 2: (128, 128), 3: (128, 128), 4: (64, 128), 5: (128, 64), 6: (256, 64), 7: (256, 64),
          8: (384, 64)}
