@@ -6,10 +6,10 @@
 // accumulation). Q arrives with 3-D RoPE already applied by the QKV GEMM epilogue.
 //
 // Work split: one workgroup = 128 queries of one head, in QG query groups of QT 32-query MFMA tiles
-// (QG x QT = 4) times KS = 4 key splits, one wave each: QT = 1 is 16 waves (four per SIMD, 128
-// VGPRs each: enough waves to hide the MFMA / exp / LDS latencies of the softmax chain), QT = 2 is 8
-// waves whose every K and V^T read from LDS feeds two MFMAs; QT = 1 measured faster (30.3 against
-// 32.9 us at 2048 tokens x 16 heads). The splits are merged through LDS at the end. Keys come in
+// (QG x QT = 4) times KS key splits (1, 2 or 4 by the key count: attention_key_splits), one wave
+// each. With QT = 1 and KS = 4 that is 16 waves (four per SIMD, 128 VGPRs each); QT = 2 (8 waves
+// whose every K and V^T read from LDS feeds two MFMAs) measured slower (32.9 against 30.3 us at 2048
+// tokens x 16 heads). The splits are merged through LDS at the end. Keys come in
 // tiles of 64: the K tile (64 keys x 64 dims) and the V^T tile (64 dims x 64 keys), 128 B per row, are
 // copied HBM->LDS directly (buffer_load_dwordx4 ... lds) into a swizzled layout (lds_slot),
 // double-buffered per split: tile s + 1 is copied while tile s is used.
@@ -31,6 +31,8 @@
 #include "lanes.h"
 #include "quant_dev.h"
 
+#include <type_traits>
+
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
@@ -39,7 +41,7 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int HD = 64, QB = 128, KT = 64, KS = 4;
+constexpr int HD = 64, QB = 128, KT = 64;
 constexpr int TILE = KT * 128;                  // one K or V^T tile: 64 rows of 128 B
 constexpr int STAGE = 2 * TILE;                 // K + V^T
 constexpr int SPLIT = 2 * STAGE;                // LDS of one key split: two stages
@@ -84,11 +86,12 @@ __device__ __forceinline__ int2 key_range(int q, int R, int np, int tpf) {
 // np / tpf select the block-causal mask (tpf = 0: none); key tiles that no query of the workgroup
 // sees are not visited. MASKED = false (no block-causal mask, R a multiple of 64: every key of every
 // visited tile is visible to every query) drops the per-key mask code from the loop.
-template <int OUT, int HDO, bool MASKED, int QT>
+template <int OUT, int HDO, bool MASKED, int QT, int KS>
 __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float16 * __restrict__ Q, const _Float16 * __restrict__ Kp,
                                                                    const _Float16 * __restrict__ Vt, void * __restrict__ O,
                                                                    void * __restrict__ Od, int n_head, int64_t R, int64_t R_pad,
                                                                    float c, int np, int tpf) {
+    static_assert(KS == 1 || KS == 2 || KS == 4, "key splits");
     constexpr int NKK = HDO / 16, NDT = HDO / 32;       // Q.K^T dim steps, P.V row blocks
     constexpr int QG = 4 / QT;                          // query groups: QG x QT x 32 = 128 queries
     constexpr int QW = 32 * QT;                         // queries per wave
@@ -310,48 +313,50 @@ __global__ __launch_bounds__(64 * KS * 4 / QT, 1) void k_attn_hd64(const _Float1
     // per lane per bank), split 0 combines them in split order
     constexpr int NV = QT * (2 + 16 * NDT);             // floats per lane: per query tile m, l, acc
     __builtin_amdgcn_s_setprio(0);
-    __syncthreads();                                    // every wave is past its last stage read
-    if (ks > 0) {
-        float * xs = (float *) smem + (size_t) ((ks - 1) * QG + qg) * NV * 64 + lane;
+    if constexpr (KS > 1) {
+        __syncthreads();                                // every wave is past its last stage read
+        if (ks > 0) {
+            float * xs = (float *) smem + (size_t) ((ks - 1) * QG + qg) * NV * 64 + lane;
+#pragma unroll
+            for (int qt = 0; qt < QT; qt++) {
+                float * x = xs + (size_t) qt * (NV / QT) * 64;
+                x[0] = mcs[qt]; x[64] = l_run[qt];
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) x[(2 + 16 * dt + r) * 64] = acc[qt][dt][r];
+            }
+        }
+        __syncthreads();
+        if (ks > 0) return;
 #pragma unroll
         for (int qt = 0; qt < QT; qt++) {
-            float * x = xs + (size_t) qt * (NV / QT) * 64;
-            x[0] = mcs[qt]; x[64] = l_run[qt];
+            float mi[KS], ai[KS];
+            mi[0] = mcs[qt];
+            float m = mcs[qt];
+#pragma unroll
+            for (int k = 1; k < KS; k++) {
+                mi[k] = ((const float *) smem)[(size_t) ((k - 1) * QG + qg) * NV * 64 + (size_t) qt * (NV / QT) * 64 + lane];
+                m = fmaxf(m, mi[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < KS; k++) ai[k] = mi[k] == -INFINITY ? 0.0f : fast_exp2(mi[k] - m);
+            float l = l_run[qt] * ai[0];
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) x[(2 + 16 * dt + r) * 64] = acc[qt][dt][r];
+                for (int r = 0; r < 16; r++) acc[qt][dt][r] *= ai[0];
+#pragma unroll
+            for (int k = 1; k < KS; k++) {
+                const float * x = (const float *) smem + (size_t) ((k - 1) * QG + qg) * NV * 64 + (size_t) qt * (NV / QT) * 64 + lane;
+                l = fmaf(x[64], ai[k], l);
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[qt][dt][r] = fmaf(x[(2 + 16 * dt + r) * 64], ai[k], acc[qt][dt][r]);
+            }
+            l_run[qt] = l;
         }
-    }
-    __syncthreads();
-    if (ks > 0) return;
-#pragma unroll
-    for (int qt = 0; qt < QT; qt++) {
-        float mi[KS], ai[KS];
-        mi[0] = mcs[qt];
-        float m = mcs[qt];
-#pragma unroll
-        for (int k = 1; k < KS; k++) {
-            mi[k] = ((const float *) smem)[(size_t) ((k - 1) * QG + qg) * NV * 64 + (size_t) qt * (NV / QT) * 64 + lane];
-            m = fmaxf(m, mi[k]);
-        }
-#pragma unroll
-        for (int k = 0; k < KS; k++) ai[k] = mi[k] == -INFINITY ? 0.0f : fast_exp2(mi[k] - m);
-        float l = l_run[qt] * ai[0];
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[qt][dt][r] *= ai[0];
-#pragma unroll
-        for (int k = 1; k < KS; k++) {
-            const float * x = (const float *) smem + (size_t) ((k - 1) * QG + qg) * NV * 64 + (size_t) qt * (NV / QT) * 64 + lane;
-            l = fmaf(x[64], ai[k], l);
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[qt][dt][r] = fmaf(x[(2 + 16 * dt + r) * 64], ai[k], acc[qt][dt][r]);
-        }
-        l_run[qt] = l;
     }
 
     const int64_t DD = (int64_t) n_head * HDO;
@@ -526,6 +531,14 @@ __global__ __launch_bounds__(256) void k_attn_any(const _Float16 * __restrict__ 
 
 int attention_stored_width(int hd) { return hd <= 64 ? 64 : (hd + 31) / 32 * 32; }
 
+// Key splits by the key count R only (so an item's result does not depend on the batch). Fewer
+// splits mean fewer waves per workgroup, less LDS (32 KB per split) and no merge, and more workgroups
+// per CU. Measured (us per launch, q8_0 output, splits 1 / 2 / 4): 197 keys x 6 heads 8.1 / 8.0 /
+// 10.4, 576 x 96 17.7 / 18.2 / 24.9, 2048 x 16 34.1 / 27.8 / 27.9, 8192 x 22 461 / 461 / 481.
+int attention_key_splits(int64_t R) {
+    return R <= 1024 ? 1 : R <= 4096 ? 4 : 2;
+}
+
 bool attention_supports(int hd) { return hd == 32 || hd == 64 || (hd > 0 && hd <= 128 && hd % 16 == 0); }
 
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items,
@@ -551,17 +564,27 @@ void launch_attention(const void * q, const void * k, const void * vt, const act
         return;
     }
     const bool masked = tpf > 0 || R % KT != 0;
+    const int ks = attention_key_splits(R);
     constexpr int QT = ATTN_QT;
     static_assert(QT == 1 || QT == 2, "one or two query tiles per wave");
-    auto go = [&](auto kern, void * od) { kern<<<grid, 64 * KS * 4 / QT, 0, s>>>(Q, K, V, out.q, od, n_head, R, R_pad, c, n_prefix, tpf); };
-    if (out.fmt == A_Q8_0) {
-        if (hd == 32) masked ? go(k_attn_hd64<A_Q8_0, 32, true, QT>, out.d) : go(k_attn_hd64<A_Q8_0, 32, false, QT>, out.d);
-        else masked ? go(k_attn_hd64<A_Q8_0, 64, true, QT>, out.d) : go(k_attn_hd64<A_Q8_0, 64, false, QT>, out.d);
-    } else if (out.fmt == A_F16) {
-        if (hd == 32) masked ? go(k_attn_hd64<A_F16, 32, true, QT>, nullptr) : go(k_attn_hd64<A_F16, 32, false, QT>, nullptr);
-        else masked ? go(k_attn_hd64<A_F16, 64, true, QT>, nullptr) : go(k_attn_hd64<A_F16, 64, false, QT>, nullptr);
-    } else {
-        if (hd == 32) masked ? go(k_attn_hd64<A_F32, 32, true, QT>, nullptr) : go(k_attn_hd64<A_F32, 32, false, QT>, nullptr);
-        else masked ? go(k_attn_hd64<A_F32, 64, true, QT>, nullptr) : go(k_attn_hd64<A_F32, 64, false, QT>, nullptr);
-    }
+    // kernel instance by output format, stored head width, mask and key splits
+    auto go = [&](auto out_c, auto hdo_c, auto masked_c, void * od) {
+        constexpr int OUT = decltype(out_c)::value, HDO = decltype(hdo_c)::value;
+        constexpr bool MK = decltype(masked_c)::value;
+        auto run = [&](auto kern, int ks_) { kern<<<grid, 64 * ks_ * 4 / QT, 0, s>>>(Q, K, V, out.q, od, n_head, R, R_pad, c, n_prefix, tpf); };
+        if (ks == 1) run(k_attn_hd64<OUT, HDO, MK, QT, 1>, 1);
+        else if (ks == 2) run(k_attn_hd64<OUT, HDO, MK, QT, 2>, 2);
+        else run(k_attn_hd64<OUT, HDO, MK, QT, 4>, 4);
+    };
+    auto by_width = [&](auto out_c, void * od) {
+        using T = std::true_type;
+        using F = std::false_type;
+        using W32 = std::integral_constant<int, 32>;
+        using W64 = std::integral_constant<int, 64>;
+        if (hd == 32) masked ? go(out_c, W32{}, T{}, od) : go(out_c, W32{}, F{}, od);
+        else masked ? go(out_c, W64{}, T{}, od) : go(out_c, W64{}, F{}, od);
+    };
+    if (out.fmt == A_Q8_0) by_width(std::integral_constant<int, A_Q8_0>{}, out.d);
+    else if (out.fmt == A_F16) by_width(std::integral_constant<int, A_F16>{}, nullptr);
+    else by_width(std::integral_constant<int, A_F32>{}, nullptr);
 }

@@ -78,6 +78,8 @@ void launch_rownorm_quant(const float * x, int64_t M, int64_t D, const float * w
 // tokens_per_slot > 0 applies the block-causal mask: n_prefix leading rows read every key, a patch row
 // reads the patch keys of its own and earlier temporal slots (tokens_per_slot rows each) and no prefix
 // key. tokens_per_slot = 0: full attention.
+// key splits (waves per query group, merged through LDS) of the head-width-64 attention for R keys
+int attention_key_splits(int64_t R);
 void launch_attention(const void * q, const void * k, const void * vt, const act_view & out, int64_t n_items, int n_head,
                       int hd, int64_t R, int64_t R_pad, float scale, int n_prefix, int64_t tokens_per_slot, hipStream_t s);
 // Head widths the attention runs: 32, 64, and other multiples of 16 up to 128 (f32 output only); the

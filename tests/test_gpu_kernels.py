@@ -456,10 +456,11 @@ def _attention_ref(qkv, n_items, n_tok, H, rope=None, mask=None, hd=64):
     return out
 
 
-# token counts cover: 64-key tile counts that the four key splits of a workgroup share equally or not,
-# one tile (three splits empty), a last tile with a single valid key, padding
+# token counts cover the three key-split counts (one split up to 1024 keys, four up to 4096, two above),
+# 64-key tile counts that the splits of a workgroup share equally or not, one tile (three of four splits
+# empty), a last tile with a single valid key, padding
 ATTN_CASES = [(1, 2048, 4, True), (2, 197, 6, False), (1, 576, 2, True), (3, 17, 2, False), (1, 129, 1, False),
-              (1, 64, 1, False), (2, 65, 2, True)]
+              (1, 64, 1, False), (2, 65, 2, True), (1, 1088, 2, False), (1, 4160, 1, True)]
 
 
 @pytest.mark.parametrize("n_items,n_tok,H,rope", ATTN_CASES)
@@ -581,8 +582,9 @@ def test_attention_other_widths(jlib, oracle, n_items, n_tok, H, hd, rope):
 
 # block-causal (LeVJEPA) shapes (n_items, gt, gh, gw, n_prefix, H): the reference's mask KAT shape (65
 # rows), 513 rows (five query blocks; slots of 64 rows against tiles of 64 keys shifted by the CLS),
-# slots of 35 rows with no prefix, and the 16 x 224^2 clip (3137 rows, slots of 196)
-MASK_CASES = [(1, 4, 4, 4, 1, 2), (2, 8, 8, 8, 1, 2), (1, 3, 5, 7, 0, 2), (1, 16, 14, 14, 1, 1)]
+# slots of 35 rows with no prefix, the 16 x 224^2 clip (3137 rows, slots of 196), and 4097 rows (two key
+# splits)
+MASK_CASES = [(1, 4, 4, 4, 1, 2), (2, 8, 8, 8, 1, 2), (1, 3, 5, 7, 0, 2), (1, 16, 14, 14, 1, 1), (1, 16, 16, 16, 1, 1)]
 
 
 @pytest.mark.parametrize("n_items,gt,gh,gw,n_prefix,H", MASK_CASES)
