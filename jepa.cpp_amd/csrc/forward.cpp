@@ -161,15 +161,31 @@ void enqueue_block(const blk_shape & b, const dev_layer & L, fwd_workspace & w, 
     const int64_t D = b.D, rows = n_items * R;
     const int H = b.H, hd = b.hd;
     // attention half
-    w.actA.fmt = L.qkv.act();
-    kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln1_w, L.ln1_b, b.eps, true, w.actA, s); });
     {
         gemm_epi ep;
         ep.kind = EPI_QKV;
         ep.q = w.Q; ep.k = w.Kt; ep.vt = w.Vt;
         ep.rope_c = rope_c; ep.rope_s = rope_s;
         ep.n_head = H; ep.hd = hd; ep.hds = b.hds; ep.D = (int) D; ep.R = R; ep.R_pad = w.R_pad;
-        kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
+        if (!L.qkv_separate) {
+            w.actA.fmt = L.qkv.act();
+            kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln1_w, L.ln1_b, b.eps, true, w.actA, s); });
+            kt.run(gemm_class(L.qkv), [&] { launch_gemm(L.qkv, w.actA, rows, ep, s, &w.split); }, "qkv");
+        } else {
+            // q, k, v one by one (reference src/jepa.cpp:408-414), each on ln1 in its own activation
+            // format (the LayerNorm runs again only when the format changes)
+            int fmt = -1;
+            for (int i = 0; i < 3; i++) {
+                const dev_linear & P = L.qkv_part[i];
+                if (P.act() != fmt) {
+                    fmt = P.act();
+                    w.actA.fmt = P.act();
+                    kt.run("layernorm", [&] { launch_rownorm_quant(w.x, rows, D, L.ln1_w, L.ln1_b, b.eps, true, w.actA, s); });
+                }
+                ep.col0 = (int64_t) i * D;
+                kt.run(gemm_class(P), [&] { launch_gemm(P, w.actA, rows, ep, s, &w.split); }, "qkv");
+            }
+        }
     }
     w.actA.fmt = L.out.act();
     if ((w.actA.fmt == A_Q8_0 || w.actA.fmt == A_F16) && (hd == 64 || hd == 32)) {

@@ -161,8 +161,9 @@ __device__ __forceinline__ void epi4(const kargs & a, int64_t m, int64_t n, floa
         *(h4 *) o = v;
     } else if constexpr (EPI == EPI_QKV) {
         const int D = ep.D, hd = ep.hd, hds = ep.hds ? ep.hds : hd;
-        const int which = (int) (n / D);
-        const int nn = (int) (n - (int64_t) which * D);
+        const int64_t ng = n + ep.col0;        // column of the [q | k | v] layout (the bias above is this launch's)
+        const int which = (int) (ng / D);
+        const int nn = (int) (ng - (int64_t) which * D);
         const int h = nn / hd, d0 = nn - h * hd;
         const int64_t item = m / ep.R, tok = m - item * ep.R;
         const int64_t head = item * ep.n_head + h;
@@ -1076,7 +1077,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
     [[maybe_unused]] const unsigned char * lrs = nullptr;
     if constexpr (EPI == EPI_QKV) {
         const int hd = a.ep.hd;
-        if (a.ep.rope_c && (hd == 32 || hd == 64) && n0 < 2 * (int64_t) a.ep.D && 2 * T::BM * hd * 4 <= T::LDS) {
+        if (a.ep.rope_c && (hd == 32 || hd == 64) && n0 + a.ep.col0 < 2 * (int64_t) a.ep.D && 2 * T::BM * hd * 4 <= T::LDS) {
             __builtin_amdgcn_s_waitcnt(0);      // no HBM->LDS copy of this wave still in flight
             __syncthreads();                    // every wave is past its last read of the stage buffers
             unsigned char * wc = smem;
@@ -1258,7 +1259,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
                 // head and offset are wave-uniform, the token is one 32-bit division per lane
                 const gemm_epi & ep = a.ep;
                 const int hd = ep.hd, hds = ep.hds ? ep.hds : hd;
-                const int nbi = __builtin_amdgcn_readfirstlane((int) nb);
+                const int nbi = __builtin_amdgcn_readfirstlane((int) (nb + ep.col0));
                 const int which = nbi / ep.D, nn = nbi - which * ep.D;
                 const int h = nn / hd, dbase = nn - h * hd + 4 * g;
                 if (m >= M) continue;

@@ -44,6 +44,8 @@ struct gemm_epi {
     int hds = 0;                            // stored head width of Q / K / V^T (0: hd); 64 for hd 32 heads,
                                             // whose upper 32 dims stay zero
     int64_t R = 0, R_pad = 0;
+    int64_t col0 = 0;                       // this launch's outputs are columns col0.. of the [q | k | v]
+                                            // layout (one part of separate q / k / v linears; else 0)
 };
 
 struct dev_linear;

@@ -350,7 +350,8 @@ struct loader {
         // Parts of different dtypes: the reference runs each part as its own linear. q8_0 and q4_0 parts
         // mix exactly: both take q8_0 activations and q4_0's codes q - 8 are int8 codes under the same
         // f16 scale, so every part expands to the int8 layout and one GEMM gives each part's own dot
-        // products. Any other mix (its parts would need different activation formats) is refused.
+        // products. Any other mix needs different activation formats per part: block() loads those
+        // parts as separate linears and never stacks them here.
         bool mixed = false;
         for (const auto * p : ts) mixed |= p->type != ts[0]->type;
         if (mixed) {
@@ -450,11 +451,28 @@ struct loader {
             return false;
         }
         if (F <= 0) F = rows_of(p + "ffn_up.weight");
-        return vec(p + "ln1.weight", D, &Ly.ln1_w) && vec(p + "ln1.bias", D, &Ly.ln1_b) && vec(p + "ln2.weight", D, &Ly.ln2_w) &&
+        // separate q / k / v stack into one linear when their dtypes agree or are q8_0 / q4_0 (one
+        // activation format); other mixes stay three linears, each with its own activation format
+        static const char * const QKV[3] = {"attn_q", "attn_k", "attn_v"};
+        if (!fused) {
+            bool same = true, int8_family = true;
+            for (const char * q : QKV) {
+                const int ty = f.tensor(p + q + ".weight")->type;
+                same &= ty == f.tensor(p + "attn_q.weight")->type;
+                int8_family &= ty == T_Q8_0 || ty == T_Q4_0;
+            }
+            Ly.qkv_separate = !same && !int8_family;
+        }
+        bool qkv_ok = true;
+        if (fused) qkv_ok = linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * inner, Ly.qkv, true);
+        else if (!Ly.qkv_separate)
+            qkv_ok = linear_n({p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"},
+                              {p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"}, D, 3 * inner, Ly.qkv, true);
+        else
+            for (int i = 0; i < 3 && qkv_ok; i++)
+                qkv_ok = linear(p + QKV[i] + ".weight", p + QKV[i] + ".bias", D, inner, Ly.qkv_part[i], true);
+        return qkv_ok && vec(p + "ln1.weight", D, &Ly.ln1_w) && vec(p + "ln1.bias", D, &Ly.ln1_b) && vec(p + "ln2.weight", D, &Ly.ln2_w) &&
                vec(p + "ln2.bias", D, &Ly.ln2_b) && vec(p + "ls1", D, &Ly.ls1) && vec(p + "ls2", D, &Ly.ls2) &&
-               (fused ? linear(p + "attn_qkv.weight", p + "attn_qkv.bias", D, 3 * inner, Ly.qkv, true)
-                      : linear_n({p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"},
-                                 {p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"}, D, 3 * inner, Ly.qkv, true)) &&
                linear(p + "attn_out.weight", p + "attn_out.bias", inner, D, Ly.out, true) &&
                linear(p + "ffn_up.weight", p + "ffn_up.bias", D, F, Ly.up, true) &&
                linear(p + "ffn_down.weight", p + "ffn_down.bias", F, D, Ly.down, true);

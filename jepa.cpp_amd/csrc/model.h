@@ -137,6 +137,10 @@ struct dev_layer {
     float * ln1_w = nullptr, * ln1_b = nullptr, * ln2_w = nullptr, * ln2_b = nullptr;
     float * ls1 = nullptr, * ls2 = nullptr;
     dev_linear qkv, out, up, down;
+    // separate attn_q / attn_k / attn_v whose dtypes take different activation formats (f16 beside
+    // q8_0, q4_K beside q8_0, ...): three linears run one by one, as the reference runs them; qkv unused
+    bool qkv_separate = false;
+    dev_linear qkv_part[3];
 };
 
 // attentive-pool head (reference src/jepa.cpp:1026-1075, tensors docs/gguf-schema.md:121-137)

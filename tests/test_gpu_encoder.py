@@ -112,14 +112,17 @@ def test_tiny_separate_qkv_partial_biases_and_mixed_types(jlib, oracle, models_d
     check_parity(got, want, gtr, wtr, label=f"separate q/k/v {parts}")
 
 
-def test_tiny_separate_qkv_unsupported_mix_refused(jlib, models_dir):
-    """Parts that would need different activation formats (q8_0 with f16) are refused by name."""
-    cfg = forge.tiny("vjepa2", "q8_0", qkv_fused=False, qkv_parts="q8_0+b,f16+b,q8_0+b")
-    path = forge.cached_model(cfg, models_dir)
-    jlib.lib().jepa_error_reset()
-    with pytest.raises(RuntimeError):
-        jlib.Model(path)
-    assert "different dtypes" in jlib.error_text()
+@pytest.mark.parametrize("parts,kw", [("q8_0+b,f16+b,q8_0+b", {}), ("f32,q8_0+b,f16", {}),
+                                       ("q4_k+b,q8_0,f16+b", dict(ffn_dim=1024, embed_dim=256, n_head=4))])
+def test_tiny_separate_qkv_activation_formats_differ(jlib, oracle, models_dir, parts, kw):
+    """Separate attn_q / attn_k / attn_v whose dtypes take different activation formats (f16 or f32
+    beside q8_0, q4_K beside q8_0: the reference quantizes ln1's output per linear for each weight's
+    vec_dot type, src/jepa.cpp:408-414): loaded as three linears run one by one, each on ln1 in its own
+    format, writing its columns of the Q / K / V^T layout; against the oracle, which runs the three
+    linears with their own types."""
+    cfg = forge.tiny("vjepa2", "q8_0", ln_random=True, qkv_fused=False, qkv_parts=parts, **kw)
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 1, 4, 64)
+    check_parity(got, want, gtr, wtr, label=f"separate q/k/v {parts}")
 
 
 def test_batch_equals_single(jlib, models_dir):
