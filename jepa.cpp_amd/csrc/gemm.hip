@@ -1573,14 +1573,16 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
 // arrival atomic, the last part's loads) costs ~2 us, so only K >= 1024 (16 stages) splits, into the
 // largest S of 4, 3, 2 that leaves each part 4 stages and each workgroup its own CU. The summation order
 // then depends on the row count through the tile count (rounding-level differences between batch sizes,
-// as f16 files have in the reference's batched graph); the hook forces S (1 = off).
-int f16_split(int64_t K, int64_t tiles, int64_t tile_floats, const gemm_split_ws & sw) {
+// as f16 files have in the reference's batched graph), so only the residual GEMMs of f16 blocks split
+// by themselves: the f16 patch embedding of a q8_0 / q4_K model keeps that model's items bit-identical
+// across batch sizes. The hook forces S for any splittable epilogue (1 = off).
+int f16_split(int64_t K, int64_t tiles, int64_t tile_floats, const gemm_split_ws & sw, bool resid) {
     constexpr int KC16 = 64;
     if (K % KC16) return 1;
     const int64_t nst = K / KC16;
     const int cus = cu_count();
     const int f = g_force_split.load();
-    if (f == 1 || (f < 1 && (tiles * 2 > cus || nst < 16))) return 1;
+    if (f == 1 || (f < 1 && (!resid || tiles * 2 > cus || nst < 16))) return 1;
     for (int S : {4, 3, 2}) {
         if (f >= 2 && S != f) continue;
         if (nst % S || nst / S < (f >= 2 ? 2 : 4) || tiles * S > cus || tiles * tile_floats * S > sw.part_floats ||
@@ -1604,7 +1606,7 @@ void dispatch_mfma(kargs a, hipStream_t s, const gemm_split_ws * sw) {
     const int bn = 32 * k_tiles[c].wn * k_tiles[c].ti, bm = 32 * k_tiles[c].wm * k_tiles[c].tj;
     a.tn = (int) (a.N / bn);
     a.tm = (int) ((a.M + bm - 1) / bm);
-    if (WF == W_F16 && can_split) a.split = f16_split(a.K, (int64_t) a.tn * a.tm, (int64_t) bn * bm, *sw);
+    if (WF == W_F16 && can_split) a.split = f16_split(a.K, (int64_t) a.tn * a.tm, (int64_t) bn * bm, *sw, a.ep.kind == EPI_RESID);
     if (a.split > 1) {
         const int64_t tiles = (int64_t) a.tn * a.tm;
         if (tiles * bn * bm * a.split > sw->part_floats || tiles > sw->cnt_n) {
