@@ -9,7 +9,9 @@
 //   A_Q8_K: max = first largest-|x| value, iscale = -127/max, q = min(127, rne(iscale*x)),
 //           d = 1/iscale (f32), bsums of 16                  quantize_row_q8_K_ref
 //   A_F16 / A_F32: the values rounded to f16 / as they are
-// The double sums of D floats are exact for rows whose magnitudes span less than 2^29, so their order
+// The double sums of D floats are exact when every partial sum fits 53 bits: each value is a multiple
+// of the unit in the last place of the smallest nonzero |x|, so that holds while max|x| / min|x| <
+// 2^30 / D (2^20 at D = 1024; squares: the same bound on the squared values), and then their order
 // (a DPP tree here, sequential in ggml) does not change them.
 #pragma once
 #include "kernels.h"
@@ -116,47 +118,53 @@ __device__ __forceinline__ void load_affine(const float * w, const float * b, in
     }
 }
 
+// LayerNorm of the loaded row v in place: ggml_norm, then * w and + b where given
+template <int NOCT>
+__device__ __forceinline__ void normalize_row(float (&v)[NOCT][8], int64_t D, bool has_w, bool has_b, const float (&gw)[NOCT][8],
+                                              const float (&gb)[NOCT][8], float eps, int lane) {
+    const int n_oct = (int) (D / 8);
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < NOCT; i++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) s += (double) v[i][e];
+    s = wave_sum_f64(s);
+    const float mean = (float) s / (float) D;
+    double s2 = 0.0;
+#pragma unroll
+    for (int i = 0; i < NOCT; i++) {
+        const bool live = lane + 64 * i < n_oct;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float t = __fsub_rn(v[i][e], mean);
+            v[i][e] = t;
+            if (live) s2 += (double) __fmul_rn(t, t);
+        }
+    }
+    s2 = wave_sum_f64(s2);
+    const float var = (float) (s2 / (double) D);
+    const float scale = 1.0f / sqrtf(__fadd_rn(var, eps));
+#pragma unroll
+    for (int i = 0; i < NOCT; i++) {
+        const int o = lane + 64 * i;
+        if (o >= n_oct) continue;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float t = __fmul_rn(v[i][e], scale);
+            if (has_w) t = __fmul_rn(t, gw[i][e]);
+            if (has_b) t = __fadd_rn(t, gb[i][e]);
+            v[i][e] = t;
+        }
+    }
+}
+
 // LayerNorm (NORM) of the loaded row v, then the output conversion of row `row` of out
 template <int OUT, bool NORM, int NOCT>
 __device__ __forceinline__ void finish_row(float (&v)[NOCT][8], int64_t row, int64_t D, bool has_w, bool has_b,
                                            const float (&gw)[NOCT][8], const float (&gb)[NOCT][8], float eps, const act_view & out,
                                            int lane) {
     const int n_oct = (int) (D / 8);
-    if constexpr (NORM) {
-        double s = 0.0;
-#pragma unroll
-        for (int i = 0; i < NOCT; i++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) s += (double) v[i][e];
-        s = wave_sum_f64(s);
-        const float mean = (float) s / (float) D;
-        double s2 = 0.0;
-#pragma unroll
-        for (int i = 0; i < NOCT; i++) {
-            const bool live = lane + 64 * i < n_oct;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float t = __fsub_rn(v[i][e], mean);
-                v[i][e] = t;
-                if (live) s2 += (double) __fmul_rn(t, t);
-            }
-        }
-        s2 = wave_sum_f64(s2);
-        const float var = (float) (s2 / (double) D);
-        const float scale = 1.0f / sqrtf(__fadd_rn(var, eps));
-#pragma unroll
-        for (int i = 0; i < NOCT; i++) {
-            const int o = lane + 64 * i;
-            if (o >= n_oct) continue;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                float t = __fmul_rn(v[i][e], scale);
-                if (has_w) t = __fmul_rn(t, gw[i][e]);
-                if (has_b) t = __fadd_rn(t, gb[i][e]);
-                v[i][e] = t;
-            }
-        }
-    }
+    if constexpr (NORM) normalize_row<NOCT>(v, D, has_w, has_b, gw, gb, eps, lane);
 #pragma unroll
     for (int i = 0; i < NOCT; i++) {
         const int o = lane + 64 * i;
