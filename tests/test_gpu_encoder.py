@@ -125,6 +125,22 @@ def test_tiny_separate_qkv_activation_formats_differ(jlib, oracle, models_dir, p
     check_parity(got, want, gtr, wtr, label=f"separate q/k/v {parts}")
 
 
+def test_tiny_f16_split_residual_with_layer_scale(jlib, oracle, models_dir):
+    """f16 blocks whose fc2 (K = 1024, 16 stages) splits K into four parts over few rows, with layer
+    scale in the residual epilogue that the last part runs: against the oracle end to end and per layer,
+    and within rounding of the same forward with the split forced off."""
+    cfg = forge.tiny("vjepa2", "f16", ffn_dim=1024, layer_scale=True, ln_random=True)
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 1, 4, 64)
+    check_parity(got, want, gtr, wtr, label="tiny vjepa2 f16, fc2 in four K parts, layer scale")
+    L = jlib.lib()
+    try:
+        assert L.jepa_amd_gemm_split(1) == 0
+        unsplit = jlib.Context(m).encode(x)
+    finally:
+        L.jepa_amd_gemm_split(-1)
+    assert np.abs(got - unsplit).max() <= 1e-4 * np.abs(unsplit).max()
+
+
 def test_batch_equals_single(jlib, models_dir):
     """Items of one call equal separate calls bit for bit (reference tests/test-batch.cpp:12-21): q8_0, whose
     K halves depend on the shape only. f16 weights split K by the tile count, which the batch changes, so
