@@ -1,0 +1,143 @@
+"""The reference's own command-line tools, compiled as they lie against include/jepa.h and linked to
+libjepa.so (`make -C oracle ref-tools`, which build() runs where the reference tree is present; the
+binaries travel in oracle/_ref/), run on the GPU: a caller of the reference switches to this library
+with no change to its code. What they print or save is compared with this library's Python binding
+of the same entry points (bit for bit: the same library code on the same inputs) and, for the
+encoder rows, with the oracle.
+
+- tools/jepa-bench.cpp: --mode encoder (batched), head and predictor, with its --json record.
+- tools/jepa-embed.cpp: an image (tests/golden/media) through jepa_load_image_rgb,
+  jepa_preprocess_image_rgb, jepa_encode and --pool none / cls; a THWC uint8 clip (--frames-npy)
+  through the same route with --pool mean and the attentive-pool head (--logits).
+"""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from jepa_amd import forge
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REF_BIN = os.path.join(ROOT, "oracle", "_ref")
+IMAGE = os.path.join(ROOT, "tests", "golden", "media", "coco_000000000724.jpg")
+
+pytestmark = pytest.mark.gpu
+
+
+def _tool(name):
+    p = os.path.join(REF_BIN, name)
+    if not os.access(p, os.X_OK):
+        pytest.skip(f"oracle/_ref/{name} is not built (make -C oracle ref-tools needs the reference tree)")
+    return p
+
+
+def _run(cmd, timeout=300):
+    print("run:", " ".join(os.path.basename(c) if os.path.isabs(c) else c for c in cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-3000:])
+    return r
+
+
+def _bench_json(exe, path, tmp_path, *args):
+    out = tmp_path / "bench.json"
+    _run([exe, "-m", path, *args, "--json", str(out)])
+    d = json.loads(out.read_text())
+    assert d["tool"] == "jepa-bench" and len(d["runs"]) == 1, d
+    return d["runs"][0]
+
+
+def _cos_rows(a, b):
+    a = a.astype(np.float64)
+    b = b.astype(np.float64)
+    return (a * b).sum(1) / (np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1))
+
+
+def test_jepa_bench_encoder_batched(jlib, models_dir, tmp_path):
+    """jepa-bench --mode encoder, two clips per jepa_encode call (its own synthetic input, the
+    generator this repository's inputs.make_input is pinned to): the run is on the GPU, and its token
+    count and device name are this library's."""
+    exe = _tool("jepa-bench")
+    path = forge.cached_model(forge.tiny("vjepa2", "q8_0"), models_dir)
+    r = _bench_json(exe, path, tmp_path, "--frames", "4", "--size", "64x64", "--batch", "2", "--repeat", "3", "--warmup", "1")
+    m = jlib.Model(path)
+    assert r["gpu"] is True and r["mode"] == "encoder"
+    assert r["device"] == jlib.lib().jepa_device_name(0).decode()
+    assert r["tokens"] == 2 * m.token_grid(4, 64, 64) and r["units"] == 2
+    assert 0 < r["ms_min"] <= r["ms_mean"] and r["wall_ms_min"] >= r["ms_min"]
+
+
+@pytest.mark.parametrize("mode", ["head", "predictor"])
+def test_jepa_bench_head_and_predictor(models_dir, tmp_path, mode):
+    """jepa-bench --mode head / predictor: the attentive-pool head and the masked predictor on one
+    item's encoder rows, through jepa_head and jepa_predict."""
+    exe = _tool("jepa-bench")
+    cfg = forge.tiny("vjepa2", "q8_0", n_classes=10, n_pool_layers=1, pred_dim=128, pred_layers=2, pred_ffn=512)
+    path = forge.cached_model(cfg, models_dir)
+    r = _bench_json(exe, path, tmp_path, "--mode", mode, "--frames", "4", "--size", "64x64", "--repeat", "3", "--warmup", "1")
+    assert r["gpu"] is True and r["mode"] == mode and r["units"] == 1
+    assert r["ms_mean"] > 0 and r["encoder_ms"] > 0
+
+
+def test_jepa_bench_vitl16_16f(jlib, models_dir, tmp_path):
+    """The reference's headline row (V-JEPA 2 ViT-L/16, 16 frames of 256x256, q8_0, one clip per call)
+    timed by its own tool on this library: jepa_context_last_compute_ms per call (device time of the
+    forward, as the tool reports it) and the wall time of jepa_encode (host input and output copies
+    included)."""
+    exe = _tool("jepa-bench")
+    path = forge.cached_model(forge.CONFIGS["vitl16_q8_0"], models_dir)
+    r = _bench_json(exe, path, tmp_path, "--repeat", "10", "--warmup", "2")
+    print(f"jepa-bench {r['model']} {r['shape']} {r['ftype']} on {r['device']}: {r['ms_mean']:.3f} ms mean "
+          f"(min {r['ms_min']:.3f}), wall {r['wall_ms_mean']:.3f} ms, {r['tokens_per_s']:.0f} tokens/s")
+    assert r["gpu"] is True and r["tokens"] == 2048 and r["frames"] == 16 and r["height"] == 256
+    assert 0 < r["ms_min"] <= r["ms_mean"] and r["wall_ms_min"] >= r["ms_min"]
+
+
+def test_jepa_embed_image(jlib, oracle, models_dir, tmp_path):
+    """jepa-embed on a JPEG with an image model (CLS token): the preprocessed input it dumps equals
+    jepa_preprocess_frames_rgb_ex with the model's default parameters on jepa_load_image_rgb's pixels,
+    its --pool none rows equal jepa_encode's on that input bit for bit (and the oracle's within the
+    encoder gate), and --pool cls gives jepa_pool_cls of those rows."""
+    exe = _tool("jepa-embed")
+    path = forge.cached_model(forge.tiny("hfvit", "f16", ln_random=True), models_dir)
+    rows_f, pooled_f, x_f = tmp_path / "rows.npy", tmp_path / "cls.npy", tmp_path / "x.npy"
+    _run([exe, "-m", path, "-i", IMAGE, "--pool", "none", "-o", str(rows_f), "--dump-input", str(x_f), "--print-n", "0"])
+    _run([exe, "-m", path, "-i", IMAGE, "-o", str(pooled_f), "--print-n", "0"])
+    x, rows, pooled = np.load(x_f), np.load(rows_f), np.load(pooled_f)
+    m = jlib.Model(path)
+    want_x = jlib.preprocess_frames(jlib.lib().jepa_preprocess_default_params(m.ptr), [jlib.load_image(IMAGE)])
+    np.testing.assert_array_equal(x.view(np.uint32), want_x[None].view(np.uint32))
+    ctx = jlib.Context(m)
+    got = ctx.encode(x)
+    np.testing.assert_array_equal(rows.view(np.uint32), got.view(np.uint32))
+    np.testing.assert_array_equal(pooled.reshape(-1).view(np.uint32), m.pool_cls(got).view(np.uint32))
+    want, _ = oracle.encode(path, x, 1, got.shape[0], m.dim)
+    c = _cos_rows(got, want)
+    print(f"jepa-embed image: {rows.shape[0]} rows x {rows.shape[1]}, cosine vs oracle mean {c.mean():.7f} min {c.min():.7f}")
+    assert c.mean() >= 0.9999 and c.min() >= 0.999
+
+
+def test_jepa_embed_clip_with_head(jlib, models_dir, tmp_path):
+    """jepa-embed --frames-npy on a THWC uint8 clip with a video model that carries an attentive-pool
+    head: --pool mean equals jepa_pool_mean of jepa_encode's rows on the input it dumps, and --logits
+    equals jepa_head_ex on those rows, bit for bit."""
+    exe = _tool("jepa-embed")
+    cfg = forge.tiny("vjepa2", "q8_0", ln_random=True, n_classes=10, n_pool_layers=1)
+    path = forge.cached_model(cfg, models_dir)
+    rng = np.random.default_rng(7)
+    frames = rng.integers(0, 256, size=(4, 72, 90, 3), dtype=np.uint8)
+    clip_f, feat_f, logit_f, x_f = (tmp_path / n for n in ("clip.npy", "feat.npy", "logits.npy", "x.npy"))
+    np.save(clip_f, frames)
+    _run([exe, "-m", path, "--frames-npy", str(clip_f), "--pool", "mean", "-o", str(feat_f), "--logits", str(logit_f),
+          "--dump-input", str(x_f), "--print-n", "0"])
+    x, feat, logits = np.load(x_f), np.load(feat_f), np.load(logit_f)
+    m = jlib.Model(path)
+    want_x = jlib.preprocess_frames(jlib.lib().jepa_preprocess_default_params(m.ptr), list(frames))
+    np.testing.assert_array_equal(x.view(np.uint32), want_x[None].view(np.uint32))
+    ctx = jlib.Context(m)
+    got = ctx.encode(x)
+    np.testing.assert_array_equal(feat.reshape(-1).view(np.uint32), m.pool_mean(got).view(np.uint32))
+    _, want_logits = ctx.head(got, pooled=False, logits=True)
+    assert logits.shape == (1, m.n_classes)
+    np.testing.assert_array_equal(logits.reshape(-1).view(np.uint32), want_logits.view(np.uint32))
