@@ -18,7 +18,7 @@
 
 namespace {
 
-constexpr int64_t MAX_PIXELS = 1ll << 28;   // 16384 x 16384
+constexpr int64_t MAX_PIXELS = 1ll << 28;   // 16384 x 16384 (products of header sizes are formed only where they cannot overflow)
 
 bool read_file(const char * path, std::vector<uint8_t> & buf) {
     FILE * f = fopen(path, "rb");
@@ -92,7 +92,7 @@ uint8_t * decode_png(const std::vector<uint8_t> & f, int * ph, int * pw, const c
         p += 12 + (size_t) len;
     }
     const int chans = ctype == 0 ? 1 : ctype == 2 ? 3 : ctype == 3 ? 1 : ctype == 4 ? 2 : ctype == 6 ? 4 : 0;
-    if (!ihdr || W == 0 || H == 0 || chans == 0 || interlace > 1 || (int64_t) W * H > MAX_PIXELS ||
+    if (!ihdr || W == 0 || H == 0 || chans == 0 || interlace > 1 || (uint64_t) W * H > (uint64_t) MAX_PIXELS ||
         !(depth == 8 || depth == 16 || (depth < 8 && (ctype == 0 || ctype == 3) && (depth == 1 || depth == 2 || depth == 4))) ||
         (ctype == 3 && (plte.size() < 3 || depth == 16))) {
         jepa_log("jepa: cannot decode image %s: unsupported or corrupt PNG\n", path);
@@ -180,7 +180,8 @@ uint8_t * decode_pnm(const std::vector<uint8_t> & f, int * ph, int * pw, const c
     };
     long W = 0, H = 0, mx = 0;
     const int chans = f[1] == '6' ? 3 : 1;
-    if (!num(W) || !num(H) || !num(mx) || p >= f.size() || W <= 0 || H <= 0 || mx <= 0 || mx > 255 || (int64_t) W * H > MAX_PIXELS ||
+    if (!num(W) || !num(H) || !num(mx) || p >= f.size() || W <= 0 || H <= 0 || mx <= 0 || mx > 255 || W > MAX_PIXELS || H > MAX_PIXELS ||
+        (int64_t) W * H > MAX_PIXELS ||
         f.size() - p - 1 < (size_t) W * H * chans) {
         jepa_log("jepa: cannot decode image %s: unsupported or truncated PNM\n", path);
         return nullptr;

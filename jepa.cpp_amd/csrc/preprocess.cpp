@@ -115,9 +115,10 @@ resample_axis resample_axis_for(int n_in, int n_out, int resample) {
     double peak = 0.0;
     for (int o = 0; o < n_out; o++) {
         const double centre = scale * (o + 0.5);
-        // inputs whose window rounds into [centre - reach, centre + reach), clipped to the image
-        const int first = std::max(0, (int) (centre - reach + 0.5));
-        const int end = std::min(n_in, (int) (centre + reach + 0.5));
+        // inputs whose window rounds into [centre - reach, centre + reach), clipped to the image (in
+        // double before the conversion, so that a very wide input cannot push it past INT_MAX)
+        const int first = (int) std::max(0.0, centre - reach + 0.5);
+        const int end = (int) std::min((double) n_in, centre + reach + 0.5);
         const size_t row0 = weight.size();
         double total = 0.0;
         for (int x = first; x < end; x++) {
@@ -199,10 +200,11 @@ bool pre_plan_for(const jepa_preprocess_params * p, int h, int w, pre_plan & g) 
     }
     rh = std::max<int64_t>(rh, 1);
     rw = std::max<int64_t>(rw, 1);
-    if (rh * rw > JEPA_PRE_MAX_PIXELS) {
+    // each side first: a large resize_short at an extreme aspect ratio would overflow the product
+    if (rh > JEPA_PRE_MAX_PIXELS || rw > JEPA_PRE_MAX_PIXELS || rh * rw > JEPA_PRE_MAX_PIXELS) {
         jepa_log("jepa: preprocess: %dx%d at shortest edge %d resizes to %lldx%lld = %.1f megapixels, over the %lld-megapixel "
                  "limit (the aspect ratio makes this buffer large)\n",
-                 h, w, p->resize_short, (long long) rh, (long long) rw, (double) (rh * rw) / 1048576.0,
+                 h, w, p->resize_short, (long long) rh, (long long) rw, (double) rh * (double) rw / 1048576.0,
                  (long long) (JEPA_PRE_MAX_PIXELS >> 20));
         return false;
     }
