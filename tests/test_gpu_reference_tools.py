@@ -9,9 +9,12 @@ encoder rows, with the oracle.
 - tools/jepa-embed.cpp: an image (tests/golden/media) through jepa_load_image_rgb,
   jepa_preprocess_image_rgb, jepa_encode and --pool none / cls; a THWC uint8 clip (--frames-npy)
   through the same route with --pool mean and the attentive-pool head (--logits).
+- tools/jepa-classify.cpp: a THWC uint8 clip through its own preprocessing loop, the encoder, the
+  head and its top-k listing.
 """
 import json
 import os
+import re
 import subprocess
 
 import numpy as np
@@ -141,3 +144,33 @@ def test_jepa_embed_clip_with_head(jlib, models_dir, tmp_path):
     _, want_logits = ctx.head(got, pooled=False, logits=True)
     assert logits.shape == (1, m.n_classes)
     np.testing.assert_array_equal(logits.reshape(-1).view(np.uint32), want_logits.view(np.uint32))
+
+
+def test_jepa_classify_clip(jlib, models_dir, tmp_path):
+    """jepa-classify --frames-npy on a THWC uint8 clip with a video model that carries an attentive-pool
+    head: the logits it saves equal jepa_head_ex on jepa_encode's rows of the input it dumps, bit for
+    bit, and its printed top-k (jepa_softmax, jepa_top_k, jepa_model_label) ranks those logits with
+    their softmax percentages."""
+    exe = _tool("jepa-classify")
+    cfg = forge.tiny("vjepa2", "q8_0", ln_random=True, n_classes=10, n_pool_layers=1)
+    path = forge.cached_model(cfg, models_dir)
+    frames = np.random.default_rng(11).integers(0, 256, size=(4, 80, 64, 3), dtype=np.uint8)
+    clip_f, logit_f, x_f = (tmp_path / n for n in ("clip.npy", "logits.npy", "x.npy"))
+    np.save(clip_f, frames)
+    r = _run([exe, "-m", path, "--frames-npy", str(clip_f), "-k", "3", "--logits", str(logit_f), "--dump-input", str(x_f)])
+    x, logits = np.load(x_f), np.load(logit_f)
+    m = jlib.Model(path)
+    ctx = jlib.Context(m)
+    got = ctx.encode(x)
+    _, want = ctx.head(got, pooled=False, logits=True)
+    assert logits.shape == (m.n_classes,)
+    np.testing.assert_array_equal(logits.view(np.uint32), want.view(np.uint32))
+    # "  %2d. %6.2f%%  [%3d] label" per class
+    top = [m_.groups() for m_ in (re.match(r"^\s*(\d+)\.\s+([\d.]+)%\s+\[\s*(\d+)\]", line) for line in r.stdout.splitlines()) if m_]
+    assert len(top) == 3, r.stdout
+    p = np.exp(want.astype(np.float64) - want.max())
+    p /= p.sum()
+    order = np.argsort(-want, kind="stable")[:3]
+    for rank, ((k, pct, idx), i) in enumerate(zip(top, order)):
+        assert int(k) == rank + 1 and int(idx) == i, (top, order)
+        assert abs(float(pct) - 100 * p[i]) <= 0.006, (pct, p[i])
