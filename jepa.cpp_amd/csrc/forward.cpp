@@ -109,6 +109,9 @@ bool ws_alloc_blocks(fwd_workspace & w, int64_t n_items, int64_t R, int64_t D, i
                     ws_alloc(w, (void **) &w.out, (size_t) rows * D * 4);
     if (!ok) return false;
     gemm_split_ws_size(rows, &w.split.part_floats, &w.split.cnt_n);
+    // clips are batched into one forward here, where the reference runs a graph per clip: f16 split-K
+    // by tile count would make a clip's rounding depend on how many clips share the call
+    w.split.f16_by_tiles = !w.video;
     if (!ws_alloc(w, (void **) &w.split.part, (size_t) w.split.part_floats * 4) ||
         !ws_alloc(w, (void **) &w.split.cnt, (size_t) w.split.cnt_n * 4)) return false;
     launch_fill_zero(w.split.cnt, (size_t) w.split.cnt_n * 4, s);

@@ -1573,16 +1573,18 @@ void launch_tiles(int c, const kargs & a, hipStream_t s) {
 // arrival atomic, the last part's loads) costs ~2 us, so only K >= 1024 (16 stages) splits, into the
 // largest S of 4, 3, 2 that leaves each part 4 stages and each workgroup its own CU. The summation order
 // then depends on the row count through the tile count (rounding-level differences between batch sizes,
-// as f16 files have in the reference's batched graph), so only the residual GEMMs of f16 blocks split
-// by themselves: the f16 patch embedding of a q8_0 / q4_K model keeps that model's items bit-identical
-// across batch sizes. The hook forces S for any splittable epilogue (1 = off).
+// as f16 files have in the reference's batched image graph), so only the residual GEMMs of f16 blocks
+// split by themselves, and only where the workspace allows it: the f16 patch embedding of a q8_0 /
+// q4_K model keeps that model's items bit-identical across batch sizes, and so does every GEMM of a
+// video workspace (the reference encodes each clip in a graph of its own, so n clips in one call must
+// equal n one-clip calls exactly). The hook forces S for any splittable epilogue (1 = off).
 int f16_split(int64_t K, int64_t tiles, int64_t tile_floats, const gemm_split_ws & sw, bool resid) {
     constexpr int KC16 = 64;
     if (K % KC16) return 1;
     const int64_t nst = K / KC16;
     const int cus = cu_count();
     const int f = g_force_split.load();
-    if (f == 1 || (f < 1 && (!resid || tiles * 2 > cus || nst < 16))) return 1;
+    if (f == 1 || (f < 1 && (!sw.f16_by_tiles || !resid || tiles * 2 > cus || nst < 16))) return 1;
     for (int S : {4, 3, 2}) {
         if (f >= 2 && S != f) continue;
         if (nst % S || nst / S < (f >= 2 ? 2 : 4) || tiles * S > cus || tiles * tile_floats * S > sw.part_floats ||

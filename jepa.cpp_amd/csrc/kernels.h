@@ -58,6 +58,10 @@ struct gemm_split_ws {
     float * part = nullptr;
     int * cnt = nullptr;
     int64_t part_floats = 0, cnt_n = 0;
+    // f16 residual GEMMs may split K by the launch's tile count, so that an output's rounding can
+    // depend on the number of rows (false: only a forced split, for workspaces whose batched items
+    // must equal one-item calls bit for bit)
+    bool f16_by_tiles = true;
 };
 void gemm_split_ws_size(int64_t max_rows, int64_t * part_floats, int64_t * cnt_n);
 

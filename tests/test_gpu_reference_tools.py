@@ -11,6 +11,7 @@ encoder rows, with the oracle.
   through the same route with --pool mean and the attentive-pool head (--logits).
 - tools/jepa-classify.cpp: a THWC uint8 clip through its own preprocessing loop, the encoder, the
   head and its top-k listing.
+- tests/test-batch.cpp: the reference's own batched-against-single test, with its exit status.
 """
 import json
 import os
@@ -174,3 +175,30 @@ def test_jepa_classify_clip(jlib, models_dir, tmp_path):
     for rank, ((k, pct, idx), i) in enumerate(zip(top, order)):
         assert int(k) == rank + 1 and int(idx) == i, (top, order)
         assert abs(float(pct) - 100 * p[i]) <= 0.006, (pct, p[i])
+
+
+def test_reference_test_batch(models_dir, tmp_path):
+    """The reference's own tests/test-batch.cpp, compiled as it lies against this library: the eight
+    COCO fixture images (tests/golden/media, the reference's tests/fixtures/media) through image models
+    in one call, in chunks of 3 and one at a time (f32 bit for bit, other file types at its cosine gate),
+    and two clips of 18 frames (2304 rows each) of an f16 video model in one call against two calls,
+    bit for bit for every file type."""
+    exe = _tool("test-batch")
+    media = os.path.join(ROOT, "tests", "golden", "media")
+    models = [forge.cached_model(cfg, models_dir) for cfg in (
+        forge.tiny("hfvit", "f32", ln_random=True), forge.tiny("hfvit", "f16", ln_random=True),
+        forge.tiny("ijepa", "q8_0"))]
+    video = forge.cached_model(forge.tiny("vjepa2", "f16", ffn_dim=1024, img_size=256, ln_random=True), models_dir)
+    rng = np.random.default_rng(3)
+    clips = []
+    for i in range(2):
+        c = tmp_path / f"clip{i}.npy"
+        np.save(c, rng.integers(0, 256, size=(18, 256, 256, 3), dtype=np.uint8))
+        clips += ["--clip", str(c)]
+    args = [exe, "--media", media]
+    for p in models:
+        args += ["--image", p]
+    r = _run(args + ["--video", video] + clips)
+    print(r.stdout)
+    assert "all batched outputs match the per-item path" in r.stdout
+    assert r.stdout.count(" OK") >= 3 * 5 + 1 and " FAIL" not in r.stdout

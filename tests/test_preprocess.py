@@ -262,9 +262,15 @@ def test_jpeg_progressive_is_refused(tmp_path):
         _lib.load_image(path)
 
 
-def test_reference_fixture_jpeg():
-    """tests/fixtures/media/coco_000000000724.jpg of the reference (a COCO photo, baseline 4:4:4)."""
-    path = os.path.join(GOLDEN, "coco_000000000724.jpg")
+COCO = sorted(f for f in os.listdir(GOLDEN) if f.startswith("coco_") and f.endswith(".jpg"))
+
+
+@pytest.mark.parametrize("name", COCO)
+def test_reference_fixture_jpeg(name):
+    """The eight COCO photos of the reference's tests/fixtures/media (what its test-batch and parity
+    tests encode): decoded pixels equal PIL's (libjpeg) bit for bit, and so does the whole file
+    pipeline (jepa_preprocess_image_file with the library defaults)."""
+    path = os.path.join(GOLDEN, name)
     got = _lib.load_image(path)
     want = np.asarray(Image.open(path).convert("RGB"))
     assert np.array_equal(got, want)
