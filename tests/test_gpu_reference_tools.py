@@ -12,6 +12,8 @@ encoder rows, with the oracle.
 - tools/jepa-classify.cpp: a THWC uint8 clip through its own preprocessing loop, the encoder, the
   head and its top-k listing.
 - tests/test-batch.cpp: the reference's own batched-against-single test, with its exit status.
+- tests/test-predictor.cpp: the reference's own predictor test in its numpy-case mode, on cases the
+  oracle's predictor writes.
 """
 import json
 import os
@@ -202,3 +204,32 @@ def test_reference_test_batch(models_dir, tmp_path):
     print(r.stdout)
     assert "all batched outputs match the per-item path" in r.stdout
     assert r.stdout.count(" OK") >= 3 * 5 + 1 and " FAIL" not in r.stdout
+
+
+@pytest.mark.parametrize("family,ftype", [("vjepa2", "q8_0"), ("vjepa2", "f16"), ("vjepa2", "f32"), ("vjepa2_1", "q8_0"),
+                                          ("vitl16", "q8_0")])
+def test_reference_test_predictor_case(oracle, models_dir, tmp_path, family, ftype):
+    """The reference's own tests/test-predictor.cpp in its --case mode (DIR/{enc,ctx_idx,tgt_idx,pred}.npy,
+    tests/test-predictor.cpp:612-637), compiled as it lies against this library: jepa_predict_mod on the
+    case's encoder rows and ids against pred.npy, written here by the oracle's predictor on the same
+    file, under the reference's own GPU bars for the file type. Tiny V-JEPA 2 / 2.1 predictors, and the
+    V-JEPA 2 ViT-L predictor (384 wide, 12 blocks) over 2048 tokens split 1024 / 1024."""
+    exe = _tool("test-predictor")
+    if family == "vitl16":
+        cfg = forge.CONFIGS["vitl16_pred_q8_0"]
+        n_tok, n_ctx = 2048, 1024
+    else:
+        kw = {"pred_mlp_embed": True} if family == "vjepa2_1" else {}
+        cfg = forge.tiny(family, ftype, ln_random=True, pred_dim=128, pred_layers=2, pred_ffn=512, w_std=0.08, **kw)
+        n_tok, n_ctx = 32, 20
+    path = forge.cached_model(cfg, models_dir)
+    rng = np.random.default_rng(17)
+    enc = rng.standard_normal((n_tok, cfg.embed_dim)).astype(np.float32)
+    perm = rng.permutation(n_tok)
+    ctx_ids, tgt_ids = perm[:n_ctx], perm[n_ctx:]
+    pred = oracle.predict(path, enc, ctx_ids, tgt_ids, cfg.embed_dim, mask_index=1, modality=1)
+    for f, a in (("enc", enc), ("ctx_idx", ctx_ids.astype(np.int64)), ("tgt_idx", tgt_ids.astype(np.int64)), ("pred", pred)):
+        np.save(tmp_path / f"{f}.npy", a)
+    r = _run([exe, "--vjepa2", path, "--case", str(tmp_path)])
+    print(r.stdout)
+    assert r.stdout.rstrip().endswith("PASS") and " OK" in r.stdout, r.stdout
