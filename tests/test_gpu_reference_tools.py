@@ -233,3 +233,16 @@ def test_reference_test_predictor_case(oracle, models_dir, tmp_path, family, fty
     r = _run([exe, "--vjepa2", path, "--case", str(tmp_path)])
     print(r.stdout)
     assert r.stdout.rstrip().endswith("PASS") and " OK" in r.stdout, r.stdout
+
+
+@pytest.mark.parametrize("name", ["vitb16_2_1_q8_0", "vits16_f16"])
+def test_reference_test_batch_full_size(models_dir, name):
+    """The reference's own tests/test-batch.cpp on two of the benchmark configurations at full size: V-JEPA
+    2.1 ViT-B/16 384x384 q8_0 through its image path (eight images in one call: the batch of 8 images
+    the image benchmark runs) and the LeJEPA-shaped ViT-S/16 224x224 f16 model, over the eight COCO
+    fixtures in one call, in chunks of 3 and one at a time."""
+    exe = _tool("test-batch")
+    path = forge.cached_model(forge.CONFIGS[name], models_dir)
+    r = _run([exe, "--media", os.path.join(ROOT, "tests", "golden", "media"), "--image", path])
+    print(r.stdout)
+    assert "all batched outputs match the per-item path" in r.stdout and " FAIL" not in r.stdout
