@@ -274,8 +274,15 @@ __device__ __forceinline__ void lds_take(V & v) { asm volatile("" : "+v"(v)); }
 // Y[m][n] over the workgroup tile (n0, m0). K advances one stage (KC) per iteration; NST - 1 stages
 // are in flight as direct HBM->LDS copies (buffer_load_dwordx4 ... lds: each lane moves 16 B, a wave
 // 8 rows), so a stage's loads have NST - 1 compute phases to land. One barrier per stage.
+// The fields the prologue needs come first as scalar arguments, which the dispatch preloads into SGPRs
+// (-amdgpu-kernarg-preload-count: a struct argument is not preloaded), so that the first copies do
+// not wait on a load of the argument block; the rest of kargs follows in memory (launch: GEMM_ARGS).
 template <int WF, int EPI, int WN, int WM, int TI, int TJ>
-__global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(kargs a) {
+__global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, const void * pB, const void * pAd, const void * pBd,
+                                                               int pM, int pN, int pK, int ptn, int ptm, int psplit, kargs a_rest) {
+    kargs a = a_rest;
+    a.A = (const _Float16 *) pA; a.B = (const _Float16 *) pB; a.Ad = (const uint16_t *) pAd; a.Bd = pBd;
+    a.M = pM; a.N = pN; a.K = pK; a.tn = ptn; a.tm = ptm; a.split = psplit;
     using T = tiling<WF, WN, WM, TI, TJ>;
     constexpr int BN = T::BN, NST = T::NST, NW = T::NW, KC = T::KC, ESZ = T::ESZ;
     __shared__ __attribute__((aligned(16))) unsigned char smem[T::LDS];
@@ -1535,32 +1542,35 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
     return b;
 }
 
+// k_gemm_mfma's arguments: the prologue's fields as scalars, then the whole kargs
+#define GEMM_ARGS(a) (a).A, (a).B, (const void *) (a).Ad, (a).Bd, (int) (a).M, (int) (a).N, (int) (a).K, (a).tn, (a).tm, (a).split, (a)
+
 template <int WF, int EPI>
 void launch_tiles(int c, const kargs & a, hipStream_t s) {
     const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm * (a.split > 1 ? a.split : 1));
     if constexpr (EPI == EPI_GELU_Q8_K) {   // 256-wide tiles only (pick_tile keeps to them)
-        if (c == 6) k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a);
-        if (c == 7) k_gemm_mfma<WF, EPI, 8, 1, 1, 2><<<grid, 512, 0, s>>>(a);
+        if (c == 6) k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a));
+        if (c == 7) k_gemm_mfma<WF, EPI, 8, 1, 1, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a));
         if constexpr (WF != W_Q4K)   // q4_K runs the 256x64 tile only
-            if (c == 0) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a);
+            if (c == 0) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a));
     } else if constexpr (WF == W_Q4K || WF == W_Q40) {
         switch (c) {
-            case 0: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a); break;
-            case 8: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 3, 1><<<grid, 512, 0, s>>>(a); break;
-            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(a); break;
-            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(a); break;
-            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(a); break;
-            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a); break;
+            case 0: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 8: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 3, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
         }
     } else {
         switch (c) {
-            case 0: k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(a); break;
-            case 1: k_gemm_mfma<WF, EPI, 2, 4, 3, 1><<<grid, 512, 0, s>>>(a); break;
-            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(a); break;
-            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(a); break;
-            case 4: k_gemm_mfma<WF, EPI, 2, 4, 1, 1><<<grid, 512, 0, s>>>(a); break;
-            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(a); break;
-            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(a); break;
+            case 0: k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 1: k_gemm_mfma<WF, EPI, 2, 4, 3, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 4: k_gemm_mfma<WF, EPI, 2, 4, 1, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
         }
     }
 }
@@ -1677,6 +1687,11 @@ void launch_gemm(const dev_linear & W, const act_view & X, int64_t M, const gemm
     a.M = M; a.N = W.n_out; a.K = W.n_in;
     a.ep = ep;
     if (M <= 0) return;
+    if (M > INT32_MAX || a.N > INT32_MAX || a.K > INT32_MAX) {   // k_gemm_mfma takes them as 32-bit scalars
+        jepa_log("jepa: internal error: GEMM of %lld x %lld x %lld exceeds 32-bit sizes\n", (long long) M, (long long) a.N,
+                 (long long) a.K);
+        return;
+    }
     if (a.ep.kind == EPI_F32 && a.ep.rin <= 0) { a.ep.rin = M; a.ep.rout = M; a.ep.pre = 0; }   // identity row map
     if (W.fmt == W_F32) {
         dim3 grid((unsigned) ((a.N + 31) / 32), (unsigned) ((M + 15) / 16));
