@@ -230,7 +230,11 @@ struct tiling {
     static constexpr int X_DW = 0, X_SC = BN * 4, X_MIN = X_SC + BN * 8, X_DA = X_MIN + BN * 32, X_BS = X_DA + BM * 4;
     static constexpr int XSB = WF == W_Q4K ? X_BS + BM * 32 : 0;
     static constexpr int NXSB = WF == W_Q4K ? 3 : 0;
-    static constexpr int NST_MAX = WF == W_Q4K ? 4 : 6;
+    // At most four stages in LDS (three in flight beyond the one computed): the 128x64 tile with six
+    // (its LDS fits them) issued a 120 KB burst of copies per workgroup at the start and ran slower
+    // (ViT-L out-proj 0.39 -> 0.36 ms and fc2 0.89 -> 0.86 ms per clip with four, ViT-S/16 0.554 ->
+    // 0.529 ms per image; five and three measured in between)
+    static constexpr int NST_MAX = 4;
     static constexpr int NST_FIT = (160 * 1024 - NXSB * XSB) / STAGE;
     static constexpr int NST = NST_FIT < NST_MAX ? NST_FIT : NST_MAX;
     static constexpr int LDS = NST * STAGE + NXSB * XSB;
