@@ -281,7 +281,7 @@ __device__ __forceinline__ void lds_take(V & v) { asm volatile("" : "+v"(v)); }
 // The fields the prologue needs come first as scalar arguments, which the dispatch preloads into SGPRs
 // (-amdgpu-kernarg-preload-count: a struct argument is not preloaded), so that the first copies do
 // not wait on a load of the argument block; the rest of kargs follows in memory (launch: GEMM_ARGS).
-template <int WF, int EPI, int WN, int WM, int TI, int TJ>
+template <int WF, int EPI, int WN, int WM, int TI, int TJ, bool RE = false>
 __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, const void * pB, const void * pAd, const void * pBd,
                                                                int pM, int pN, int pK, int ptn, int ptm, int psplit, kargs a_rest) {
     kargs a = a_rest;
@@ -371,10 +371,39 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, 
     // q8_0 / q4_0 stages issue their PARTS copies one per compute step of the stage NST - 1 earlier
     // (spread, so that no wave stalls behind a burst of copies). Stages past the end copy the last
     // stage's data again into the buffer of the stage just finished, which no one reads any more:
-    // the copies stay unconditional (a branch around them would split the software pipeline).
+    // the copies stay unconditional (a branch around them would split the software pipeline). In the
+    // RE kernels they all go to the buffer of stage nst (that of stage nst - 4, long finished, or one
+    // no stage uses), so that the buffers of stages nst - 3 and nst - 2 are free for the RoPE rows.
     [[maybe_unused]] auto issue_part = [&](int64_t st, int p) {
         const int64_t sa = st < nst ? st : nst - 1;
-        issue_tile(st, sa, p);
+        issue_tile(RE ? (st < nst ? st : nst) : st, sa, p);
+    };
+    // RE (QKV epilogue with early RoPE rows, chosen on the host for q8_0 / q4_0 weights, heads of 64, K
+    // a whole number of at least three stages and tiles with four stage buffers): the main loop copies
+    // the cos and sin rows of the tile's tokens before its last two stages, cos rows into the buffer of
+    // stage nst - 3, sin rows into that of stage nst - 2 (both read for the last time before the
+    // barrier of the stage after them), so that they land during those stages instead of after them.
+    // The layout is the epilogue's: copy L holds rows 4 L .. 4 L + 3, 16-byte chunk c of row r in
+    // slot c ^ (r mod 16). Tiles of V columns take no RoPE: their copies go through empty resources
+    // and read nothing (no branch splits the pipeline).
+    constexpr int RCH = T::BM * 64 * 4 / 1024;   // 1 KB copies per table
+    [[maybe_unused]] brsrc rRc, rRs;
+    if constexpr (RE) {
+        static_assert(EPI == EPI_QKV && (WF == W_Q32 || WF == W_Q40) && RCH % NW == 0 && T::BM * 64 * 4 <= T::STAGE &&
+                      NST >= 4, "early RoPE rows need four stage buffers of at least BM rows of 64 floats");
+        const int64_t tb = n0 + a.ep.col0 < 2 * (int64_t) a.ep.D ? (int64_t) a.ep.R * 64 * 4 : 0;
+        rRc = make_brsrc(a.ep.rope_c, tb);
+        rRs = make_brsrc(a.ep.rope_s, tb);
+    }
+    [[maybe_unused]] auto issue_rope_rows = [&](const brsrc & r, int64_t st) {
+        unsigned char * dst = smem + (int) (st % NST) * T::STAGE;
+        const int r_l = lane >> 4, sl = lane & 15;
+#pragma unroll
+        for (int c = 0; c < RCH / NW; c++) {
+            const int L = NW * c + wave, row = 4 * L + r_l;
+            const int64_t m = m0 + row, mm = m < M ? m : M - 1;
+            dma_to_lds<16>(r, (uint32_t) ((mm % a.ep.R) * 256 + ((sl ^ (row & 15)) << 4)), 0, dst + 1024 * L);
+        }
     };
     // q4_K super-block data of this workgroup's super-block st / 2 (data of K super-block (st + kst0) / 2),
     // copied with stage st when st is even, into buffer (st / 2) % 3; nothing past the last stage
@@ -592,11 +621,12 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, 
         __builtin_amdgcn_sched_barrier(0);
         // one full stage; CROSS: publish stage st+1 and start its pipeline in the last two steps;
         // FIRST (stage 0): issue the copies of stages 1..NST-1 instead of those of stage NST-1 alone
-        auto body = [&](int64_t st, auto cross_c, auto first_c) {
+        auto body = [&](int64_t st, auto cross_c, auto first_c, auto extra_c) {
             constexpr bool CROSS = decltype(cross_c)::value, FIRST = decltype(first_c)::value;
             constexpr int Q = FIRST ? (NST - 1) * P1 : P1;          // copies this stage issues
             // copies younger than the last one of stage st+1 at its publication (step U-2)
-            constexpr int NB = FIRST ? (U - 1) * Q / U - P1 : NBAR;
+            // copies issued before this body that are younger than stage st+1's (the RoPE rows)
+            constexpr int NB = (FIRST ? (U - 1) * Q / U - P1 : NBAR) + decltype(extra_c)::value;
             static_assert(NB >= 0 && NB < 64, "barrier count");
             const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
             const unsigned char * nbase = smem + (int) ((st + 1) % NST) * T::STAGE;
@@ -636,10 +666,19 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, 
         };
         // stage 0 always publishes stage 1 (with a single full stage that is a copy of stage 0 into an
         // unused buffer, read and discarded)
-        if (nfull > 0) body(0, std::true_type{}, std::true_type{});
-        for (int64_t st = 1; st + 1 < nfull; st++) body(st, std::true_type{}, std::false_type{});
-        prefetch_resid();
-        if (nfull > 1) body(nfull - 1, std::false_type{}, std::false_type{});
+        using X0 = std::integral_constant<int, 0>;
+        if (nfull > 0) body(0, std::true_type{}, std::true_type{}, X0{});
+        if constexpr (RE) {   // nfull == nst >= 3
+            for (int64_t st = 1; st + 2 < nfull; st++) body(st, std::true_type{}, std::false_type{}, X0{});
+            issue_rope_rows(rRc, nfull - 3);
+            body(nfull - 2, std::true_type{}, std::false_type{}, std::integral_constant<int, RCH / NW>{});
+            issue_rope_rows(rRs, nfull - 2);
+            body(nfull - 1, std::false_type{}, std::false_type{}, X0{});
+        } else {
+            for (int64_t st = 1; st + 1 < nfull; st++) body(st, std::true_type{}, std::false_type{}, X0{});
+            prefetch_resid();
+            if (nfull > 1) body(nfull - 1, std::false_type{}, std::false_type{}, X0{});
+        }
         // final half stage (K % 128 == 64): blocks 0 and 1 of stage nfull, after all copies landed
         if (nfull < nst) {
             stage_barrier<0>();
@@ -1083,12 +1122,24 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, 
     // tokens are contiguous), and read per lane from LDS; gathering them per lane from the tables (a
     // 16-byte piece of 32 different rows per load) cost ~4 us of the ViT-L QKV GEMM's 31. 16-byte
     // chunk c of row r sits in slot c ^ (r mod chunks per row), so the 32 tokens of one LDS read fall
-    // on different banks. Rows past M copy row M - 1 (their results are dropped).
+    // on different banks. Rows past M copy row M - 1 (their results are dropped). RE kernels have
+    // copied them during the main loop's last two stages (ViT-L 16f q8_0 QKV 0.686 -> 0.672 ms per
+    // clip; without any RoPE rows it would take 0.609).
     [[maybe_unused]] const unsigned char * lrc = nullptr;
     [[maybe_unused]] const unsigned char * lrs = nullptr;
+    [[maybe_unused]] bool rope_late = false;
     if constexpr (EPI == EPI_QKV) {
         const int hd = a.ep.hd;
-        if (a.ep.rope_c && (hd == 32 || hd == 64) && n0 + a.ep.col0 < 2 * (int64_t) a.ep.D && 2 * T::BM * hd * 4 <= T::LDS) {
+        if constexpr (RE) {
+            // copied by the main loop before its last two stages; every wave has waited for its own
+            // copies (vmcnt(0) at the loop's end), the barrier makes all of them visible
+            if (n0 + a.ep.col0 < 2 * (int64_t) a.ep.D) {
+                __syncthreads();
+                lrc = smem + (int) ((nst - 3) % NST) * T::STAGE;
+                lrs = smem + (int) ((nst - 2) % NST) * T::STAGE;
+            }
+        } else if (a.ep.rope_c && (hd == 32 || hd == 64) && n0 + a.ep.col0 < 2 * (int64_t) a.ep.D && 2 * T::BM * hd * 4 <= T::LDS) {
+            rope_late = true;
             __builtin_amdgcn_s_waitcnt(0);      // no HBM->LDS copy of this wave still in flight
             __syncthreads();                    // every wave is past its last read of the stage buffers
             unsigned char * wc = smem;
@@ -1120,7 +1171,7 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, 
                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     if constexpr (EPI == EPI_QKV) {
-        if (lrc) {
+        if (rope_late) {
             __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0): this wave's row copies (and bias loads) have landed
             __syncthreads();
         }
@@ -1549,32 +1600,48 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
 // k_gemm_mfma's arguments: the prologue's fields as scalars, then the whole kargs
 #define GEMM_ARGS(a) (a).A, (a).B, (const void *) (a).Ad, (a).Bd, (int) (a).M, (int) (a).N, (int) (a).K, (a).tn, (a).tm, (a).split, (a)
 
+// The QKV GEMM of q8_0 / q4_0 weights with heads of 64 runs the RE kernel (RoPE rows copied during the
+// last two stages) wherever K is a whole number of at least three stages and the tile has four stage
+// buffers of at least BM rows of 64 floats; elsewhere the rows are copied after the main loop.
+template <int WF, int EPI, int WN, int WM, int TI, int TJ>
+void launch_tile(const kargs & a, unsigned grid, hipStream_t s) {
+    using T = tiling<WF, WN, WM, TI, TJ>;
+    if constexpr (EPI == EPI_QKV && (WF == W_Q32 || WF == W_Q40) && (T::BM * 64 * 4 / 1024) % T::NW == 0 &&
+                  T::BM * 64 * 4 <= T::STAGE && T::NST >= 4) {
+        if (a.ep.rope_c && a.ep.rope_s && a.ep.hd == 64 && a.K % T::KC == 0 && a.K / T::KC >= 3) {
+            k_gemm_mfma<WF, EPI, WN, WM, TI, TJ, true><<<grid, T::NT, 0, s>>>(GEMM_ARGS(a));
+            return;
+        }
+    }
+    k_gemm_mfma<WF, EPI, WN, WM, TI, TJ><<<grid, T::NT, 0, s>>>(GEMM_ARGS(a));
+}
+
 template <int WF, int EPI>
 void launch_tiles(int c, const kargs & a, hipStream_t s) {
     const unsigned grid = (unsigned) ((int64_t) a.tn * a.tm * (a.split > 1 ? a.split : 1));
     if constexpr (EPI == EPI_GELU_Q8_K) {   // 256-wide tiles only (pick_tile keeps to them)
-        if (c == 6) k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a));
-        if (c == 7) k_gemm_mfma<WF, EPI, 8, 1, 1, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a));
+        if (c == 6) launch_tile<WF, EPI, 4, 2, 2, 1>(a, grid, s);
+        if (c == 7) launch_tile<WF, EPI, 8, 1, 1, 2>(a, grid, s);
         if constexpr (WF != W_Q4K)   // q4_K runs the 256x64 tile only
-            if (c == 0) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a));
+            if (c == 0) launch_tile<WF, EPI, 4, 2, 2, 2>(a, grid, s);
     } else if constexpr (WF == W_Q4K || WF == W_Q40) {
         switch (c) {
-            case 0: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 8: if constexpr (WF == W_Q40) k_gemm_mfma<WF, EPI, 4, 2, 3, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 0: if constexpr (WF == W_Q40) launch_tile<WF, EPI, 4, 2, 2, 2>(a, grid, s); break;
+            case 8: if constexpr (WF == W_Q40) launch_tile<WF, EPI, 4, 2, 3, 1>(a, grid, s); break;
+            case 2: launch_tile<WF, EPI, 2, 4, 2, 1>(a, grid, s); break;
+            case 3: launch_tile<WF, EPI, 4, 2, 1, 2>(a, grid, s); break;
+            case 5: launch_tile<WF, EPI, 4, 2, 1, 1>(a, grid, s); break;
+            default: launch_tile<WF, EPI, 4, 2, 2, 1>(a, grid, s); break;
         }
     } else {
         switch (c) {
-            case 0: k_gemm_mfma<WF, EPI, 4, 2, 2, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 1: k_gemm_mfma<WF, EPI, 2, 4, 3, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 2: k_gemm_mfma<WF, EPI, 2, 4, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 3: k_gemm_mfma<WF, EPI, 4, 2, 1, 2><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 4: k_gemm_mfma<WF, EPI, 2, 4, 1, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            case 5: k_gemm_mfma<WF, EPI, 4, 2, 1, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
-            default: k_gemm_mfma<WF, EPI, 4, 2, 2, 1><<<grid, 512, 0, s>>>(GEMM_ARGS(a)); break;
+            case 0: launch_tile<WF, EPI, 4, 2, 2, 2>(a, grid, s); break;
+            case 1: launch_tile<WF, EPI, 2, 4, 3, 1>(a, grid, s); break;
+            case 2: launch_tile<WF, EPI, 2, 4, 2, 1>(a, grid, s); break;
+            case 3: launch_tile<WF, EPI, 4, 2, 1, 2>(a, grid, s); break;
+            case 4: launch_tile<WF, EPI, 2, 4, 1, 1>(a, grid, s); break;
+            case 5: launch_tile<WF, EPI, 4, 2, 1, 1>(a, grid, s); break;
+            default: launch_tile<WF, EPI, 4, 2, 2, 1>(a, grid, s); break;
         }
     }
 }
