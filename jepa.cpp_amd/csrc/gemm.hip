@@ -281,9 +281,15 @@ __device__ __forceinline__ void lds_take(V & v) { asm volatile("" : "+v"(v)); }
 // The fields the prologue needs come first as scalar arguments, which the dispatch preloads into SGPRs
 // (-amdgpu-kernarg-preload-count: a struct argument is not preloaded), so that the first copies do
 // not wait on a load of the argument block; the rest of kargs follows in memory (launch: GEMM_ARGS).
-template <int WF, int EPI, int WN, int WM, int TI, int TJ, bool RE = false>
+// EPI_QKV_RE: the QKV epilogue in the form that copies its RoPE rows during the last two K stages
+// (chosen by the launcher, below; its kernels run with EPI = EPI_QKV and RE set).
+constexpr int EPI_QKV_RE = EPI_GELU_Q8_K + 1;
+
+template <int WF, int EPI_, int WN, int WM, int TI, int TJ>
 __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, const void * pB, const void * pAd, const void * pBd,
                                                                int pM, int pN, int pK, int ptn, int ptm, int psplit, kargs a_rest) {
+    constexpr bool RE = EPI_ == EPI_QKV_RE;
+    constexpr int EPI = RE ? EPI_QKV : EPI_;
     kargs a = a_rest;
     a.A = (const _Float16 *) pA; a.B = (const _Float16 *) pB; a.Ad = (const uint16_t *) pAd; a.Bd = pBd;
     a.M = pM; a.N = pN; a.K = pK; a.tn = ptn; a.tm = ptm; a.split = psplit;
@@ -1600,7 +1606,7 @@ int pick_tile(int wf, int64_t N, int64_t M, int need_bn = 0, int split = 1) {
 // k_gemm_mfma's arguments: the prologue's fields as scalars, then the whole kargs
 #define GEMM_ARGS(a) (a).A, (a).B, (const void *) (a).Ad, (a).Bd, (int) (a).M, (int) (a).N, (int) (a).K, (a).tn, (a).tm, (a).split, (a)
 
-// The QKV GEMM of q8_0 / q4_0 weights with heads of 64 runs the RE kernel (RoPE rows copied during the
+// The QKV GEMM of q8_0 / q4_0 weights with heads of 64 runs the EPI_QKV_RE kernel (RoPE rows copied during the
 // last two stages) wherever K is a whole number of at least three stages and the tile has four stage
 // buffers of at least BM rows of 64 floats; elsewhere the rows are copied after the main loop.
 template <int WF, int EPI, int WN, int WM, int TI, int TJ>
@@ -1609,7 +1615,7 @@ void launch_tile(const kargs & a, unsigned grid, hipStream_t s) {
     if constexpr (EPI == EPI_QKV && (WF == W_Q32 || WF == W_Q40) && (T::BM * 64 * 4 / 1024) % T::NW == 0 &&
                   T::BM * 64 * 4 <= T::STAGE && T::NST >= 4) {
         if (a.ep.rope_c && a.ep.rope_s && a.ep.hd == 64 && a.K % T::KC == 0 && a.K / T::KC >= 3) {
-            k_gemm_mfma<WF, EPI, WN, WM, TI, TJ, true><<<grid, T::NT, 0, s>>>(GEMM_ARGS(a));
+            k_gemm_mfma<WF, EPI_QKV_RE, WN, WM, TI, TJ><<<grid, T::NT, 0, s>>>(GEMM_ARGS(a));
             return;
         }
     }
