@@ -143,19 +143,22 @@ def test_tiny_f16_split_residual_with_layer_scale(jlib, oracle, models_dir):
     assert not np.array_equal(got, unsplit)   # the forced split did run
 
 
-@pytest.mark.parametrize("ftype,tiles", [("q8_0", [0, 1, 2, 3, 4, 5, 6]), ("q4_0", [0, 2, 3, 5, 6, 8])])
-def test_qkv_rope_rows_on_every_tile(jlib, oracle, models_dir, ftype, tiles):
+@pytest.mark.parametrize("ftype,tiles,n_reg", [("q8_0", [0, 1, 2, 3, 4, 5, 6], 0), ("q4_0", [0, 2, 3, 5, 6, 8], 0),
+                                              ("q8_0", [1, 4], 2)])
+def test_qkv_rope_rows_on_every_tile(jlib, oracle, models_dir, ftype, tiles, n_reg):
     """The QKV GEMM of q8_0 / q4_0 weights with heads of 64 copies the RoPE rows of its tokens during its
     last two K stages on tiles with four stage buffers of at least BM rows of 64 floats (q8_0 tiles 1, 2,
     3, 5, 6; q4_0 tiles 0, 5, 6, 8), and after the main loop on the others (q8_0 tiles 0, 4; q4_0 tiles
     2, 3). A V-JEPA 2 model of width 512 (K = 512: four stages; N = 1536, which every tile width
     divides), three clips of 72 tokens in one call (216 rows: ragged against 64 and 128, the table rows
     wrapping per clip): the automatic choice passes the oracle's gates, and every forced tile gives
-    the same bits (the block-quantized GEMMs sum in the same order on every tile)."""
-    cfg = forge.tiny("vjepa2", ftype, embed_dim=512, n_head=8, ffn_dim=1024, ln_random=True)
+    the same bits (the block-quantized GEMMs sum in the same order on every tile). With two register
+    tokens each clip has 74 rows, the first two with identity RoPE rows (tile 1 copies the rows early,
+    tile 4 late)."""
+    cfg = forge.tiny("vjepa2", ftype, embed_dim=512, n_head=8, ffn_dim=1024, ln_random=True, n_registers=n_reg)
     got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 3, 4, 96)
-    assert got.shape[0] == 216
-    check_parity(got, want, gtr, wtr, label=f"vjepa2 {ftype} width 512")
+    assert got.shape[0] == 3 * (72 + n_reg)
+    check_parity(got, want, gtr, wtr, label=f"vjepa2 {ftype} width 512, {n_reg} registers")
     L = jlib.lib()
     for t in tiles:
         print(f"{ftype}: tile {t}", flush=True)
