@@ -630,8 +630,8 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void k_gemm_mfma(const void * pA, 
         auto body = [&](int64_t st, auto cross_c, auto first_c, auto extra_c) {
             constexpr bool CROSS = decltype(cross_c)::value, FIRST = decltype(first_c)::value;
             constexpr int Q = FIRST ? (NST - 1) * P1 : P1;          // copies this stage issues
-            // copies younger than the last one of stage st+1 at its publication (step U-2)
-            // copies issued before this body that are younger than stage st+1's (the RoPE rows)
+            // copies younger than the last one of stage st+1 at its publication (step U-2); extra_c
+            // counts those issued just before this body (the RoPE rows of the RE kernels)
             constexpr int NB = (FIRST ? (U - 1) * Q / U - P1 : NBAR) + decltype(extra_c)::value;
             static_assert(NB >= 0 && NB < 64, "barrier count");
             const unsigned char * base = smem + (int) (st % NST) * T::STAGE;
