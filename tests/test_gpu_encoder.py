@@ -171,6 +171,27 @@ def test_qkv_rope_rows_on_every_tile(jlib, oracle, models_dir, ftype, tiles, n_r
         assert d.size == 0, (t, len(d), d[:4].tolist(), float(np.abs(y - got).max()))
 
 
+def test_qkv_rope_rows_vitl_width(jlib, oracle, models_dir):
+    """The ViT-L block shape (width 1024, 16 heads of 64, FFN 4096, one 16-frame 256x256 clip of 2048
+    tokens; two layers): the automatic QKV tile (192x128, RoPE rows copied during the last two of its
+    eight K stages) against the oracle's gates, and bit-identical to the 256x128 and 64x128 tiles,
+    which copy the rows after the main loop."""
+    cfg = forge.tiny("vjepa2", "q8_0", embed_dim=1024, n_head=16, ffn_dim=4096, img_size=256, n_frames=16, ln_random=True)
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 1, 16, 256)
+    assert got.shape == (2048, 1024)
+    check_parity(got, want, gtr, wtr, label="vjepa2 q8_0 ViT-L width, 2 layers")
+    L = jlib.lib()
+    for t in (0, 4):
+        print(f"tile {t}", flush=True)
+        assert L.jepa_amd_gemm_tile(t) == 0
+        try:
+            y = jlib.Context(m).encode(x)
+        finally:
+            L.jepa_amd_gemm_tile(-1)
+        d = np.argwhere(y.view(np.uint32) != got.view(np.uint32))
+        assert d.size == 0, (t, len(d), d[:4].tolist(), float(np.abs(y - got).max()))
+
+
 def test_batch_equals_single(jlib, models_dir):
     """Items of one call equal separate calls bit for bit (reference tests/test-batch.cpp:12-21): q8_0, whose
     K halves depend on the shape only, and every clip of a video model (the reference runs a graph per
