@@ -171,6 +171,18 @@ def test_qkv_rope_rows_on_every_tile(jlib, oracle, models_dir, ftype, tiles, n_r
         assert d.size == 0, (t, len(d), d[:4].tolist(), float(np.abs(y - got).max()))
 
 
+@pytest.mark.parametrize("parts", ["q8_0+b,f16+b,q8_0+b", "q4_0+b,q8_0,q8_0+b"])
+def test_qkv_rope_rows_separate_parts(jlib, oracle, models_dir, parts):
+    """Separate q / k / v linears of width 512 (K = 512: four stages) whose types differ, so each runs as
+    its own GEMM writing its columns of the Q / K / V^T layout: the q8_0 / q4_0 parts copy their RoPE
+    rows early, the Q part from column 0, the K part from column D, and the V part (no RoPE) from
+    column 2 D, through empty resources. Against the oracle, which runs the three linears one by one."""
+    cfg = forge.tiny("vjepa2", "q8_0", embed_dim=512, n_head=8, ffn_dim=1024, ln_random=True, qkv_fused=False,
+                     qkv_parts=parts)
+    got, want, gtr, wtr, m, ctx, x = _case(jlib, oracle, models_dir, cfg, 3, 4, 96)
+    check_parity(got, want, gtr, wtr, label=f"vjepa2 width 512, separate q/k/v {parts}")
+
+
 def test_qkv_rope_rows_vitl_width(jlib, oracle, models_dir):
     """The ViT-L block shape (width 1024, 16 heads of 64, FFN 4096, one 16-frame 256x256 clip of 2048
     tokens; two layers): the automatic QKV tile (192x128, RoPE rows copied during the last two of its
